@@ -1,0 +1,159 @@
+/*
+ * vllm_musa_amd.h -- C ABI of the MI355X (gfx950) quantized-MoE / block-fp8
+ * matmul library (libvllm_musa_amd.so).
+ *
+ * Conventions (shared by every entry point):
+ *   - Pointers are device pointers (hipMalloc'd or torch CUDA tensors);
+ *     sizes are element counts; row-major, innermost stride 1 unless a
+ *     stride argument says otherwise.
+ *   - Work is enqueued on `stream` (a hipStream_t); nothing synchronises
+ *     the host and no entry point allocates device memory.  Scratch memory,
+ *     where needed, is passed in and sized by the matching *_workspace_size().
+ *   - Each call returns VMAMD_OK (0) or an error code; the message of the
+ *     last failure on the calling thread is returned by vmamd_last_error().
+ *   - fp8 means OCP float8 e4m3fn (one byte per value); bf16 and f16 are
+ *     passed as their 16-bit patterns.
+ *
+ * Each declaration names the reference interface (MooreThreads/vllm-musa,
+ * file:line) that it replaces.
+ */
+#ifndef VLLM_MUSA_AMD_H_
+#define VLLM_MUSA_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* vmamd_stream_t; /* == hipStream_t */
+
+#define VMAMD_OK 0
+#define VMAMD_ERR_INVALID 1 /* bad argument: shape, dtype, alignment, size */
+#define VMAMD_ERR_HIP 2     /* a HIP runtime call or kernel launch failed   */
+
+#define VMAMD_DTYPE_F32 0
+#define VMAMD_DTYPE_F16 1
+#define VMAMD_DTYPE_BF16 2
+
+/* Message of the last error on this thread ("" if none). */
+const char* vmamd_last_error(void);
+/* ABI version of the library (bumped on incompatible changes). */
+int vmamd_abi_version(void);
+
+/* ------------------------------------------------------------ quantizers --
+ * Per-token-group fp8 quantisation of activations:
+ *   s[r,g] = max(eps, max_{c in g} |x[r,c]|) / fp8_max
+ *   q[r,c] = e4m3fn(clamp(x[r,c] / s[r,g], fp8_min, fp8_max))
+ * x: [rows, cols] (bf16/f16/f32, row stride x_row_stride elements), q: [rows,
+ * cols] contiguous fp8, s: scale of (row r, group g) at
+ * s[r*s_stride_row + g*s_stride_group] (row-major: (cols/group, 1);
+ * column-major: (1, rows)).  group_size must be 128.
+ * Replaces per_token_group_quant_8bit_vec
+ * (csrc/musa/quantization/per_token_group_quant_8bit_vec.cu:111-178) and the
+ * Python per_token_group_quant_fp8
+ * (vllm_musa/model_executor/layers/quantization/utils/fp8_utils.py:33-152).
+ */
+int vmamd_per_token_group_quant_fp8(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                                    int64_t x_row_stride, int group_size, float eps,
+                                    float fp8_min, float fp8_max, void* q, float* s,
+                                    int64_t s_stride_row, int64_t s_stride_group,
+                                    vmamd_stream_t stream);
+
+/* out[r, c] = silu(x[r, c]) * x[r, d + c] rounded to the activation dtype;
+ * x: [rows, 2d], out: [rows, d].  Replaces torch.ops._C.silu_and_mul /
+ * maybe_fast_silu_and_mul (vllm_musa/jit_kernel/csrc/moe.py:102-116). */
+int vmamd_silu_and_mul(const void* x, int dtype, int64_t rows, int64_t d, void* out,
+                       vmamd_stream_t stream);
+
+/* SiLU-and-mul fused with the 1x128 fp8 group quantiser.  The product is
+ * rounded to the activation dtype before quantisation.  swiglu_limit > 0
+ * clamps gate <= L and up to [-L, L] (L rounded to the activation dtype).
+ * x: [rows, 2d]; q: [rows, d] fp8; s: [rows, d/128] f32 row-major.
+ * Replaces silu_and_mul_per_token_group_fp8_quant and
+ * silu_and_mul_clamp_per_token_group_fp8_quant
+ * (csrc/musa/quantization/silu_and_mul_per_token_group_fp8_quant.cu:133-213). */
+int vmamd_silu_and_mul_quant_fp8(const void* x, int dtype, int64_t rows, int64_t d,
+                                 int group_size, float eps, float fp8_min, float fp8_max,
+                                 float swiglu_limit, void* q, float* s, vmamd_stream_t stream);
+
+/* ---------------------------------------------------------------- routing --
+ * Softmax top-k.  l' = gating (+ bias[e] if bias != NULL), optionally
+ * soft-capped (softcap > 0: l' = tanh(l'/softcap)*softcap).  ids = the top-k
+ * of l' in descending order, ties to the lower expert id; weights =
+ * softmax(l')[ids], renormalised over the selection when renormalize != 0.
+ * gating: [tokens, experts] f32/f16/bf16; weights f32 and ids i32 [tokens, topk].
+ * experts <= 1024.  Replaces topk_softmax
+ * (vllm_musa/jit_kernel/csrc/topk.py:211-242; kernels
+ * jit_kernel/csrc/topk/topk_gating.mu:63-147, 458-529, 612-702). */
+int vmamd_topk_softmax(const void* gating, int dtype, int64_t tokens, int experts, int topk,
+                       int renormalize, float softcap, const float* bias, float* topk_weights,
+                       int32_t* topk_ids, vmamd_stream_t stream);
+
+/* Sigmoid top-k.  s = sigmoid(gating); ids = top-k of s (+ bias), ties to the
+ * lower id; weights = s[ids], renormalised when renormalize != 0.  Replaces
+ * topk_sigmoid (vllm_musa/jit_kernel/csrc/topk.py:245-275). */
+int vmamd_topk_sigmoid(const void* gating, int dtype, int64_t tokens, int experts, int topk,
+                       int renormalize, const float* bias, float* topk_weights,
+                       int32_t* topk_ids, vmamd_stream_t stream);
+
+#define VMAMD_SCORING_SOFTMAX 0
+#define VMAMD_SCORING_SIGMOID 1
+
+/* Grouped top-k (DeepSeek-V3 routing).  scores = softmax or sigmoid of the
+ * gating row; sel = scores + bias (bias may be NULL); group score = sum of
+ * the top-2 sel in the group when bias != NULL, else the group max; keep the
+ * topk_group best groups (ties to the lower group); ids = top-k of sel over
+ * the kept groups (ties to the lower id); weights = scores[ids], renormalised
+ * when renormalize != 0, times routed_scaling_factor.  experts <= 1024,
+ * experts % num_expert_group == 0, experts / num_expert_group <= 64.
+ * Replaces grouped_topk / _grouped_topk_general
+ * (vllm_musa/model_executor/layers/fused_moe/router/grouped_topk_router.py:257-357,
+ * 388-469) and the MATE moe_fused_gate call it makes (277-303). */
+int vmamd_grouped_topk(const void* gating, int dtype, int64_t tokens, int experts,
+                       int num_expert_group, int topk_group, int topk, int renormalize,
+                       int scoring, float routed_scaling_factor, const float* bias,
+                       float* topk_weights, int32_t* topk_ids, vmamd_stream_t stream);
+
+/* ------------------------------------------------------------ align/sort --
+ * moe_align_block_size.  Routes r = 0..numel-1 (r = token*topk + slot) are
+ * grouped by expert (after expert_map, if given: entries < 0 drop the route;
+ * ids >= num_experts are dropped too); each expert's segment is padded to a
+ * multiple of block_size.  Within a segment routes keep ascending r.
+ *   sorted_token_ids[0..capacity): route ids, padding = numel;
+ *   expert_ids[b]: expert of block b, -1 past the used blocks
+ *                  (array length ceil(capacity / block_size));
+ *   num_tokens_post_pad[0] = sum_e ceil(cnt_e / block_size) * block_size;
+ *   expert_offsets (optional, length num_experts + 1): segment starts;
+ *   scatter_idx (optional, length numel): position of route r in
+ *                sorted_token_ids, -1 for dropped routes.
+ * capacity must be >= numel + num_experts * (block_size - 1).
+ * num_experts <= 1024.  Replaces moe_align_block_size
+ * (schema: vllm_musa/patches/series/0041-MUSA-MUSA-csrc-csrc-moe-torch_bindings.cpp.patch:36-58;
+ * signature: 0048-MUSA-MUSA-csrc-csrc-moe-moe_align_sum_kernels.cu.patch:49-56). */
+int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int num_experts,
+                               int block_size, const int32_t* expert_map,
+                               int64_t expert_map_len, int32_t* sorted_token_ids,
+                               int64_t capacity, int32_t* expert_ids,
+                               int32_t* num_tokens_post_pad, int32_t* expert_offsets,
+                               int32_t* scatter_idx, vmamd_stream_t stream);
+
+/* ---------------------------------------------------------------- combine --
+ * out[t, h] = round(sum_{k<topk} x[t, k, h]) with an fp32 accumulator in slot
+ * order.  x: [tokens, topk, hidden], out: [tokens, hidden], same dtype.
+ * topk_ids (optional, [tokens, topk] i32): slots with a negative id, or an id
+ * that expert_map (optional, length expert_map_len) maps to a negative local
+ * id, are skipped.
+ * Replaces moe_sum (0041-…torch_bindings.cpp.patch:44-50) and
+ * maybe_fast_moe_sum (vllm_musa/jit_kernel/csrc/moe.py:119-133;
+ * jit_kernel/csrc/moe/moe_sum_reduce.mu:104-147). */
+int vmamd_moe_sum(const void* x, int dtype, int64_t tokens, int topk, int64_t hidden,
+                  const int32_t* topk_ids, const int32_t* expert_map, int64_t expert_map_len,
+                  void* out, vmamd_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VLLM_MUSA_AMD_H_ */

@@ -1,0 +1,51 @@
+"""The C-ABI library: it loads, exports every symbol include/vllm_musa_amd.h
+declares, and its argument checks reject bad calls before touching a GPU."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "vllm_musa_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(vmamd_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "vmamd_last_error" in names and len(names) >= 8
+
+
+def test_library_exports_every_declared_symbol():
+    from vllm_musa_amd import _lib
+    lib = _lib.load()
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    # the Python binding describes every declared entry point
+    assert set(_declared()) == set(_lib.SIGNATURES)
+
+
+def test_abi_version():
+    from vllm_musa_amd import _lib
+    assert _lib.load().vmamd_abi_version() >= 1
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    from vllm_musa_amd import _lib
+    with pytest.raises(ValueError, match="experts must be in"):
+        _lib.call("vmamd_topk_softmax", None, 2, 4, 0, 1, 0, 0.0, None, None, None, None)
+    with pytest.raises(ValueError, match="group_size must be 128"):
+        _lib.call("vmamd_per_token_group_quant_fp8", None, 2, 1, 128, 128, 64, 1e-10, -448.0,
+                  448.0, None, None, 1, 1, None)
+    with pytest.raises(ValueError, match="capacity"):
+        _lib.call("vmamd_moe_align_block_size", None, 100, 8, 16, None, 0, None, 10, None, None,
+                  None, None, None)
+    msg = _lib.load().vmamd_last_error().decode()
+    assert "capacity" in msg

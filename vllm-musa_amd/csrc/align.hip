@@ -1,0 +1,170 @@
+// moe_align_block_size: group routes by expert, pad each expert's segment to
+// a multiple of the block size, and keep ascending route order inside each
+// segment (a stable counting sort), so the result is deterministic.
+//
+// One 1024-thread workgroup does the whole job:
+//   1. LDS histogram of the (mapped) expert ids;
+//   2. block-wide exclusive scan of the padded counts -> segment bases;
+//   3. stable placement, 1024 routes per step: the rank of a route among the
+//      same-expert routes of its wave comes from bit-sliced ballots (one
+//      64-bit ballot per expert-id bit, no loops over lanes), the rank across
+//      the 16 waves of the step from a [wave][expert] count table in LDS, and
+//      the rank across steps from a running per-expert counter.
+// Every position of sorted_token_ids that no route takes is written with the
+// sentinel `numel` exactly once, so no ordering between writers is needed.
+#include "common.h"
+
+namespace vmamd {
+
+constexpr int kAlignThreads = 1024;
+constexpr int kAlignWaves = kAlignThreads / kWave;  // 16
+constexpr int kMaxAlignExperts = 1024;
+
+__device__ __forceinline__ int mapped_expert(const int32_t* __restrict__ ids, int64_t r, int E,
+                                             const int32_t* __restrict__ map, int64_t map_len) {
+  int e = ids[r];
+  if (map) {
+    if (e < 0 || e >= map_len) return -1;
+    e = map[e];
+  }
+  return (e >= 0 && e < E) ? e : -1;
+}
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int E, int bs, const int32_t* __restrict__ map,
+    int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out, int32_t* __restrict__ scatter_idx) {
+  __shared__ int cnt[kMaxAlignExperts];
+  __shared__ int base[kMaxAlignExperts + 1];
+  __shared__ int run[kMaxAlignExperts];
+  __shared__ uint16_t wcnt[kAlignWaves][kMaxAlignExperts];
+  __shared__ int wave_tot[kAlignWaves];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+
+  for (int e = tid; e < E; e += kAlignThreads) {
+    cnt[e] = 0;
+    run[e] = 0;
+  }
+  __syncthreads();
+
+  // 1. histogram
+  for (int64_t r = tid; r < numel; r += kAlignThreads) {
+    const int e = mapped_expert(ids, r, E, map, map_len);
+    if (e >= 0) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+
+  // 2. exclusive scan of padded counts (E <= 1024: one expert per thread)
+  int padded = 0;
+  if (tid < E) padded = (cnt[tid] + bs - 1) / bs * bs;
+  int incl = padded;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
+  }
+  if (lane == kWave - 1) wave_tot[wave] = incl;
+  __syncthreads();
+  int wave_off = 0;
+  for (int w = 0; w < wave; ++w) wave_off += wave_tot[w];
+  if (tid < E) base[tid] = wave_off + incl - padded;
+  if (tid == kAlignThreads - 1) base[E] = wave_off + incl;  // last thread sees the total
+  __syncthreads();
+  const int total = base[E];
+  if (tid == 0) ntpp[0] = total;
+  if (offsets_out)
+    for (int e = tid; e <= E; e += kAlignThreads) offsets_out[e] = base[e];
+
+  // expert_ids: binary search of the segment holding each block
+  const int64_t nblocks = (capacity + bs - 1) / bs;
+  for (int64_t b = tid; b < nblocks; b += kAlignThreads) {
+    int out = -1;
+    const int64_t pos = b * bs;
+    if (pos < total) {
+      int lo = 0, hi = E - 1;  // largest e with base[e] <= pos
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (base[mid] <= pos) lo = mid; else hi = mid - 1;
+      }
+      out = lo;
+    }
+    expert_ids[b] = out;
+  }
+  // sentinel for the padding of each segment and the unused tail
+  const int32_t sentinel = static_cast<int32_t>(numel);
+  for (int e = tid; e < E; e += kAlignThreads)
+    for (int p = base[e] + cnt[e]; p < base[e + 1]; ++p) sorted[p] = sentinel;
+  for (int64_t p = total + tid; p < capacity; p += kAlignThreads) sorted[p] = sentinel;
+
+  // 3. stable placement
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  for (int64_t c0 = 0; c0 < numel; c0 += kAlignThreads) {
+    for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) wcnt[i / E][i % E] = 0;
+    const int64_t r = c0 + tid;
+    const int e = r < numel ? mapped_expert(ids, r, E, map, map_len) : -1;
+    const bool valid = e >= 0;
+    uint64_t same = ballot(valid);
+#pragma unroll 1
+    for (int b = 0; b < nbits; ++b) {
+      const uint64_t on = ballot(valid && ((e >> b) & 1));
+      same &= ((e >> b) & 1) ? on : ~on;
+    }
+    __syncthreads();
+    const int rank_in_wave = __popcll(same & lt_mask);
+    if (valid && rank_in_wave == 0) wcnt[wave][e] = static_cast<uint16_t>(__popcll(same));
+    __syncthreads();
+    if (valid) {
+      int before = run[e];
+      for (int w = 0; w < wave; ++w) before += wcnt[w][e];
+      const int pos = base[e] + before + rank_in_wave;
+      if (pos < base[e + 1]) {  // always true; keeps a corrupted count from writing out of range
+        sorted[pos] = static_cast<int32_t>(r);
+        if (scatter_idx) scatter_idx[r] = pos;
+      }
+    } else if (r < numel && scatter_idx) {
+      scatter_idx[r] = -1;
+    }
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += kAlignThreads) {
+      int add = 0;
+      for (int w = 0; w < kAlignWaves; ++w) add += wcnt[w][ee];
+      run[ee] += add;
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace vmamd
+
+using namespace vmamd;
+
+extern "C" int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int num_experts,
+                                          int block_size, const int32_t* expert_map,
+                                          int64_t expert_map_len, int32_t* sorted_token_ids,
+                                          int64_t capacity, int32_t* expert_ids,
+                                          int32_t* num_tokens_post_pad, int32_t* expert_offsets,
+                                          int32_t* scatter_idx, vmamd_stream_t stream) {
+  VMAMD_REQUIRE(num_experts > 0 && num_experts <= kMaxAlignExperts,
+                "moe_align_block_size: num_experts must be in [1, %d] (got %d)", kMaxAlignExperts,
+                num_experts);
+  VMAMD_REQUIRE(block_size > 0, "moe_align_block_size: block_size must be positive");
+  VMAMD_REQUIRE(numel >= 0 && numel < (1ll << 31) - 1, "moe_align_block_size: bad numel %lld",
+                (long long)numel);
+  VMAMD_REQUIRE(capacity >= numel + static_cast<int64_t>(num_experts) * (block_size - 1),
+                "moe_align_block_size: capacity %lld < numel + num_experts * (block_size - 1) = %lld",
+                (long long)capacity,
+                (long long)(numel + static_cast<int64_t>(num_experts) * (block_size - 1)));
+  VMAMD_REQUIRE(capacity < (1ll << 31), "moe_align_block_size: capacity too large");
+  VMAMD_REQUIRE(!expert_map || expert_map_len > 0, "moe_align_block_size: empty expert_map");
+  VMAMD_REQUIRE((topk_ids || numel == 0) && sorted_token_ids && expert_ids && num_tokens_post_pad,
+                "moe_align_block_size: null pointer");
+  moe_align_kernel<<<1, kAlignThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      topk_ids, numel, num_experts, block_size, expert_map, expert_map_len, sorted_token_ids,
+      capacity, expert_ids, num_tokens_post_pad, expert_offsets, scatter_idx);
+  return check_launch("moe_align_block_size");
+}

@@ -1,0 +1,348 @@
+// Router top-k kernels: softmax top-k, sigmoid top-k and grouped top-k.
+//
+// One wave64 owns one token row.  Expert e lives in lane e % 64, register
+// slot e / 64, so the row is read with fully coalesced loads and every
+// selection round is a 6-step xor-shuffle argmax (ties to the lower expert
+// id).  Selection never depends on the order of a floating-point reduction:
+//   - softmax top-k selects on the (biased) logits, which softmax preserves;
+//   - sigmoid/softmax scores that feed a selection together with a bias are
+//     evaluated in double precision and rounded once to float, so they are
+//     the correctly rounded float values (up to a ~2^-29 chance per value of
+//     a double-rounding tie), independent of the device's float exp.
+#include <float.h>
+
+#include "common.h"
+
+namespace vmamd {
+
+constexpr int kRouteWaves = 4;  // token rows per 256-thread block
+
+template <int DT>
+__device__ __forceinline__ float load_gate(const void* g, int64_t i) {
+  return Elem<DT>::load(static_cast<const typename Elem<DT>::T*>(g), i);
+}
+
+// Correctly rounded (to float) logistic function, evaluated in double.
+__device__ __forceinline__ float sigmoid_cr(float x) {
+  return static_cast<float>(1.0 / (1.0 + exp(-static_cast<double>(x))));
+}
+
+// One selection round over the live entries of a wave: returns the winning
+// (value, expert id) to every lane and retires the winner in its owner lane.
+template <int VPT>
+__device__ __forceinline__ int select_round(const float (&v)[VPT], uint32_t& alive, float& best) {
+  const int lane = lane_id();
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const bool live = (alive >> i) & 1u;
+    // Lower slot index means lower expert id, so strict '>' keeps ties low.
+    if (live && (v[i] > bv || bi == 0x7fffffff)) {
+      bv = v[i];
+      bi = lane + kWave * i;
+    }
+  }
+  wave_argmax(bv, bi);
+  if (bi != 0x7fffffff && (bi % kWave) == lane) alive &= ~(1u << (bi / kWave));
+  best = bv;
+  return bi;
+}
+
+// ------------------------------------------------------- softmax top-k ----
+template <int DT, int VPT>
+__global__ __launch_bounds__(kRouteWaves * kWave) void topk_softmax_kernel(
+    const void* __restrict__ gating, int64_t tokens, int experts, int topk, bool renorm,
+    float softcap, const float* __restrict__ bias, float* __restrict__ w_out,
+    int32_t* __restrict__ id_out) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRouteWaves + threadIdx.x / kWave;
+  if (row >= tokens) return;
+  const int lane = lane_id();
+  float v[VPT];
+  uint32_t alive = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e = lane + kWave * i;
+    v[i] = -INFINITY;
+    if (e < experts) {
+      float x = load_gate<DT>(gating, row * experts + e);
+      if (bias) x += bias[e];
+      if (softcap > 0.f) x = tanhf(x / softcap) * softcap;
+      v[i] = x;
+      alive |= 1u << i;
+    }
+  }
+  // Row max is the first selected value; softmax denominators use it.
+  float first = 0.f, chosen_sum = 0.f, my_w = 0.f;
+  int my_id = 0;
+  for (int k = 0; k < topk; ++k) {
+    float bv;
+    const int bi = select_round<VPT>(v, alive, bv);
+    if (k == 0) first = bv;
+    const float ek = expf(bv - first);
+    chosen_sum += ek;  // fixed order k = 0, 1, ... in every lane
+    if (lane == k) {
+      my_w = ek;
+      my_id = bi;
+    }
+  }
+  float denom = chosen_sum;
+  if (!renorm) {
+    // Full softmax denominator over all experts.
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      if (lane + kWave * i < experts) part += expf(v[i] - first);
+    // Retired entries still hold their logits in v[], so the sum is complete.
+    denom = wave_sum(part);
+  }
+  if (lane < topk) {
+    w_out[row * topk + lane] = my_w / denom;
+    id_out[row * topk + lane] = my_id;
+  }
+}
+
+// ------------------------------------------------------- sigmoid top-k ----
+template <int DT, int VPT>
+__global__ __launch_bounds__(kRouteWaves * kWave) void topk_sigmoid_kernel(
+    const void* __restrict__ gating, int64_t tokens, int experts, int topk, bool renorm,
+    const float* __restrict__ bias, float* __restrict__ w_out, int32_t* __restrict__ id_out) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRouteWaves + threadIdx.x / kWave;
+  if (row >= tokens) return;
+  const int lane = lane_id();
+  float sel[VPT], sc[VPT];
+  uint32_t alive = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e = lane + kWave * i;
+    sel[i] = -INFINITY;
+    sc[i] = 0.f;
+    if (e < experts) {
+      const float s = sigmoid_cr(load_gate<DT>(gating, row * experts + e));
+      sc[i] = s;
+      sel[i] = bias ? s + bias[e] : s;
+      alive |= 1u << i;
+    }
+  }
+  float my_w = 0.f, sum = 0.f;
+  int my_id = 0;
+  for (int k = 0; k < topk; ++k) {
+    float bv;
+    const int bi = select_round<VPT>(sel, alive, bv);
+    // Fetch the unbiased score of the winner from its owner lane.
+    float s_local = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      if (lane + kWave * i == bi) s_local = sc[i];
+    const float s = __shfl(s_local, bi % kWave, kWave);
+    sum += s;
+    if (lane == k) {
+      my_w = s;
+      my_id = bi;
+    }
+  }
+  if (lane < topk) {
+    w_out[row * topk + lane] = renorm ? my_w / sum : my_w;
+    id_out[row * topk + lane] = my_id;
+  }
+}
+
+// ------------------------------------------------------- grouped top-k ----
+// Scores per expert (softmax or sigmoid, double-evaluated), sel = score (+
+// bias); group g is the S = experts / groups consecutive experts g*S..g*S+S-1.
+template <int DT, int VPT>
+__global__ __launch_bounds__(kRouteWaves * kWave) void grouped_topk_kernel(
+    const void* __restrict__ gating, int64_t tokens, int experts, int groups, int topk_group,
+    int topk, bool renorm, int scoring, float scale, const float* __restrict__ bias,
+    float* __restrict__ w_out, int32_t* __restrict__ id_out) {
+  const int wave = threadIdx.x / kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRouteWaves + wave;
+  if (row >= tokens) return;
+  const int lane = lane_id();
+  const int gsize = experts / groups;
+
+  float logit[VPT], sc[VPT], sel[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e = lane + kWave * i;
+    logit[i] = e < experts ? load_gate<DT>(gating, row * experts + e) : -INFINITY;
+  }
+  if (scoring == VMAMD_SCORING_SOFTMAX) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) m = fmaxf(m, logit[i]);
+    m = wave_max(m);
+    double part = 0.0;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      if (lane + kWave * i < experts) part += exp(static_cast<double>(logit[i]) - m);
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) part += __shfl_xor(part, s, kWave);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      sc[i] = lane + kWave * i < experts
+                  ? static_cast<float>(exp(static_cast<double>(logit[i]) - m) / part)
+                  : 0.f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) sc[i] = lane + kWave * i < experts ? sigmoid_cr(logit[i]) : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e = lane + kWave * i;
+    sel[i] = e < experts ? (bias ? sc[i] + bias[e] : sc[i]) : -INFINITY;
+  }
+
+  // Group scores: the members of each group are broadcast in turn, so every
+  // lane holds the same (t1, t2) and lane g keeps the score of group g.
+  float gv = -INFINITY;
+  for (int g = 0; g < groups; ++g) {
+    float t1 = -INFINITY, t2 = -INFINITY;
+    for (int j = 0; j < gsize; ++j) {
+      const int e = g * gsize + j;
+      float mine = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+        if (lane + kWave * i == e) mine = sel[i];
+      const float x = __shfl(mine, e % kWave, kWave);
+      if (x > t1) {
+        t2 = t1;
+        t1 = x;
+      } else if (x > t2) {
+        t2 = x;
+      }
+    }
+    if (lane == g) gv = bias ? t1 + t2 : t1;
+  }
+  uint64_t keep = 0;  // bit g set when group g is kept
+  {
+    uint32_t alive_g = lane < groups ? 1u : 0u;
+    float gsel[1] = {gv};
+    for (int k = 0; k < topk_group; ++k) {
+      float bv;
+      const int bg = select_round<1>(gsel, alive_g, bv);
+      keep |= 1ull << bg;
+    }
+  }
+  uint32_t alive = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e = lane + kWave * i;
+    if (e < experts && ((keep >> (e / gsize)) & 1ull)) alive |= 1u << i;
+  }
+  float my_w = 0.f, sum = 0.f;
+  int my_id = 0;
+  for (int k = 0; k < topk; ++k) {
+    float bv;
+    const int bi = select_round<VPT>(sel, alive, bv);
+    float s_local = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      if (lane + kWave * i == bi) s_local = sc[i];
+    const float s = __shfl(s_local, bi % kWave, kWave);
+    sum += s;
+    if (lane == k) {
+      my_w = s;
+      my_id = bi;
+    }
+  }
+  if (lane < topk) {
+    float w = renorm ? my_w / sum : my_w;
+    if (scale != 1.0f) w *= scale;
+    w_out[row * topk + lane] = w;
+    id_out[row * topk + lane] = my_id;
+  }
+}
+
+static int vpt_for(int experts) {
+  if (experts <= 64) return 1;
+  if (experts <= 128) return 2;
+  if (experts <= 256) return 4;
+  if (experts <= 512) return 8;
+  return 16;
+}
+
+}  // namespace vmamd
+
+using namespace vmamd;
+
+#define VMAMD_ROUTE_DISPATCH(KERNEL, ...)                                                      \
+  do {                                                                                        \
+    const int vpt_ = vpt_for(experts);                                                        \
+    const int64_t blocks_ = (tokens + kRouteWaves - 1) / kRouteWaves;                         \
+    hipStream_t st_ = reinterpret_cast<hipStream_t>(stream);                                  \
+    switch (dtype * 32 + vpt_) {                                                              \
+      case kF32 * 32 + 1: KERNEL<kF32, 1><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;      \
+      case kF32 * 32 + 2: KERNEL<kF32, 2><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;      \
+      case kF32 * 32 + 4: KERNEL<kF32, 4><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;      \
+      case kF32 * 32 + 8: KERNEL<kF32, 8><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;      \
+      case kF32 * 32 + 16: KERNEL<kF32, 16><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;    \
+      case kF16 * 32 + 1: KERNEL<kF16, 1><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;      \
+      case kF16 * 32 + 2: KERNEL<kF16, 2><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;      \
+      case kF16 * 32 + 4: KERNEL<kF16, 4><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;      \
+      case kF16 * 32 + 8: KERNEL<kF16, 8><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;      \
+      case kF16 * 32 + 16: KERNEL<kF16, 16><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;    \
+      case kBF16 * 32 + 1: KERNEL<kBF16, 1><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;    \
+      case kBF16 * 32 + 2: KERNEL<kBF16, 2><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;    \
+      case kBF16 * 32 + 4: KERNEL<kBF16, 4><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;    \
+      case kBF16 * 32 + 8: KERNEL<kBF16, 8><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;    \
+      case kBF16 * 32 + 16: KERNEL<kBF16, 16><<<blocks_, 256, 0, st_>>>(__VA_ARGS__); break;  \
+      default: VMAMD_REQUIRE(false, #KERNEL ": unsupported dtype %d", dtype);                 \
+    }                                                                                         \
+  } while (0)
+
+extern "C" int vmamd_topk_softmax(const void* gating, int dtype, int64_t tokens, int experts,
+                                  int topk, int renormalize, float softcap, const float* bias,
+                                  float* topk_weights, int32_t* topk_ids, vmamd_stream_t stream) {
+  VMAMD_REQUIRE(experts > 0 && experts <= 1024, "topk_softmax: experts must be in [1, 1024] (got %d)",
+                experts);
+  VMAMD_REQUIRE(topk > 0 && topk <= experts && topk <= 64,
+                "topk_softmax: topk must be in [1, min(experts, 64)] (got %d)", topk);
+  VMAMD_REQUIRE(tokens >= 0, "topk_softmax: negative token count");
+  if (tokens == 0) return VMAMD_OK;
+  VMAMD_REQUIRE(gating && topk_weights && topk_ids, "topk_softmax: null pointer");
+  VMAMD_ROUTE_DISPATCH(topk_softmax_kernel, gating, tokens, experts, topk, renormalize != 0, softcap,
+                       bias, topk_weights, topk_ids);
+  return check_launch("topk_softmax");
+}
+
+extern "C" int vmamd_topk_sigmoid(const void* gating, int dtype, int64_t tokens, int experts,
+                                  int topk, int renormalize, const float* bias, float* topk_weights,
+                                  int32_t* topk_ids, vmamd_stream_t stream) {
+  VMAMD_REQUIRE(experts > 0 && experts <= 1024, "topk_sigmoid: experts must be in [1, 1024] (got %d)",
+                experts);
+  VMAMD_REQUIRE(topk > 0 && topk <= experts && topk <= 64,
+                "topk_sigmoid: topk must be in [1, min(experts, 64)] (got %d)", topk);
+  VMAMD_REQUIRE(tokens >= 0, "topk_sigmoid: negative token count");
+  if (tokens == 0) return VMAMD_OK;
+  VMAMD_REQUIRE(gating && topk_weights && topk_ids, "topk_sigmoid: null pointer");
+  VMAMD_ROUTE_DISPATCH(topk_sigmoid_kernel, gating, tokens, experts, topk, renormalize != 0, bias,
+                       topk_weights, topk_ids);
+  return check_launch("topk_sigmoid");
+}
+
+extern "C" int vmamd_grouped_topk(const void* gating, int dtype, int64_t tokens, int experts,
+                                  int num_expert_group, int topk_group, int topk, int renormalize,
+                                  int scoring, float routed_scaling_factor, const float* bias,
+                                  float* topk_weights, int32_t* topk_ids, vmamd_stream_t stream) {
+  VMAMD_REQUIRE(experts > 0 && experts <= 1024, "grouped_topk: experts must be in [1, 1024] (got %d)",
+                experts);
+  VMAMD_REQUIRE(num_expert_group > 0 && num_expert_group <= 64 && experts % num_expert_group == 0,
+                "grouped_topk: experts (%d) must split into 1..64 equal groups (got %d)", experts,
+                num_expert_group);
+  VMAMD_REQUIRE(topk_group > 0 && topk_group <= num_expert_group,
+                "grouped_topk: topk_group must be in [1, num_expert_group] (got %d)", topk_group);
+  VMAMD_REQUIRE(topk > 0 && topk <= 64 && topk <= topk_group * (experts / num_expert_group),
+                "grouped_topk: topk (%d) exceeds the experts of the kept groups", topk);
+  VMAMD_REQUIRE(!bias || experts / num_expert_group >= 2,
+                "grouped_topk: the biased group score needs at least 2 experts per group");
+  VMAMD_REQUIRE(scoring == VMAMD_SCORING_SOFTMAX || scoring == VMAMD_SCORING_SIGMOID,
+                "grouped_topk: unknown scoring function %d", scoring);
+  VMAMD_REQUIRE(tokens >= 0, "grouped_topk: negative token count");
+  if (tokens == 0) return VMAMD_OK;
+  VMAMD_REQUIRE(gating && topk_weights && topk_ids, "grouped_topk: null pointer");
+  VMAMD_ROUTE_DISPATCH(grouped_topk_kernel, gating, tokens, experts, num_expert_group, topk_group,
+                       topk, renormalize != 0, scoring, routed_scaling_factor, bias, topk_weights,
+                       topk_ids);
+  return check_launch("grouped_topk");
+}

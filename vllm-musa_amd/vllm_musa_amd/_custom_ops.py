@@ -1,0 +1,202 @@
+"""torch-facing wrappers of the C ABI with the reference's op signatures.
+
+Outputs are caller-allocated and written in place, as the reference's
+``Tensor!`` schemas (csrc/musa/torch_bindings.cpp:9-273, and the upstream
+``_moe_C`` schemas restated in
+vllm_musa/patches/series/0041-MUSA-MUSA-csrc-csrc-moe-torch_bindings.cpp.patch:20-58).
+Every call launches on torch's current stream and never synchronises.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import call, check_cuda, dtype_code, ptr, stream_of
+
+FP8_DTYPE = torch.float8_e4m3fn
+FP8_MAX = float(torch.finfo(FP8_DTYPE).max)  # 448
+FP8_MIN = -FP8_MAX
+
+
+def _contig(t: torch.Tensor, name: str) -> None:
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+# ------------------------------------------------------------- quantisers --
+def per_token_group_quant_8bit_vec(input: torch.Tensor, output_q: torch.Tensor,
+                                   output_s: torch.Tensor, group_size: int, eps: float,
+                                   min_8bit: float, max_8bit: float) -> None:
+    """Reference: per_token_group_quant_8bit_vec
+    (csrc/musa/quantization/per_token_group_quant_8bit_vec.cu:111-178).  Row- or
+    column-major scales are taken from output_s's strides."""
+    check_cuda(input, output_q, output_s)
+    if input.dim() != 2 or output_s.dim() != 2:
+        raise ValueError("per_token_group_quant_8bit_vec expects 2-D input and scales")
+    if input.stride(-1) != 1:
+        raise ValueError("input groups must be contiguous")
+    _contig(output_q, "output_q")
+    if output_q.dtype != FP8_DTYPE or output_s.dtype != torch.float32:
+        raise ValueError("output_q must be float8_e4m3fn and output_s float32")
+    rows, cols = input.shape
+    if tuple(output_q.shape) != (rows, cols) or tuple(output_s.shape) != (rows, cols // group_size):
+        raise ValueError("output shapes do not match the input")
+    call("vmamd_per_token_group_quant_fp8", ptr(input), dtype_code(input.dtype), rows, cols,
+         input.stride(0), group_size, eps, min_8bit, max_8bit, ptr(output_q), ptr(output_s),
+         output_s.stride(0), output_s.stride(1), stream_of(input))
+
+
+def silu_and_mul(out: torch.Tensor, x: torch.Tensor) -> None:
+    """Reference: torch.ops._C.silu_and_mul(out, x) / maybe_fast_silu_and_mul
+    (vllm_musa/jit_kernel/csrc/moe.py:102-116)."""
+    check_cuda(out, x)
+    _contig(x, "x")
+    _contig(out, "out")
+    d = x.shape[-1] // 2
+    if out.shape[-1] != d or out.dtype != x.dtype or x.numel() != 2 * out.numel():
+        raise ValueError("silu_and_mul: out must be x[..., :d]-shaped with x's dtype")
+    call("vmamd_silu_and_mul", ptr(x), dtype_code(x.dtype), x.numel() // (2 * d) if d else 0, d,
+         ptr(out), stream_of(x))
+
+
+def _silu_quant(input, output_q, output_s, group_size, eps, fp8_min, fp8_max, limit):
+    check_cuda(input, output_q, output_s)
+    for t, n in ((input, "input"), (output_q, "output_q"), (output_s, "output_s")):
+        _contig(t, n)
+    if input.dim() != 2:
+        raise ValueError("input must be 2-D [rows, 2*hidden]")
+    rows, d2 = input.shape
+    d = d2 // 2
+    if tuple(output_q.shape) != (rows, d) or tuple(output_s.shape) != (rows, d // group_size):
+        raise ValueError("output shapes do not match the input")
+    call("vmamd_silu_and_mul_quant_fp8", ptr(input), dtype_code(input.dtype), rows, d, group_size,
+         eps, fp8_min, fp8_max, limit, ptr(output_q), ptr(output_s), stream_of(input))
+
+
+def silu_and_mul_per_token_group_fp8_quant(input: torch.Tensor, output_q: torch.Tensor,
+                                           output_s: torch.Tensor, group_size: int, eps: float,
+                                           fp8_min: float, fp8_max: float) -> None:
+    """Reference: silu_and_mul_per_token_group_fp8_quant
+    (csrc/musa/quantization/silu_and_mul_per_token_group_fp8_quant.cu:197-203)."""
+    _silu_quant(input, output_q, output_s, group_size, eps, fp8_min, fp8_max, 0.0)
+
+
+def silu_and_mul_clamp_per_token_group_fp8_quant(input: torch.Tensor, output_q: torch.Tensor,
+                                                 output_s: torch.Tensor, group_size: int,
+                                                 eps: float, fp8_min: float, fp8_max: float,
+                                                 swiglu_limit: float) -> None:
+    """Reference: silu_and_mul_clamp_per_token_group_fp8_quant (same file, 205-213)."""
+    if not (swiglu_limit > 0 and swiglu_limit < float("inf")):
+        raise ValueError("swiglu_limit must be finite and positive.")
+    _silu_quant(input, output_q, output_s, group_size, eps, fp8_min, fp8_max, swiglu_limit)
+
+
+# ---------------------------------------------------------------- routing --
+def _check_routing_out(topk_weights, topk_ids, gating_output):
+    check_cuda(topk_weights, topk_ids, gating_output)
+    _contig(gating_output, "gating_output")
+    _contig(topk_weights, "topk_weights")
+    _contig(topk_ids, "topk_ids")
+    if topk_weights.dtype != torch.float32 or topk_ids.dtype != torch.int32:
+        raise ValueError("topk_weights must be float32 and topk_ids int32")
+    if gating_output.dim() != 2 or topk_weights.shape != topk_ids.shape or \
+            topk_weights.shape[0] != gating_output.shape[0]:
+        raise ValueError("routing shapes do not match")
+
+
+def topk_softmax(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_output: torch.Tensor,
+                 renormalize: bool = False, moe_softcapping: float = 0.0,
+                 correction_bias: torch.Tensor | None = None) -> None:
+    """Reference: topk_softmax (vllm_musa/jit_kernel/csrc/topk.py:211-242)."""
+    _check_routing_out(topk_weights, topk_ids, gating_output)
+    if correction_bias is not None:
+        check_cuda(correction_bias)
+        if correction_bias.dtype != torch.float32 or correction_bias.numel() != gating_output.shape[1]:
+            raise ValueError("correction_bias must be float32 [num_experts]")
+    t, e = gating_output.shape
+    call("vmamd_topk_softmax", ptr(gating_output), dtype_code(gating_output.dtype), t, e,
+         topk_weights.shape[1], int(bool(renormalize)), float(moe_softcapping),
+         ptr(correction_bias), ptr(topk_weights), ptr(topk_ids), stream_of(gating_output))
+
+
+def topk_sigmoid(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_output: torch.Tensor,
+                 renormalize: bool = False, correction_bias: torch.Tensor | None = None) -> None:
+    """Reference: topk_sigmoid (vllm_musa/jit_kernel/csrc/topk.py:245-275)."""
+    _check_routing_out(topk_weights, topk_ids, gating_output)
+    if correction_bias is not None:
+        check_cuda(correction_bias)
+        if correction_bias.dtype != torch.float32 or correction_bias.numel() != gating_output.shape[1]:
+            raise ValueError("correction_bias must be float32 [num_experts]")
+    t, e = gating_output.shape
+    call("vmamd_topk_sigmoid", ptr(gating_output), dtype_code(gating_output.dtype), t, e,
+         topk_weights.shape[1], int(bool(renormalize)), ptr(correction_bias), ptr(topk_weights),
+         ptr(topk_ids), stream_of(gating_output))
+
+
+def grouped_topk_into(topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                      gating_output: torch.Tensor, num_expert_group: int, topk_group: int,
+                      renormalize: bool, scoring_func: str, routed_scaling_factor: float,
+                      e_score_correction_bias: torch.Tensor | None) -> None:
+    _check_routing_out(topk_weights, topk_ids, gating_output)
+    bias = e_score_correction_bias
+    if bias is not None:
+        check_cuda(bias)
+        if bias.dtype != torch.float32:
+            bias = bias.float()
+        bias = bias.contiguous()
+    scoring = {"softmax": 0, "sigmoid": 1}.get(scoring_func)
+    if scoring is None:
+        raise ValueError(f"Unsupported scoring function: {scoring_func}")
+    t, e = gating_output.shape
+    call("vmamd_grouped_topk", ptr(gating_output), dtype_code(gating_output.dtype), t, e,
+         num_expert_group, topk_group, topk_weights.shape[1], int(bool(renormalize)), scoring,
+         float(routed_scaling_factor), ptr(bias), ptr(topk_weights), ptr(topk_ids),
+         stream_of(gating_output))
+
+
+# ------------------------------------------------------------ align / sum --
+def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int, block_size: int,
+                         sorted_token_ids: torch.Tensor, experts_ids: torch.Tensor,
+                         num_tokens_post_pad: torch.Tensor,
+                         maybe_expert_map: torch.Tensor | None = None,
+                         scatter_idx: torch.Tensor | None = None,
+                         expert_offsets: torch.Tensor | None = None) -> None:
+    """Reference: _moe_C.moe_align_block_size (schema
+    patches/series/0041-…torch_bindings.cpp.patch:36-58).  ``expert_offsets``
+    (optional, [num_experts + 1] int32) additionally receives the segment starts."""
+    check_cuda(topk_ids, sorted_token_ids, experts_ids, num_tokens_post_pad, maybe_expert_map,
+               scatter_idx, expert_offsets)
+    if topk_ids.dtype != torch.int32:
+        raise ValueError("topk_ids must be int32")
+    for t, n in ((topk_ids, "topk_ids"), (sorted_token_ids, "sorted_token_ids"),
+                 (experts_ids, "experts_ids")):
+        _contig(t, n)
+    cap = sorted_token_ids.numel()
+    if experts_ids.numel() < -(-cap // block_size):
+        raise ValueError("experts_ids is shorter than ceil(len(sorted_token_ids) / block_size)")
+    emap = None if maybe_expert_map is None else maybe_expert_map.to(torch.int32).contiguous()
+    call("vmamd_moe_align_block_size", ptr(topk_ids), topk_ids.numel(), num_experts, block_size,
+         ptr(emap), 0 if emap is None else emap.numel(), ptr(sorted_token_ids), cap,
+         ptr(experts_ids), ptr(num_tokens_post_pad), ptr(expert_offsets), ptr(scatter_idx),
+         stream_of(topk_ids))
+
+
+def moe_sum(input: torch.Tensor, output: torch.Tensor, topk_ids: torch.Tensor | None = None,
+            expert_map: torch.Tensor | None = None) -> None:
+    """Reference: _moe_C.moe_sum (schema 0041-…torch_bindings.cpp.patch:44-50) and
+    maybe_fast_moe_sum (vllm_musa/jit_kernel/csrc/moe.py:119-133)."""
+    check_cuda(input, output, topk_ids, expert_map)
+    _contig(input, "input")
+    _contig(output, "output")
+    if input.dim() != 3 or output.dim() != 2 or input.shape[0] != output.shape[0] or \
+            input.shape[2] != output.shape[1] or input.dtype != output.dtype:
+        raise ValueError("moe_sum expects input [T, K, H] and output [T, H] of one dtype")
+    ids = None if topk_ids is None else topk_ids.to(torch.int32).contiguous()
+    emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
+    t, k, h = input.shape
+    call("vmamd_moe_sum", ptr(input), dtype_code(input.dtype), t, k, h, ptr(ids), ptr(emap),
+         0 if emap is None else emap.numel(), ptr(output), stream_of(input))
+
+
+def lib_version() -> int:
+    return _lib.load().vmamd_abi_version()
