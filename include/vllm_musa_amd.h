@@ -127,7 +127,10 @@ int vmamd_grouped_topk(const void* gating, int dtype, int64_t tokens, int expert
  *   num_tokens_post_pad[0] = sum_e ceil(cnt_e / block_size) * block_size;
  *   expert_offsets (optional, length num_experts + 1): segment starts;
  *   scatter_idx (optional, length numel): position of route r in
- *                sorted_token_ids, -1 for dropped routes.
+ *                sorted_token_ids, -1 for dropped routes;
+ *   active_experts (optional, length num_experts) and num_active (optional,
+ *                length 1, given together): the experts that received at
+ *                least one route, ascending, and their count.
  * capacity must be >= numel + num_experts * (block_size - 1).
  * num_experts <= 1024.  Replaces moe_align_block_size
  * (schema: vllm_musa/patches/series/0041-MUSA-MUSA-csrc-csrc-moe-torch_bindings.cpp.patch:36-58;
@@ -137,7 +140,8 @@ int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int num_e
                                int64_t expert_map_len, int32_t* sorted_token_ids,
                                int64_t capacity, int32_t* expert_ids,
                                int32_t* num_tokens_post_pad, int32_t* expert_offsets,
-                               int32_t* scatter_idx, vmamd_stream_t stream);
+                               int32_t* scatter_idx, int32_t* active_experts,
+                               int32_t* num_active, vmamd_stream_t stream);
 
 /* ---------------------------------------------------------------- combine --
  * out[t, h] = round(sum_{k<topk} x[t, k, h]) with an fp32 accumulator in slot
@@ -151,6 +155,24 @@ int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int num_e
 int vmamd_moe_sum(const void* x, int dtype, int64_t tokens, int topk, int64_t hidden,
                   const int32_t* topk_ids, const int32_t* expert_map, int64_t expert_map_len,
                   void* out, vmamd_stream_t stream);
+
+/* ------------------------------------------------------- block-fp8 GEMM --
+ * C[M, N] = bf16( sum_kb (sum_{k in kb} A[m,k] B[n,k]) * As[m,kb] * Bs[n/128, kb] )
+ * A [M, K] fp8 with As[m*as_stride_m + kb*as_stride_k] (1x128 groups),
+ * B [N, K] fp8 with Bs [ceil(N/128), K/128] f32 (128x128 blocks), C [M, N]
+ * bf16.  K % 128 == 0, N % 16 == 0, block_n == block_k == 128.  M <= 64
+ * runs the split-K GEMV (weights read once; needs
+ * vmamd_w8a8_block_fp8_matmul_workspace_size() bytes of workspace, 0 for
+ * some shapes), larger M the tiled MFMA GEMM.  Replaces
+ * w8a8_triton_block_scaled_mm(A, B, As, Bs, block_size, output_dtype) as
+ * called at vllm_musa/deepseek_v4_jit/fp8_einsum.py:399-406, fp8_gemm_nt in
+ * _musa_deepgemm_fp8_op (model_executor/kernels/linear/scaled_mm/deep_gemm.py:233-262)
+ * and the small-M GEMV musa_fused_gemv (csrc/musa/gemv.mu:723-925). */
+size_t vmamd_w8a8_block_fp8_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
+int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64_t as_stride_m,
+                                int64_t as_stride_k, const void* B, const float* Bs, void* C,
+                                int64_t M, int64_t N, int64_t K, int block_n, int block_k,
+                                void* workspace, size_t workspace_bytes, vmamd_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -51,3 +51,20 @@ def dequant_block_weight(b_q: np.ndarray, b_s: np.ndarray, block_n: int = 128,
     s = np.repeat(np.repeat(np.asarray(b_s, np.float32), block_n, axis=-2)[..., :n, :], block_k,
                   axis=-1)[..., :k]
     return (w * s).astype(np.float32)
+
+
+def block_fp8_matmul_sampled(a_q: np.ndarray, a_s: np.ndarray, b_q: np.ndarray, b_s: np.ndarray,
+                             rows: np.ndarray, cols: np.ndarray, block_n: int = 128,
+                             block_k: int = 128) -> np.ndarray:
+    """The closed form restricted to output rows `rows` and columns `cols`
+    (float64), for checking large GEMMs on a sample of their outputs."""
+    a = e4m3_decode(a_q[rows]).astype(np.float64)
+    b = e4m3_decode(b_q[cols]).astype(np.float64)
+    sa = np.asarray(a_s, np.float64)[rows]
+    sb = np.asarray(b_s, np.float64)[np.asarray(cols) // block_n]
+    kb = a.shape[1] // block_k
+    out = np.zeros((len(rows), len(cols)), dtype=np.float64)
+    for j in range(kb):
+        sl = slice(j * block_k, (j + 1) * block_k)
+        out += (a[:, sl] @ b[:, sl].T) * sa[:, j:j + 1] * sb[:, j][None, :]
+    return out

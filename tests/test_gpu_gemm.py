@@ -1,0 +1,93 @@
+"""GPU parity of the dense w8a8 block-fp8 GEMM / split-K GEMV against the
+float64 closed form of the oracle (sampled outputs for the big shapes).
+
+Tolerance (the block-fp8 bar of the path): rel-L2 <= 1e-2 and
+max-abs <= 2e-2 * max|ref|; the kernels accumulate in fp32 and round once to
+bf16, so the test also asserts the tighter rel-L2 <= 4e-3 and an elementwise
+bound of 2^-7 |ref| + 1e-3 max|ref|."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.gemm import block_fp8_matmul_sampled
+from oracle.quant import group_quant_fp8
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(24576, 1536), (7168, 18432), (2112, 7168), (7168, 2048)]
+
+
+def _check(out: np.ndarray, ref: np.ndarray):
+    err = out.astype(np.float64) - ref
+    rel_l2 = np.linalg.norm(err) / max(np.linalg.norm(ref), 1e-30)
+    mref = np.abs(ref).max()
+    assert rel_l2 <= 4e-3, rel_l2
+    assert np.abs(err).max() <= 2e-2 * mref
+    assert np.all(np.abs(err) <= 2 ** -7 * np.abs(ref) + 1e-3 * mref)
+
+
+def _run(M, N, K, seed, sample_rows=16, sample_cols=768):
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import apply_w8a8_block_fp8_linear
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    w, ws = synthetic.dense_fp8_weight(N, K, seed)
+    x = synthetic.activations(M, K, seed + 1)
+    out = apply_w8a8_block_fp8_linear(x, w, ws).float().cpu().numpy()
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    # activation quantisation is itself checked against the oracle
+    q_ref, s_ref = group_quant_fp8(x.float().cpu().numpy())
+    np.testing.assert_array_equal(xq.view(torch.uint8).cpu().numpy(), q_ref)
+    g = np.random.Generator(np.random.PCG64(seed))
+    rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, min(M, sample_rows))]))
+    cols = np.unique(np.concatenate([[0, N - 1], g.integers(0, N, min(N, sample_cols))]))
+    ref = block_fp8_matmul_sampled(q_ref, s_ref, w.view(torch.uint8).cpu().numpy(),
+                                   ws.cpu().numpy(), rows, cols)
+    _check(out[np.ix_(rows, cols)], ref)
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+@pytest.mark.parametrize("M", [1, 4, 16, 64, 512])
+def test_block_fp8_gemm_shapes(M, N, K):
+    _run(M, N, K, seed=1000 + M + N // 16 + K // 128)
+
+
+@pytest.mark.parametrize("N,K", [(2112, 7168), (24576, 1536)])
+def test_block_fp8_gemm_m4096(N, K):
+    _run(4096, N, K, seed=77, sample_rows=24, sample_cols=512)
+
+
+@pytest.mark.parametrize("M", [3, 17, 33, 65, 100, 130])
+def test_block_fp8_gemm_ragged_m(M):
+    _run(M, 2112, 1024, seed=5 + M, sample_rows=200, sample_cols=2112)
+
+
+def test_block_fp8_matmul_full_small():
+    """Every output element on a small case, through w8a8_block_fp8_matmul."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    M, N, K = 96, 400, 640
+    w, ws = synthetic.dense_fp8_weight(N, K, 3)
+    x = synthetic.activations(M, K, 4)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    out = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128]).float().cpu().numpy()
+    ref = block_fp8_matmul_sampled(xq.view(torch.uint8).cpu().numpy(), xs.cpu().numpy(),
+                                   w.view(torch.uint8).cpu().numpy(), ws.cpu().numpy(),
+                                   np.arange(M), np.arange(N))
+    _check(out, ref)
+
+
+def test_block_fp8_column_major_scales():
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    M, N, K = 8, 256, 512
+    w, ws = synthetic.dense_fp8_weight(N, K, 9)
+    x = synthetic.activations(M, K, 10)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    xq2, xs2 = per_token_group_quant_fp8(x, 128, column_major_scales=True)
+    a = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    b = w8a8_block_fp8_matmul(xq2, w, xs2, ws, [128, 128])
+    assert torch.equal(a, b)

@@ -33,7 +33,8 @@ __device__ __forceinline__ int mapped_expert(const int32_t* __restrict__ ids, in
 __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int E, int bs, const int32_t* __restrict__ map,
     int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity, int32_t* __restrict__ expert_ids,
-    int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out, int32_t* __restrict__ scatter_idx) {
+    int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out, int32_t* __restrict__ scatter_idx,
+    int32_t* __restrict__ active_out, int32_t* __restrict__ num_active_out) {
   __shared__ int cnt[kMaxAlignExperts];
   __shared__ int base[kMaxAlignExperts + 1];
   __shared__ int run[kMaxAlignExperts];
@@ -77,6 +78,21 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   if (tid == 0) ntpp[0] = total;
   if (offsets_out)
     for (int e = tid; e <= E; e += kAlignThreads) offsets_out[e] = base[e];
+
+  // compact list of the experts that received routes (ascending ids)
+  if (active_out) {
+    const bool act = tid < E && cnt[tid] > 0;
+    const uint64_t m = ballot(act);
+    const int below = __popcll(m & ((lane == 0) ? 0ull : (~0ull >> (kWave - lane))));
+    __syncthreads();  // wave_tot is reused below
+    if (lane == 0) wave_tot[wave] = __popcll(m);
+    __syncthreads();
+    int off = 0;
+    for (int w = 0; w < wave; ++w) off += wave_tot[w];
+    if (act) active_out[off + below] = tid;
+    if (tid == kAlignThreads - 1) num_active_out[0] = off + __popcll(m);
+    __syncthreads();
+  }
 
   // expert_ids: binary search of the segment holding each block
   const int64_t nblocks = (capacity + bs - 1) / bs;
@@ -148,7 +164,8 @@ extern "C" int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel
                                           int64_t expert_map_len, int32_t* sorted_token_ids,
                                           int64_t capacity, int32_t* expert_ids,
                                           int32_t* num_tokens_post_pad, int32_t* expert_offsets,
-                                          int32_t* scatter_idx, vmamd_stream_t stream) {
+                                          int32_t* scatter_idx, int32_t* active_experts,
+                                          int32_t* num_active, vmamd_stream_t stream) {
   VMAMD_REQUIRE(num_experts > 0 && num_experts <= kMaxAlignExperts,
                 "moe_align_block_size: num_experts must be in [1, %d] (got %d)", kMaxAlignExperts,
                 num_experts);
@@ -161,10 +178,13 @@ extern "C" int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel
                 (long long)(numel + static_cast<int64_t>(num_experts) * (block_size - 1)));
   VMAMD_REQUIRE(capacity < (1ll << 31), "moe_align_block_size: capacity too large");
   VMAMD_REQUIRE(!expert_map || expert_map_len > 0, "moe_align_block_size: empty expert_map");
+  VMAMD_REQUIRE(!active_experts == !num_active,
+                "moe_align_block_size: active_experts and num_active go together");
   VMAMD_REQUIRE((topk_ids || numel == 0) && sorted_token_ids && expert_ids && num_tokens_post_pad,
                 "moe_align_block_size: null pointer");
   moe_align_kernel<<<1, kAlignThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
       topk_ids, numel, num_experts, block_size, expert_map, expert_map_len, sorted_token_ids,
-      capacity, expert_ids, num_tokens_post_pad, expert_offsets, scatter_idx);
+      capacity, expert_ids, num_tokens_post_pad, expert_offsets, scatter_idx, active_experts,
+      num_active);
   return check_launch("moe_align_block_size");
 }

@@ -1,0 +1,303 @@
+// Dense w8a8 block-fp8 GEMM:  C[M,N] = bf16( sum_kb (A_kb . B_kb^T) * As[m,kb] * Bs[n/128,kb] )
+//   A  [M, K] e4m3 (1x128 activation groups, scales As[m*as_sm + kb*as_sk])
+//   B  [N, K] e4m3 (128x128 weight blocks, scales Bs[ceil(N/128), K/128])
+//
+// Two kernels:
+//  * gemm_fp8_bs_kernel  -- tiled BM x BN workgroup tile, 4 waves, K-block of
+//    128 per step, LDS double buffer fed by register prefetch (one barrier per
+//    K-block), XCD-aware tile order.  For M > 64.
+//  * gemv_fp8_bs_kernel  -- decode-sized M (<= 64): one wave per 16 weight rows
+//    streams its rows straight from HBM (no LDS), each 16x128 weight fragment
+//    multiplies every 16-row activation tile held in registers, so weights are
+//    read exactly once.  Split-K over blockIdx.y writes fp32 partials that
+//    splitk_reduce_kernel sums in a fixed order (deterministic), one rounding.
+#include "mfma_fp8.h"
+
+namespace vmamd {
+
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * kWave, 2) void gemm_fp8_bs_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t as_sm, int64_t as_sk,
+    const uint8_t* __restrict__ B, const float* __restrict__ Bs, uint16_t* __restrict__ C, int M,
+    int N, int K, int TM, int TN) {
+  constexpr int THREADS = WM * WN * kWave;
+  constexpr int WTM = BM / WM, WTN = BN / WN, MT = WTM / 16, NT = WTN / 16;
+  constexpr int ACH = BM * 8 / THREADS, BCH = BN * 8 / THREADS;
+  static_assert(ACH * THREADS == BM * 8 && BCH * THREADS == BN * 8, "tile / thread mismatch");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2][(BM + BN) * 128];
+
+  int tm, tn;
+  if (!xcd_tile(blockIdx.x, TM, TN, tm, tn)) return;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int wm = wave / WN, wn = wave % WN;
+  const int li = lane % 16, lg = lane / 16;
+  const int KB = K / 128;
+
+  // Thread t copies 16-byte chunk (t % 8) of rows t/8 + c*(THREADS/8); rows
+  // past M / N are clamped to the last row, so loads stay in bounds and their
+  // results are never stored.  Rows 32 apart share (row & 7), hence the same
+  // swizzled chunk slot.
+  constexpr int RSTEP = THREADS / 8;
+  const int crow = tid / 8, cch = tid % 8;
+  const int l0 = lds_off(crow, cch);
+  int64_t goff_a[ACH], goff_b[BCH];
+#pragma unroll
+  for (int c = 0; c < ACH; ++c)
+    goff_a[c] = static_cast<int64_t>(min(m0 + crow + c * RSTEP, M - 1)) * K + cch * 16;
+#pragma unroll
+  for (int c = 0; c < BCH; ++c)
+    goff_b[c] = static_cast<int64_t>(min(n0 + crow + c * RSTEP, N - 1)) * K + cch * 16;
+  const int sa_row0 = m0 + wm * WTM + li;
+  const int sb_col0 = n0 + wn * WTN;
+
+  v4f acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  uint4 ra[ACH], rb[BCH];
+#pragma unroll
+  for (int c = 0; c < ACH; ++c) ra[c] = *reinterpret_cast<const uint4*>(A + goff_a[c]);
+#pragma unroll
+  for (int c = 0; c < BCH; ++c) rb[c] = *reinterpret_cast<const uint4*>(B + goff_b[c]);
+#pragma unroll
+  for (int c = 0; c < ACH; ++c) *reinterpret_cast<uint4*>(&smem[0][l0 + c * RSTEP * 128]) = ra[c];
+#pragma unroll
+  for (int c = 0; c < BCH; ++c)
+    *reinterpret_cast<uint4*>(&smem[0][BM * 128 + l0 + c * RSTEP * 128]) = rb[c];
+  __syncthreads();
+
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < KB; ++kb) {
+    const int cur = kb & 1;
+    const bool more = kb + 1 < KB;
+    if (more) {
+      const int off = (kb + 1) * 128;
+#pragma unroll
+      for (int c = 0; c < ACH; ++c) ra[c] = *reinterpret_cast<const uint4*>(A + goff_a[c] + off);
+#pragma unroll
+      for (int c = 0; c < BCH; ++c) rb[c] = *reinterpret_cast<const uint4*>(B + goff_b[c] + off);
+    }
+    float sa[MT], sb[NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      sa[mt] = As[static_cast<int64_t>(min(sa_row0 + mt * 16, M - 1)) * as_sm + kb * as_sk];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      sb[nt] = Bs[static_cast<int64_t>(min(sb_col0 + nt * 16, N - 1) / 128) * KB + kb];
+
+    const uint8_t* tile = smem[cur];
+    v8i xf[MT], wf[NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xf[mt] = lds_frag(tile, wm * WTM + mt * 16 + li, lg);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) wf[nt] = lds_frag(tile + BM * 128, wn * WTN + nt * 16 + li, lg);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const v4f p = mfma_fp8(wf[nt], xf[mt], zero);
+        fma4(acc[mt][nt], p, sa[mt] * sb[nt]);
+      }
+    if (more) {
+#pragma unroll
+      for (int c = 0; c < ACH; ++c)
+        *reinterpret_cast<uint4*>(&smem[cur ^ 1][l0 + c * RSTEP * 128]) = ra[c];
+#pragma unroll
+      for (int c = 0; c < BCH; ++c)
+        *reinterpret_cast<uint4*>(&smem[cur ^ 1][BM * 128 + l0 + c * RSTEP * 128]) = rb[c];
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = m0 + wm * WTM + mt * 16 + li;
+    if (m >= M) continue;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = n0 + wn * WTN + nt * 16 + 4 * lg;
+      if (n >= N) continue;
+      const v4f a = acc[mt][nt];
+      *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) = pack_bf16x4(a[0], a[1], a[2], a[3]);
+    }
+  }
+}
+
+// ------------------------------------------------------------ split-K GEMV --
+constexpr int kGemvWaves = 4;
+
+template <int MT>
+__global__ __launch_bounds__(kGemvWaves * kWave) void gemv_fp8_bs_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t as_sm, int64_t as_sk,
+    const uint8_t* __restrict__ B, const float* __restrict__ Bs, int M, int N, int K, int splits,
+    float* __restrict__ partial, uint16_t* __restrict__ C) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int li = lane % 16, lg = lane / 16;
+  const int ntile = blockIdx.x * kGemvWaves + wave;
+  if (ntile * 16 >= N) return;  // wave-uniform; this kernel has no barriers
+  const int split = blockIdx.y;
+  const int KB = K / 128;
+  const int kb0 = static_cast<int>(static_cast<int64_t>(split) * KB / splits);
+  const int kb1 = static_cast<int>(static_cast<int64_t>(split + 1) * KB / splits);
+  const uint8_t* wrow = B + static_cast<int64_t>(ntile * 16 + li) * K;
+  const float* bs = Bs + static_cast<int64_t>((ntile * 16) / 128) * KB;
+  const uint8_t* xrow[MT];
+  const float* as[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = min(mt * 16 + li, M - 1);
+    xrow[mt] = A + static_cast<int64_t>(m) * K;
+    as[mt] = As + static_cast<int64_t>(m) * as_sm;
+  }
+  v4f acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+
+  constexpr int U = 4;  // K-blocks in flight per wave
+  int kb = kb0;
+  for (; kb + U <= kb1; kb += U) {
+    v8i w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) w[u] = global_frag(wrow + (kb + u) * 128, lg);
+    float sbv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) sbv[u] = bs[kb + u];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      v8i x[U];
+      float sav[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        x[u] = global_frag(xrow[mt] + (kb + u) * 128, lg);
+        sav[u] = as[mt][(kb + u) * as_sk];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) fma4(acc[mt], mfma_fp8(w[u], x[u], zero), sav[u] * sbv[u]);
+    }
+  }
+  for (; kb < kb1; ++kb) {
+    const v8i w = global_frag(wrow + kb * 128, lg);
+    const float sb = bs[kb];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      fma4(acc[mt], mfma_fp8(w, global_frag(xrow[mt] + kb * 128, lg), zero), as[mt][kb * as_sk] * sb);
+  }
+
+  const int n = ntile * 16 + 4 * lg;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + li;
+    if (m >= M) continue;
+    const v4f a = acc[mt];
+    if (splits == 1) {
+      *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) = pack_bf16x4(a[0], a[1], a[2], a[3]);
+    } else {
+      float4 v = {a[0], a[1], a[2], a[3]};
+      *reinterpret_cast<float4*>(partial + (static_cast<int64_t>(split) * M + m) * N + n) = v;
+    }
+  }
+}
+
+// C[m, n] = bf16(sum_{s < splits} partial[s, m, n]) in split order.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial,
+                                                            int splits, int64_t mn,
+                                                            uint16_t* __restrict__ C) {
+  const int64_t i4 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (i4 >= mn) return;
+  float4 acc = *reinterpret_cast<const float4*>(partial + i4);
+  for (int s = 1; s < splits; ++s) {
+    const float4 v = *reinterpret_cast<const float4*>(partial + s * mn + i4);
+    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+  }
+  *reinterpret_cast<uint2*>(C + i4) = pack_bf16x4(acc.x, acc.y, acc.z, acc.w);
+}
+
+// ------------------------------------------------------------ dispatch ------
+constexpr int kGemvMaxM = 64;
+
+static int gemv_splits(int M, int N, int K) {
+  const int tiles = N / 16;
+  const int KB = K / 128;
+  int s = (2048 + tiles - 1) / tiles;  // aim for >= 2048 waves (8 per CU)
+  s = max(1, min(s, KB / 2 > 0 ? KB / 2 : 1));
+  (void)M;
+  return s;
+}
+
+size_t w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M > kGemvMaxM || M <= 0) return 0;
+  const int s = gemv_splits(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+  return s > 1 ? static_cast<size_t>(s) * M * N * sizeof(float) : 0;
+}
+
+}  // namespace vmamd
+
+using namespace vmamd;
+
+extern "C" size_t vmamd_w8a8_block_fp8_matmul_workspace_size(int64_t M, int64_t N, int64_t K) {
+  return w8a8_workspace_bytes(M, N, K);
+}
+
+extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64_t as_stride_m,
+                                           int64_t as_stride_k, const void* B, const float* Bs,
+                                           void* C, int64_t M, int64_t N, int64_t K, int block_n,
+                                           int block_k, void* workspace, size_t workspace_bytes,
+                                           vmamd_stream_t stream) {
+  VMAMD_REQUIRE(block_n == 128 && block_k == 128,
+                "w8a8_block_fp8_matmul: only 128x128 weight blocks are supported (got %dx%d)",
+                block_n, block_k);
+  VMAMD_REQUIRE(M >= 0 && N > 0 && K > 0, "w8a8_block_fp8_matmul: bad sizes");
+  VMAMD_REQUIRE(K % 128 == 0, "w8a8_block_fp8_matmul: K (%lld) must be a multiple of 128",
+                (long long)K);
+  VMAMD_REQUIRE(N % 16 == 0, "w8a8_block_fp8_matmul: N (%lld) must be a multiple of 16",
+                (long long)N);
+  VMAMD_REQUIRE(M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31),
+                "w8a8_block_fp8_matmul: sizes must fit in int32");
+  if (M == 0) return VMAMD_OK;
+  VMAMD_REQUIRE(A && As && B && Bs && C, "w8a8_block_fp8_matmul: null pointer");
+  VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(C) % 8 == 0,
+                "w8a8_block_fp8_matmul: A and B must be 16-byte and C 8-byte aligned");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+  uint16_t* c = static_cast<uint16_t*>(C);
+  const uint8_t* a = static_cast<const uint8_t*>(A);
+  const uint8_t* b = static_cast<const uint8_t*>(B);
+  if (m <= kGemvMaxM) {
+    const int splits = gemv_splits(m, n, k);
+    float* part = nullptr;
+    if (splits > 1) {
+      const size_t need = static_cast<size_t>(splits) * m * n * sizeof(float);
+      VMAMD_REQUIRE(workspace && workspace_bytes >= need,
+                    "w8a8_block_fp8_matmul: workspace of %zu bytes required (got %zu)", need,
+                    workspace_bytes);
+      VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+                    "w8a8_block_fp8_matmul: workspace must be 16-byte aligned");
+      part = static_cast<float*>(workspace);
+    }
+    dim3 grid((n / 16 + kGemvWaves - 1) / kGemvWaves, splits);
+    if (m <= 16)
+      gemv_fp8_bs_kernel<1><<<grid, kGemvWaves * kWave, 0, st>>>(a, As, as_stride_m, as_stride_k, b, Bs,
+                                                                m, n, k, splits, part, c);
+    else if (m <= 32)
+      gemv_fp8_bs_kernel<2><<<grid, kGemvWaves * kWave, 0, st>>>(a, As, as_stride_m, as_stride_k, b, Bs,
+                                                                m, n, k, splits, part, c);
+    else
+      gemv_fp8_bs_kernel<4><<<grid, kGemvWaves * kWave, 0, st>>>(a, As, as_stride_m, as_stride_k, b, Bs,
+                                                                m, n, k, splits, part, c);
+    if (splits > 1) {
+      const int64_t mn = static_cast<int64_t>(m) * n;
+      splitk_reduce_kernel<<<static_cast<int>((mn / 4 + 255) / 256), 256, 0, st>>>(part, splits, mn, c);
+    }
+    return check_launch("w8a8_block_fp8_matmul(gemv)");
+  }
+  constexpr int BM = 128, BN = 128;
+  const int TM = (m + BM - 1) / BM, TN = (n + BN - 1) / BN;
+  gemm_fp8_bs_kernel<BM, BN, 2, 2><<<xcd_grid(TM * TN), 256, 0, st>>>(a, As, as_stride_m, as_stride_k,
+                                                                      b, Bs, c, m, n, k, TM, TN);
+  return check_launch("w8a8_block_fp8_matmul(gemm)");
+}

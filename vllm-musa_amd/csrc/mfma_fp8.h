@@ -1,0 +1,92 @@
+// Building blocks of the fp8 block-scaled GEMMs on CDNA4 MFMA.
+//
+// MFMA shape: v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3 -> f32), one K-block of
+// the 128x128 scale grid per instruction.  The weight tile is the "A" operand
+// (16 output rows n) and the activation tile the "B" operand (16 columns m),
+// so lane (i = lane % 16, g = lane / 16) ends up holding
+//     C[n = 4g + r][m = i],  r = 0..3
+// -- four consecutive n of one row m: one activation scale and one weight-
+// block scale per lane and K-block, and an 8-byte bf16 store per tile.
+//
+// Operand bytes: lane (i, g) supplies row i, bytes [16g, 16g+16) and
+// [64+16g, 64+16g+16) of the 128-byte K-block, for both operands (any
+// bijection of K that is the same for both operands gives the same dot
+// product; this one makes every 16-lane group read 64 contiguous bytes).
+//
+// LDS tiles store a row as 8 chunks of 16 bytes with chunk c of row r at
+// slot c ^ (r & 7), so the 8 lanes served per LDS cycle hit 8 distinct
+// chunk slots (all banks) when reading the same chunk of 8 consecutive rows.
+#pragma once
+
+#include "common.h"
+
+namespace vmamd {
+
+__device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+  return row * 128 + ((chunk ^ (row & 7)) << 4);
+}
+
+// Operand fragment of `row` from an LDS tile.
+__device__ __forceinline__ v8i lds_frag(const uint8_t* tile, int row, int g) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(tile + lds_off(row, g));
+  const uint4 hi = *reinterpret_cast<const uint4*>(tile + lds_off(row, g + 4));
+  v8i f;
+  f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+  f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+  return f;
+}
+
+// Operand fragment straight from global memory (row start + K-block start).
+__device__ __forceinline__ v8i global_frag(const uint8_t* p, int g) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(p + 16 * g);
+  const uint4 hi = *reinterpret_cast<const uint4*>(p + 64 + 16 * g);
+  v8i f;
+  f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+  f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+  return f;
+}
+
+// acc += p * s, element-wise (the per-K-block scale promotion).
+__device__ __forceinline__ void fma4(v4f& acc, const v4f& p, float s) {
+  acc[0] = fmaf(p[0], s, acc[0]);
+  acc[1] = fmaf(p[1], s, acc[1]);
+  acc[2] = fmaf(p[2], s, acc[2]);
+  acc[3] = fmaf(p[3], s, acc[3]);
+}
+
+__device__ __forceinline__ uint2 pack_bf16x4(float a, float b, float c, float d) {
+  uint2 r;
+  r.x = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+  r.y = static_cast<uint32_t>(f32_to_bf16(c)) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16);
+  return r;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own
+// L2).  Give each XCD a contiguous range of logical tiles and walk that
+// range in bands of kGroupM row-tiles, so the tiles resident on one XCD at a
+// time share activation rows and weight columns in its L2.  Returns false for
+// the (at most 7) padding workgroups of a grid rounded up to a multiple of 8.
+constexpr int kXcds = 8;
+constexpr int kGroupM = 8;
+
+__host__ __device__ inline int xcd_grid(int total) { return (total + kXcds - 1) / kXcds * kXcds; }
+
+__device__ __forceinline__ bool xcd_tile(int wg, int TM, int TN, int& tm, int& tn) {
+  const int total = TM * TN;
+  const int per = (total + kXcds - 1) / kXcds;
+  const int L = (wg % kXcds) * per + wg / kXcds;
+  if (L >= total) return false;
+  const int band = L / (kGroupM * TN);
+  const int first = band * kGroupM;
+  const int gsz = min(TM - first, kGroupM);
+  const int in = L - band * kGroupM * TN;
+  tm = first + in % gsz;
+  tn = in / gsz;
+  return true;
+}
+
+}  // namespace vmamd

@@ -160,12 +160,15 @@ def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int, block_size: i
                          num_tokens_post_pad: torch.Tensor,
                          maybe_expert_map: torch.Tensor | None = None,
                          scatter_idx: torch.Tensor | None = None,
-                         expert_offsets: torch.Tensor | None = None) -> None:
+                         expert_offsets: torch.Tensor | None = None,
+                         active_experts: torch.Tensor | None = None,
+                         num_active: torch.Tensor | None = None) -> None:
     """Reference: _moe_C.moe_align_block_size (schema
-    patches/series/0041-…torch_bindings.cpp.patch:36-58).  ``expert_offsets``
-    (optional, [num_experts + 1] int32) additionally receives the segment starts."""
+    patches/series/0041-…torch_bindings.cpp.patch:36-58).  Optional extra
+    outputs: ``expert_offsets`` ([num_experts + 1] int32 segment starts) and
+    ``active_experts`` / ``num_active`` (the experts with routes, ascending)."""
     check_cuda(topk_ids, sorted_token_ids, experts_ids, num_tokens_post_pad, maybe_expert_map,
-               scatter_idx, expert_offsets)
+               scatter_idx, expert_offsets, active_experts, num_active)
     if topk_ids.dtype != torch.int32:
         raise ValueError("topk_ids must be int32")
     for t, n in ((topk_ids, "topk_ids"), (sorted_token_ids, "sorted_token_ids"),
@@ -178,7 +181,7 @@ def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int, block_size: i
     call("vmamd_moe_align_block_size", ptr(topk_ids), topk_ids.numel(), num_experts, block_size,
          ptr(emap), 0 if emap is None else emap.numel(), ptr(sorted_token_ids), cap,
          ptr(experts_ids), ptr(num_tokens_post_pad), ptr(expert_offsets), ptr(scatter_idx),
-         stream_of(topk_ids))
+         ptr(active_experts), ptr(num_active), stream_of(topk_ids))
 
 
 def moe_sum(input: torch.Tensor, output: torch.Tensor, topk_ids: torch.Tensor | None = None,

@@ -1,0 +1,81 @@
+"""Dense w8a8 block-fp8 linear with the reference's interfaces.
+
+  w8a8_block_fp8_matmul(A, B, As, Bs, block_size, output_dtype)
+      upstream w8a8_triton_block_scaled_mm as called at
+      vllm_musa/deepseek_v4_jit/fp8_einsum.py:399-406
+  apply_w8a8_block_fp8_linear(input, weight, weight_scale, block_size)
+      quantise bf16 activations per 1x128 group, then the block GEMM
+      (_musa_deepgemm_fp8_op, model_executor/kernels/linear/scaled_mm/deep_gemm.py:233-262)
+  Fp8BlockScaledMMKernel.apply_block_scaled_mm(A, B, As, Bs, **kwargs)
+      MUSADeepGemmFp8BlockScaledMMKernel.apply_block_scaled_mm (deep_gemm.py:177-197)
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import call, check_cuda, ptr, stream_of
+from .fp8_utils import FP8_DTYPE, per_token_group_quant_fp8
+
+
+def w8a8_block_fp8_matmul(A: torch.Tensor, B: torch.Tensor, As: torch.Tensor, Bs: torch.Tensor,
+                          block_size: list[int], output_dtype: torch.dtype = torch.bfloat16,
+                          out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = (A * As) @ (B * Bs)^T with 1x128 activation and 128x128 weight scales."""
+    check_cuda(A, B, As, Bs, out)
+    if output_dtype != torch.bfloat16:
+        raise ValueError("only bfloat16 output is supported")
+    if A.dtype != FP8_DTYPE or B.dtype != FP8_DTYPE:
+        raise ValueError("A and B must be float8_e4m3fn")
+    if list(block_size) != [128, 128]:
+        raise ValueError(f"block_size must be [128, 128], got {block_size}")
+    if B.dim() != 2 or not B.is_contiguous():
+        raise ValueError("B must be a contiguous [N, K] matrix")
+    n, k = B.shape
+    if A.shape[-1] != k:
+        raise ValueError(f"K mismatch: A has {A.shape[-1]}, B has {k}")
+    lead = A.shape[:-1]
+    a2 = A.reshape(-1, k).contiguous()
+    m = a2.shape[0]
+    as2 = As.reshape(-1, As.shape[-1])
+    if as2.shape != (m, k // 128) or As.dtype != torch.float32:
+        raise ValueError(f"As must be float32 [M, K/128] = {(m, k // 128)}, got {tuple(As.shape)}")
+    if Bs.shape != ((n + 127) // 128, k // 128) or Bs.dtype != torch.float32:
+        raise ValueError("Bs must be float32 [ceil(N/128), K/128]")
+    Bs = Bs.contiguous()
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=A.device)
+    ws_bytes = _lib.load().vmamd_w8a8_block_fp8_matmul_workspace_size(m, n, k)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=A.device) if ws_bytes else None
+    call("vmamd_w8a8_block_fp8_matmul", ptr(a2), ptr(as2), as2.stride(0), as2.stride(1), ptr(B),
+         ptr(Bs), ptr(out), m, n, k, 128, 128, ptr(ws), ws_bytes, stream_of(A))
+    return out.view(*lead, n)
+
+
+def apply_w8a8_block_fp8_linear(input: torch.Tensor, weight: torch.Tensor,
+                                weight_scale: torch.Tensor, block_size: list[int] = (128, 128),
+                                bias: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 input -> 1x128 fp8 quantisation -> block-fp8 GEMM (+ bias)."""
+    q, s = per_token_group_quant_fp8(input.reshape(-1, input.shape[-1]), block_size[1])
+    out = w8a8_block_fp8_matmul(q, weight, s, weight_scale, list(block_size))
+    if bias is not None:
+        out = out + bias
+    return out.view(*input.shape[:-1], weight.shape[0])
+
+
+class Fp8BlockScaledMMKernel:
+    """Drop-in for the reference's block-scaled MM kernel object: its
+    apply_block_scaled_mm receives the bf16 activations A, the fp8 weight B,
+    (unused) As and the weight scales Bs, quantises A itself and returns bf16."""
+
+    def __init__(self, weight_group_shape=(128, 128)):
+        self.weight_group_shape = tuple(weight_group_shape)
+
+    def apply_block_scaled_mm(self, A: torch.Tensor, B: torch.Tensor, As: torch.Tensor | None,
+                              Bs: torch.Tensor, **kwargs) -> torch.Tensor:
+        out = apply_w8a8_block_fp8_linear(A, B, Bs, list(self.weight_group_shape))
+        dst = kwargs.get("output")
+        if dst is not None:
+            dst.copy_(out)
+            return dst
+        return out
