@@ -174,6 +174,39 @@ int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64_t as_strid
                                 int64_t M, int64_t N, int64_t K, int block_n, int block_k,
                                 void* workspace, size_t workspace_bytes, vmamd_stream_t stream);
 
+/* ------------------------------------------------------------ fused MoE --
+ * One fused-experts layer with 128x128 block-fp8 weights, the whole pipeline
+ * on `stream`: 1x128 quantisation of x, moe_align_block_size, W13 grouped
+ * GEMM, SiLU-and-mul (+ optional clamp) and 1x128 quantisation of the
+ * intermediate, W2 grouped GEMM with the routed weight applied in its
+ * epilogue, and the top-k combine:
+ *   out[t] = bf16( sum_k bf16( W2[e] . q(bf16(silu(h_g) * h_u)) * w[t,k] ) ),
+ *   h = bf16(W13[e] . q(x[t])),  e = (expert_map ? expert_map[id] : id)
+ * x [T, H] bf16; w13 [E, 2I, H] fp8 (rows [0, I) gate, [I, 2I) up) with
+ * w13_s [E, 2I/128, H/128] f32; w2 [E, H, I] fp8 with w2_s [E, H/128, I/128];
+ * topk_weights f32 / topk_ids i32 [T, topk] (negative ids and experts mapped
+ * to a negative local id contribute nothing); out [T, H] bf16.
+ * swiglu_limit > 0 selects the clamped activation.  path: AUTO picks the
+ * decode (expert-major GEMV, weights streamed once) or the prefill (grouped
+ * MFMA GEMM) kernels by T; GEMV / GEMM force one.  Workspace:
+ * vmamd_fused_moe_fp8_workspace_size() bytes, 256-byte aligned.
+ * Replaces fused_experts_impl / _musa_fused_experts_impl_dispatch
+ * (vllm_musa/model_executor/layers/fused_moe/fused_moe.py:1935-2184,
+ * 2214-2760) for use_fp8_w8a8 with block_shape [128, 128], including the
+ * DeepGEMM prefill path (824-951) and the native GEMV-MoE
+ * musa_fused_gemv_moe (csrc/musa/gemv.mu:927-1170). */
+#define VMAMD_MOE_PATH_AUTO 0
+#define VMAMD_MOE_PATH_GEMV 1
+#define VMAMD_MOE_PATH_GEMM 2
+size_t vmamd_fused_moe_fp8_workspace_size(int64_t T, int topk, int num_experts, int64_t H,
+                                          int64_t I, int path);
+int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H, const void* w13,
+                        const float* w13_s, const void* w2, const float* w2_s, int num_experts,
+                        int64_t I, const float* topk_weights, const int32_t* topk_ids, int topk,
+                        const int32_t* expert_map, int64_t expert_map_len, float swiglu_limit,
+                        int path, void* out, void* workspace, size_t workspace_bytes,
+                        vmamd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

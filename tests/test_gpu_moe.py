@@ -1,0 +1,167 @@
+"""GPU parity of the fused fp8 block MoE layer (decode GEMV path and prefill
+grouped-GEMM path) against the oracle on identical seeded inputs.
+
+Tolerance (the path's bar for bf16/fp8 outputs): rel-L2 <= 1e-2 and
+max-abs <= 2e-2 * max|ref|."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as omoe
+from oracle import routing as oroute
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _check(out: torch.Tensor, ref: np.ndarray, rel_l2=1e-2, max_frac=2e-2):
+    o = out.float().cpu().numpy().astype(np.float64)
+    err = o - ref
+    rl2 = np.linalg.norm(err) / max(np.linalg.norm(ref), 1e-30)
+    assert np.isfinite(o).all()
+    assert rl2 <= rel_l2, f"rel-L2 {rl2}"
+    assert np.abs(err).max() <= max_frac * np.abs(ref).max(), f"max-abs {np.abs(err).max()}"
+    return rl2
+
+
+def _routing(T, E, K, seed, hot=None):
+    g = torch.Generator().manual_seed(seed)
+    if hot is None:
+        ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    else:  # every token takes the hot expert plus K-1 distinct others
+        others = torch.tensor([e for e in range(E) if e != hot])
+        ids = torch.stack([torch.cat([torch.tensor([hot]),
+                                      others[torch.randperm(E - 1, generator=g)[:K - 1]]])
+                           for _ in range(T)])
+    ids = ids.to(torch.int32)
+    w = torch.softmax(torch.randn(T, K, generator=g), dim=-1)
+    return w, ids
+
+
+def _case(T, E, H, I, K, seed, hot=None):
+    from vllm_musa_amd import synthetic
+    w13, s13, w2, s2 = synthetic.moe_fp8_weights(E, H, I, seed)
+    x = synthetic.activations(T, H, seed + 1)
+    w, ids = _routing(T, E, K, seed + 2, hot)
+    return x, w13, s13, w2, s2, w.to(DEV), ids.to(DEV)
+
+
+def _oracle(x, w13, s13, w2, s2, w, ids, emap=None):
+    """Oracle on the experts the routing touches (only those weights are copied
+    to the host); ids are remapped onto the compact expert stack."""
+    ids_np = ids.cpu().numpy()
+    loc = omoe.local_experts(ids_np, None if emap is None else emap.cpu().numpy(), w13.shape[0])
+    used = np.unique(loc[loc >= 0])
+    remap = np.full(w13.shape[0], -1, np.int64)
+    remap[used] = np.arange(used.size)
+    cids = np.where(loc >= 0, remap[np.maximum(loc, 0)], -1).astype(np.int32)
+    sel = torch.from_numpy(used).to(w13.device)
+    u8 = lambda t: t.view(torch.uint8).index_select(0, sel).cpu().numpy()
+    f32 = lambda t: t.index_select(0, sel).cpu().numpy()
+    return omoe.fused_experts_fp8(x.float().cpu().numpy(), u8(w13), f32(s13), u8(w2), f32(s2),
+                                  w.cpu().numpy(), cids)
+
+
+def _run(x, w13, s13, w2, s2, w, ids, path, emap=None, limit=None):
+    from vllm_musa_amd.fused_moe import fused_experts_impl
+    return fused_experts_impl(x, w13, w2, w, ids, use_fp8_w8a8=True, w1_scale=s13, w2_scale=s2,
+                              block_shape=[128, 128], expert_map=emap, gemm1_clamp_limit=limit,
+                              path=path)
+
+
+@pytest.mark.parametrize("path", ["gemv", "gemm"])
+@pytest.mark.parametrize("T", [1, 3, 16, 64, 257])
+def test_fp8_moe_small_vs_oracle(T, path):
+    case = _case(T, 16, 1024, 512, 4, seed=100 + T)
+    out = _run(*case, path=path)
+    _check(out, _oracle(*case))
+
+
+@pytest.mark.parametrize("path", ["gemv", "gemm"])
+def test_fp8_moe_hot_expert_multi_block(path):
+    # 600 routes on one expert: several 16-route and 128-route blocks
+    case = _case(600, 16, 1024, 256, 4, seed=7, hot=3)
+    out = _run(*case, path=path)
+    _check(out, _oracle(*case))
+
+
+@pytest.mark.parametrize("path", ["gemv", "gemm"])
+def test_fp8_moe_expert_map(path):
+    x, w13, s13, w2, s2, w, ids = _case(40, 8, 512, 256, 4, seed=11)
+    # global ids 0..15; this rank owns global experts 8..15 as local 0..7
+    g = torch.Generator().manual_seed(12)
+    gids = torch.stack([torch.randperm(16, generator=g)[:4] for _ in range(40)]).to(torch.int32).to(DEV)
+    emap = torch.full((16,), -1, dtype=torch.int32)
+    emap[8:] = torch.arange(8, dtype=torch.int32)
+    emap = emap.to(DEV)
+    out = _run(x, w13, s13, w2, s2, w, gids, path, emap=emap)
+    _check(out, _oracle(x, w13, s13, w2, s2, w, gids, emap=emap))
+
+
+def test_fp8_moe_paths_agree():
+    case = _case(48, 32, 2048, 768, 8, seed=21)
+    a = _run(*case, path="gemv").float()
+    b = _run(*case, path="gemm").float()
+    rl2 = (torch.linalg.norm(a - b) / torch.linalg.norm(b)).item()
+    assert rl2 < 5e-3, rl2
+
+
+def test_fp8_moe_deterministic():
+    case = _case(200, 16, 1024, 512, 4, seed=31)
+    for path in ("gemv", "gemm"):
+        a = _run(*case, path=path)
+        b = _run(*case, path=path)
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("path", ["gemv", "gemm"])
+def test_fp8_moe_dsv3_shape(path):
+    """DeepSeek-V3 layer shape (E=256, H=7168, I=2048, grouped sigmoid routing,
+    top-8) at T=2, checked against the oracle on every output."""
+    from vllm_musa_amd import grouped_topk, synthetic
+    T, E, H, I = 2, 256, 7168, 2048
+    w13, s13, w2, s2 = synthetic.moe_fp8_weights(E, H, I, seed=3000)
+    x = synthetic.activations(T, H, 3001)
+    logits = synthetic.router_logits(T, E, 3002)
+    bias = synthetic.score_bias(E, 3003)
+    w, ids = grouped_topk(x, logits, 8, True, 8, 4, "sigmoid", 2.5, bias)
+    w_ref, ids_ref = oroute.grouped_topk(logits.cpu().numpy(), 8, True, 8, 4, "sigmoid", 2.5,
+                                         bias.cpu().numpy())
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    out = _run(x, w13, s13, w2, s2, w, ids, path)
+    _check(out, _oracle(x, w13, s13, w2, s2, w, ids))
+
+
+def test_fp8_moe_empty_and_inplace():
+    from vllm_musa_amd.fused_moe import fused_experts_impl
+    x, w13, s13, w2, s2, w, ids = _case(5, 8, 512, 256, 2, seed=41)
+    empty = fused_experts_impl(x[:0], w13, w2, w[:0], ids[:0], use_fp8_w8a8=True, w1_scale=s13,
+                               w2_scale=s2, block_shape=[128, 128])
+    assert empty.shape == (0, 512)
+    ref = _run(x, w13, s13, w2, s2, w, ids, "auto")
+    xi = x.clone()
+    got = fused_experts_impl(xi, w13, w2, w, ids, use_fp8_w8a8=True, w1_scale=s13, w2_scale=s2,
+                             block_shape=[128, 128], inplace=True)
+    assert got.data_ptr() == xi.data_ptr() and torch.equal(got, ref)
+
+
+def test_fp8_moe_poisoned_workspace(monkeypatch):
+    """Workspace and outputs start as NaN bytes: every value the layer reads
+    must have been written by it."""
+    case = _case(33, 16, 1024, 512, 4, seed=51)
+    ref = _oracle(*case)
+    real_empty = torch.empty
+
+    def poisoned(*args, **kwargs):
+        t = real_empty(*args, **kwargs)
+        if t.is_cuda:
+            t.view(torch.uint8).fill_(0xFF)
+        return t
+
+    monkeypatch.setattr(torch, "empty", poisoned)
+    monkeypatch.setattr(torch, "empty_like", lambda t, **kw: poisoned(t.shape, dtype=t.dtype,
+                                                                      device=t.device))
+    for path in ("gemv", "gemm"):
+        _check(_run(*case, path=path), ref)

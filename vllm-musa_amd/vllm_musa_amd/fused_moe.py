@@ -3,12 +3,18 @@
 This module keeps the reference's Python entry points:
   moe_align_block_size(topk_ids, block_size, num_experts, expert_map=None, pad_sorted_ids=False)
       upstream wrapper of the _moe_C op (sizing as fused_moe.py:881-884)
+  fused_experts_impl(...)   fused_moe.py:1935-1965 / the dispatcher 2214-2240
+  fused_experts(..., quant_config)
+The whole layer is one C-ABI call (vmamd_fused_moe_*) that enqueues all of its
+kernels on the current stream; Python only validates and allocates.
 """
 from __future__ import annotations
 
 import torch
 
 from . import _custom_ops as ops
+from . import _lib
+from ._lib import call, ptr, stream_of
 
 
 def _round_up(x: int, m: int) -> int:
@@ -37,3 +43,122 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: i
     if return_offsets:
         return sorted_ids, expert_ids, ntpp, offsets
     return sorted_ids, expert_ids, ntpp
+
+
+# ---------------------------------------------------------------- experts --
+PATHS = {"auto": 0, "gemv": 1, "gemm": 2}
+
+
+def _expand_fp8_scale(scale: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """Per-tensor / per-expert fp8 scales -> the [E, ceil(N/128), K/128] block
+    view (reference: _maybe_expand_fp8_moe_per_tensor_scale, fused_moe.py:1212-1259)."""
+    e, n, k = w.shape
+    want = (e, (n + 127) // 128, k // 128)
+    s = scale.to(torch.float32)
+    if tuple(s.shape) == want:
+        return s.contiguous()
+    if s.numel() == 1:
+        return s.reshape(1, 1, 1).expand(want).contiguous()
+    if s.numel() == e:
+        return s.reshape(e, 1, 1).expand(want).contiguous()
+    raise ValueError(f"fp8 MoE scale of shape {tuple(scale.shape)} does not match the "
+                     f"128x128 block grid {want}")
+
+
+def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                       topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                       activation: str = "silu", apply_router_weight_on_input: bool = False,
+                       use_fp8_w8a8: bool = False, use_int8_w8a8: bool = False,
+                       use_int8_w8a16: bool = False, use_int4_w4a16: bool = False,
+                       ocp_mx_scheme: str | None = None, per_channel_quant: bool = False,
+                       global_num_experts: int = -1, expert_map: torch.Tensor | None = None,
+                       w1_scale: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
+                       w1_zp: torch.Tensor | None = None, w2_zp: torch.Tensor | None = None,
+                       a1_scale: torch.Tensor | None = None, a2_scale: torch.Tensor | None = None,
+                       block_shape: list[int] | None = None, w1_bias: torch.Tensor | None = None,
+                       w2_bias: torch.Tensor | None = None,
+                       gemm1_clamp_limit: float | None = None, *, inplace: bool = False,
+                       path: str = "auto") -> torch.Tensor:
+    """Drop-in for the reference's fused_experts_impl
+    (vllm_musa/model_executor/layers/fused_moe/fused_moe.py:1935-1965, 2214-2240):
+    out[t] = sum_k w[t,k] * W2[e] . act(W13[e] . x[t]) with the reference's
+    rounding points.  Supported: bf16 weights, and fp8 weights with 128x128
+    block scales (use_fp8_w8a8, block_shape=[128, 128]) and dynamic 1x128
+    activation quantisation.  ``path`` forces the decode ("gemv") or prefill
+    ("gemm") kernels; "auto" picks by token count."""
+    if activation != "silu":
+        raise NotImplementedError(f"activation {activation!r}: only silu (SwiGLU) is on this path")
+    if use_int8_w8a8 or use_int8_w8a16 or use_int4_w4a16 or ocp_mx_scheme or per_channel_quant:
+        raise NotImplementedError("int8 / int4-w4a16 / MX / per-channel MoE are not on this path")
+    if apply_router_weight_on_input:
+        raise NotImplementedError("apply_router_weight_on_input is not on this path")
+    if w1_bias is not None or w2_bias is not None or w1_zp is not None or w2_zp is not None:
+        raise NotImplementedError("expert biases / zero points are not on this path")
+    if a1_scale is not None or a2_scale is not None:
+        raise NotImplementedError("static activation scales: only dynamic 1x128 quantisation")
+    if hidden_states.dim() != 2 or hidden_states.dtype != torch.bfloat16:
+        raise ValueError("hidden_states must be bf16 [T, H]")
+    if hidden_states.shape[1] != w1.shape[2]:
+        raise ValueError(f"Hidden size mismatch {hidden_states.shape[1]} != {w1.shape[2]}")
+    if topk_weights.shape != topk_ids.shape:
+        raise ValueError("topk shape mismatch")
+    if not hidden_states.is_contiguous():
+        raise ValueError("Hidden_states must be contiguous")
+    t, h = hidden_states.shape
+    e, n2, _ = w1.shape
+    i = n2 // 2
+    if w2.shape != (e, h, i):
+        raise ValueError(f"w2 must be [E, H, I] = {(e, h, i)}, got {tuple(w2.shape)}")
+    topk = topk_ids.shape[1]
+    out = hidden_states if (inplace and t > 0) else torch.empty_like(hidden_states)
+    if t == 0:
+        return out
+    ids = topk_ids.to(torch.int32).contiguous()
+    wts = topk_weights.to(torch.float32).contiguous()
+    emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
+    limit = 0.0 if gemm1_clamp_limit is None else float(gemm1_clamp_limit)
+    code = PATHS[path]
+    if use_fp8_w8a8:
+        if block_shape is None or list(block_shape) != [128, 128]:
+            raise NotImplementedError("fp8 MoE on this path needs block_shape=[128, 128]")
+        if w1.dtype != torch.float8_e4m3fn or w2.dtype != torch.float8_e4m3fn:
+            raise ValueError("fp8 MoE weights must be float8_e4m3fn")
+        if w1_scale is None or w2_scale is None:
+            raise ValueError("fp8 MoE needs w1_scale and w2_scale")
+        s1 = _expand_fp8_scale(w1_scale, w1)
+        s2 = _expand_fp8_scale(w2_scale, w2)
+        w1c, w2c = w1.contiguous(), w2.contiguous()
+        _lib.check_cuda(hidden_states, w1c, w2c, s1, s2, wts, ids, emap)
+        lib = _lib.load()
+        nbytes = lib.vmamd_fused_moe_fp8_workspace_size(t, topk, e, h, i, code)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=hidden_states.device)
+        call("vmamd_fused_moe_fp8", ptr(hidden_states), _lib.DTYPE_BF16, t, h, ptr(w1c), ptr(s1),
+             ptr(w2c), ptr(s2), e, i, ptr(wts), ptr(ids), topk, ptr(emap),
+             0 if emap is None else emap.numel(), limit, code, ptr(out), ptr(ws), nbytes,
+             stream_of(hidden_states))
+        return out
+    if w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16:
+        return _fused_experts_bf16(hidden_states, w1, w2, wts, ids, emap, limit, code, out)
+    raise NotImplementedError(f"MoE weights of dtype {w1.dtype} are not on this path")
+
+
+def _fused_experts_bf16(x, w1, w2, wts, ids, emap, limit, code, out):
+    raise NotImplementedError("bf16 MoE kernels are not built yet")
+
+
+def fused_experts(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                  topk_weights: torch.Tensor, topk_ids: torch.Tensor, inplace: bool = False,
+                  activation: str = "silu", apply_router_weight_on_input: bool = False,
+                  global_num_experts: int = -1, expert_map: torch.Tensor | None = None,
+                  quant_config=None) -> torch.Tensor:
+    """Upstream fused_experts(..., quant_config) entry (called from the quant
+    methods, quantization/fp8.py:261-272 and unquantized_fused_moe_method.py:119-130)."""
+    qc = quant_config
+    return fused_experts_impl(
+        hidden_states, w1, w2, topk_weights, topk_ids, activation=activation,
+        apply_router_weight_on_input=apply_router_weight_on_input,
+        use_fp8_w8a8=bool(getattr(qc, "use_fp8_w8a8", False)),
+        global_num_experts=global_num_experts, expert_map=expert_map,
+        w1_scale=getattr(qc, "w1_scale", None), w2_scale=getattr(qc, "w2_scale", None),
+        block_shape=getattr(qc, "block_shape", None),
+        gemm1_clamp_limit=getattr(qc, "gemm1_clamp_limit", None), inplace=inplace)
