@@ -46,6 +46,6 @@ def test_argument_errors_are_reported_without_a_gpu():
                   448.0, None, None, 1, 1, None)
     with pytest.raises(ValueError, match="capacity"):
         _lib.call("vmamd_moe_align_block_size", None, 100, 8, 16, None, 0, None, 10, None, None,
-                  None, None, None)
+                  None, None, None, None, None)
     msg = _lib.load().vmamd_last_error().decode()
     assert "capacity" in msg
