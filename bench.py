@@ -1,0 +1,268 @@
+"""Benchmark of the fp8 block-quantised fused-MoE layer on one MI355X.
+
+Workload (the headline line): one DeepSeek-V3-shape MoE layer -- E=256 routed
+experts, grouped sigmoid+bias routing (8 groups, top-4 groups, top-8 experts,
+renormalised, x2.5), H=7168, I=2048, W13/W2 in e4m3fn with 128x128 block
+scales, activations quantised per 1x128 group -- at T=4096 tokens.  A step is
+routing (grouped_topk) + fused_experts_impl over one batch whose inputs are
+already in HBM.  Synthetic data: weights ~N(0, 0.02) quantised per block,
+activations ~N(0, 1), logits ~N(0, 1), score bias ~N(0, 0.1).
+
+Printed (rank 0, one JSON line): value = algorithmic TFLOP/s of the layer at
+T=4096 (2*T*topk*3*H*I flops per call), ms_per_step from HIP events around the
+K timed steps; `sweep` gives us / TFLOP/s / GB/s and roofline fractions at
+T = 1, 16, 256, 4096 (cold weights: a 1 GiB buffer is rewritten between
+iterations); `roofline` is the dominant kernel (W13 grouped GEMM at T=4096)
+timed on its own with HIP events on its launch stream; `cpu_baseline` times
+the CPU oracle on a bounded sample of the same layer.
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-sweep] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "vllm-musa_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+# MI355X published peaks.
+PEAK_HBM_GBS = 8000.0
+PEAK_FP8_TFLOPS = 5000.0
+
+E, H, I, TOPK, GROUPS, TOPK_GROUP, SCALE = 256, 7168, 2048, 8, 8, 4, 2.5
+T_HEADLINE = 4096
+SWEEP_T = (1, 16, 256, 4096)
+WEIGHT_SEED = 3000
+
+METRIC = "fp8-block MoE layer µs, TFLOPS & HBM GB/s (% roofline) at T=1..4096"
+
+
+def layer_flops(routes: int) -> float:
+    return 2.0 * routes * (2 * I * H + H * I)
+
+
+def layer_bytes(t: int, used_experts: int) -> float:
+    """Algorithmic HBM bytes of one layer call: each touched expert's fp8
+    weights and block scales once, x (bf16) in, out (bf16) out, logits in,
+    routing weights/ids out."""
+    w = 3 * I * H + 4 * ((2 * I // 128) * (H // 128) + (H // 128) * (I // 128))
+    return used_experts * w + 4.0 * t * H + 4.0 * t * E + 8.0 * t * TOPK
+
+
+def w13_bytes(t: int, used_experts: int) -> float:
+    """Algorithmic bytes of one W13 launch: touched experts' W13 + scales,
+    fp8 x + scales in, fp8 a2 + scales out."""
+    w = 2 * I * H + 4 * (2 * I // 128) * (H // 128)
+    routes = t * TOPK
+    return used_experts * w + t * (H + 4 * H // 128) + routes * (I + 4 * I // 128)
+
+
+class Layer:
+    def __init__(self, torch, t: int, weights):
+        from vllm_musa_amd import synthetic
+        self.torch = torch
+        self.t = t
+        self.w13, self.s13, self.w2, self.s2 = weights
+        self.x = synthetic.activations(t, H, WEIGHT_SEED + 10 * t + 1)
+        self.logits = synthetic.router_logits(t, E, WEIGHT_SEED + 10 * t + 2)
+        self.bias = synthetic.score_bias(E, WEIGHT_SEED + 3)
+
+    def route(self):
+        from vllm_musa_amd import grouped_topk
+        return grouped_topk(self.x, self.logits, TOPK, True, GROUPS, TOPK_GROUP, "sigmoid", SCALE,
+                            self.bias)
+
+    def step(self):
+        from vllm_musa_amd.fused_moe import fused_experts_impl
+        w, ids = self.route()
+        return fused_experts_impl(self.x, self.w13, self.w2, w, ids, use_fp8_w8a8=True,
+                                  w1_scale=self.s13, w2_scale=self.s2, block_shape=[128, 128])
+
+    def used_experts(self) -> int:
+        _, ids = self.route()
+        return int(self.torch.unique(ids).numel())
+
+
+def time_events(torch, fn, iters: int, flush=None) -> list[float]:
+    """Per-call milliseconds from HIP events on the current stream; `flush`
+    (untimed) runs before each call."""
+    out = []
+    for _ in range(iters):
+        if flush is not None:
+            flush()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        b.synchronize()
+        out.append(a.elapsed_time(b))
+    return out
+
+
+def cpu_baseline(torch, layer: Layer, target_s: float = 15.0) -> dict:
+    """Time the CPU oracle on a bounded sample of the T=4096 layer: the routes
+    of a few experts (their tokens, their weights), same arithmetic as the
+    full layer.  Reported in the layer's unit (TFLOP/s)."""
+    import numpy as np
+
+    from oracle import moe as omoe
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([d.get("num_threads", 1) for d in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = 1
+    w, ids = layer.route()
+    ids_np = ids.cpu().numpy()
+    w_np = w.cpu().numpy()
+    x_np = layer.x.float().cpu().numpy()
+    counts = np.bincount(ids_np.ravel(), minlength=E)
+    order = np.argsort(-counts, kind="stable")
+    done_routes, elapsed, n_exp = 0, 0.0, 0
+    for e in order:
+        if elapsed >= target_s or n_exp >= 16:
+            break
+        toks = np.nonzero((ids_np == e).any(axis=1))[0]
+        sub_ids = np.where(ids_np[toks] == e, 0, -1).astype(np.int32)
+        sel = torch.tensor([int(e)], device=layer.w13.device)
+        u8 = lambda t: t.view(torch.uint8).index_select(0, sel).cpu().numpy()
+        f32 = lambda t: t.index_select(0, sel).cpu().numpy()
+        args = (x_np[toks], u8(layer.w13), f32(layer.s13), u8(layer.w2), f32(layer.s2),
+                w_np[toks], sub_ids)
+        t0 = time.perf_counter()
+        omoe.fused_experts_fp8(*args)
+        elapsed += time.perf_counter() - t0
+        done_routes += int((sub_ids >= 0).sum())
+        n_exp += 1
+    tflops = layer_flops(done_routes) / elapsed / 1e12
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+            "sample": f"numpy float64 oracle (oracle/moe.py fused_experts_fp8) on {n_exp} experts of "
+                      f"the T={layer.t} layer ({done_routes} routes, {elapsed:.1f} s); full-layer "
+                      f"CPU time extrapolates to "
+                      f"{layer_flops(layer.t * TOPK) / (tflops * 1e12):.0f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--sweep-iters", type=int, default=20)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the MoE layer runs on a single MI355X here "
+              f"(--gpus {args.gpus} is not supported)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import vllm_musa_amd
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.fused_moe import Fp8MoeStages
+    vllm_musa_amd.load()
+    torch.cuda.set_device(0)
+    log = lambda *a: print(*a, file=sys.stderr, flush=True)
+
+    log(f"bench: building E={E} H={H} I={I} fp8 expert stack")
+    weights = synthetic.moe_fp8_weights(E, H, I, WEIGHT_SEED)
+    torch.cuda.synchronize()
+
+    # ---------------------------------------------------------- headline --
+    layer = Layer(torch, T_HEADLINE, weights)
+    u_head = layer.used_experts()
+    for _ in range(args.warmup):
+        layer.step()
+    torch.cuda.synchronize()
+    log(f"bench: timing {args.steps} steps at T={T_HEADLINE}")
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        layer.step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    ms = ev0.elapsed_time(ev1) / args.steps
+    flops = layer_flops(T_HEADLINE * TOPK)
+    value = flops / (ms * 1e-3) / 1e12
+    head_bytes = layer_bytes(T_HEADLINE, u_head)
+
+    # --------------------------------------------- dominant kernel: W13 ----
+    w, ids = layer.route()
+    st = Fp8MoeStages(layer.x, *weights, w, ids, path="auto")
+    st.quant()
+    st.align()
+    for _ in range(3):
+        st.w13_stage()
+    torch.cuda.synchronize()
+    k_ms = statistics.mean(time_events(torch, st.w13_stage, max(args.steps, 10)))
+    k_bytes = w13_bytes(T_HEADLINE, u_head)
+    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": "moe_w13_gemm_fp8_kernel",
+                "kernel_us": round(k_ms * 1e3, 1),
+                "kernel_tflops": round(2.0 * T_HEADLINE * TOPK * 2 * I * H / (k_ms * 1e-3) / 1e12, 1),
+                "algorithmic_bytes": int(k_bytes)}
+    del st
+
+    # ------------------------------------------------------------- sweep ---
+    sweep = []
+    if not args.no_sweep:
+        flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        flush = lambda: flush_buf.fill_(1)
+        for t in SWEEP_T:
+            lay = layer if t == T_HEADLINE else Layer(torch, t, weights)
+            u = lay.used_experts()
+            for _ in range(3):
+                lay.step()
+            torch.cuda.synchronize()
+            times = time_events(torch, lay.step, args.sweep_iters, flush)
+            med = statistics.median(times)
+            f = layer_flops(t * TOPK)
+            b = layer_bytes(t, u)
+            ideal = max(f / (PEAK_FP8_TFLOPS * 1e12), b / (PEAK_HBM_GBS * 1e9))
+            sweep.append({"T": t, "experts_touched": u, "us": round(med * 1e3, 1),
+                          "tflops": round(f / (med * 1e-3) / 1e12, 2),
+                          "gbps": round(b / (med * 1e-3) / 1e9, 1),
+                          "frac_hbm": round(b / (med * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                          "frac_fp8_peak": round(f / (med * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+                          "frac_roofline": round(ideal / (med * 1e-3), 4)})
+            log(f"bench: sweep {sweep[-1]}")
+        del flush_buf
+
+    cpu = None
+    if not args.no_cpu:
+        log("bench: CPU baseline (bounded sample)")
+        cpu = cpu_baseline(torch, layer)
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "wall_s_timed": round(wall, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8", "data": "synthetic",
+        "config": {"workload": "DeepSeek-V3-shape fp8 block MoE layer (routing + fused experts)",
+                   "T": T_HEADLINE, "E": E, "topk": TOPK, "H": H, "I": I,
+                   "routing": "grouped sigmoid+bias, 8 groups / top-4, renorm, x2.5",
+                   "weights": "e4m3fn, 128x128 block scales", "activations": "1x128 fp8 groups",
+                   "experts_touched": u_head, "algorithmic_gbps":
+                       round(head_bytes / (ms * 1e-3) / 1e9, 1)},
+        "roofline": roofline, "cpu_baseline": cpu, "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

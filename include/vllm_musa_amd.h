@@ -207,6 +207,47 @@ int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H, const 
                         int path, void* out, void* workspace, size_t workspace_bytes,
                         vmamd_stream_t stream);
 
+/* ------------------------------------------------ fused-MoE fp8 stages --
+ * The two grouped expert GEMMs of vmamd_fused_moe_fp8, callable one by one
+ * over the outputs of vmamd_per_token_group_quant_fp8 (xq, xs) and
+ * vmamd_moe_align_block_size (sorted_token_ids of length `capacity`,
+ * expert_offsets, num_tokens_post_pad, and for block_m 16 active_experts /
+ * num_active).  block_m selects the kernels and must equal the align call's
+ * block_size: 16 = decode (expert-major GEMV, each weight row streamed once
+ * per call), 128 = prefill (grouped MFMA GEMM over 128-route blocks).
+ *
+ * W13:  a = bf16(silu(h_gate) * h_up), h = bf16(W13[e] . q(x[t])), then a is
+ *       quantised per 1x128 group into a2q (fp8) / a2s (f32, [rows, I/128]).
+ *       Rows of a2q/a2s are routes (r = t*topk + k, [T*topk, I]) for
+ *       block_m 16, positions of sorted_token_ids ([capacity, I]) for 128.
+ * W2:   y[r] = bf16(W2[e] . dequant(a2q[row(r)]) * topk_weights[r]),
+ *       y [T*topk, H] bf16; rows of dropped routes are left unwritten.
+ * Scratch: vmamd_moe_fp8_stage_workspace_size() bytes, 16-byte aligned
+ * (enough for either stage).
+ * Replace the two invoke_fused_moe_kernel launches of the upstream
+ * fused_experts_impl (block-scaled accumulate:
+ * vllm_musa/patches/series/0081-MUSA-vllm.model_executor.layers.fused_moe.fused_moe.patch:64-108;
+ * activation then a2 quantisation: 0144-…:62-78) and the two
+ * m_grouped_fp8_gemm_nt_contiguous calls of the DeepGEMM prefill path
+ * (vllm_musa/model_executor/layers/fused_moe/fused_moe.py:914-934). */
+size_t vmamd_moe_fp8_stage_workspace_size(int64_t T, int topk, int num_experts, int64_t H,
+                                          int64_t I, int block_m);
+int vmamd_moe_fp8_w13(const void* xq, const float* xs, int64_t T, int64_t H, int topk,
+                      const int32_t* sorted_token_ids, int64_t capacity, int block_m,
+                      const int32_t* expert_offsets, const int32_t* num_tokens_post_pad,
+                      const int32_t* active_experts, const int32_t* num_active, const void* w13,
+                      const float* w13_s, int num_experts, int64_t I, float swiglu_limit,
+                      void* a2q, float* a2s, void* workspace, size_t workspace_bytes,
+                      vmamd_stream_t stream);
+int vmamd_moe_fp8_w2(const void* a2q, const float* a2s, int64_t T, int topk,
+                     const int32_t* sorted_token_ids, int64_t capacity, int block_m,
+                     const int32_t* expert_offsets, const int32_t* num_tokens_post_pad,
+                     const int32_t* active_experts, const int32_t* num_active, const void* w2,
+                     const float* w2_s, int num_experts, int64_t H, int64_t I,
+                     const float* topk_weights, const int32_t* topk_ids,
+                     const int32_t* expert_map, int64_t expert_map_len, void* y,
+                     void* workspace, size_t workspace_bytes, vmamd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

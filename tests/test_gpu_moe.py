@@ -165,3 +165,16 @@ def test_fp8_moe_poisoned_workspace(monkeypatch):
                                                                       device=t.device))
     for path in ("gemv", "gemm"):
         _check(_run(*case, path=path), ref)
+
+
+@pytest.mark.parametrize("path", ["gemv", "gemm"])
+def test_fp8_moe_stages_match_fused(path):
+    """The stage-by-stage launches (quant, align, W13, W2, combine) give the
+    fused call's output bit for bit."""
+    from vllm_musa_amd.fused_moe import Fp8MoeStages
+    case = _case(70, 16, 1024, 512, 4, seed=61)
+    ref = _run(*case, path=path)
+    x, w13, s13, w2, s2, w, ids = case
+    st = Fp8MoeStages(x, w13, s13, w2, s2, w, ids, path=path)
+    assert torch.equal(st.run(), ref)
+    assert torch.equal(st.run(), ref)  # buffers reused on a second pass

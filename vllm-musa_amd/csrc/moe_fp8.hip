@@ -491,18 +491,115 @@ __global__ __launch_bounds__(256, 2) void moe_w2_gemm_fp8_kernel(
 }
 
 // ------------------------------------------------------------ host side ---
-// Workspace carve-up shared by the size query and the launcher.
-struct MoeFp8Ws {
-  size_t xq, xs, sorted, eids, ntpp, offs, active, nact, hpart, a2q, a2s, y2part, y, total;
-};
+// Split-K factor of the decode GEMVs: enough waves to cover the chip
+// (>= 4096 over the active experts' n-tiles), at least 4 K-blocks per split.
+static int moe_splits(int64_t waves_per_split, int KB) {
+  int s = static_cast<int>((4096 + waves_per_split - 1) / waves_per_split);
+  return max(1, min(s, max(1, KB / 4)));
+}
+
+static int64_t moe_umax(int64_t numel, int E) { return std::min<int64_t>(E, numel); }
+
+static int w13_splits(int64_t numel, int E, int64_t H, int64_t I) {
+  return moe_splits(moe_umax(numel, E) * (2 * I / 16), static_cast<int>(H / 128));
+}
+static int w2_splits(int64_t numel, int E, int64_t H, int64_t I) {
+  return moe_splits(moe_umax(numel, E) * (H / 16), static_cast<int>(I / 128));
+}
 
 static size_t al256(size_t x) { return (x + 255) / 256 * 256; }
 
-static MoeFp8Ws moe_fp8_layout(int64_t T, int topk, int E, int64_t H, int64_t I, bool gemv,
-                               int s13, int s2) {
+// Stage scratch: fp32 split-K partials of the decode GEMVs (none for GEMMs).
+static size_t w13_scratch(int64_t numel, int E, int64_t H, int64_t I, int block_m) {
+  if (block_m != kGemvBlock) return 0;
+  return al256(static_cast<size_t>(w13_splits(numel, E, H, I)) * numel * 2 * I * 4);
+}
+static size_t w2_scratch(int64_t numel, int E, int64_t H, int64_t I, int block_m) {
+  if (block_m != kGemvBlock) return 0;
+  const int s = w2_splits(numel, E, H, I);
+  return s > 1 ? al256(static_cast<size_t>(s) * numel * H * 4) : 0;
+}
+
+static bool g_w13_lds_raised = false;
+
+// Launches of the two stages; arguments are validated by the callers.
+static int launch_w13(const uint8_t* xq, const float* xs, int T, int H, int topk, const int32_t* sorted,
+                      int64_t cap, int block_m, const int32_t* offs, const int32_t* ntpp,
+                      const int32_t* active, const int32_t* nact, const uint8_t* w13,
+                      const float* w13_s, int E, int I, float limit, uint8_t* a2q, float* a2s,
+                      float* scratch, hipStream_t st) {
+  const int numel = T * topk;
+  if (block_m == kGemvBlock) {
+    const int s13 = w13_splits(numel, E, H, I);
+    const int umax = static_cast<int>(moe_umax(numel, E));
+    dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s13);
+    moe_gemv_fp8_kernel<4><<<g13, kMoeGemvWaves * kWave, 0, st>>>(
+        xq, xs, topk, H, sorted, offs, active, nact, w13, w13_s, 2 * I, numel, s13, scratch,
+        nullptr, nullptr);
+    int rc = check_launch("moe_fp8_w13(gemv)");
+    if (rc) return rc;
+    const int64_t groups = static_cast<int64_t>(numel) * (I / 128);
+    moe_act_quant_kernel<<<static_cast<int>((groups + 15) / 16), 256, 0, st>>>(scratch, s13, numel, I,
+                                                                               limit, a2q, a2s);
+    return check_launch("moe_fp8_w13(act quant)");
+  }
+  const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
+  const int tiles = max_blocks * (I / 128);
+  if (!g_w13_lds_raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_w13_gemm_fp8_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kW13Lds) != hipSuccess) {
+      set_error("moe_fp8_w13: cannot raise the LDS limit of the W13 kernel");
+      return VMAMD_ERR_HIP;
+    }
+    g_w13_lds_raised = true;
+  }
+  moe_w13_gemm_fp8_kernel<<<xcd_grid(tiles), kW13Threads, kW13Lds, st>>>(
+      xq, xs, topk, H, sorted, offs, ntpp, E, numel, tiles, w13, w13_s, I, limit, a2q, a2s);
+  return check_launch("moe_fp8_w13(gemm)");
+}
+
+static int launch_w2(const uint8_t* a2q, const float* a2s, int T, int topk, const int32_t* sorted,
+                     int64_t cap, int block_m, const int32_t* offs, const int32_t* ntpp,
+                     const int32_t* active, const int32_t* nact, const uint8_t* w2, const float* w2_s,
+                     int E, int H, int I, const float* topk_weights, const int32_t* topk_ids,
+                     const int32_t* emap, int64_t emap_len, uint16_t* y, float* scratch,
+                     hipStream_t st) {
+  const int numel = T * topk;
+  if (block_m == kGemvBlock) {
+    const int s2 = w2_splits(numel, E, H, I);
+    const int umax = static_cast<int>(moe_umax(numel, E));
+    dim3 g2((H / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s2);
+    if (s2 == 1) {
+      moe_gemv_fp8_kernel<4><<<g2, kMoeGemvWaves * kWave, 0, st>>>(
+          a2q, a2s, 1, I, sorted, offs, active, nact, w2, w2_s, H, numel, 1, nullptr, topk_weights, y);
+      return check_launch("moe_fp8_w2(gemv)");
+    }
+    moe_gemv_fp8_kernel<4><<<g2, kMoeGemvWaves * kWave, 0, st>>>(
+        a2q, a2s, 1, I, sorted, offs, active, nact, w2, w2_s, H, numel, s2, scratch, nullptr, nullptr);
+    int rc = check_launch("moe_fp8_w2(gemv)");
+    if (rc) return rc;
+    const int64_t mn = static_cast<int64_t>(numel) * H;
+    moe_w2_reduce_kernel<<<static_cast<int>((mn / 4 + 255) / 256), 256, 0, st>>>(
+        scratch, s2, numel, H, topk_ids, emap, emap_len, topk_weights, y);
+    return check_launch("moe_fp8_w2(reduce)");
+  }
+  const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
+  const int tiles = max_blocks * ((H + 127) / 128);
+  moe_w2_gemm_fp8_kernel<<<xcd_grid(tiles), 256, 0, st>>>(a2q, a2s, I, sorted, offs, ntpp, E, numel,
+                                                          tiles, w2, w2_s, H, topk_weights, y);
+  return check_launch("moe_fp8_w2(gemm)");
+}
+
+// Workspace carve-up of the fused layer, shared by the size query and the
+// launcher.  The two stages run one after the other on one stream, so their
+// scratch shares one region.
+struct MoeFp8Ws {
+  size_t xq, xs, sorted, eids, ntpp, offs, active, nact, a2q, a2s, y, scratch, total;
+};
+
+static MoeFp8Ws moe_fp8_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm) {
   MoeFp8Ws w{};
   const int64_t numel = T * topk;
-  const int bm = gemv ? kGemvBlock : kMoeBM;
   const int64_t cap = numel + static_cast<int64_t>(E) * (bm - 1);
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o += al256(bytes); return at; };
@@ -514,44 +611,109 @@ static MoeFp8Ws moe_fp8_layout(int64_t T, int topk, int E, int64_t H, int64_t I,
   w.offs = take((E + 1) * 4);
   w.active = take(E * 4);
   w.nact = take(4);
-  const int64_t arows = gemv ? numel : cap;  // a2 rows: route order (decode) or padded order
-  w.hpart = gemv ? take(static_cast<size_t>(s13) * numel * 2 * I * 4) : 0;
+  const int64_t arows = bm == kGemvBlock ? numel : cap;  // route order (decode) or padded order
   w.a2q = take(arows * I);
   w.a2s = take(arows * (I / 128) * 4);
-  w.y2part = (gemv && s2 > 1) ? take(static_cast<size_t>(s2) * numel * H * 4) : 0;
   w.y = take(numel * H * 2);
+  w.scratch = take(std::max(w13_scratch(numel, E, H, I, bm), w2_scratch(numel, E, H, I, bm)));
   w.total = o;
   return w;
 }
 
-static int moe_splits(int64_t waves_per_split, int KB) {
-  int s = static_cast<int>((4096 + waves_per_split - 1) / waves_per_split);
-  return max(1, min(s, max(1, KB / 4)));
+// Decode (GEMV, 16-route blocks) up to 64 tokens, grouped GEMM above.
+static int moe_block_m(int64_t T, int path) {
+  if (path == VMAMD_MOE_PATH_GEMV) return kGemvBlock;
+  if (path == VMAMD_MOE_PATH_GEMM) return kMoeBM;
+  return T <= 64 ? kGemvBlock : kMoeBM;
 }
 
-struct MoeFp8Plan {
-  bool gemv;
-  int s13, s2;
-};
-
-static MoeFp8Plan moe_fp8_plan(int64_t T, int topk, int E, int64_t H, int64_t I, int path) {
-  MoeFp8Plan p{};
-  const int64_t numel = T * topk;
-  p.gemv = path == VMAMD_MOE_PATH_GEMV || (path == VMAMD_MOE_PATH_AUTO && T <= 64);
-  const int64_t umax = std::min<int64_t>(E, numel);
-  p.s13 = p.gemv ? moe_splits(umax * (2 * I / 16), static_cast<int>(H / 128)) : 1;
-  p.s2 = p.gemv ? moe_splits(umax * (H / 16), static_cast<int>(I / 128)) : 1;
-  return p;
+static int check_stage_common(const char* who, int64_t T, int topk, int E, int64_t H, int64_t I,
+                              int block_m, int64_t cap) {
+  VMAMD_REQUIRE(T >= 0 && topk > 0 && E > 0 && E <= 1024, "%s: bad sizes (T=%lld topk=%d E=%d)",
+                who, (long long)T, topk, E);
+  VMAMD_REQUIRE(H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0,
+                "%s: hidden (%lld) and intermediate (%lld) sizes must be multiples of 128", who,
+                (long long)H, (long long)I);
+  VMAMD_REQUIRE(block_m == kGemvBlock || block_m == kMoeBM, "%s: block_m must be %d or %d (got %d)",
+                who, kGemvBlock, kMoeBM, block_m);
+  VMAMD_REQUIRE(T * topk < (1ll << 30) && T * H < (1ll << 40), "%s: problem too large", who);
+  VMAMD_REQUIRE(cap >= T * topk + static_cast<int64_t>(E) * (block_m - 1) && cap < (1ll << 31),
+                "%s: capacity %lld < T*topk + E*(block_m-1)", who, (long long)cap);
+  return VMAMD_OK;
 }
 
 }  // namespace vmamd
 
 using namespace vmamd;
 
+extern "C" size_t vmamd_moe_fp8_stage_workspace_size(int64_t T, int topk, int num_experts,
+                                                     int64_t H, int64_t I, int block_m) {
+  const int64_t numel = T * topk;
+  return std::max(w13_scratch(numel, num_experts, H, I, block_m),
+                  w2_scratch(numel, num_experts, H, I, block_m));
+}
+
+extern "C" int vmamd_moe_fp8_w13(const void* xq, const float* xs, int64_t T, int64_t H, int topk,
+                                 const int32_t* sorted_token_ids, int64_t capacity, int block_m,
+                                 const int32_t* expert_offsets, const int32_t* num_tokens_post_pad,
+                                 const int32_t* active_experts, const int32_t* num_active,
+                                 const void* w13, const float* w13_s, int num_experts, int64_t I,
+                                 float swiglu_limit, void* a2q, float* a2s, void* workspace,
+                                 size_t workspace_bytes, vmamd_stream_t stream) {
+  int rc = check_stage_common("moe_fp8_w13", T, topk, num_experts, H, I, block_m, capacity);
+  if (rc) return rc;
+  if (T == 0) return VMAMD_OK;
+  VMAMD_REQUIRE(xq && xs && sorted_token_ids && expert_offsets && num_tokens_post_pad && w13 &&
+                    w13_s && a2q && a2s,
+                "moe_fp8_w13: null pointer");
+  VMAMD_REQUIRE(block_m == kMoeBM || (active_experts && num_active),
+                "moe_fp8_w13: the decode path (block_m 16) needs active_experts / num_active");
+  const size_t need = w13_scratch(T * topk, num_experts, H, I, block_m);
+  VMAMD_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
+                "moe_fp8_w13: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(xq) % 16 == 0 && reinterpret_cast<uintptr_t>(a2q) % 16 == 0,
+                "moe_fp8_w13: xq, a2q and workspace must be 16-byte aligned");
+  return launch_w13(static_cast<const uint8_t*>(xq), xs, static_cast<int>(T), static_cast<int>(H), topk,
+                    sorted_token_ids, capacity, block_m, expert_offsets, num_tokens_post_pad,
+                    active_experts, num_active, static_cast<const uint8_t*>(w13), w13_s, num_experts,
+                    static_cast<int>(I), swiglu_limit, static_cast<uint8_t*>(a2q), a2s,
+                    static_cast<float*>(workspace), reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int vmamd_moe_fp8_w2(const void* a2q, const float* a2s, int64_t T, int topk,
+                                const int32_t* sorted_token_ids, int64_t capacity, int block_m,
+                                const int32_t* expert_offsets, const int32_t* num_tokens_post_pad,
+                                const int32_t* active_experts, const int32_t* num_active,
+                                const void* w2, const float* w2_s, int num_experts, int64_t H,
+                                int64_t I, const float* topk_weights, const int32_t* topk_ids,
+                                const int32_t* expert_map, int64_t expert_map_len, void* y,
+                                void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
+  int rc = check_stage_common("moe_fp8_w2", T, topk, num_experts, H, I, block_m, capacity);
+  if (rc) return rc;
+  if (T == 0) return VMAMD_OK;
+  VMAMD_REQUIRE(a2q && a2s && sorted_token_ids && expert_offsets && num_tokens_post_pad && w2 &&
+                    w2_s && topk_ids && y,
+                "moe_fp8_w2: null pointer");
+  VMAMD_REQUIRE(block_m == kMoeBM || (active_experts && num_active),
+                "moe_fp8_w2: the decode path (block_m 16) needs active_experts / num_active");
+  const size_t need = w2_scratch(T * topk, num_experts, H, I, block_m);
+  VMAMD_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
+                "moe_fp8_w2: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(a2q) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0,
+                "moe_fp8_w2: a2q and workspace must be 16-byte and y 8-byte aligned");
+  return launch_w2(static_cast<const uint8_t*>(a2q), a2s, static_cast<int>(T), topk, sorted_token_ids,
+                   capacity, block_m, expert_offsets, num_tokens_post_pad, active_experts, num_active,
+                   static_cast<const uint8_t*>(w2), w2_s, num_experts, static_cast<int>(H),
+                   static_cast<int>(I), topk_weights, topk_ids, expert_map, expert_map_len,
+                   static_cast<uint16_t*>(y), static_cast<float*>(workspace),
+                   reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" size_t vmamd_fused_moe_fp8_workspace_size(int64_t T, int topk, int num_experts,
                                                      int64_t H, int64_t I, int path) {
-  const MoeFp8Plan p = moe_fp8_plan(T, topk, num_experts, H, I, path);
-  return moe_fp8_layout(T, topk, num_experts, H, I, p.gemv, p.s13, p.s2).total;
+  return moe_fp8_layout(T, topk, num_experts, H, I, moe_block_m(T, path)).total;
 }
 
 extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H,
@@ -561,20 +723,17 @@ extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_
                                    const int32_t* expert_map, int64_t expert_map_len,
                                    float swiglu_limit, int path, void* out, void* workspace,
                                    size_t workspace_bytes, vmamd_stream_t stream) {
-  VMAMD_REQUIRE(T >= 0 && topk > 0 && num_experts > 0 && num_experts <= 1024,
-                "fused_moe_fp8: bad sizes (T=%lld topk=%d E=%d)", (long long)T, topk, num_experts);
-  VMAMD_REQUIRE(H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0,
-                "fused_moe_fp8: hidden (%lld) and intermediate (%lld) sizes must be multiples of 128",
-                (long long)H, (long long)I);
-  VMAMD_REQUIRE(x_dtype == kBF16, "fused_moe_fp8: hidden states must be bf16");
   VMAMD_REQUIRE(path >= VMAMD_MOE_PATH_AUTO && path <= VMAMD_MOE_PATH_GEMM,
                 "fused_moe_fp8: unknown path %d", path);
-  VMAMD_REQUIRE(T * topk < (1ll << 30) && T * H < (1ll << 40), "fused_moe_fp8: problem too large");
+  const int bm = moe_block_m(T, path);
+  const int64_t cap = T * topk + static_cast<int64_t>(num_experts) * (bm - 1);
+  int rc = check_stage_common("fused_moe_fp8", T, topk, num_experts, H, I, bm, cap);
+  if (rc) return rc;
+  VMAMD_REQUIRE(x_dtype == kBF16, "fused_moe_fp8: hidden states must be bf16");
   if (T == 0) return VMAMD_OK;
   VMAMD_REQUIRE(x && w13 && w13_s && w2 && w2_s && topk_weights && topk_ids && out,
                 "fused_moe_fp8: null pointer");
-  const MoeFp8Plan plan = moe_fp8_plan(T, topk, num_experts, H, I, path);
-  const MoeFp8Ws L = moe_fp8_layout(T, topk, num_experts, H, I, plan.gemv, plan.s13, plan.s2);
+  const MoeFp8Ws L = moe_fp8_layout(T, topk, num_experts, H, I, bm);
   VMAMD_REQUIRE(workspace && workspace_bytes >= L.total,
                 "fused_moe_fp8: workspace of %zu bytes required (got %zu)", L.total, workspace_bytes);
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
@@ -591,69 +750,25 @@ extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_
   uint8_t* a2q = ws + L.a2q;
   float* a2s = reinterpret_cast<float*>(ws + L.a2s);
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
+  float* scratch = reinterpret_cast<float*>(ws + L.scratch);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int numel = static_cast<int>(T * topk);
-  const int E = num_experts;
-  const int h = static_cast<int>(H), i = static_cast<int>(I);
+  const int h = static_cast<int>(H), i = static_cast<int>(I), t = static_cast<int>(T);
 
-  int rc = vmamd_per_token_group_quant_fp8(x, kBF16, T, H, H, 128, 1e-10f, -448.f, 448.f, xq, xs,
-                                           H / 128, 1, stream);
+  rc = vmamd_per_token_group_quant_fp8(x, kBF16, T, H, H, 128, 1e-10f, -448.f, 448.f, xq, xs,
+                                       H / 128, 1, stream);
   if (rc) return rc;
-  const int bm = plan.gemv ? kGemvBlock : kMoeBM;
-  const int64_t cap = numel + static_cast<int64_t>(E) * (bm - 1);
-  rc = vmamd_moe_align_block_size(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
-                                  eids, ntpp, offs, nullptr, active, nact, stream);
+  rc = vmamd_moe_align_block_size(topk_ids, numel, num_experts, bm, expert_map, expert_map_len,
+                                  sorted, cap, eids, ntpp, offs, nullptr, active, nact, stream);
   if (rc) return rc;
-
-  if (plan.gemv) {
-    float* hpart = reinterpret_cast<float*>(ws + L.hpart);
-    const int umax = static_cast<int>(std::min<int64_t>(E, numel));
-    dim3 g13((2 * i / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, plan.s13);
-    moe_gemv_fp8_kernel<4><<<g13, kMoeGemvWaves * kWave, 0, st>>>(
-        xq, xs, topk, h, sorted, offs, active, nact, static_cast<const uint8_t*>(w13), w13_s, 2 * i,
-        numel, plan.s13, hpart, nullptr, nullptr);
-    if ((rc = check_launch("fused_moe_fp8(w13 gemv)"))) return rc;
-    const int64_t groups = static_cast<int64_t>(numel) * (i / 128);
-    moe_act_quant_kernel<<<static_cast<int>((groups + 15) / 16), 256, 0, st>>>(
-        hpart, plan.s13, numel, i, swiglu_limit, a2q, a2s);
-    if ((rc = check_launch("fused_moe_fp8(act quant)"))) return rc;
-    dim3 g2((h / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, plan.s2);
-    if (plan.s2 == 1) {
-      moe_gemv_fp8_kernel<4><<<g2, kMoeGemvWaves * kWave, 0, st>>>(
-          a2q, a2s, 1, i, sorted, offs, active, nact, static_cast<const uint8_t*>(w2), w2_s, h,
-          numel, 1, nullptr, topk_weights, y);
-    } else {
-      float* ypart = reinterpret_cast<float*>(ws + L.y2part);
-      moe_gemv_fp8_kernel<4><<<g2, kMoeGemvWaves * kWave, 0, st>>>(
-          a2q, a2s, 1, i, sorted, offs, active, nact, static_cast<const uint8_t*>(w2), w2_s, h,
-          numel, plan.s2, ypart, nullptr, nullptr);
-      const int64_t mn = static_cast<int64_t>(numel) * h;
-      moe_w2_reduce_kernel<<<static_cast<int>((mn / 4 + 255) / 256), 256, 0, st>>>(
-          ypart, plan.s2, numel, h, topk_ids, expert_map, expert_map_len, topk_weights, y);
-    }
-    if ((rc = check_launch("fused_moe_fp8(w2 gemv)"))) return rc;
-  } else {
-    const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
-    const int tiles13 = max_blocks * (i / 128);
-    static bool attr_set = false;
-    if (!attr_set) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_w13_gemm_fp8_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kW13Lds) != hipSuccess) {
-        set_error("fused_moe_fp8: cannot raise the LDS limit of the W13 kernel");
-        return VMAMD_ERR_HIP;
-      }
-      attr_set = true;
-    }
-    moe_w13_gemm_fp8_kernel<<<xcd_grid(tiles13), kW13Threads, kW13Lds, st>>>(
-        xq, xs, topk, h, sorted, offs, ntpp, E, numel, tiles13, static_cast<const uint8_t*>(w13),
-        w13_s, i, swiglu_limit, a2q, a2s);
-    if ((rc = check_launch("fused_moe_fp8(w13 gemm)"))) return rc;
-    const int tiles2 = max_blocks * ((h + 127) / 128);
-    moe_w2_gemm_fp8_kernel<<<xcd_grid(tiles2), 256, 0, st>>>(
-        a2q, a2s, i, sorted, offs, ntpp, E, numel, tiles2, static_cast<const uint8_t*>(w2), w2_s, h,
-        topk_weights, y);
-    if ((rc = check_launch("fused_moe_fp8(w2 gemm)"))) return rc;
-  }
+  rc = launch_w13(xq, xs, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
+                  static_cast<const uint8_t*>(w13), w13_s, num_experts, i, swiglu_limit, a2q, a2s,
+                  scratch, st);
+  if (rc) return rc;
+  rc = launch_w2(a2q, a2s, t, topk, sorted, cap, bm, offs, ntpp, active, nact,
+                 static_cast<const uint8_t*>(w2), w2_s, num_experts, h, i, topk_weights, topk_ids,
+                 expert_map, expert_map_len, y, scratch, st);
+  if (rc) return rc;
   // Slots of dropped routes (negative ids, or non-local experts) hold no
   // expert output and are skipped by the combine.
   return vmamd_moe_sum(y, kBF16, T, topk, H, topk_ids, expert_map, expert_map_len, out, stream);
