@@ -57,36 +57,48 @@ __global__ __launch_bounds__(WM * WN * kWave, 2) void gemm_fp8_bs_kernel(
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  uint4 ra[ACH], rb[BCH];
+  // Scale rows / columns of this lane (clamped like the tile rows).
+  const float* as_row[MT];
 #pragma unroll
-  for (int c = 0; c < ACH; ++c) ra[c] = *reinterpret_cast<const uint4*>(A + goff_a[c]);
+  for (int mt = 0; mt < MT; ++mt)
+    as_row[mt] = As + static_cast<int64_t>(min(sa_row0 + mt * 16, M - 1)) * as_sm;
+  const float* bs_row[NT];
 #pragma unroll
-  for (int c = 0; c < BCH; ++c) rb[c] = *reinterpret_cast<const uint4*>(B + goff_b[c]);
+  for (int nt = 0; nt < NT; ++nt)
+    bs_row[nt] = Bs + static_cast<int64_t>(min(sb_col0 + nt * 16, N - 1) / 128) * KB;
+
+  v4i ra[ACH], rb[BCH];
 #pragma unroll
-  for (int c = 0; c < ACH; ++c) *reinterpret_cast<uint4*>(&smem[0][l0 + c * RSTEP * 128]) = ra[c];
+  for (int c = 0; c < ACH; ++c) ra[c] = ld16(A + goff_a[c]);
 #pragma unroll
-  for (int c = 0; c < BCH; ++c)
-    *reinterpret_cast<uint4*>(&smem[0][BM * 128 + l0 + c * RSTEP * 128]) = rb[c];
+  for (int c = 0; c < BCH; ++c) rb[c] = ld16(B + goff_b[c]);
+#pragma unroll
+  for (int c = 0; c < ACH; ++c) st16(&smem[0][l0 + c * RSTEP * 128], ra[c]);
+#pragma unroll
+  for (int c = 0; c < BCH; ++c) st16(&smem[0][BM * 128 + l0 + c * RSTEP * 128], rb[c]);
+  float sa[MT], sb[NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) sa[mt] = as_row[mt][0];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) sb[nt] = bs_row[nt][0];
   __syncthreads();
 
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
   for (int kb = 0; kb < KB; ++kb) {
     const int cur = kb & 1;
-    const bool more = kb + 1 < KB;
-    if (more) {
-      const int off = (kb + 1) * 128;
+    // Prefetch K-block kb+1 (the last iteration re-reads block KB-1; the
+    // copy lands in the idle buffer and is never used).
+    const int kn = min(kb + 1, KB - 1);
+    const int off = kn * 128;
 #pragma unroll
-      for (int c = 0; c < ACH; ++c) ra[c] = *reinterpret_cast<const uint4*>(A + goff_a[c] + off);
+    for (int c = 0; c < ACH; ++c) ra[c] = ld16(A + goff_a[c] + off);
 #pragma unroll
-      for (int c = 0; c < BCH; ++c) rb[c] = *reinterpret_cast<const uint4*>(B + goff_b[c] + off);
-    }
-    float sa[MT], sb[NT];
+    for (int c = 0; c < BCH; ++c) rb[c] = ld16(B + goff_b[c] + off);
+    float san[MT], sbn[NT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      sa[mt] = As[static_cast<int64_t>(min(sa_row0 + mt * 16, M - 1)) * as_sm + kb * as_sk];
+    for (int mt = 0; mt < MT; ++mt) san[mt] = as_row[mt][kn * as_sk];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      sb[nt] = Bs[static_cast<int64_t>(min(sb_col0 + nt * 16, N - 1) / 128) * KB + kb];
+    for (int nt = 0; nt < NT; ++nt) sbn[nt] = bs_row[nt][kn];
 
     const uint8_t* tile = smem[cur];
     v8i xf[MT], wf[NT];
@@ -101,14 +113,14 @@ __global__ __launch_bounds__(WM * WN * kWave, 2) void gemm_fp8_bs_kernel(
         const v4f p = mfma_fp8(wf[nt], xf[mt], zero);
         fma4(acc[mt][nt], p, sa[mt] * sb[nt]);
       }
-    if (more) {
 #pragma unroll
-      for (int c = 0; c < ACH; ++c)
-        *reinterpret_cast<uint4*>(&smem[cur ^ 1][l0 + c * RSTEP * 128]) = ra[c];
+    for (int c = 0; c < ACH; ++c) st16(&smem[cur ^ 1][l0 + c * RSTEP * 128], ra[c]);
 #pragma unroll
-      for (int c = 0; c < BCH; ++c)
-        *reinterpret_cast<uint4*>(&smem[cur ^ 1][BM * 128 + l0 + c * RSTEP * 128]) = rb[c];
-    }
+    for (int c = 0; c < BCH; ++c) st16(&smem[cur ^ 1][BM * 128 + l0 + c * RSTEP * 128], rb[c]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) sa[mt] = san[mt];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) sb[nt] = sbn[nt];
     __syncthreads();
   }
 

@@ -50,6 +50,12 @@ __device__ __forceinline__ v8i global_frag(const uint8_t* p, int g) {
   return f;
 }
 
+// 16-byte global / LDS moves in a native vector type (keeps prefetch arrays in
+// registers: the compiler can scalarise them, which it does not do reliably
+// for the HIP uint4 struct).
+__device__ __forceinline__ v4i ld16(const uint8_t* p) { return *reinterpret_cast<const v4i*>(p); }
+__device__ __forceinline__ void st16(uint8_t* p, const v4i& v) { *reinterpret_cast<v4i*>(p) = v; }
+
 // acc += p * s, element-wise (the per-K-block scale promotion).
 __device__ __forceinline__ void fma4(v4f& acc, const v4f& p, float s) {
   acc[0] = fmaf(p[0], s, acc[0]);

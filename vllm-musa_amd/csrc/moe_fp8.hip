@@ -268,11 +268,14 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_fp8_kernel(
 
   const int crow = tid / 8, cch = tid % 8;
   const int l0 = lds_off(crow, cch);
+  // Padding rows of the block load row 0 and are zeroed in registers.
   int64_t goff_a[ACH];
+  bool aval[ACH];
 #pragma unroll
   for (int c = 0; c < ACH; ++c) {
     const int r = sorted[mb * BM + crow + c * RSTEP];
-    goff_a[c] = r < numel ? static_cast<int64_t>(r / topk) * H + cch * 16 : -1;
+    aval[c] = r < numel;
+    goff_a[c] = (aval[c] ? static_cast<int64_t>(r / topk) * H : 0) + cch * 16;
   }
   int64_t goff_b[BCH];
 #pragma unroll
@@ -281,11 +284,13 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_fp8_kernel(
     const int row = q < 16 ? n0 + 16 * p + q : I + n0 + 16 * p + (q - 16);
     goff_b[c] = (static_cast<int64_t>(e) * 2 * I + row) * H + cch * 16;
   }
-  int tok[MT];
+  const float* xs_row[MT];
+  bool tval[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int r = sorted[mb * BM + wm * WTM + mt * 16 + li];
-    tok[mt] = r < numel ? r / topk : -1;
+    tval[mt] = r < numel;
+    xs_row[mt] = xs + (tval[mt] ? static_cast<int64_t>(r / topk) * KB : 0);
   }
   const float* sg = w13s + (static_cast<int64_t>(e) * NB2 + n0 / 128) * KB;
   const float* su = w13s + (static_cast<int64_t>(e) * NB2 + (I + n0) / 128) * KB;
@@ -296,35 +301,47 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_fp8_kernel(
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  const uint4 z4 = {0u, 0u, 0u, 0u};
-  uint4 ra[ACH], rb[BCH];
+  const v4i z4 = {0, 0, 0, 0};
+  v4i ra[ACH], rb[BCH];
 #pragma unroll
-  for (int c = 0; c < ACH; ++c) ra[c] = goff_a[c] >= 0 ? *reinterpret_cast<const uint4*>(xq + goff_a[c]) : z4;
+  for (int c = 0; c < ACH; ++c) {
+    const v4i v = ld16(xq + goff_a[c]);
+    ra[c] = aval[c] ? v : z4;
+  }
 #pragma unroll
-  for (int c = 0; c < BCH; ++c) rb[c] = *reinterpret_cast<const uint4*>(w13 + goff_b[c]);
+  for (int c = 0; c < BCH; ++c) rb[c] = ld16(w13 + goff_b[c]);
 #pragma unroll
-  for (int c = 0; c < ACH; ++c) *reinterpret_cast<uint4*>(&smem_dyn[l0 + c * RSTEP * 128]) = ra[c];
+  for (int c = 0; c < ACH; ++c) st16(&smem_dyn[l0 + c * RSTEP * 128], ra[c]);
 #pragma unroll
-  for (int c = 0; c < BCH; ++c)
-    *reinterpret_cast<uint4*>(&smem_dyn[BM * 128 + l0 + c * RSTEP * 128]) = rb[c];
+  for (int c = 0; c < BCH; ++c) st16(&smem_dyn[BM * 128 + l0 + c * RSTEP * 128], rb[c]);
+  float sa[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) sa[mt] = tval[mt] ? xs_row[mt][0] : 0.f;
+  float sbg = sg[0], sbu = su[0];
   __syncthreads();
 
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
   for (int kb = 0; kb < KB; ++kb) {
     const int cur = kb & 1;
-    const bool more = kb + 1 < KB;
-    if (more) {
-      const int off = (kb + 1) * 128;
+    // Prefetch K-block kb+1 (the last iteration re-reads block KB-1 into the
+    // idle buffer; that copy is never used).
+    const int kn = min(kb + 1, KB - 1);
+    const int off = kn * 128;
 #pragma unroll
-      for (int c = 0; c < ACH; ++c)
-        ra[c] = goff_a[c] >= 0 ? *reinterpret_cast<const uint4*>(xq + goff_a[c] + off) : z4;
-#pragma unroll
-      for (int c = 0; c < BCH; ++c) rb[c] = *reinterpret_cast<const uint4*>(w13 + goff_b[c] + off);
+    for (int c = 0; c < ACH; ++c) {
+      const v4i v = ld16(xq + goff_a[c] + off);
+      ra[c] = aval[c] ? v : z4;
     }
-    float sa[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) sa[mt] = tok[mt] >= 0 ? xs[static_cast<int64_t>(tok[mt]) * KB + kb] : 0.f;
-    const float sbg = sg[kb], sbu = su[kb];
+    for (int c = 0; c < BCH; ++c) rb[c] = ld16(w13 + goff_b[c] + off);
+    float san[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float v = xs_row[mt][kn];
+      san[mt] = tval[mt] ? v : 0.f;
+    }
+    const float sbgn = sg[kn], sbun = su[kn];
+
     const uint8_t* tile = smem_dyn + cur * STAGE;
     v8i xf[MT];
 #pragma unroll
@@ -336,14 +353,15 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_fp8_kernel(
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) fma4(acc[mt][nt], mfma_fp8(wf, xf[mt], zero), sa[mt] * sb);
     }
-    if (more) {
-      uint8_t* nxt = smem_dyn + (cur ^ 1) * STAGE;
+    uint8_t* nxt = smem_dyn + (cur ^ 1) * STAGE;
 #pragma unroll
-      for (int c = 0; c < ACH; ++c) *reinterpret_cast<uint4*>(&nxt[l0 + c * RSTEP * 128]) = ra[c];
+    for (int c = 0; c < ACH; ++c) st16(&nxt[l0 + c * RSTEP * 128], ra[c]);
 #pragma unroll
-      for (int c = 0; c < BCH; ++c)
-        *reinterpret_cast<uint4*>(&nxt[BM * 128 + l0 + c * RSTEP * 128]) = rb[c];
-    }
+    for (int c = 0; c < BCH; ++c) st16(&nxt[BM * 128 + l0 + c * RSTEP * 128], rb[c]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) sa[mt] = san[mt];
+    sbg = sbgn;
+    sbu = sbun;
     __syncthreads();
   }
 
@@ -426,33 +444,34 @@ __global__ __launch_bounds__(256, 2) void moe_w2_gemm_fp8_kernel(
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  uint4 ra[ACH], rb[BCH];
+  v4i ra[ACH], rb[BCH];
 #pragma unroll
-  for (int c = 0; c < ACH; ++c) ra[c] = *reinterpret_cast<const uint4*>(a2q + goff_a[c]);
+  for (int c = 0; c < ACH; ++c) ra[c] = ld16(a2q + goff_a[c]);
 #pragma unroll
-  for (int c = 0; c < BCH; ++c) rb[c] = *reinterpret_cast<const uint4*>(w2 + goff_b[c]);
+  for (int c = 0; c < BCH; ++c) rb[c] = ld16(w2 + goff_b[c]);
 #pragma unroll
-  for (int c = 0; c < ACH; ++c) *reinterpret_cast<uint4*>(&smem[0][l0 + c * RSTEP * 128]) = ra[c];
+  for (int c = 0; c < ACH; ++c) st16(&smem[0][l0 + c * RSTEP * 128], ra[c]);
 #pragma unroll
-  for (int c = 0; c < BCH; ++c)
-    *reinterpret_cast<uint4*>(&smem[0][BM * 128 + l0 + c * RSTEP * 128]) = rb[c];
+  for (int c = 0; c < BCH; ++c) st16(&smem[0][BM * 128 + l0 + c * RSTEP * 128], rb[c]);
+  float sa[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) sa[mt] = a2s[(arow0 + mt * 16) * KB];
+  float sb = sb_p[0];
   __syncthreads();
 
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
   for (int kb = 0; kb < KB; ++kb) {
     const int cur = kb & 1;
-    const bool more = kb + 1 < KB;
-    if (more) {
-      const int off = (kb + 1) * 128;
+    const int kn = min(kb + 1, KB - 1);
+    const int off = kn * 128;
 #pragma unroll
-      for (int c = 0; c < ACH; ++c) ra[c] = *reinterpret_cast<const uint4*>(a2q + goff_a[c] + off);
+    for (int c = 0; c < ACH; ++c) ra[c] = ld16(a2q + goff_a[c] + off);
 #pragma unroll
-      for (int c = 0; c < BCH; ++c) rb[c] = *reinterpret_cast<const uint4*>(w2 + goff_b[c] + off);
-    }
-    float sa[MT];
+    for (int c = 0; c < BCH; ++c) rb[c] = ld16(w2 + goff_b[c] + off);
+    float san[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) sa[mt] = a2s[(arow0 + mt * 16) * KB + kb];
-    const float sb = sb_p[kb];
+    for (int mt = 0; mt < MT; ++mt) san[mt] = a2s[(arow0 + mt * 16) * KB + kn];
+    const float sbn = sb_p[kn];
     const uint8_t* tile = smem[cur];
     v8i xf[MT];
 #pragma unroll
@@ -463,14 +482,13 @@ __global__ __launch_bounds__(256, 2) void moe_w2_gemm_fp8_kernel(
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) fma4(acc[mt][nt], mfma_fp8(wf, xf[mt], zero), sa[mt] * sb);
     }
-    if (more) {
 #pragma unroll
-      for (int c = 0; c < ACH; ++c)
-        *reinterpret_cast<uint4*>(&smem[cur ^ 1][l0 + c * RSTEP * 128]) = ra[c];
+    for (int c = 0; c < ACH; ++c) st16(&smem[cur ^ 1][l0 + c * RSTEP * 128], ra[c]);
 #pragma unroll
-      for (int c = 0; c < BCH; ++c)
-        *reinterpret_cast<uint4*>(&smem[cur ^ 1][BM * 128 + l0 + c * RSTEP * 128]) = rb[c];
-    }
+    for (int c = 0; c < BCH; ++c) st16(&smem[cur ^ 1][BM * 128 + l0 + c * RSTEP * 128], rb[c]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) sa[mt] = san[mt];
+    sb = sbn;
     __syncthreads();
   }
 
@@ -620,11 +638,13 @@ static MoeFp8Ws moe_fp8_layout(int64_t T, int topk, int E, int64_t H, int64_t I,
   return w;
 }
 
-// Decode (GEMV, 16-route blocks) up to 64 tokens, grouped GEMM above.
-static int moe_block_m(int64_t T, int path) {
+// Decode kernels (GEMV over 16-route blocks) while an expert receives about
+// one block of routes on average (or up to 64 tokens), the grouped GEMM over
+// 128-route blocks above: below that the 128-row tiles are mostly padding.
+static int moe_block_m(int64_t T, int topk, int E, int path) {
   if (path == VMAMD_MOE_PATH_GEMV) return kGemvBlock;
   if (path == VMAMD_MOE_PATH_GEMM) return kMoeBM;
-  return T <= 64 ? kGemvBlock : kMoeBM;
+  return (T <= 64 || T * topk <= static_cast<int64_t>(kGemvBlock) * E) ? kGemvBlock : kMoeBM;
 }
 
 static int check_stage_common(const char* who, int64_t T, int topk, int E, int64_t H, int64_t I,
@@ -713,7 +733,7 @@ extern "C" int vmamd_moe_fp8_w2(const void* a2q, const float* a2s, int64_t T, in
 
 extern "C" size_t vmamd_fused_moe_fp8_workspace_size(int64_t T, int topk, int num_experts,
                                                      int64_t H, int64_t I, int path) {
-  return moe_fp8_layout(T, topk, num_experts, H, I, moe_block_m(T, path)).total;
+  return moe_fp8_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path)).total;
 }
 
 extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H,
@@ -725,7 +745,7 @@ extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_
                                    size_t workspace_bytes, vmamd_stream_t stream) {
   VMAMD_REQUIRE(path >= VMAMD_MOE_PATH_AUTO && path <= VMAMD_MOE_PATH_GEMM,
                 "fused_moe_fp8: unknown path %d", path);
-  const int bm = moe_block_m(T, path);
+  const int bm = moe_block_m(T, topk, num_experts, path);
   const int64_t cap = T * topk + static_cast<int64_t>(num_experts) * (bm - 1);
   int rc = check_stage_common("fused_moe_fp8", T, topk, num_experts, H, I, bm, cap);
   if (rc) return rc;

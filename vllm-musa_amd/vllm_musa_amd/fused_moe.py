@@ -161,7 +161,8 @@ class Fp8MoeStages:
         self.i = n2 // 2
         self.topk = topk_ids.shape[1]
         self.t = t
-        gemv = path == "gemv" or (path == "auto" and t <= 64)
+        numel = t * topk_ids.shape[1]
+        gemv = path == "gemv" or (path == "auto" and (t <= 64 or numel <= 16 * w13.shape[0]))
         self.block_m = 16 if gemv else 128
         self.w13, self.w2 = w13.contiguous(), w2.contiguous()
         self.s13 = _expand_fp8_scale(w13_scale, w13)
