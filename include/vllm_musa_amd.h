@@ -248,6 +248,39 @@ int vmamd_moe_fp8_w2(const void* a2q, const float* a2s, int64_t T, int topk,
                      const int32_t* expert_map, int64_t expert_map_len, void* y,
                      void* workspace, size_t workspace_bytes, vmamd_stream_t stream);
 
+/* ------------------------------------------------------------ bf16 MoE --
+ * The same layer and stages with bf16 expert weights (the reference's
+ * unquantised path: MusaUnquantizedFusedMoEMethod.forward_oot ->
+ * fused_experts, vllm_musa/model_executor/layers/fused_moe/unquantized_fused_moe_method.py:81-130,
+ * upstream Triton fused_moe_kernel in bf16):
+ *   out[t] = bf16( sum_k bf16( W2[e] . a * w[t,k] ) ),
+ *   a = bf16(silu(h_g) * h_u),  h = bf16(W13[e] . x[t])   (fp32 accumulation)
+ * x [T, H] bf16; w13 [E, 2I, H] bf16; w2 [E, H, I] bf16; a2 bf16 rows as for
+ * fp8 ([T*topk, I] for block_m 16, [capacity, I] for 128).  Routing,
+ * expert_map, swiglu_limit, path and workspace rules as for fp8. */
+size_t vmamd_fused_moe_bf16_workspace_size(int64_t T, int topk, int num_experts, int64_t H,
+                                           int64_t I, int path);
+int vmamd_fused_moe_bf16(const void* x, int64_t T, int64_t H, const void* w13, const void* w2,
+                         int num_experts, int64_t I, const float* topk_weights,
+                         const int32_t* topk_ids, int topk, const int32_t* expert_map,
+                         int64_t expert_map_len, float swiglu_limit, int path, void* out,
+                         void* workspace, size_t workspace_bytes, vmamd_stream_t stream);
+size_t vmamd_moe_bf16_stage_workspace_size(int64_t T, int topk, int num_experts, int64_t H,
+                                           int64_t I, int block_m);
+int vmamd_moe_bf16_w13(const void* x, int64_t T, int64_t H, int topk,
+                       const int32_t* sorted_token_ids, int64_t capacity, int block_m,
+                       const int32_t* expert_offsets, const int32_t* num_tokens_post_pad,
+                       const int32_t* active_experts, const int32_t* num_active, const void* w13,
+                       int num_experts, int64_t I, float swiglu_limit, void* a2, void* workspace,
+                       size_t workspace_bytes, vmamd_stream_t stream);
+int vmamd_moe_bf16_w2(const void* a2, int64_t T, int topk, const int32_t* sorted_token_ids,
+                      int64_t capacity, int block_m, const int32_t* expert_offsets,
+                      const int32_t* num_tokens_post_pad, const int32_t* active_experts,
+                      const int32_t* num_active, const void* w2, int num_experts, int64_t H,
+                      int64_t I, const float* topk_weights, const int32_t* topk_ids,
+                      const int32_t* expert_map, int64_t expert_map_len, void* y, void* workspace,
+                      size_t workspace_bytes, vmamd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

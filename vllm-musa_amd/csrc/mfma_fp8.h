@@ -1,4 +1,4 @@
-// Building blocks of the fp8 block-scaled GEMMs on CDNA4 MFMA.
+// Building blocks of the fp8 block-scaled and bf16 GEMMs on CDNA4 MFMA.
 //
 // MFMA shape: v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3 -> f32), one K-block of
 // the 128x128 scale grid per instruction.  The weight tile is the "A" operand
@@ -28,6 +28,20 @@ __device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c
 
 __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * 128 + ((chunk ^ (row & 7)) << 4);
+}
+
+// Two chained v_mfma_f32_16x16x32_bf16 over one 128-byte row chunk (64 bf16
+// of K): the low halves of the fragments (chunk g) are K-slice 0, the high
+// halves (chunk g + 4) K-slice 1.  Both operands use the same K order, so the
+// sum is the chunk's dot product.
+__device__ __forceinline__ v4f mfma_bf16x2(const v8i& a, const v8i& b, v4f c) {
+  const v4i alo = {a[0], a[1], a[2], a[3]}, ahi = {a[4], a[5], a[6], a[7]};
+  const v4i blo = {b[0], b[1], b[2], b[3]}, bhi = {b[4], b[5], b[6], b[7]};
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, alo),
+                                               __builtin_bit_cast(v8bf, blo), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ahi),
+                                               __builtin_bit_cast(v8bf, bhi), c, 0, 0, 0);
+  return c;
 }
 
 // Operand fragment of `row` from an LDS tile.

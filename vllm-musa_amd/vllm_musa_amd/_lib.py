@@ -54,8 +54,18 @@ SIGNATURES: dict[str, list] = {
                           _i64, _f32, _p, _p, _p, _sz, _p],
     "vmamd_moe_fp8_w2": [_p, _p, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _p, _p, _i32, _i64,
                          _i64, _p, _p, _p, _i64, _p, _p, _sz, _p],
+    "vmamd_fused_moe_bf16_workspace_size": [_i64, _i32, _i32, _i64, _i64, _i32],
+    "vmamd_fused_moe_bf16": [_p, _i64, _i64, _p, _p, _i32, _i64, _p, _p, _i32, _p, _i64, _f32,
+                             _i32, _p, _p, _sz, _p],
+    "vmamd_moe_bf16_stage_workspace_size": [_i64, _i32, _i32, _i64, _i64, _i32],
+    "vmamd_moe_bf16_w13": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _p, _i32, _i64,
+                           _f32, _p, _p, _sz, _p],
+    "vmamd_moe_bf16_w2": [_p, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _p, _i32, _i64, _i64,
+                          _p, _p, _p, _i64, _p, _p, _sz, _p],
 }
 _RESTYPES = {"vmamd_last_error": ctypes.c_char_p,
+             "vmamd_fused_moe_bf16_workspace_size": ctypes.c_size_t,
+             "vmamd_moe_bf16_stage_workspace_size": ctypes.c_size_t,
              "vmamd_w8a8_block_fp8_matmul_workspace_size": ctypes.c_size_t,
              "vmamd_fused_moe_fp8_workspace_size": ctypes.c_size_t,
              "vmamd_moe_fp8_stage_workspace_size": ctypes.c_size_t}

@@ -85,7 +85,7 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
     rounding points.  Supported: bf16 weights, and fp8 weights with 128x128
     block scales (use_fp8_w8a8, block_shape=[128, 128]) and dynamic 1x128
     activation quantisation.  ``path`` forces the decode ("gemv") or prefill
-    ("gemm") kernels; "auto" picks by token count."""
+    ("gemm") kernels; "auto" picks by routes per expert."""
     if activation != "silu":
         raise NotImplementedError(f"activation {activation!r}: only silu (SwiGLU) is on this path")
     if use_int8_w8a8 or use_int8_w8a16 or use_int4_w4a16 or ocp_mx_scheme or per_channel_quant:
@@ -138,45 +138,67 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
              stream_of(hidden_states))
         return out
     if w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16:
+        if w1_scale is not None or w2_scale is not None:
+            raise ValueError("bf16 MoE weights take no scales")
         return _fused_experts_bf16(hidden_states, w1, w2, wts, ids, emap, limit, code, out)
     raise NotImplementedError(f"MoE weights of dtype {w1.dtype} are not on this path")
 
 
-class Fp8MoeStages:
-    """The fp8 block MoE layer as its separate launches, in the order the
-    fused call enqueues them: ``quant`` (1x128 of x), ``align``
-    (moe_align_block_size), ``w13`` (grouped W13 GEMM + SiLU-and-mul + a2
-    quantisation), ``w2`` (grouped W2 GEMM with the routed weight) and
-    ``combine`` (top-k sum).  This is the upstream fused_experts_impl
-    decomposition (quantize input -> invoke_fused_moe_kernel(W13) -> activation
-    + a2 quant -> invoke_fused_moe_kernel(W2) -> moe_sum; patches/series/0144-…:22-78);
-    each method launches exactly its kernels on the current stream, so one
-    stage can be timed or profiled on its own.  Buffers are allocated once here."""
+def _fused_experts_bf16(x, w1, w2, wts, ids, emap, limit, code, out):
+    e, n2, h = w1.shape
+    i = n2 // 2
+    t, topk = ids.shape
+    w1c, w2c = w1.contiguous(), w2.contiguous()
+    _lib.check_cuda(x, w1c, w2c, wts, ids, emap)
+    nbytes = _lib.load().vmamd_fused_moe_bf16_workspace_size(t, topk, e, h, i, code)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    call("vmamd_fused_moe_bf16", ptr(x), t, h, ptr(w1c), ptr(w2c), e, i, ptr(wts), ptr(ids), topk,
+         ptr(emap), 0 if emap is None else emap.numel(), limit, code, ptr(out), ptr(ws), nbytes,
+         stream_of(x))
+    return out
+
+
+class MoeStages:
+    """One MoE layer as its separate launches, in the order the fused call
+    enqueues them: ``quant`` (1x128 of x; fp8 only), ``align``
+    (moe_align_block_size), ``w13_stage`` (grouped W13 GEMM + SiLU-and-mul,
+    + a2 quantisation for fp8), ``w2_stage`` (grouped W2 GEMM with the routed
+    weight) and ``combine`` (top-k sum).  This is the upstream
+    fused_experts_impl decomposition (quantize input ->
+    invoke_fused_moe_kernel(W13) -> activation + a2 quant ->
+    invoke_fused_moe_kernel(W2) -> moe_sum; patches/series/0144-…:22-78).
+    Each method launches exactly its kernels on the current stream, so one
+    stage can be timed or profiled on its own.  Buffers are allocated here.
+
+    fp8 weights (float8_e4m3fn) need w13_scale / w2_scale (128x128 blocks);
+    bf16 weights take none."""
 
     def __init__(self, hidden_states, w13, w13_scale, w2, w2_scale, topk_weights, topk_ids,
                  path: str = "auto", expert_map=None, swiglu_limit: float | None = None):
+        self.fp8 = w13.dtype == torch.float8_e4m3fn
         self.x = hidden_states
         t, self.h = hidden_states.shape
         self.e, n2, _ = w13.shape
         self.i = n2 // 2
         self.topk = topk_ids.shape[1]
         self.t = t
-        numel = t * topk_ids.shape[1]
-        gemv = path == "gemv" or (path == "auto" and (t <= 64 or numel <= 16 * w13.shape[0]))
+        numel = t * self.topk
+        gemv = path == "gemv" or (path == "auto" and (t <= 64 or numel <= 16 * self.e))
         self.block_m = 16 if gemv else 128
         self.w13, self.w2 = w13.contiguous(), w2.contiguous()
-        self.s13 = _expand_fp8_scale(w13_scale, w13)
-        self.s2 = _expand_fp8_scale(w2_scale, w2)
+        if self.fp8:
+            self.s13 = _expand_fp8_scale(w13_scale, w13)
+            self.s2 = _expand_fp8_scale(w2_scale, w2)
         self.ids = topk_ids.to(torch.int32).contiguous()
         self.wts = topk_weights.to(torch.float32).contiguous()
         self.emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
         self.limit = 0.0 if swiglu_limit is None else float(swiglu_limit)
         dev = hidden_states.device
-        numel = t * self.topk
         self.cap = numel + self.e * (self.block_m - 1)
         i32 = dict(dtype=torch.int32, device=dev)
-        self.xq = torch.empty(t, self.h, dtype=torch.float8_e4m3fn, device=dev)
-        self.xs = torch.empty(t, self.h // 128, dtype=torch.float32, device=dev)
+        if self.fp8:
+            self.xq = torch.empty(t, self.h, dtype=torch.float8_e4m3fn, device=dev)
+            self.xs = torch.empty(t, self.h // 128, dtype=torch.float32, device=dev)
         self.sorted = torch.empty(self.cap, **i32)
         self.eids = torch.empty(-(-self.cap // self.block_m), **i32)
         self.ntpp = torch.empty(1, **i32)
@@ -184,36 +206,51 @@ class Fp8MoeStages:
         self.active = torch.empty(self.e, **i32)
         self.nact = torch.empty(1, **i32)
         rows = numel if gemv else self.cap
-        self.a2q = torch.empty(rows, self.i, dtype=torch.float8_e4m3fn, device=dev)
-        self.a2s = torch.empty(rows, self.i // 128, dtype=torch.float32, device=dev)
+        adt = torch.float8_e4m3fn if self.fp8 else torch.bfloat16
+        self.a2 = torch.empty(rows, self.i, dtype=adt, device=dev)
+        if self.fp8:
+            self.a2s = torch.empty(rows, self.i // 128, dtype=torch.float32, device=dev)
         self.y = torch.empty(t, self.topk, self.h, dtype=torch.bfloat16, device=dev)
         self.out = torch.empty(t, self.h, dtype=torch.bfloat16, device=dev)
-        nbytes = _lib.load().vmamd_moe_fp8_stage_workspace_size(t, self.topk, self.e, self.h,
-                                                                self.i, self.block_m)
+        q = "vmamd_moe_fp8_stage_workspace_size" if self.fp8 else \
+            "vmamd_moe_bf16_stage_workspace_size"
+        nbytes = getattr(_lib.load(), q)(t, self.topk, self.e, self.h, self.i, self.block_m)
         self.ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
         self.ws_bytes = nbytes
 
     def quant(self):
-        ops.per_token_group_quant_8bit_vec(self.x, self.xq, self.xs, 128, 1e-10, ops.FP8_MIN,
-                                           ops.FP8_MAX)
+        if self.fp8:
+            ops.per_token_group_quant_8bit_vec(self.x, self.xq, self.xs, 128, 1e-10, ops.FP8_MIN,
+                                               ops.FP8_MAX)
 
     def align(self):
         ops.moe_align_block_size(self.ids, self.e, self.block_m, self.sorted, self.eids,
                                  self.ntpp, self.emap, None, self.offsets, self.active, self.nact)
 
+    def _route_args(self):
+        return (ptr(self.sorted), self.cap, self.block_m, ptr(self.offsets), ptr(self.ntpp),
+                ptr(self.active), ptr(self.nact))
+
     def w13_stage(self):
-        call("vmamd_moe_fp8_w13", ptr(self.xq), ptr(self.xs), self.t, self.h, self.topk,
-             ptr(self.sorted), self.cap, self.block_m, ptr(self.offsets), ptr(self.ntpp),
-             ptr(self.active), ptr(self.nact), ptr(self.w13), ptr(self.s13), self.e, self.i,
-             self.limit, ptr(self.a2q), ptr(self.a2s), ptr(self.ws), self.ws_bytes,
-             stream_of(self.x))
+        if self.fp8:
+            call("vmamd_moe_fp8_w13", ptr(self.xq), ptr(self.xs), self.t, self.h, self.topk,
+                 *self._route_args(), ptr(self.w13), ptr(self.s13), self.e, self.i, self.limit,
+                 ptr(self.a2), ptr(self.a2s), ptr(self.ws), self.ws_bytes, stream_of(self.x))
+        else:
+            call("vmamd_moe_bf16_w13", ptr(self.x), self.t, self.h, self.topk,
+                 *self._route_args(), ptr(self.w13), self.e, self.i, self.limit, ptr(self.a2),
+                 ptr(self.ws), self.ws_bytes, stream_of(self.x))
 
     def w2_stage(self):
-        call("vmamd_moe_fp8_w2", ptr(self.a2q), ptr(self.a2s), self.t, self.topk,
-             ptr(self.sorted), self.cap, self.block_m, ptr(self.offsets), ptr(self.ntpp),
-             ptr(self.active), ptr(self.nact), ptr(self.w2), ptr(self.s2), self.e, self.h, self.i,
-             ptr(self.wts), ptr(self.ids), ptr(self.emap), 0 if self.emap is None else
-             self.emap.numel(), ptr(self.y), ptr(self.ws), self.ws_bytes, stream_of(self.x))
+        tail = (ptr(self.wts), ptr(self.ids), ptr(self.emap),
+                0 if self.emap is None else self.emap.numel(), ptr(self.y), ptr(self.ws),
+                self.ws_bytes, stream_of(self.x))
+        if self.fp8:
+            call("vmamd_moe_fp8_w2", ptr(self.a2), ptr(self.a2s), self.t, self.topk,
+                 *self._route_args(), ptr(self.w2), ptr(self.s2), self.e, self.h, self.i, *tail)
+        else:
+            call("vmamd_moe_bf16_w2", ptr(self.a2), self.t, self.topk, *self._route_args(),
+                 ptr(self.w2), self.e, self.h, self.i, *tail)
 
     def combine(self):
         ops.moe_sum(self.y, self.out, self.ids, self.emap)
@@ -227,8 +264,7 @@ class Fp8MoeStages:
         return self.out
 
 
-def _fused_experts_bf16(x, w1, w2, wts, ids, emap, limit, code, out):
-    raise NotImplementedError("bf16 MoE kernels are not built yet")
+Fp8MoeStages = MoeStages
 
 
 def fused_experts(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
