@@ -78,6 +78,17 @@ int vmamd_silu_and_mul_quant_fp8(const void* x, int dtype, int64_t rows, int64_t
                                  int group_size, float eps, float fp8_min, float fp8_max,
                                  float swiglu_limit, void* q, float* s, vmamd_stream_t stream);
 
+/* Per-row (per-token) fp8 quantisation: s[r] = max(eps, max_c |x[r,c]|) /
+ * fp8_max over the whole row, q[r,c] = e4m3fn(clamp(x[r,c] / s[r], fp8_min,
+ * fp8_max)).  x: [rows, cols] bf16 (row stride x_row_stride elements, 16-byte
+ * aligned rows), q: [rows, cols] fp8 contiguous, s: [rows] f32.  cols must be
+ * a multiple of 8 and at most 16384.  Replaces the dynamic per-row activation
+ * quantisation of the w4afp8 MoE (vllm_musa/kernels/w4afp8_moe.py:47-78
+ * _scatter_quantized_rows and 81-124 _swiglu_quantized_rows, eps 1e-4). */
+int vmamd_per_token_quant_fp8(const void* x, int64_t rows, int64_t cols, int64_t x_row_stride,
+                              float eps, float fp8_min, float fp8_max, void* q, float* s,
+                              vmamd_stream_t stream);
+
 /* ---------------------------------------------------------------- routing --
  * Softmax top-k.  l' = gating (+ bias[e] if bias != NULL), optionally
  * soft-capped (softcap > 0: l' = tanh(l'/softcap)*softcap).  ids = the top-k
@@ -155,6 +166,16 @@ int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int num_e
 int vmamd_moe_sum(const void* x, int dtype, int64_t tokens, int topk, int64_t hidden,
                   const int32_t* topk_ids, const int32_t* expert_map, int64_t expert_map_len,
                   void* out, vmamd_stream_t stream);
+
+/* Weighted top-k combine: out[t, h] = round(sum_k x[t, k, h] * w[t, k]), fp32
+ * accumulator in slot order, one rounding; skipping rules as vmamd_moe_sum.
+ * Replaces _combine_expert_rows (vllm_musa/kernels/w4afp8_moe.py:127-161) and
+ * post_reorder_triton_kernel (vllm_musa/jit_kernel/post_reorder.py:13-44),
+ * with an fp32 accumulator for both. */
+int vmamd_moe_weighted_sum(const void* x, int dtype, int64_t tokens, int topk, int64_t hidden,
+                           const float* topk_weights, const int32_t* topk_ids,
+                           const int32_t* expert_map, int64_t expert_map_len, void* out,
+                           vmamd_stream_t stream);
 
 /* ------------------------------------------------------- block-fp8 GEMM --
  * C[M, N] = bf16( sum_kb (sum_{k in kb} A[m,k] B[n,k]) * As[m,kb] * Bs[n/128, kb] )
@@ -280,6 +301,30 @@ int vmamd_moe_bf16_w2(const void* a2, int64_t T, int topk, const int32_t* sorted
                       int64_t I, const float* topk_weights, const int32_t* topk_ids,
                       const int32_t* expert_map, int64_t expert_map_len, void* y, void* workspace,
                       size_t workspace_bytes, vmamd_stream_t stream);
+
+/* ---------------------------------------------------------- w4afp8 MoE --
+ * One MoE layer with signed int4 expert weights (two per byte, element 2j in
+ * the low nibble of byte j) and bf16 scales per (output row, 128-K group),
+ * fp8 activations with one dynamic scale per row:
+ *   xq = q_row(x)                          (s = max(1e-4, absmax(row)) / 448)
+ *   h  = bf16(sum_kb (xq . W13_int4[e]^T)_kb * s13[e, n, kb] * s_x)
+ *   a  = bf16(silu(min(h_g, L)) * clamp(h_u, -L, L))   (no clamp if L <= 0)
+ *   y  = bf16(sum_kb (q_row(a) . W2_int4[e]^T)_kb * s2[e, n, kb] * s_a)
+ *   out[t] = bf16(sum_k y[t, k] * w[t, k])  (fp32 accumulator)
+ * x [T, H] bf16; w13 [E, 2I, H/2] int8 with w13_s [E, 2I, H/128] bf16; w2
+ * [E, H, I/2] int8 with w2_s [E, H, I/128] bf16; topk / expert_map / path /
+ * workspace rules as vmamd_fused_moe_fp8.  H, I <= 16384.
+ * Replaces w4afp8_moe (vllm_musa/kernels/w4afp8_moe.py:164-362) and the MATE
+ * S4FP8 grouped GEMMs it calls (283-318), reached from
+ * MusaW4AFp8MoEMethod.apply (model_executor/layers/quantization/w4afp8.py:147-170). */
+size_t vmamd_w4afp8_moe_workspace_size(int64_t T, int topk, int num_experts, int64_t H,
+                                       int64_t I, int path);
+int vmamd_w4afp8_moe(const void* x, int64_t T, int64_t H, const void* w13, const void* w13_s,
+                     const void* w2, const void* w2_s, int num_experts, int64_t I,
+                     const float* topk_weights, const int32_t* topk_ids, int topk,
+                     const int32_t* expert_map, int64_t expert_map_len, float swiglu_limit,
+                     int path, void* out, void* workspace, size_t workspace_bytes,
+                     vmamd_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -44,6 +44,25 @@ __device__ __forceinline__ v4f mfma_bf16x2(const v8i& a, const v8i& b, v4f c) {
   return c;
 }
 
+// 16 signed int4 values (element 2j in the low nibble of byte j of `p`) ->
+// their 16 e4m3 codes, in element order.  Every integer in [-8, 7] is exact in
+// e4m3; the codes come from two byte-permute lookups (nibble & 7 indexes a
+// table of the non-negative codes 0..7 and one of the codes of -8..-1) and a
+// per-byte select on the nibble's sign bit.
+__device__ __forceinline__ uint32_t int4x4_to_fp8(uint32_t t) {
+  // t: 4 nibbles in its low 16 bits -> one nibble per byte
+  const uint32_t s = (t & 0xFu) | ((t & 0xF0u) << 4) | ((t & 0xF00u) << 8) | ((t & 0xF000u) << 12);
+  const uint32_t sel = s & 0x07070707u;
+  const uint32_t neg = ((s >> 3) & 0x01010101u) * 0xFFu;
+  const uint32_t pos = __builtin_amdgcn_perm(0x4E4C4A48u, 0x44403800u, sel);  // 0..7
+  const uint32_t ngv = __builtin_amdgcn_perm(0xB8C0C4C8u, 0xCACCCED0u, sel);  // -8..-1
+  return (pos & ~neg) | (ngv & neg);
+}
+__device__ __forceinline__ v4i int4x16_to_fp8(uint2 p) {
+  return v4i{static_cast<int>(int4x4_to_fp8(p.x & 0xFFFFu)), static_cast<int>(int4x4_to_fp8(p.x >> 16)),
+             static_cast<int>(int4x4_to_fp8(p.y & 0xFFFFu)), static_cast<int>(int4x4_to_fp8(p.y >> 16))};
+}
+
 // Operand fragment of `row` from an LDS tile.
 __device__ __forceinline__ v8i lds_frag(const uint8_t* tile, int row, int g) {
   const uint4 lo = *reinterpret_cast<const uint4*>(tile + lds_off(row, g));
@@ -70,12 +89,33 @@ __device__ __forceinline__ v8i global_frag(const uint8_t* p, int g) {
 __device__ __forceinline__ v4i ld16(const uint8_t* p) { return *reinterpret_cast<const v4i*>(p); }
 __device__ __forceinline__ void st16(uint8_t* p, const v4i& v) { *reinterpret_cast<v4i*>(p) = v; }
 
+// Operand fragment of one 128-element K-block of a packed int4 row (64 bytes
+// at p), converted to e4m3 in the same K order as global_frag: lane group g
+// takes elements [16g, 16g+16) and [64+16g, 64+16g+16).
+__device__ __forceinline__ v8i global_frag_int4(const uint8_t* p, int g) {
+  const uint2 lo = *reinterpret_cast<const uint2*>(p + 8 * g);
+  const uint2 hi = *reinterpret_cast<const uint2*>(p + 32 + 8 * g);
+  const v4i a = int4x16_to_fp8(lo), b = int4x16_to_fp8(hi);
+  v8i f;
+  f[0] = a[0]; f[1] = a[1]; f[2] = a[2]; f[3] = a[3];
+  f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
+  return f;
+}
+
 // acc += p * s, element-wise (the per-K-block scale promotion).
 __device__ __forceinline__ void fma4(v4f& acc, const v4f& p, float s) {
   acc[0] = fmaf(p[0], s, acc[0]);
   acc[1] = fmaf(p[1], s, acc[1]);
   acc[2] = fmaf(p[2], s, acc[2]);
   acc[3] = fmaf(p[3], s, acc[3]);
+}
+
+// acc[r] += p[r] * s[r] (per-row weight scales of the w4afp8 kernels).
+__device__ __forceinline__ void fma4v(v4f& acc, const v4f& p, const v4f& s) {
+  acc[0] = fmaf(p[0], s[0], acc[0]);
+  acc[1] = fmaf(p[1], s[1], acc[1]);
+  acc[2] = fmaf(p[2], s[2], acc[2]);
+  acc[3] = fmaf(p[3], s[3], acc[3]);
 }
 
 __device__ __forceinline__ uint2 pack_bf16x4(float a, float b, float c, float d) {

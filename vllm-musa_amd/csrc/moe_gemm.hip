@@ -1,25 +1,31 @@
-// Fused-MoE expert GEMMs (W13 gate/up, W2 down) for 128x128 block-fp8 and
-// for bf16 expert weights.
+// Fused-MoE expert GEMMs (W13 gate/up, W2 down) for three weight formats:
 //
-// Layouts (row-major):
-//   fp8:  xq [T, H] e4m3, xs [T, H/128] f32 (1x128 activation groups)
-//         w13 [E, 2I, H] e4m3, w13_s [E, 2I/128, H/128]; w2 [E, H, I], w2_s [E, H/128, I/128]
-//   bf16: x [T, H] bf16; w13 [E, 2I, H] bf16; w2 [E, H, I] bf16
+//   kFp8  128x128 block-fp8 weights, 1x128 fp8 activation groups:
+//         xq [T, H] e4m3 + xs [T, H/128] f32; w13 [E, 2I, H] e4m3 +
+//         w13_s [E, 2I/128, H/128] f32; w2 [E, H, I] + w2_s [E, H/128, I/128]
+//   kBf16 bf16 weights and activations: x [T, H]; w13 [E, 2I, H]; w2 [E, H, I]
+//   kW4   w4afp8: signed int4 weights two per byte (element 2j in the low
+//         nibble of byte j), bf16 scale per (output row, 128-K group):
+//         w13 [E, 2I, H/2] + [E, 2I, H/128]; w2 [E, H, I/2] + [E, H, I/128];
+//         activations fp8 with one scale per row: xq [T, H] + xs [T]
 //   w13 rows [0, I) gate, [I, 2I) up; routes r = t * topk + k; sorted /
 //   offsets / active come from moe_align_block_size.
 //
-// Both operand kinds move 128-byte row chunks: for fp8 a chunk is one
-// 128-wide K-block (one 16x16x128 MFMA, then the scale promotion
-// acc += p * sa[m] * sb[n/128]); for bf16 it is 64 K-elements (two chained
-// 16x16x32 bf16 MFMAs, no scales).
+// Every kind moves K in "steps": 128 K-elements for kFp8 / kW4 (one 16x16x128
+// fp8 MFMA; kW4 nibbles are converted to e4m3 codes on the way in, every
+// integer in [-8, 7] being exact in e4m3), 64 for kBf16 (two 16x16x32 bf16
+// MFMAs).  Per step kFp8 promotes acc += p * sa[m] * sb[n/128], kW4 promotes
+// acc += p * sw[n] with the row's own weight scale and applies the activation
+// row scale once at the end, kBf16 accumulates directly.
 //
 // Decode path (few routes per expert): moe_gemv_kernel.  A wave owns 16
 // weight rows of one active expert and a K range; it streams the rows from
 // HBM once (no LDS) and applies each 16-row fragment to every 16-route block
-// of that expert.  W13 writes fp32 split-K partials per route; the act kernel
-// sums them in a fixed order, rounds gate/up to bf16, applies SiLU-and-mul
-// and (fp8) quantises a2 per 1x128 group.  W2 writes bf16(acc * routed
-// weight) per route, or fp32 partials reduced by moe_w2_reduce_kernel.
+// of that expert.  W13 writes fp32 split-K partials per route; the act
+// kernels sum them in a fixed order, round gate/up to bf16, apply
+// SiLU-and-mul and quantise a2.  W2 writes bf16(acc * routed weight) per
+// route (kW4: bf16(acc * a2 row scale), the routed weight is applied by the
+// combine), or fp32 partials reduced by moe_w2_reduce_kernel.
 //
 // Prefill path (many routes per expert): grouped MFMA GEMMs over 128-route
 // blocks.  Tiles are ordered expert-major -- all blocks of one (expert,
@@ -27,12 +33,22 @@
 // the blocks of an expert that share a weight tile run together on one XCD
 // and the tile is fetched from HBM once.  W13 covers 128 gate + 128 up rows
 // per tile (interleaved by 16 so each lane holds matching gate/up values) and
-// fuses SiLU-and-mul (and the fp8 a2 quantiser) into its epilogue.
+// fuses SiLU-and-mul (and the kFp8 1x128 a2 quantiser) into its epilogue.
 #include <algorithm>
+#include <type_traits>
 
 #include "mfma_fp8.h"
 
 namespace vmamd {
+
+constexpr int kFp8 = 0, kBf16 = 1, kW4 = 2;
+
+// Bytes of one K step: activation row, weight row.
+template <int KIND> struct KindBytes {
+  static constexpr int kAct = 128;
+  static constexpr int kW = KIND == kW4 ? 64 : 128;
+  static constexpr int kElems = KIND == kBf16 ? 64 : 128;  // K elements per step
+};
 
 // --------------------------------------------------------------- helpers --
 __device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
@@ -56,28 +72,36 @@ __device__ __forceinline__ float swiglu_bf16(float hg, float hu, float limit) {
   return bf16r(hg / (1.0f + expf(-hg)) * hu);
 }
 
-// One 128-byte chunk of both operands into an accumulator.
-template <bool FP8>
-__device__ __forceinline__ void chunk_mma(v4f& acc, const v8i& w, const v8i& x, float s) {
-  if constexpr (FP8) {
-    fma4(acc, mfma_fp8(w, x, v4f{0.f, 0.f, 0.f, 0.f}), s);
-  } else {
-    acc = mfma_bf16x2(w, x, acc);
+// w4afp8 activation: the limit clamps gate <= L and up to [-L, L], then one
+// rounding of silu(gate) * up to bf16.
+__device__ __forceinline__ float swiglu_w4(float g, float u, float limit) {
+  if (limit > 0.f) {
+    g = fminf(g, limit);
+    u = fmaxf(fminf(u, limit), -limit);
   }
+  return bf16r(g / (1.0f + expf(-g)) * u);
+}
+
+template <int KIND>
+__device__ __forceinline__ v8i weight_frag(const uint8_t* p, int g) {
+  if constexpr (KIND == kW4) return global_frag_int4(p, g);
+  else return global_frag(p, g);
 }
 
 // ---------------------------------------------------------- decode GEMV ---
 constexpr int kMoeGemvWaves = 4;
 constexpr int kGemvBlock = 16;  // routes per block (one MFMA column tile)
 
-template <int MAXB, bool FP8>
+// act_s: kFp8 [rows, K/128] group scales (read here); kW4 / kBf16 unused.
+// ws: kFp8 f32 block scales; kW4 bf16 row scales.
+template <int MAXB, int KIND>
 __global__ __launch_bounds__(kMoeGemvWaves * kWave) void moe_gemv_kernel(
     const uint8_t* __restrict__ act, const float* __restrict__ act_s, int act_div, int K,
     const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ active, const int32_t* __restrict__ num_active,
-    const uint8_t* __restrict__ w, const float* __restrict__ ws, int N, int numel, int splits,
+    const uint8_t* __restrict__ w, const void* __restrict__ ws, int N, int numel, int splits,
     float* __restrict__ partial, const float* __restrict__ route_w, uint16_t* __restrict__ y) {
-  constexpr int EB = FP8 ? 1 : 2;
+  using KB_ = KindBytes<KIND>;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int li = lane % 16, lg = lane / 16;
   const int ntile = blockIdx.x * kMoeGemvWaves + wave;
@@ -88,14 +112,22 @@ __global__ __launch_bounds__(kMoeGemvWaves * kWave) void moe_gemv_kernel(
   const int seg0 = offsets[e];
   const int nblk = (offsets[e + 1] - seg0) / kGemvBlock;
   const int split = blockIdx.z;
-  const int64_t rowb = static_cast<int64_t>(K) * EB;
-  const int KC = static_cast<int>(rowb / 128);  // 128-byte chunks (== scale blocks for fp8)
+  const int KS = K / KB_::kElems;                    // K steps
+  const int64_t arowb = static_cast<int64_t>(KS) * KB_::kAct;
+  const int64_t wrowb = static_cast<int64_t>(KS) * KB_::kW;
   const int NB = (N + 127) / 128;
-  const int kb0 = split * KC / splits, kb1 = (split + 1) * KC / splits;
-  const uint8_t* wrow = w + (static_cast<int64_t>(e) * N + ntile * 16 + li) * rowb;
-  const float* wsr = nullptr;
-  if constexpr (FP8) wsr = ws + (static_cast<int64_t>(e) * NB + (ntile * 16) / 128) * KC;
+  const int kb0 = split * KS / splits, kb1 = (split + 1) * KS / splits;
   const int n = ntile * 16 + 4 * lg;
+  const uint8_t* wrow = w + (static_cast<int64_t>(e) * N + ntile * 16 + li) * wrowb;
+  const float* wsr = nullptr;                        // kFp8: block scales of the 16 rows
+  const uint16_t* wsw[4] = {nullptr, nullptr, nullptr, nullptr};  // kW4: scales of rows n..n+3
+  if constexpr (KIND == kFp8)
+    wsr = static_cast<const float*>(ws) + (static_cast<int64_t>(e) * NB + (ntile * 16) / 128) * KS;
+  if constexpr (KIND == kW4) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      wsw[r] = static_cast<const uint16_t*>(ws) + (static_cast<int64_t>(e) * N + n + r) * KS;
+  }
 
   for (int b0 = 0; b0 < nblk; b0 += MAXB) {
     const int nb = min(MAXB, nblk - b0);
@@ -108,47 +140,48 @@ __global__ __launch_bounds__(kMoeGemvWaves * kWave) void moe_gemv_kernel(
       const bool valid = r < numel;
       rr[b] = valid ? r : -1;
       const int64_t row = valid ? r / act_div : 0;
-      arow[b] = act + row * rowb;
-      asr[b] = FP8 ? act_s + row * KC : nullptr;
+      arow[b] = act + row * arowb;
+      asr[b] = KIND == kFp8 ? act_s + row * KS : nullptr;
     }
     v4f acc[MAXB];
 #pragma unroll
     for (int b = 0; b < MAXB; ++b) acc[b] = v4f{0.f, 0.f, 0.f, 0.f};
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
 
     constexpr int U = 4;
     int kb = kb0;
-    for (; kb + U <= kb1; kb += U) {
+    for (; kb <= kb1 - 1; kb += U) {
+      const int nu = min(U, kb1 - kb);
       v8i wf[U];
       float sb[U];
+      v4f sw[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        wf[u] = global_frag(wrow + (kb + u) * 128, lg);
+        const int k = kb + min(u, nu - 1);
+        wf[u] = weight_frag<KIND>(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
         sb[u] = 0.f;
-        if constexpr (FP8) sb[u] = wsr[kb + u];
+        sw[u] = zero;
+        if constexpr (KIND == kFp8) sb[u] = wsr[k];
+        if constexpr (KIND == kW4)
+          sw[u] = v4f{bf16_to_f32(wsw[0][k]), bf16_to_f32(wsw[1][k]), bf16_to_f32(wsw[2][k]),
+                      bf16_to_f32(wsw[3][k])};
       }
 #pragma unroll
       for (int b = 0; b < MAXB; ++b) {
         if (b < nb) {
 #pragma unroll
           for (int u = 0; u < U; ++u) {
-            const v8i xf = global_frag(arow[b] + (kb + u) * 128, lg);
-            float s = 0.f;
-            if constexpr (FP8) s = asr[b][kb + u] * sb[u];
-            chunk_mma<FP8>(acc[b], wf[u], xf, s);
+            if (u < nu) {
+              const v8i xf = global_frag(arow[b] + static_cast<int64_t>(kb + u) * KB_::kAct, lg);
+              if constexpr (KIND == kFp8) {
+                fma4(acc[b], mfma_fp8(wf[u], xf, zero), asr[b][kb + u] * sb[u]);
+              } else if constexpr (KIND == kW4) {
+                fma4v(acc[b], mfma_fp8(wf[u], xf, zero), sw[u]);
+              } else {
+                acc[b] = mfma_bf16x2(wf[u], xf, acc[b]);
+              }
+            }
           }
-        }
-      }
-    }
-    for (; kb < kb1; ++kb) {
-      const v8i wf = global_frag(wrow + kb * 128, lg);
-      float sb = 0.f;
-      if constexpr (FP8) sb = wsr[kb];
-#pragma unroll
-      for (int b = 0; b < MAXB; ++b) {
-        if (b < nb) {
-          float s = 0.f;
-          if constexpr (FP8) s = asr[b][kb] * sb;
-          chunk_mma<FP8>(acc[b], wf, global_frag(arow[b] + kb * 128, lg), s);
         }
       }
     }
@@ -169,10 +202,11 @@ __global__ __launch_bounds__(kMoeGemvWaves * kWave) void moe_gemv_kernel(
   }
 }
 
-// Gate/up of 8 consecutive columns c0.. of route r, split partials summed in
-// a fixed order, each rounded to bf16 and combined by SiLU-and-mul.
-__device__ __forceinline__ void act8(const float* __restrict__ partial, int splits, int numel, int I,
-                                     int r, int c0, float limit, float (&v)[8]) {
+// Gate/up sums of 8 consecutive columns c0.. of route r: split partials in a
+// fixed order, times `scale`.
+__device__ __forceinline__ void gate_up8(const float* __restrict__ partial, int splits, int numel,
+                                         int I, int r, int c0, float scale, float (&g)[8],
+                                         float (&u)[8]) {
   const int64_t plane = static_cast<int64_t>(numel) * 2 * I;
   const float* src = partial + static_cast<int64_t>(r) * 2 * I + c0;
 #pragma unroll
@@ -185,14 +219,12 @@ __device__ __forceinline__ void act8(const float* __restrict__ partial, int spli
       gs.x += ga.x; gs.y += ga.y; gs.z += ga.z; gs.w += ga.w;
       us.x += ua.x; us.y += ua.y; us.z += ua.z; us.w += ua.w;
     }
-    v[j + 0] = swiglu_bf16(bf16r(gs.x), bf16r(us.x), limit);
-    v[j + 1] = swiglu_bf16(bf16r(gs.y), bf16r(us.y), limit);
-    v[j + 2] = swiglu_bf16(bf16r(gs.z), bf16r(us.z), limit);
-    v[j + 3] = swiglu_bf16(bf16r(gs.w), bf16r(us.w), limit);
+    g[j + 0] = gs.x * scale; g[j + 1] = gs.y * scale; g[j + 2] = gs.z * scale; g[j + 3] = gs.w * scale;
+    u[j + 0] = us.x * scale; u[j + 1] = us.y * scale; u[j + 2] = us.z * scale; u[j + 3] = us.w * scale;
   }
 }
 
-// fp8: activation then a2 quantisation per 1x128 group (one 16-lane segment
+// kFp8: activation then a2 quantisation per 1x128 group (one 16-lane segment
 // per group, 8 columns per lane).  NaN activations (clamped variant) quantise
 // to fp8_min.
 __global__ __launch_bounds__(256) void moe_act_quant_kernel(const float* __restrict__ partial,
@@ -205,8 +237,10 @@ __global__ __launch_bounds__(256) void moe_act_quant_kernel(const float* __restr
   if (g >= static_cast<int64_t>(numel) * gpr) return;
   const int r = static_cast<int>(g / gpr);
   const int c0 = static_cast<int>(g % gpr) * 128 + sub * 8;
-  float v[8];
-  act8(partial, splits, numel, I, r, c0, limit, v);
+  float gv[8], uv[8], v[8];
+  gate_up8(partial, splits, numel, I, r, c0, 1.0f, gv, uv);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = swiglu_bf16(bf16r(gv[j]), bf16r(uv[j]), limit);
   float amax = 1e-10f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
@@ -222,17 +256,27 @@ __global__ __launch_bounds__(256) void moe_act_quant_kernel(const float* __restr
   *reinterpret_cast<uint2*>(a2q + static_cast<int64_t>(r) * I + c0) = out;
 }
 
-// bf16: a2[r, c] = the bf16 activation, 8 columns per thread (16-byte store).
+// kBf16 / kW4: a[r, c] = the bf16 activation, 8 columns per thread (16-byte
+// store).  kW4 first scales the sums by the token's activation scale
+// xs[r / topk] and rounds gate/up to bf16, then applies swiglu_w4; its a2
+// quantiser (one scale per row) runs as a separate row kernel.
+template <int KIND>
 __global__ __launch_bounds__(256) void moe_act_bf16_kernel(const float* __restrict__ partial,
                                                            int splits, int numel, int I,
-                                                           float limit, uint16_t* __restrict__ a2) {
+                                                           float limit, const float* __restrict__ xs,
+                                                           int topk, uint16_t* __restrict__ a2) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int cpr = I / 8;
   if (idx >= static_cast<int64_t>(numel) * cpr) return;
   const int r = static_cast<int>(idx / cpr);
   const int c0 = static_cast<int>(idx % cpr) * 8;
-  float v[8];
-  act8(partial, splits, numel, I, r, c0, limit, v);
+  const float scale = KIND == kW4 ? xs[r / topk] : 1.0f;
+  float gv[8], uv[8], v[8];
+  gate_up8(partial, splits, numel, I, r, c0, scale, gv, uv);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    v[j] = KIND == kW4 ? swiglu_w4(bf16r(gv[j]), bf16r(uv[j]), limit)
+                       : swiglu_bf16(bf16r(gv[j]), bf16r(uv[j]), limit);
   uint4 o;
   o.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
   o.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
@@ -241,7 +285,8 @@ __global__ __launch_bounds__(256) void moe_act_bf16_kernel(const float* __restri
   *reinterpret_cast<uint4*>(a2 + static_cast<int64_t>(r) * I + c0) = o;
 }
 
-// y[r, n] = bf16(sum_s partial[s, r, n] * w_r) for the W2 split path.
+// y[r, n] = bf16(sum_s partial[s, r, n] * w_r) for the W2 split path (kW4:
+// w_r is the a2 row scale).
 __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(const float* __restrict__ partial,
                                                             int splits, int numel, int N,
                                                             const int32_t* __restrict__ ids,
@@ -293,26 +338,67 @@ __device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* _
   return true;
 }
 
+// Weight-tile loader of the prefill GEMMs.  One pass moves THREADS/CPR rows;
+// kFp8 / kBf16 copy 16-byte chunks (CPR = 8 per 128-byte row step), kW4 reads
+// 16 packed bytes (32 elements) per thread (CPR = 4) and writes the two
+// 16-byte e4m3 chunks they expand to.
+template <int KIND, int THREADS, int BN>
+struct WLoader {
+  static constexpr int CPR = KIND == kW4 ? 4 : 8;
+  static constexpr int RSTEP = THREADS / CPR;
+  static constexpr int BCH = BN / RSTEP;
+  using Raw = typename std::conditional<KIND == kW4, uint4, v4i>::type;
+  int64_t goff[BCH];
+  int l0, l1;  // LDS byte offsets (row 0 of the pass) of the chunks written
+  Raw raw[BCH];
+
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ w, int step) {
+#pragma unroll
+    for (int c = 0; c < BCH; ++c) {
+      const uint8_t* p = w + goff[c] + static_cast<int64_t>(step) * KindBytes<KIND>::kW;
+      if constexpr (KIND == kW4) raw[c] = *reinterpret_cast<const uint4*>(p);
+      else raw[c] = ld16(p);
+    }
+  }
+  __device__ __forceinline__ void store(uint8_t* tile) const {
+#pragma unroll
+    for (int c = 0; c < BCH; ++c) {
+      if constexpr (KIND == kW4) {
+        st16(tile + l0 + c * RSTEP * 128, int4x16_to_fp8(uint2{raw[c].x, raw[c].y}));
+        st16(tile + l1 + c * RSTEP * 128, int4x16_to_fp8(uint2{raw[c].z, raw[c].w}));
+      } else {
+        st16(tile + l0 + c * RSTEP * 128, raw[c]);
+      }
+    }
+  }
+};
+
 // W13: tile = 128 routes x (128 gate + 128 up rows); 8 waves as 2 (m) x 4 (n);
 // local weight row j: pair p = j / 32, q = j % 32 -> gate row n0 + 16p + q
-// (q < 16) or up row I + n0 + 16p + q - 16.  Dynamic LDS: 2 x 48 KiB.
+// (q < 16) or up row I + n0 + 16p + q - 16.  Dynamic LDS per stage: the two
+// tiles, plus (kW4) the fp32 scales of the 256 weight rows.
 constexpr int kW13Threads = 512;
-constexpr int kW13Lds = 2 * (kMoeBM + 256) * 128;
+constexpr int kW13BN = 256;
+template <int KIND>
+constexpr int w13_stage_bytes() { return (kMoeBM + kW13BN) * 128 + (KIND == kW4 ? kW13BN * 4 : 0); }
 
-template <bool FP8>
+// xs: kFp8 [T, H/128] group scales, kW4 [T] row scales.  w13s: kFp8 f32
+// block scales, kW4 bf16 row scales.  a2: kFp8 e4m3 [rows, I] (+ a2s), kBf16 /
+// kW4 bf16 [rows, I].
+template <int KIND>
 __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
     const uint8_t* __restrict__ xa, const float* __restrict__ xs, int topk, int H,
     const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles,
-    const uint8_t* __restrict__ w13, const float* __restrict__ w13s, int I, float limit,
+    const uint8_t* __restrict__ w13, const void* __restrict__ w13s, int I, float limit,
     uint8_t* __restrict__ a2, float* __restrict__ a2s) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
-  constexpr int EB = FP8 ? 1 : 2;
-  constexpr int BM = kMoeBM, BN = 256, THREADS = kW13Threads;
+  using KB_ = KindBytes<KIND>;
+  constexpr int BM = kMoeBM, BN = kW13BN, THREADS = kW13Threads;
   constexpr int WN = 4, WTM = 64, WTN = 64, MT = 4, NT = 4;
-  constexpr int RSTEP = THREADS / 8;                 // 64 rows per copy pass
-  constexpr int ACH = BM / RSTEP, BCH = BN / RSTEP;  // 2, 4
-  constexpr int STAGE = (BM + BN) * 128;
+  constexpr int RSTEP = THREADS / 8;   // activation rows per copy pass
+  constexpr int ACH = BM / RSTEP;      // 2
+  constexpr int STAGE = w13_stage_bytes<KIND>();
 
   const int TN = I / 128;
   int e, mb, tn;
@@ -321,12 +407,13 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int wm = wave / WN, wn = wave % WN;
   const int li = lane % 16, lg = lane / 16;
-  const int64_t rowb = static_cast<int64_t>(H) * EB;
-  const int KC = static_cast<int>(rowb / 128);  // chunks; == scale blocks for fp8
+  const int KS = H / KB_::kElems;
+  const int64_t arowb = static_cast<int64_t>(KS) * KB_::kAct;
+  const int64_t wrowb = static_cast<int64_t>(KS) * KB_::kW;
   const int NB2 = (2 * I + 127) / 128;
 
   const int crow = tid / 8, cch = tid % 8;
-  const int l0 = lds_off(crow, cch);
+  const int la0 = lds_off(crow, cch);
   // Padding rows of the block load row 0 and are zeroed in registers.
   int64_t goff_a[ACH];
   bool aval[ACH];
@@ -334,25 +421,45 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
   for (int c = 0; c < ACH; ++c) {
     const int r = sorted[mb * BM + crow + c * RSTEP];
     aval[c] = r < numel;
-    goff_a[c] = (aval[c] ? static_cast<int64_t>(r / topk) * rowb : 0) + cch * 16;
+    goff_a[c] = (aval[c] ? static_cast<int64_t>(r / topk) * arowb : 0) + cch * 16;
   }
-  int64_t goff_b[BCH];
+  auto w13_row = [&](int j) {  // local weight row -> row of w13[e]
+    const int p = j / 32, q = j % 32;
+    return q < 16 ? n0 + 16 * p + q : I + n0 + 16 * p + (q - 16);
+  };
+  WLoader<KIND, THREADS, BN> wl;
+  {
+    using WL = WLoader<KIND, THREADS, BN>;
+    const int wr = tid / WL::CPR, wc = tid % WL::CPR;
 #pragma unroll
-  for (int c = 0; c < BCH; ++c) {
-    const int j = crow + c * RSTEP, p = j / 32, q = j % 32;
-    const int row = q < 16 ? n0 + 16 * p + q : I + n0 + 16 * p + (q - 16);
-    goff_b[c] = (static_cast<int64_t>(e) * 2 * I + row) * rowb + cch * 16;
+    for (int c = 0; c < WL::BCH; ++c)
+      wl.goff[c] = (static_cast<int64_t>(e) * 2 * I + w13_row(wr + c * WL::RSTEP)) * wrowb + wc * 16;
+    wl.l0 = BM * 128 + lds_off(wr, KIND == kW4 ? 2 * wc : wc);
+    wl.l1 = BM * 128 + lds_off(wr, 2 * wc + 1);
   }
+  // kW4: thread j < BN stages the scale of local weight row j.
+  const uint16_t* wsc_row = nullptr;
+  if constexpr (KIND == kW4)
+    wsc_row = tid < BN ? static_cast<const uint16_t*>(w13s) +
+                             (static_cast<int64_t>(e) * 2 * I + w13_row(tid)) * KS
+                       : nullptr;
   const float* xs_row[MT];
   bool tval[MT];
+  float srow[MT];  // kW4: activation row scales
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int r = sorted[mb * BM + wm * WTM + mt * 16 + li];
     tval[mt] = r < numel;
-    xs_row[mt] = FP8 ? xs + (tval[mt] ? static_cast<int64_t>(r / topk) * KC : 0) : nullptr;
+    const int64_t tok = tval[mt] ? r / topk : 0;
+    xs_row[mt] = KIND == kFp8 ? xs + tok * KS : nullptr;
+    srow[mt] = KIND == kW4 ? (tval[mt] ? xs[tok] : 0.f) : 0.f;
   }
-  const float* sg = FP8 ? w13s + (static_cast<int64_t>(e) * NB2 + n0 / 128) * KC : nullptr;
-  const float* su = FP8 ? w13s + (static_cast<int64_t>(e) * NB2 + (I + n0) / 128) * KC : nullptr;
+  const float* sg = nullptr;
+  const float* su = nullptr;
+  if constexpr (KIND == kFp8) {
+    sg = static_cast<const float*>(w13s) + (static_cast<int64_t>(e) * NB2 + n0 / 128) * KS;
+    su = static_cast<const float*>(w13s) + (static_cast<int64_t>(e) * NB2 + (I + n0) / 128) * KS;
+  }
 
   v4f acc[MT][NT];
 #pragma unroll
@@ -361,22 +468,25 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
 
   const v4i z4 = {0, 0, 0, 0};
-  v4i ra[ACH], rb[BCH];
+  v4i ra[ACH];
 #pragma unroll
   for (int c = 0; c < ACH; ++c) {
     const v4i v = ld16(xa + goff_a[c]);
     ra[c] = aval[c] ? v : z4;
   }
+  wl.load(w13, 0);
+  float wsc = 0.f;
+  if constexpr (KIND == kW4)
+    if (wsc_row) wsc = bf16_to_f32(wsc_row[0]);
 #pragma unroll
-  for (int c = 0; c < BCH; ++c) rb[c] = ld16(w13 + goff_b[c]);
-#pragma unroll
-  for (int c = 0; c < ACH; ++c) st16(&smem_dyn[l0 + c * RSTEP * 128], ra[c]);
-#pragma unroll
-  for (int c = 0; c < BCH; ++c) st16(&smem_dyn[BM * 128 + l0 + c * RSTEP * 128], rb[c]);
+  for (int c = 0; c < ACH; ++c) st16(&smem_dyn[la0 + c * RSTEP * 128], ra[c]);
+  wl.store(smem_dyn);
+  if constexpr (KIND == kW4)
+    if (wsc_row) reinterpret_cast<float*>(smem_dyn + (BM + BN) * 128)[tid] = wsc;
   float sa[MT], sbg = 0.f, sbu = 0.f;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) sa[mt] = 0.f;
-  if constexpr (FP8) {
+  if constexpr (KIND == kFp8) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) sa[mt] = tval[mt] ? xs_row[mt][0] : 0.f;
     sbg = sg[0];
@@ -384,23 +494,22 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
   }
   __syncthreads();
 
-  for (int kb = 0; kb < KC; ++kb) {
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < KS; ++kb) {
     const int cur = kb & 1;
-    // Prefetch chunk kb+1 (the last iteration re-reads chunk KC-1 into the
-    // idle buffer; that copy is never used).
-    const int kn = min(kb + 1, KC - 1);
-    const int off = kn * 128;
+    // Prefetch step kb+1 (the last iteration re-reads step KS-1 into the idle
+    // buffer; that copy is never used).
+    const int kn = min(kb + 1, KS - 1);
 #pragma unroll
     for (int c = 0; c < ACH; ++c) {
-      const v4i v = ld16(xa + goff_a[c] + off);
+      const v4i v = ld16(xa + goff_a[c] + static_cast<int64_t>(kn) * KB_::kAct);
       ra[c] = aval[c] ? v : z4;
     }
-#pragma unroll
-    for (int c = 0; c < BCH; ++c) rb[c] = ld16(w13 + goff_b[c] + off);
-    float san[MT], sbgn = 0.f, sbun = 0.f;
+    wl.load(w13, kn);
+    float san[MT], sbgn = 0.f, sbun = 0.f, wscn = 0.f;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) san[mt] = 0.f;
-    if constexpr (FP8) {
+    if constexpr (KIND == kFp8) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const float v = xs_row[mt][kn];
@@ -409,6 +518,8 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
       sbgn = sg[kn];
       sbun = su[kn];
     }
+    if constexpr (KIND == kW4)
+      if (wsc_row) wscn = bf16_to_f32(wsc_row[kn]);
 
     const uint8_t* tile = smem_dyn + cur * STAGE;
     v8i xf[MT];
@@ -416,16 +527,27 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
     for (int mt = 0; mt < MT; ++mt) xf[mt] = lds_frag(tile, wm * WTM + mt * 16 + li, lg);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const v8i wf = lds_frag(tile + BM * 128, wn * WTN + nt * 16 + li, lg);
-      const float sb = (nt & 1) ? sbu : sbg;
+      const int wrow_l = wn * WTN + nt * 16;
+      const v8i wf = lds_frag(tile + BM * 128, wrow_l + li, lg);
+      if constexpr (KIND == kFp8) {
+        const float sb = (nt & 1) ? sbu : sbg;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) chunk_mma<FP8>(acc[mt][nt], wf, xf[mt], sa[mt] * sb);
+        for (int mt = 0; mt < MT; ++mt) fma4(acc[mt][nt], mfma_fp8(wf, xf[mt], zero), sa[mt] * sb);
+      } else if constexpr (KIND == kW4) {
+        const v4f swv = *reinterpret_cast<const v4f*>(tile + (BM + BN) * 128 + (wrow_l + 4 * lg) * 4);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) fma4v(acc[mt][nt], mfma_fp8(wf, xf[mt], zero), swv);
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma_bf16x2(wf, xf[mt], acc[mt][nt]);
+      }
     }
     uint8_t* nxt = smem_dyn + (cur ^ 1) * STAGE;
 #pragma unroll
-    for (int c = 0; c < ACH; ++c) st16(&nxt[l0 + c * RSTEP * 128], ra[c]);
-#pragma unroll
-    for (int c = 0; c < BCH; ++c) st16(&nxt[BM * 128 + l0 + c * RSTEP * 128], rb[c]);
+    for (int c = 0; c < ACH; ++c) st16(&nxt[la0 + c * RSTEP * 128], ra[c]);
+    wl.store(nxt);
+    if constexpr (KIND == kW4)
+      if (wsc_row) reinterpret_cast<float*>(nxt + (BM + BN) * 128)[tid] = wscn;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) sa[mt] = san[mt];
     sbg = sbgn;
@@ -433,7 +555,7 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
     __syncthreads();
   }
 
-  if constexpr (FP8) {
+  if constexpr (KIND == kFp8) {
     // Epilogue: activation, row amax across the 4 n-waves through LDS, quantise.
     float* red = reinterpret_cast<float*>(smem_dyn);  // [WN][BM]
     float v[MT][2][4];
@@ -484,8 +606,13 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
       for (int q = 0; q < 2; ++q) {
         float o[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          o[r] = swiglu_bf16(bf16r(acc[mt][2 * q][r]), bf16r(acc[mt][2 * q + 1][r]), limit);
+        for (int r = 0; r < 4; ++r) {
+          if constexpr (KIND == kW4)
+            o[r] = swiglu_w4(bf16r(acc[mt][2 * q][r] * srow[mt]),
+                             bf16r(acc[mt][2 * q + 1][r] * srow[mt]), limit);
+          else
+            o[r] = swiglu_bf16(bf16r(acc[mt][2 * q][r]), bf16r(acc[mt][2 * q + 1][r]), limit);
+        }
         const int col = n0 + (wn * 2 + q) * 16 + 4 * lg;
         *reinterpret_cast<uint2*>(a2b + row * I + col) = pack_bf16x4(o[0], o[1], o[2], o[3]);
       }
@@ -494,17 +621,20 @@ __global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
 }
 
 // W2: tile = 128 routes x 128 hidden rows, 4 waves as 2 x 2, K = I.
-template <bool FP8>
+// a2s: kFp8 [rows, I/128] group scales, kW4 [rows] row scales.
+// y[r] = bf16(acc * route_w[r]) (kFp8 / kBf16) or bf16(acc * a2s[row]) (kW4).
+template <int KIND>
 __global__ __launch_bounds__(256, 2) void moe_w2_gemm_kernel(
     const uint8_t* __restrict__ a2, const float* __restrict__ a2s, int I,
     const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles,
-    const uint8_t* __restrict__ w2, const float* __restrict__ w2s, int H,
+    const uint8_t* __restrict__ w2, const void* __restrict__ w2s, int H,
     const float* __restrict__ route_w, uint16_t* __restrict__ y) {
-  constexpr int EB = FP8 ? 1 : 2;
+  using KB_ = KindBytes<KIND>;
   constexpr int BM = kMoeBM, BN = 128, THREADS = 256, WN = 2, WTM = 64, WTN = 64, MT = 4, NT = 4;
-  constexpr int RSTEP = THREADS / 8, ACH = BM / RSTEP, BCH = BN / RSTEP;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][(BM + BN) * 128];
+  constexpr int RSTEP = THREADS / 8, ACH = BM / RSTEP;
+  constexpr int STAGE = (BM + BN) * 128 + (KIND == kW4 ? BN * 4 : 0);
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2][STAGE];
 
   const int TN = (H + BN - 1) / BN;
   int e, mb, tn;
@@ -513,20 +643,35 @@ __global__ __launch_bounds__(256, 2) void moe_w2_gemm_kernel(
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int wm = wave / WN, wn = wave % WN;
   const int li = lane % 16, lg = lane / 16;
-  const int64_t rowb = static_cast<int64_t>(I) * EB;
-  const int KC = static_cast<int>(rowb / 128);
+  const int KS = I / KB_::kElems;
+  const int64_t arowb = static_cast<int64_t>(KS) * KB_::kAct;
+  const int64_t wrowb = static_cast<int64_t>(KS) * KB_::kW;
   const int NBH = (H + 127) / 128;
 
   const int crow = tid / 8, cch = tid % 8;
-  const int l0 = lds_off(crow, cch);
-  int64_t goff_a[ACH], goff_b[BCH];
+  const int la0 = lds_off(crow, cch);
+  int64_t goff_a[ACH];
 #pragma unroll
   for (int c = 0; c < ACH; ++c)
-    goff_a[c] = (static_cast<int64_t>(mb) * BM + crow + c * RSTEP) * rowb + cch * 16;
+    goff_a[c] = (static_cast<int64_t>(mb) * BM + crow + c * RSTEP) * arowb + cch * 16;
+  WLoader<KIND, THREADS, BN> wl;
+  {
+    using WL = WLoader<KIND, THREADS, BN>;
+    const int wr = tid / WL::CPR, wc = tid % WL::CPR;
 #pragma unroll
-  for (int c = 0; c < BCH; ++c)
-    goff_b[c] = (static_cast<int64_t>(e) * H + min(n0 + crow + c * RSTEP, H - 1)) * rowb + cch * 16;
-  const float* sb_p = FP8 ? w2s + (static_cast<int64_t>(e) * NBH + n0 / 128) * KC : nullptr;
+    for (int c = 0; c < WL::BCH; ++c)
+      wl.goff[c] = (static_cast<int64_t>(e) * H + min(n0 + wr + c * WL::RSTEP, H - 1)) * wrowb + wc * 16;
+    wl.l0 = BM * 128 + lds_off(wr, KIND == kW4 ? 2 * wc : wc);
+    wl.l1 = BM * 128 + lds_off(wr, 2 * wc + 1);
+  }
+  const uint16_t* wsc_row = nullptr;
+  if constexpr (KIND == kW4)
+    wsc_row = tid < BN ? static_cast<const uint16_t*>(w2s) +
+                             (static_cast<int64_t>(e) * H + min(n0 + tid, H - 1)) * KS
+                       : nullptr;
+  const float* sb_p = nullptr;
+  if constexpr (KIND == kFp8)
+    sb_p = static_cast<const float*>(w2s) + (static_cast<int64_t>(e) * NBH + n0 / 128) * KS;
   const int64_t arow0 = static_cast<int64_t>(mb) * BM + wm * WTM + li;
 
   v4f acc[MT][NT];
@@ -535,55 +680,70 @@ __global__ __launch_bounds__(256, 2) void moe_w2_gemm_kernel(
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  v4i ra[ACH], rb[BCH];
+  v4i ra[ACH];
 #pragma unroll
   for (int c = 0; c < ACH; ++c) ra[c] = ld16(a2 + goff_a[c]);
+  wl.load(w2, 0);
+  float wsc = 0.f;
+  if constexpr (KIND == kW4)
+    if (wsc_row) wsc = bf16_to_f32(wsc_row[0]);
 #pragma unroll
-  for (int c = 0; c < BCH; ++c) rb[c] = ld16(w2 + goff_b[c]);
-#pragma unroll
-  for (int c = 0; c < ACH; ++c) st16(&smem[0][l0 + c * RSTEP * 128], ra[c]);
-#pragma unroll
-  for (int c = 0; c < BCH; ++c) st16(&smem[0][BM * 128 + l0 + c * RSTEP * 128], rb[c]);
+  for (int c = 0; c < ACH; ++c) st16(&smem[0][la0 + c * RSTEP * 128], ra[c]);
+  wl.store(smem[0]);
+  if constexpr (KIND == kW4)
+    if (wsc_row) reinterpret_cast<float*>(smem[0] + (BM + BN) * 128)[tid] = wsc;
   float sa[MT], sb = 0.f;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) sa[mt] = 0.f;
-  if constexpr (FP8) {
+  if constexpr (KIND == kFp8) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) sa[mt] = a2s[(arow0 + mt * 16) * KC];
+    for (int mt = 0; mt < MT; ++mt) sa[mt] = a2s[(arow0 + mt * 16) * KS];
     sb = sb_p[0];
   }
   __syncthreads();
 
-  for (int kb = 0; kb < KC; ++kb) {
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < KS; ++kb) {
     const int cur = kb & 1;
-    const int kn = min(kb + 1, KC - 1);
-    const int off = kn * 128;
+    const int kn = min(kb + 1, KS - 1);
 #pragma unroll
-    for (int c = 0; c < ACH; ++c) ra[c] = ld16(a2 + goff_a[c] + off);
-#pragma unroll
-    for (int c = 0; c < BCH; ++c) rb[c] = ld16(w2 + goff_b[c] + off);
-    float san[MT], sbn = 0.f;
+    for (int c = 0; c < ACH; ++c) ra[c] = ld16(a2 + goff_a[c] + static_cast<int64_t>(kn) * KB_::kAct);
+    wl.load(w2, kn);
+    float san[MT], sbn = 0.f, wscn = 0.f;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) san[mt] = 0.f;
-    if constexpr (FP8) {
+    if constexpr (KIND == kFp8) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) san[mt] = a2s[(arow0 + mt * 16) * KC + kn];
+      for (int mt = 0; mt < MT; ++mt) san[mt] = a2s[(arow0 + mt * 16) * KS + kn];
       sbn = sb_p[kn];
     }
+    if constexpr (KIND == kW4)
+      if (wsc_row) wscn = bf16_to_f32(wsc_row[kn]);
     const uint8_t* tile = smem[cur];
     v8i xf[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) xf[mt] = lds_frag(tile, wm * WTM + mt * 16 + li, lg);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const v8i wf = lds_frag(tile + BM * 128, wn * WTN + nt * 16 + li, lg);
+      const int wrow_l = wn * WTN + nt * 16;
+      const v8i wf = lds_frag(tile + BM * 128, wrow_l + li, lg);
+      if constexpr (KIND == kFp8) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) chunk_mma<FP8>(acc[mt][nt], wf, xf[mt], sa[mt] * sb);
+        for (int mt = 0; mt < MT; ++mt) fma4(acc[mt][nt], mfma_fp8(wf, xf[mt], zero), sa[mt] * sb);
+      } else if constexpr (KIND == kW4) {
+        const v4f swv = *reinterpret_cast<const v4f*>(tile + (BM + BN) * 128 + (wrow_l + 4 * lg) * 4);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) fma4v(acc[mt][nt], mfma_fp8(wf, xf[mt], zero), swv);
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma_bf16x2(wf, xf[mt], acc[mt][nt]);
+      }
     }
 #pragma unroll
-    for (int c = 0; c < ACH; ++c) st16(&smem[cur ^ 1][l0 + c * RSTEP * 128], ra[c]);
-#pragma unroll
-    for (int c = 0; c < BCH; ++c) st16(&smem[cur ^ 1][BM * 128 + l0 + c * RSTEP * 128], rb[c]);
+    for (int c = 0; c < ACH; ++c) st16(&smem[cur ^ 1][la0 + c * RSTEP * 128], ra[c]);
+    wl.store(smem[cur ^ 1]);
+    if constexpr (KIND == kW4)
+      if (wsc_row) reinterpret_cast<float*>(smem[cur ^ 1] + (BM + BN) * 128)[tid] = wscn;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) sa[mt] = san[mt];
     sb = sbn;
@@ -594,7 +754,9 @@ __global__ __launch_bounds__(256, 2) void moe_w2_gemm_kernel(
   for (int mt = 0; mt < MT; ++mt) {
     const int r = sorted[arow0 + mt * 16];
     if (r >= numel) continue;
-    const float rw = route_w ? route_w[r] : 1.0f;
+    float rw = 1.0f;
+    if constexpr (KIND == kW4) rw = a2s[arow0 + mt * 16];
+    else rw = route_w ? route_w[r] : 1.0f;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int n = n0 + wn * WTN + nt * 16 + 4 * lg;
@@ -608,44 +770,47 @@ __global__ __launch_bounds__(256, 2) void moe_w2_gemm_kernel(
 
 // ------------------------------------------------------------ host side ---
 // Split-K factor of the decode GEMVs: enough waves to cover the chip
-// (>= 4096 over the active experts' n-tiles), at least 4 chunks per split.
-static int moe_splits(int64_t waves_per_split, int KC) {
+// (>= 4096 over the active experts' n-tiles), at least 4 K steps per split.
+static int moe_splits(int64_t waves_per_split, int KS) {
   int s = static_cast<int>((4096 + waves_per_split - 1) / waves_per_split);
-  return max(1, min(s, max(1, KC / 4)));
+  return max(1, min(s, max(1, KS / 4)));
 }
 
 static int64_t moe_umax(int64_t numel, int E) { return std::min<int64_t>(E, numel); }
 
-// eb = operand bytes per element (1 fp8, 2 bf16).
-static int w13_splits(int64_t numel, int E, int64_t H, int64_t I, int eb) {
-  return moe_splits(moe_umax(numel, E) * (2 * I / 16), static_cast<int>(H * eb / 128));
+static int ksteps(int64_t K, int kind) { return static_cast<int>(K / (kind == kBf16 ? 64 : 128)); }
+
+static int w13_splits(int64_t numel, int E, int64_t H, int64_t I, int kind) {
+  return moe_splits(moe_umax(numel, E) * (2 * I / 16), ksteps(H, kind));
 }
-static int w2_splits(int64_t numel, int E, int64_t H, int64_t I, int eb) {
-  return moe_splits(moe_umax(numel, E) * (H / 16), static_cast<int>(I * eb / 128));
+static int w2_splits(int64_t numel, int E, int64_t H, int64_t I, int kind) {
+  return moe_splits(moe_umax(numel, E) * (H / 16), ksteps(I, kind));
 }
 
 static size_t al256(size_t x) { return (x + 255) / 256 * 256; }
 
 // Stage scratch: fp32 split-K partials of the decode GEMVs (none for GEMMs).
-static size_t w13_scratch(int64_t numel, int E, int64_t H, int64_t I, int block_m, int eb) {
+static size_t w13_scratch(int64_t numel, int E, int64_t H, int64_t I, int block_m, int kind) {
   if (block_m != kGemvBlock) return 0;
-  return al256(static_cast<size_t>(w13_splits(numel, E, H, I, eb)) * numel * 2 * I * 4);
+  return al256(static_cast<size_t>(w13_splits(numel, E, H, I, kind)) * numel * 2 * I * 4);
 }
-static size_t w2_scratch(int64_t numel, int E, int64_t H, int64_t I, int block_m, int eb) {
+static size_t w2_scratch(int64_t numel, int E, int64_t H, int64_t I, int block_m, int kind) {
   if (block_m != kGemvBlock) return 0;
-  const int s = w2_splits(numel, E, H, I, eb);
+  const int s = w2_splits(numel, E, H, I, kind);
   return s > 1 ? al256(static_cast<size_t>(s) * numel * H * 4) : 0;
 }
-static size_t stage_scratch(int64_t numel, int E, int64_t H, int64_t I, int block_m, int eb) {
-  return std::max(w13_scratch(numel, E, H, I, block_m, eb), w2_scratch(numel, E, H, I, block_m, eb));
+static size_t stage_scratch(int64_t numel, int E, int64_t H, int64_t I, int block_m, int kind) {
+  return std::max(w13_scratch(numel, E, H, I, block_m, kind),
+                  w2_scratch(numel, E, H, I, block_m, kind));
 }
 
-template <bool FP8>
+template <int KIND>
 static int raise_w13_lds() {
   static bool done = false;
   if (done) return VMAMD_OK;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_w13_gemm_kernel<FP8>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kW13Lds) != hipSuccess) {
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_w13_gemm_kernel<KIND>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          2 * w13_stage_bytes<KIND>()) != hipSuccess) {
     set_error("moe w13: cannot raise the LDS limit of the W13 kernel");
     return VMAMD_ERR_HIP;
   }
@@ -653,96 +818,97 @@ static int raise_w13_lds() {
   return VMAMD_OK;
 }
 
-// Launches of the two stages; arguments are validated by the callers.  For
-// bf16 `xa` is x itself and xs / w13_s / a2s are unused.
-template <bool FP8>
+// Launches of the two stages; arguments are validated by the callers.  kBf16:
+// xa is x itself, xs / w13_s / a2s unused.  kW4: xs are the token row scales,
+// a2 receives the bf16 activation (quantised per row by the caller).
+template <int KIND>
 static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk,
                       const int32_t* sorted, int64_t cap, int block_m, const int32_t* offs,
                       const int32_t* ntpp, const int32_t* active, const int32_t* nact,
-                      const uint8_t* w13, const float* w13_s, int E, int I, float limit,
+                      const uint8_t* w13, const void* w13_s, int E, int I, float limit,
                       uint8_t* a2, float* a2s, float* scratch, hipStream_t st) {
-  constexpr int EB = FP8 ? 1 : 2;
   const int numel = T * topk;
   if (block_m == kGemvBlock) {
-    const int s13 = w13_splits(numel, E, H, I, EB);
+    const int s13 = w13_splits(numel, E, H, I, KIND);
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s13);
-    moe_gemv_kernel<4, FP8><<<g13, kMoeGemvWaves * kWave, 0, st>>>(
+    moe_gemv_kernel<4, KIND><<<g13, kMoeGemvWaves * kWave, 0, st>>>(
         xa, xs, topk, H, sorted, offs, active, nact, w13, w13_s, 2 * I, numel, s13, scratch,
         nullptr, nullptr);
     int rc = check_launch("moe w13 (gemv)");
     if (rc) return rc;
-    if constexpr (FP8) {
+    if constexpr (KIND == kFp8) {
       const int64_t groups = static_cast<int64_t>(numel) * (I / 128);
       moe_act_quant_kernel<<<static_cast<int>((groups + 15) / 16), 256, 0, st>>>(
           scratch, s13, numel, I, limit, a2, a2s);
     } else {
       const int64_t chunks = static_cast<int64_t>(numel) * (I / 8);
-      moe_act_bf16_kernel<<<static_cast<int>((chunks + 255) / 256), 256, 0, st>>>(
-          scratch, s13, numel, I, limit, reinterpret_cast<uint16_t*>(a2));
+      moe_act_bf16_kernel<KIND><<<static_cast<int>((chunks + 255) / 256), 256, 0, st>>>(
+          scratch, s13, numel, I, limit, xs, topk, reinterpret_cast<uint16_t*>(a2));
     }
     return check_launch("moe w13 (activation)");
   }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
   const int tiles = max_blocks * (I / 128);
-  int rc = raise_w13_lds<FP8>();
+  int rc = raise_w13_lds<KIND>();
   if (rc) return rc;
-  moe_w13_gemm_kernel<FP8><<<xcd_grid(tiles), kW13Threads, kW13Lds, st>>>(
+  moe_w13_gemm_kernel<KIND><<<xcd_grid(tiles), kW13Threads, 2 * w13_stage_bytes<KIND>(), st>>>(
       xa, xs, topk, H, sorted, offs, ntpp, E, numel, tiles, w13, w13_s, I, limit, a2, a2s);
   return check_launch("moe w13 (gemm)");
 }
 
-template <bool FP8>
+// kW4: a2s are the a2 row scales and take the routed weight's place in y.
+template <int KIND>
 static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const int32_t* sorted,
                      int64_t cap, int block_m, const int32_t* offs, const int32_t* ntpp,
-                     const int32_t* active, const int32_t* nact, const uint8_t* w2, const float* w2_s,
+                     const int32_t* active, const int32_t* nact, const uint8_t* w2, const void* w2_s,
                      int E, int H, int I, const float* topk_weights, const int32_t* topk_ids,
                      const int32_t* emap, int64_t emap_len, uint16_t* y, float* scratch,
                      hipStream_t st) {
-  constexpr int EB = FP8 ? 1 : 2;
   const int numel = T * topk;
+  const float* yscale = KIND == kW4 ? a2s : topk_weights;
   if (block_m == kGemvBlock) {
-    const int s2 = w2_splits(numel, E, H, I, EB);
+    const int s2 = w2_splits(numel, E, H, I, KIND);
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g2((H / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s2);
     if (s2 == 1) {
-      moe_gemv_kernel<4, FP8><<<g2, kMoeGemvWaves * kWave, 0, st>>>(
-          a2, a2s, 1, I, sorted, offs, active, nact, w2, w2_s, H, numel, 1, nullptr, topk_weights, y);
+      moe_gemv_kernel<4, KIND><<<g2, kMoeGemvWaves * kWave, 0, st>>>(
+          a2, a2s, 1, I, sorted, offs, active, nact, w2, w2_s, H, numel, 1, nullptr, yscale, y);
       return check_launch("moe w2 (gemv)");
     }
-    moe_gemv_kernel<4, FP8><<<g2, kMoeGemvWaves * kWave, 0, st>>>(
+    moe_gemv_kernel<4, KIND><<<g2, kMoeGemvWaves * kWave, 0, st>>>(
         a2, a2s, 1, I, sorted, offs, active, nact, w2, w2_s, H, numel, s2, scratch, nullptr, nullptr);
     int rc = check_launch("moe w2 (gemv)");
     if (rc) return rc;
     const int64_t mn = static_cast<int64_t>(numel) * H;
     moe_w2_reduce_kernel<<<static_cast<int>((mn / 4 + 255) / 256), 256, 0, st>>>(
-        scratch, s2, numel, H, topk_ids, emap, emap_len, topk_weights, y);
+        scratch, s2, numel, H, topk_ids, emap, emap_len, yscale, y);
     return check_launch("moe w2 (reduce)");
   }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
   const int tiles = max_blocks * ((H + 127) / 128);
-  moe_w2_gemm_kernel<FP8><<<xcd_grid(tiles), 256, 0, st>>>(a2, a2s, I, sorted, offs, ntpp, E, numel,
-                                                           tiles, w2, w2_s, H, topk_weights, y);
+  moe_w2_gemm_kernel<KIND><<<xcd_grid(tiles), 256, 0, st>>>(a2, a2s, I, sorted, offs, ntpp, E, numel,
+                                                            tiles, w2, w2_s, H, topk_weights, y);
   return check_launch("moe w2 (gemm)");
 }
 
 // Workspace carve-up of a fused layer, shared by the size query and the
 // launcher.  The two stages run one after the other on one stream, so their
-// scratch shares one region.  fp8 adds the quantised x and a2 scales.
+// scratch shares one region.  kFp8 / kW4 add the quantised x and scales; kW4
+// also keeps the bf16 activation before its row quantiser.
 struct MoeWs {
-  size_t xq, xs, sorted, eids, ntpp, offs, active, nact, a2, a2s, y, scratch, total;
+  size_t xq, xs, sorted, eids, ntpp, offs, active, nact, abf, a2, a2s, y, scratch, total;
 };
 
-static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm, bool fp8) {
+static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm, int kind) {
   MoeWs w{};
-  const int eb = fp8 ? 1 : 2;
   const int64_t numel = T * topk;
   const int64_t cap = numel + static_cast<int64_t>(E) * (bm - 1);
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o += al256(bytes); return at; };
-  if (fp8) {
+  if (kind != kBf16) {
     w.xq = take(T * H);
-    w.xs = take(T * (H / 128) * 4);
+    w.xs = take(kind == kFp8 ? T * (H / 128) * 4 : T * 4);
   }
   w.sorted = take(cap * 4);
   w.eids = take(((cap + bm - 1) / bm) * 4);
@@ -751,10 +917,12 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   w.active = take(E * 4);
   w.nact = take(4);
   const int64_t arows = bm == kGemvBlock ? numel : cap;  // route order (decode) or padded order
-  w.a2 = take(arows * I * eb);
-  if (fp8) w.a2s = take(arows * (I / 128) * 4);
+  if (kind == kW4) w.abf = take(arows * I * 2);
+  w.a2 = take(arows * I * (kind == kBf16 ? 2 : 1));
+  if (kind == kFp8) w.a2s = take(arows * (I / 128) * 4);
+  if (kind == kW4) w.a2s = take(arows * 4);
   w.y = take(numel * H * 2);
-  w.scratch = take(stage_scratch(numel, E, H, I, bm, eb));
+  w.scratch = take(stage_scratch(numel, E, H, I, bm, kind));
   w.total = o;
   return w;
 }
@@ -783,9 +951,9 @@ static int check_stage_common(const char* who, int64_t T, int topk, int E, int64
   return VMAMD_OK;
 }
 
-template <bool FP8>
+template <int KIND>
 static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, const void* w13,
-                       const float* w13_s, const void* w2, const float* w2_s, int E, int64_t I,
+                       const void* w13_s, const void* w2, const void* w2_s, int E, int64_t I,
                        const float* topk_weights, const int32_t* topk_ids, int topk,
                        const int32_t* expert_map, int64_t expert_map_len, float swiglu_limit,
                        int path, void* out, void* workspace, size_t workspace_bytes,
@@ -796,10 +964,13 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   const int64_t cap = T * topk + static_cast<int64_t>(E) * (bm - 1);
   int rc = check_stage_common(who, T, topk, E, H, I, bm, cap);
   if (rc) return rc;
+  VMAMD_REQUIRE(KIND != kW4 || (H <= 16384 && I <= 16384),
+                "%s: per-row quantisation supports rows of up to 16384", who);
   if (T == 0) return VMAMD_OK;
-  VMAMD_REQUIRE(x && w13 && w2 && topk_weights && topk_ids && out && (!FP8 || (w13_s && w2_s)),
+  VMAMD_REQUIRE(x && w13 && w2 && topk_weights && topk_ids && out &&
+                    (KIND == kBf16 || (w13_s && w2_s)),
                 "%s: null pointer", who);
-  const MoeWs L = moe_layout(T, topk, E, H, I, bm, FP8);
+  const MoeWs L = moe_layout(T, topk, E, H, I, bm, KIND);
   VMAMD_REQUIRE(workspace && workspace_bytes >= L.total, "%s: workspace of %zu bytes required (got %zu)",
                 who, L.total, workspace_bytes);
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0 &&
@@ -813,7 +984,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   int32_t* active = reinterpret_cast<int32_t*>(ws + L.active);
   int32_t* nact = reinterpret_cast<int32_t*>(ws + L.nact);
   uint8_t* a2 = ws + L.a2;
-  float* a2s = FP8 ? reinterpret_cast<float*>(ws + L.a2s) : nullptr;
+  float* a2s = KIND == kBf16 ? nullptr : reinterpret_cast<float*>(ws + L.a2s);
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
   float* scratch = reinterpret_cast<float*>(ws + L.scratch);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -822,11 +993,14 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
 
   const uint8_t* xa = static_cast<const uint8_t*>(x);
   const float* xs = nullptr;
-  if constexpr (FP8) {
+  if constexpr (KIND != kBf16) {
     uint8_t* xq = ws + L.xq;
     float* xsw = reinterpret_cast<float*>(ws + L.xs);
-    rc = vmamd_per_token_group_quant_fp8(x, kBF16, T, H, H, 128, 1e-10f, -448.f, 448.f, xq, xsw,
-                                         H / 128, 1, stream);
+    if constexpr (KIND == kFp8)
+      rc = vmamd_per_token_group_quant_fp8(x, kBF16, T, H, H, 128, 1e-10f, -448.f, 448.f, xq, xsw,
+                                           H / 128, 1, stream);
+    else
+      rc = vmamd_per_token_quant_fp8(x, T, H, H, 1e-4f, -448.f, 448.f, xq, xsw, stream);
     if (rc) return rc;
     xa = xq;
     xs = xsw;
@@ -834,70 +1008,81 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   rc = vmamd_moe_align_block_size(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
                                   eids, ntpp, offs, nullptr, active, nact, stream);
   if (rc) return rc;
-  rc = launch_w13<FP8>(xa, xs, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
-                       static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, a2, a2s, scratch,
-                       st);
+  uint8_t* act_out = KIND == kW4 ? ws + L.abf : a2;  // kW4: bf16 activation, quantised below
+  rc = launch_w13<KIND>(xa, xs, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
+                        static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, act_out, a2s,
+                        scratch, st);
   if (rc) return rc;
-  rc = launch_w2<FP8>(a2, a2s, t, topk, sorted, cap, bm, offs, ntpp, active, nact,
-                      static_cast<const uint8_t*>(w2), w2_s, E, h, i, topk_weights, topk_ids,
-                      expert_map, expert_map_len, y, scratch, st);
+  if constexpr (KIND == kW4) {
+    const int64_t arows = bm == kGemvBlock ? numel : cap;
+    rc = vmamd_per_token_quant_fp8(act_out, arows, I, I, 1e-4f, -448.f, 448.f, a2, a2s, stream);
+    if (rc) return rc;
+  }
+  rc = launch_w2<KIND>(a2, a2s, t, topk, sorted, cap, bm, offs, ntpp, active, nact,
+                       static_cast<const uint8_t*>(w2), w2_s, E, h, i, topk_weights, topk_ids,
+                       expert_map, expert_map_len, y, scratch, st);
   if (rc) return rc;
   // Slots of dropped routes (negative ids, or non-local experts) hold no
   // expert output and are skipped by the combine.
+  if constexpr (KIND == kW4)
+    return vmamd_moe_weighted_sum(y, kBF16, T, topk, H, topk_weights, topk_ids, expert_map,
+                                  expert_map_len, out, stream);
   return vmamd_moe_sum(y, kBF16, T, topk, H, topk_ids, expert_map, expert_map_len, out, stream);
 }
 
-template <bool FP8>
+template <int KIND>
 static int stage_w13(const char* who, const void* xa, const float* xs, int64_t T, int64_t H, int topk,
                      const int32_t* sorted, int64_t capacity, int block_m, const int32_t* offs,
                      const int32_t* ntpp, const int32_t* active, const int32_t* nact,
-                     const void* w13, const float* w13_s, int E, int64_t I, float limit, void* a2,
+                     const void* w13, const void* w13_s, int E, int64_t I, float limit, void* a2,
                      float* a2s, void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
   int rc = check_stage_common(who, T, topk, E, H, I, block_m, capacity);
   if (rc) return rc;
   if (T == 0) return VMAMD_OK;
-  VMAMD_REQUIRE(xa && sorted && offs && ntpp && w13 && a2 && (!FP8 || (xs && w13_s && a2s)),
+  VMAMD_REQUIRE(xa && sorted && offs && ntpp && w13 && a2 &&
+                    (KIND == kBf16 || (xs && w13_s)) && (KIND != kFp8 || a2s),
                 "%s: null pointer", who);
   VMAMD_REQUIRE(block_m == kMoeBM || (active && nact),
                 "%s: the decode path (block_m 16) needs active_experts / num_active", who);
-  const size_t need = w13_scratch(T * topk, E, H, I, block_m, FP8 ? 1 : 2);
+  const size_t need = w13_scratch(T * topk, E, H, I, block_m, KIND);
   VMAMD_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
                 "%s: workspace of %zu bytes required (got %zu)", who, need, workspace_bytes);
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(xa) % 16 == 0 && reinterpret_cast<uintptr_t>(a2) % 16 == 0,
                 "%s: activations, a2 and workspace must be 16-byte aligned", who);
-  return launch_w13<FP8>(static_cast<const uint8_t*>(xa), xs, static_cast<int>(T), static_cast<int>(H),
-                         topk, sorted, capacity, block_m, offs, ntpp, active, nact,
-                         static_cast<const uint8_t*>(w13), w13_s, E, static_cast<int>(I), limit,
-                         static_cast<uint8_t*>(a2), a2s, static_cast<float*>(workspace),
-                         reinterpret_cast<hipStream_t>(stream));
+  return launch_w13<KIND>(static_cast<const uint8_t*>(xa), xs, static_cast<int>(T), static_cast<int>(H),
+                          topk, sorted, capacity, block_m, offs, ntpp, active, nact,
+                          static_cast<const uint8_t*>(w13), w13_s, E, static_cast<int>(I), limit,
+                          static_cast<uint8_t*>(a2), a2s, static_cast<float*>(workspace),
+                          reinterpret_cast<hipStream_t>(stream));
 }
 
-template <bool FP8>
+template <int KIND>
 static int stage_w2(const char* who, const void* a2, const float* a2s, int64_t T, int topk,
                     const int32_t* sorted, int64_t capacity, int block_m, const int32_t* offs,
                     const int32_t* ntpp, const int32_t* active, const int32_t* nact, const void* w2,
-                    const float* w2_s, int E, int64_t H, int64_t I, const float* topk_weights,
+                    const void* w2_s, int E, int64_t H, int64_t I, const float* topk_weights,
                     const int32_t* topk_ids, const int32_t* emap, int64_t emap_len, void* y,
                     void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
   int rc = check_stage_common(who, T, topk, E, H, I, block_m, capacity);
   if (rc) return rc;
   if (T == 0) return VMAMD_OK;
-  VMAMD_REQUIRE(a2 && sorted && offs && ntpp && w2 && topk_ids && y && (!FP8 || (a2s && w2_s)),
+  VMAMD_REQUIRE(a2 && sorted && offs && ntpp && w2 && topk_ids && y &&
+                    (KIND == kBf16 || (a2s && w2_s)) && (KIND == kW4 || topk_weights),
                 "%s: null pointer", who);
   VMAMD_REQUIRE(block_m == kMoeBM || (active && nact),
                 "%s: the decode path (block_m 16) needs active_experts / num_active", who);
-  const size_t need = w2_scratch(T * topk, E, H, I, block_m, FP8 ? 1 : 2);
+  const size_t need = w2_scratch(T * topk, E, H, I, block_m, KIND);
   VMAMD_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
                 "%s: workspace of %zu bytes required (got %zu)", who, need, workspace_bytes);
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(a2) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0,
                 "%s: a2 and workspace must be 16-byte and y 8-byte aligned", who);
-  return launch_w2<FP8>(static_cast<const uint8_t*>(a2), a2s, static_cast<int>(T), topk, sorted,
-                        capacity, block_m, offs, ntpp, active, nact, static_cast<const uint8_t*>(w2),
-                        w2_s, E, static_cast<int>(H), static_cast<int>(I), topk_weights, topk_ids,
-                        emap, emap_len, static_cast<uint16_t*>(y), static_cast<float*>(workspace),
-                        reinterpret_cast<hipStream_t>(stream));
+  return launch_w2<KIND>(static_cast<const uint8_t*>(a2), a2s, static_cast<int>(T), topk, sorted,
+                         capacity, block_m, offs, ntpp, active, nact, static_cast<const uint8_t*>(w2),
+                         w2_s, E, static_cast<int>(H), static_cast<int>(I), topk_weights, topk_ids,
+                         emap, emap_len, static_cast<uint16_t*>(y), static_cast<float*>(workspace),
+                         reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // namespace vmamd
@@ -907,7 +1092,7 @@ using namespace vmamd;
 // ------------------------------------------------------------------ fp8 ---
 extern "C" size_t vmamd_moe_fp8_stage_workspace_size(int64_t T, int topk, int num_experts,
                                                      int64_t H, int64_t I, int block_m) {
-  return stage_scratch(T * topk, num_experts, H, I, block_m, 1);
+  return stage_scratch(T * topk, num_experts, H, I, block_m, kFp8);
 }
 
 extern "C" int vmamd_moe_fp8_w13(const void* xq, const float* xs, int64_t T, int64_t H, int topk,
@@ -917,7 +1102,7 @@ extern "C" int vmamd_moe_fp8_w13(const void* xq, const float* xs, int64_t T, int
                                  const void* w13, const float* w13_s, int num_experts, int64_t I,
                                  float swiglu_limit, void* a2q, float* a2s, void* workspace,
                                  size_t workspace_bytes, vmamd_stream_t stream) {
-  return stage_w13<true>("moe_fp8_w13", xq, xs, T, H, topk, sorted_token_ids, capacity, block_m,
+  return stage_w13<kFp8>("moe_fp8_w13", xq, xs, T, H, topk, sorted_token_ids, capacity, block_m,
                          expert_offsets, num_tokens_post_pad, active_experts, num_active, w13, w13_s,
                          num_experts, I, swiglu_limit, a2q, a2s, workspace, workspace_bytes, stream);
 }
@@ -930,7 +1115,7 @@ extern "C" int vmamd_moe_fp8_w2(const void* a2q, const float* a2s, int64_t T, in
                                 int64_t I, const float* topk_weights, const int32_t* topk_ids,
                                 const int32_t* expert_map, int64_t expert_map_len, void* y,
                                 void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
-  return stage_w2<true>("moe_fp8_w2", a2q, a2s, T, topk, sorted_token_ids, capacity, block_m,
+  return stage_w2<kFp8>("moe_fp8_w2", a2q, a2s, T, topk, sorted_token_ids, capacity, block_m,
                         expert_offsets, num_tokens_post_pad, active_experts, num_active, w2, w2_s,
                         num_experts, H, I, topk_weights, topk_ids, expert_map, expert_map_len, y,
                         workspace, workspace_bytes, stream);
@@ -938,7 +1123,7 @@ extern "C" int vmamd_moe_fp8_w2(const void* a2q, const float* a2s, int64_t T, in
 
 extern "C" size_t vmamd_fused_moe_fp8_workspace_size(int64_t T, int topk, int num_experts,
                                                      int64_t H, int64_t I, int path) {
-  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path), true).total;
+  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path), kFp8).total;
 }
 
 extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H,
@@ -949,7 +1134,7 @@ extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_
                                    float swiglu_limit, int path, void* out, void* workspace,
                                    size_t workspace_bytes, vmamd_stream_t stream) {
   VMAMD_REQUIRE(x_dtype == kBF16, "fused_moe_fp8: hidden states must be bf16");
-  return fused_layer<true>("fused_moe_fp8", x, T, H, w13, w13_s, w2, w2_s, num_experts, I,
+  return fused_layer<kFp8>("fused_moe_fp8", x, T, H, w13, w13_s, w2, w2_s, num_experts, I,
                            topk_weights, topk_ids, topk, expert_map, expert_map_len, swiglu_limit,
                            path, out, workspace, workspace_bytes, stream);
 }
@@ -957,7 +1142,7 @@ extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_
 // ----------------------------------------------------------------- bf16 ---
 extern "C" size_t vmamd_moe_bf16_stage_workspace_size(int64_t T, int topk, int num_experts,
                                                       int64_t H, int64_t I, int block_m) {
-  return stage_scratch(T * topk, num_experts, H, I, block_m, 2);
+  return stage_scratch(T * topk, num_experts, H, I, block_m, kBf16);
 }
 
 extern "C" int vmamd_moe_bf16_w13(const void* x, int64_t T, int64_t H, int topk,
@@ -967,7 +1152,7 @@ extern "C" int vmamd_moe_bf16_w13(const void* x, int64_t T, int64_t H, int topk,
                                   const void* w13, int num_experts, int64_t I, float swiglu_limit,
                                   void* a2, void* workspace, size_t workspace_bytes,
                                   vmamd_stream_t stream) {
-  return stage_w13<false>("moe_bf16_w13", x, nullptr, T, H, topk, sorted_token_ids, capacity,
+  return stage_w13<kBf16>("moe_bf16_w13", x, nullptr, T, H, topk, sorted_token_ids, capacity,
                           block_m, expert_offsets, num_tokens_post_pad, active_experts, num_active,
                           w13, nullptr, num_experts, I, swiglu_limit, a2, nullptr, workspace,
                           workspace_bytes, stream);
@@ -981,7 +1166,7 @@ extern "C" int vmamd_moe_bf16_w2(const void* a2, int64_t T, int topk,
                                  const float* topk_weights, const int32_t* topk_ids,
                                  const int32_t* expert_map, int64_t expert_map_len, void* y,
                                  void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
-  return stage_w2<false>("moe_bf16_w2", a2, nullptr, T, topk, sorted_token_ids, capacity, block_m,
+  return stage_w2<kBf16>("moe_bf16_w2", a2, nullptr, T, topk, sorted_token_ids, capacity, block_m,
                          expert_offsets, num_tokens_post_pad, active_experts, num_active, w2, nullptr,
                          num_experts, H, I, topk_weights, topk_ids, expert_map, expert_map_len, y,
                          workspace, workspace_bytes, stream);
@@ -989,7 +1174,7 @@ extern "C" int vmamd_moe_bf16_w2(const void* a2, int64_t T, int topk,
 
 extern "C" size_t vmamd_fused_moe_bf16_workspace_size(int64_t T, int topk, int num_experts,
                                                       int64_t H, int64_t I, int path) {
-  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path), false).total;
+  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path), kBf16).total;
 }
 
 extern "C" int vmamd_fused_moe_bf16(const void* x, int64_t T, int64_t H, const void* w13,
@@ -998,7 +1183,24 @@ extern "C" int vmamd_fused_moe_bf16(const void* x, int64_t T, int64_t H, const v
                                     const int32_t* expert_map, int64_t expert_map_len,
                                     float swiglu_limit, int path, void* out, void* workspace,
                                     size_t workspace_bytes, vmamd_stream_t stream) {
-  return fused_layer<false>("fused_moe_bf16", x, T, H, w13, nullptr, w2, nullptr, num_experts, I,
+  return fused_layer<kBf16>("fused_moe_bf16", x, T, H, w13, nullptr, w2, nullptr, num_experts, I,
                             topk_weights, topk_ids, topk, expert_map, expert_map_len, swiglu_limit,
                             path, out, workspace, workspace_bytes, stream);
+}
+
+// --------------------------------------------------------------- w4afp8 ---
+extern "C" size_t vmamd_w4afp8_moe_workspace_size(int64_t T, int topk, int num_experts, int64_t H,
+                                                  int64_t I, int path) {
+  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path), kW4).total;
+}
+
+extern "C" int vmamd_w4afp8_moe(const void* x, int64_t T, int64_t H, const void* w13,
+                                const void* w13_s, const void* w2, const void* w2_s,
+                                int num_experts, int64_t I, const float* topk_weights,
+                                const int32_t* topk_ids, int topk, const int32_t* expert_map,
+                                int64_t expert_map_len, float swiglu_limit, int path, void* out,
+                                void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
+  return fused_layer<kW4>("w4afp8_moe", x, T, H, w13, w13_s, w2, w2_s, num_experts, I, topk_weights,
+                          topk_ids, topk, expert_map, expert_map_len, swiglu_limit, path, out,
+                          workspace, workspace_bytes, stream);
 }

@@ -1,5 +1,7 @@
-// Top-k combine: out[t, h] = round(sum_k x[t, k, h]), fp32 accumulation in
-// slot order k = 0, 1, ..., one rounding to the output dtype.  With topk_ids
+// Top-k combine: out[t, h] = round(sum_k x[t, k, h] (* w[t, k])), fp32
+// accumulation in slot order k = 0, 1, ..., one rounding to the output dtype;
+// the routed weights w are applied here only when given (otherwise the expert
+// outputs already carry them).  With topk_ids
 // given, slots whose expert id is negative, or maps to a negative local id
 // through expert_map, are skipped (their rows hold no expert output).
 //
@@ -23,7 +25,8 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const typename Elem<DT>::T
                                                       int64_t tokens, int topk, int64_t hidden,
                                                       typename Elem<DT>::T* __restrict__ out,
                                                       const int32_t* __restrict__ ids,
-                                                      const int32_t* __restrict__ map, int64_t map_len) {
+                                                      const int32_t* __restrict__ map, int64_t map_len,
+                                                      const float* __restrict__ wts) {
   using E = Elem<DT>;
   using T = typename E::T;
   const int64_t chunks = hidden / 8;
@@ -39,11 +42,18 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const typename Elem<DT>::T
       if constexpr (VEC && sizeof(T) == 2) {
         const uint4 raw = *reinterpret_cast<const uint4*>(src);
         const uint16_t* p = reinterpret_cast<const uint16_t*>(&raw);
+        if (wts) {
+          const float wk = wts[t * topk + k];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] += E::to_f(p[j]);
+          for (int j = 0; j < 8; ++j) acc[j] += E::to_f(p[j]) * wk;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[j] += E::to_f(p[j]);
+        }
       } else {
+        const float wk = wts ? wts[t * topk + k] : 1.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] += E::to_f(src[j]);
+        for (int j = 0; j < 8; ++j) acc[j] += wts ? E::to_f(src[j]) * wk : E::to_f(src[j]);
       }
     }
     T* dst = out + t * hidden + h;
@@ -67,7 +77,8 @@ __global__ __launch_bounds__(256) void moe_sum_scalar_kernel(const typename Elem
                                                              typename Elem<DT>::T* __restrict__ out,
                                                              const int32_t* __restrict__ ids,
                                                              const int32_t* __restrict__ map,
-                                                             int64_t map_len) {
+                                                             int64_t map_len,
+                                                             const float* __restrict__ wts) {
   using E = Elem<DT>;
   const int64_t total = tokens * hidden;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
@@ -75,7 +86,10 @@ __global__ __launch_bounds__(256) void moe_sum_scalar_kernel(const typename Elem
     const int64_t t = i / hidden, h = i - t * hidden;
     float acc = 0.f;
     for (int k = 0; k < topk; ++k)
-      if (slot_live(ids, map, map_len, t * topk + k)) acc += E::to_f(x[(t * topk + k) * hidden + h]);
+      if (slot_live(ids, map, map_len, t * topk + k)) {
+        const float v = E::to_f(x[(t * topk + k) * hidden + h]);
+        acc += wts ? v * wts[t * topk + k] : v;
+      }
     out[i] = E::from_f(acc);
   }
 }
@@ -84,36 +98,55 @@ __global__ __launch_bounds__(256) void moe_sum_scalar_kernel(const typename Elem
 
 using namespace vmamd;
 
-extern "C" int vmamd_moe_sum(const void* x, int dtype, int64_t tokens, int topk, int64_t hidden,
-                             const int32_t* topk_ids, const int32_t* expert_map,
-                             int64_t expert_map_len, void* out, vmamd_stream_t stream) {
-  VMAMD_REQUIRE(tokens >= 0 && topk > 0 && hidden >= 0, "moe_sum: bad sizes");
-  VMAMD_REQUIRE(!expert_map || topk_ids, "moe_sum: expert_map needs topk_ids");
+static int moe_sum_impl(const char* who, const void* x, int dtype, int64_t tokens, int topk,
+                        int64_t hidden, const int32_t* topk_ids, const int32_t* expert_map,
+                        int64_t expert_map_len, const float* wts, void* out, vmamd_stream_t stream) {
+  VMAMD_REQUIRE(tokens >= 0 && topk > 0 && hidden >= 0, "%s: bad sizes", who);
+  VMAMD_REQUIRE(!expert_map || topk_ids, "%s: expert_map needs topk_ids", who);
   if (tokens * hidden == 0) return VMAMD_OK;
-  VMAMD_REQUIRE(x && out, "moe_sum: null pointer");
+  VMAMD_REQUIRE(x && out, "%s: null pointer", who);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int esize = dtype == kF32 ? 4 : 2;
   const bool vec = hidden % 8 == 0 && esize == 2 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(out) % 16 == 0;
   const int64_t work = hidden % 8 == 0 ? tokens * (hidden / 8) : tokens * hidden;
   const int blocks = static_cast<int>(work / 256 + 1 < 65536 ? work / 256 + 1 : 65536);
-#define VMAMD_SUM(DT, TY)                                                                          \
-  do {                                                                                             \
-    const TY* xi = static_cast<const TY*>(x);                                                      \
-    TY* oi = static_cast<TY*>(out);                                                                \
-    if (hidden % 8 != 0)                                                                           \
-      moe_sum_scalar_kernel<DT><<<blocks, 256, 0, st>>>(xi, tokens, topk, hidden, oi, topk_ids, expert_map, expert_map_len);             \
-    else if (vec)                                                                                  \
-      moe_sum_kernel<DT, true><<<blocks, 256, 0, st>>>(xi, tokens, topk, hidden, oi, topk_ids, expert_map, expert_map_len);              \
-    else                                                                                           \
-      moe_sum_kernel<DT, false><<<blocks, 256, 0, st>>>(xi, tokens, topk, hidden, oi, topk_ids, expert_map, expert_map_len);             \
+#define VMAMD_SUM(DT, TY)                                                                       \
+  do {                                                                                          \
+    const TY* xi = static_cast<const TY*>(x);                                                   \
+    TY* oi = static_cast<TY*>(out);                                                             \
+    if (hidden % 8 != 0)                                                                        \
+      moe_sum_scalar_kernel<DT><<<blocks, 256, 0, st>>>(xi, tokens, topk, hidden, oi, topk_ids, \
+                                                        expert_map, expert_map_len, wts);       \
+    else if (vec)                                                                               \
+      moe_sum_kernel<DT, true><<<blocks, 256, 0, st>>>(xi, tokens, topk, hidden, oi, topk_ids,  \
+                                                       expert_map, expert_map_len, wts);        \
+    else                                                                                        \
+      moe_sum_kernel<DT, false><<<blocks, 256, 0, st>>>(xi, tokens, topk, hidden, oi, topk_ids, \
+                                                        expert_map, expert_map_len, wts);       \
   } while (0)
   switch (dtype) {
     case kBF16: VMAMD_SUM(kBF16, uint16_t); break;
     case kF16: VMAMD_SUM(kF16, uint16_t); break;
     case kF32: VMAMD_SUM(kF32, float); break;
-    default: VMAMD_REQUIRE(false, "moe_sum: unsupported dtype %d", dtype);
+    default: VMAMD_REQUIRE(false, "%s: unsupported dtype %d", who, dtype);
   }
 #undef VMAMD_SUM
-  return check_launch("moe_sum");
+  return check_launch(who);
+}
+
+extern "C" int vmamd_moe_sum(const void* x, int dtype, int64_t tokens, int topk, int64_t hidden,
+                             const int32_t* topk_ids, const int32_t* expert_map,
+                             int64_t expert_map_len, void* out, vmamd_stream_t stream) {
+  return moe_sum_impl("moe_sum", x, dtype, tokens, topk, hidden, topk_ids, expert_map,
+                      expert_map_len, nullptr, out, stream);
+}
+
+extern "C" int vmamd_moe_weighted_sum(const void* x, int dtype, int64_t tokens, int topk,
+                                      int64_t hidden, const float* topk_weights,
+                                      const int32_t* topk_ids, const int32_t* expert_map,
+                                      int64_t expert_map_len, void* out, vmamd_stream_t stream) {
+  VMAMD_REQUIRE(topk_weights || tokens * hidden == 0, "moe_weighted_sum: null topk_weights");
+  return moe_sum_impl("moe_weighted_sum", x, dtype, tokens, topk, hidden, topk_ids, expert_map,
+                      expert_map_len, topk_weights, out, stream);
 }

@@ -142,6 +142,49 @@ __global__ __launch_bounds__(kQuantThreads) void silu_mul_quant_fp8_kernel(
   *reinterpret_cast<uint2*>(q + row * d + col) = quant8(v, scale, qmin, qmax);
 }
 
+
+// ------------------------------------------------- per-row quantiser -----
+// s[r] = max(eps, max_c |x[r,c]|) / qmax over the whole row,
+// q[r,c] = e4m3(clamp(x[r,c] / s[r], qmin, qmax)).  One 256-thread block per
+// row, 8 columns per thread per pass; up to kRowChunks passes stay in
+// registers between the amax and the quantise steps.
+constexpr int kRowThreads = 256;
+constexpr int kRowChunks = 8;  // rows of up to 256 * 8 * 8 = 16384 columns
+
+__global__ __launch_bounds__(kRowThreads) void row_quant_fp8_kernel(
+    const uint16_t* __restrict__ x, int64_t x_row_stride, int cols, float eps, float qmin,
+    float qmax, uint8_t* __restrict__ q, float* __restrict__ s) {
+  __shared__ float red[kRowThreads / kWave];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * x_row_stride;
+  const int nchunk = cols / 8;
+  float v[kRowChunks][8];
+  float amax = eps;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int ch = threadIdx.x + c * kRowThreads;
+    if (ch < nchunk) {
+      load8<kBF16>(xr + ch * 8, true, v[c]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
+    }
+  }
+  amax = wave_max(amax);
+  if (lane_id() == 0) red[threadIdx.x / kWave] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kRowThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
+  const float scale = amax / qmax;
+  if (threadIdx.x == 0) s[row] = scale;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int ch = threadIdx.x + c * kRowThreads;
+    if (ch < nchunk)
+      *reinterpret_cast<uint2*>(q + row * cols + ch * 8) = quant8(v[c], scale, qmin, qmax);
+  }
+}
+
 }  // namespace vmamd
 
 using namespace vmamd;
@@ -249,4 +292,25 @@ extern "C" int vmamd_silu_and_mul_quant_fp8(const void* x, int dtype, int64_t ro
   }
 #undef VMAMD_SMQ
   return check_launch("silu_and_mul_quant_fp8");
+}
+
+extern "C" int vmamd_per_token_quant_fp8(const void* x, int64_t rows, int64_t cols,
+                                         int64_t x_row_stride, float eps, float fp8_min,
+                                         float fp8_max, void* q, float* s, vmamd_stream_t stream) {
+  VMAMD_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= kRowThreads * 8 * kRowChunks,
+                "per_token_quant_fp8: cols (%lld) must be a positive multiple of 8 up to %d",
+                (long long)cols, kRowThreads * 8 * kRowChunks);
+  VMAMD_REQUIRE(x_row_stride >= cols && x_row_stride % 8 == 0,
+                "per_token_quant_fp8: row stride must be >= cols and a multiple of 8");
+  VMAMD_REQUIRE(fp8_max > 0.f, "per_token_quant_fp8: fp8_max must be positive");
+  VMAMD_REQUIRE(rows < (1ll << 31), "per_token_quant_fp8: too many rows");
+  if (rows == 0) return VMAMD_OK;
+  VMAMD_REQUIRE(x && q && s, "per_token_quant_fp8: null pointer");
+  VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0,
+                "per_token_quant_fp8: x must be 16-byte and q 8-byte aligned");
+  row_quant_fp8_kernel<<<static_cast<unsigned>(rows), kRowThreads, 0,
+                         reinterpret_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(x), x_row_stride, static_cast<int>(cols), eps, fp8_min, fp8_max,
+      static_cast<uint8_t*>(q), s);
+  return check_launch("per_token_quant_fp8");
 }

@@ -12,9 +12,10 @@ from . import _custom_ops  # noqa: F401
 from ._lib import LIB_PATH, VmamdError, load  # noqa: F401
 from .fp8_utils import per_token_group_quant_fp8, silu_mul_per_token_group_quant_fp8  # noqa: F401
 from .router import fused_topk, grouped_topk, topk_sigmoid, topk_softmax  # noqa: F401
+from .w4afp8_moe import w4afp8_moe  # noqa: F401
 
 __all__ = [
     "LIB_PATH", "VmamdError", "load",
     "per_token_group_quant_fp8", "silu_mul_per_token_group_quant_fp8",
-    "fused_topk", "grouped_topk", "topk_sigmoid", "topk_softmax",
+    "fused_topk", "grouped_topk", "topk_sigmoid", "topk_softmax", "w4afp8_moe",
 ]

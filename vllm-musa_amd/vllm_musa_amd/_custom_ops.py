@@ -203,3 +203,40 @@ def moe_sum(input: torch.Tensor, output: torch.Tensor, topk_ids: torch.Tensor | 
 
 def lib_version() -> int:
     return _lib.load().vmamd_abi_version()
+
+
+def per_token_quant_fp8(x: torch.Tensor, eps: float = 1e-4) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dynamic per-row fp8 quantisation of bf16 x [rows, cols]: one scale
+    max(eps, absmax(row)) / 448 per row (the w4afp8 activation quantiser,
+    vllm_musa/kernels/w4afp8_moe.py:47-78).  Returns (q e4m3fn, s f32 [rows])."""
+    check_cuda(x)
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(-1) != 1:
+        raise ValueError("per_token_quant_fp8 expects a bf16 [rows, cols] tensor with unit "
+                         "column stride")
+    rows, cols = x.shape
+    q = torch.empty(rows, cols, dtype=FP8_DTYPE, device=x.device)
+    s = torch.empty(rows, dtype=torch.float32, device=x.device)
+    call("vmamd_per_token_quant_fp8", ptr(x), rows, cols, x.stride(0), eps, FP8_MIN, FP8_MAX,
+         ptr(q), ptr(s), stream_of(x))
+    return q, s
+
+
+def moe_weighted_sum(input: torch.Tensor, topk_weights: torch.Tensor, output: torch.Tensor,
+                     topk_ids: torch.Tensor | None = None,
+                     expert_map: torch.Tensor | None = None) -> None:
+    """output[t] = round(sum_k input[t, k] * topk_weights[t, k]) with an fp32
+    accumulator in slot order (_combine_expert_rows, vllm_musa/kernels/w4afp8_moe.py:127-161)."""
+    check_cuda(input, topk_weights, output, topk_ids, expert_map)
+    _contig(input, "input")
+    _contig(output, "output")
+    if input.dim() != 3 or output.shape != (input.shape[0], input.shape[2]) or \
+            input.dtype != output.dtype:
+        raise ValueError("moe_weighted_sum expects input [T, K, H] and output [T, H] of one dtype")
+    w = topk_weights.to(torch.float32).contiguous()
+    if w.shape != input.shape[:2]:
+        raise ValueError("topk_weights must be [T, K]")
+    ids = None if topk_ids is None else topk_ids.to(torch.int32).contiguous()
+    emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
+    t, k, h = input.shape
+    call("vmamd_moe_weighted_sum", ptr(input), dtype_code(input.dtype), t, k, h, ptr(w), ptr(ids),
+         ptr(emap), 0 if emap is None else emap.numel(), ptr(output), stream_of(input))

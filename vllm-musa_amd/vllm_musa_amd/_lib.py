@@ -62,8 +62,14 @@ SIGNATURES: dict[str, list] = {
                            _f32, _p, _p, _sz, _p],
     "vmamd_moe_bf16_w2": [_p, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _p, _i32, _i64, _i64,
                           _p, _p, _p, _i64, _p, _p, _sz, _p],
+    "vmamd_per_token_quant_fp8": [_p, _i64, _i64, _i64, _f32, _f32, _f32, _p, _p, _p],
+    "vmamd_moe_weighted_sum": [_p, _i32, _i64, _i32, _i64, _p, _p, _p, _i64, _p, _p],
+    "vmamd_w4afp8_moe_workspace_size": [_i64, _i32, _i32, _i64, _i64, _i32],
+    "vmamd_w4afp8_moe": [_p, _i64, _i64, _p, _p, _p, _p, _i32, _i64, _p, _p, _i32, _p, _i64, _f32,
+                         _i32, _p, _p, _sz, _p],
 }
 _RESTYPES = {"vmamd_last_error": ctypes.c_char_p,
+             "vmamd_w4afp8_moe_workspace_size": ctypes.c_size_t,
              "vmamd_fused_moe_bf16_workspace_size": ctypes.c_size_t,
              "vmamd_moe_bf16_stage_workspace_size": ctypes.c_size_t,
              "vmamd_w8a8_block_fp8_matmul_workspace_size": ctypes.c_size_t,
