@@ -110,17 +110,59 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
-// Argmax over the wave with ties broken towards the lower index.
-__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) {
-    float ov = __shfl_xor(v, m, kWave);
-    int oi = __shfl_xor(idx, m, kWave);
-    if (ov > v || (ov == v && oi < idx)) {
-      v = ov;
-      idx = oi;
-    }
+// Cross-lane moves in DPP form (a VALU operand modifier: no LDS round trip).
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8 lanes
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within each 16 lanes
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// Merge (v, idx) with a partner's under the order (value desc, index asc).
+__device__ __forceinline__ void argmax_merge(float& v, int& idx, float ov, int oi) {
+  if (ov > v || (ov == v && oi < idx)) {
+    v = ov;
+    idx = oi;
   }
+}
+
+// Argmax over the wave with ties broken towards the lower index; every lane
+// ends with the result.  The merge is a maximum under a total order, so any
+// pairing that joins disjoint lane sets works: quad swaps and the 8- and
+// 16-lane mirrors run as DPP moves, the 32- and 64-lane steps as shuffles.
+__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
+  argmax_merge(v, idx, dpp_f<kDppXor1>(v), dpp_i<kDppXor1>(idx));
+  argmax_merge(v, idx, dpp_f<kDppXor2>(v), dpp_i<kDppXor2>(idx));
+  argmax_merge(v, idx, dpp_f<kDppHalfMirror>(v), dpp_i<kDppHalfMirror>(idx));
+  argmax_merge(v, idx, dpp_f<kDppMirror>(v), dpp_i<kDppMirror>(idx));
+  argmax_merge(v, idx, __shfl_xor(v, 16, kWave), __shfl_xor(idx, 16, kWave));
+  argmax_merge(v, idx, __shfl_xor(v, 32, kWave), __shfl_xor(idx, 32, kWave));
+}
+
+// Top-2 (t1 >= t2) of the union of two disjoint value sets.
+__device__ __forceinline__ void top2_merge(float& t1, float& t2, float o1, float o2) {
+  const float hi = fmaxf(t1, o1), lo = fminf(t1, o1);
+  t2 = fmaxf(lo, fmaxf(t2, o2));
+  t1 = hi;
+}
+
+// Top-2 over aligned groups of S lanes (S a power of two <= 64), every lane
+// of a group ending with its group's (t1, t2).
+template <int S>
+__device__ __forceinline__ void group_top2(float& t1, float& t2) {
+  if constexpr (S >= 2) top2_merge(t1, t2, dpp_f<kDppXor1>(t1), dpp_f<kDppXor1>(t2));
+  if constexpr (S >= 4) top2_merge(t1, t2, dpp_f<kDppXor2>(t1), dpp_f<kDppXor2>(t2));
+  if constexpr (S >= 8) top2_merge(t1, t2, dpp_f<kDppHalfMirror>(t1), dpp_f<kDppHalfMirror>(t2));
+  if constexpr (S >= 16) top2_merge(t1, t2, dpp_f<kDppMirror>(t1), dpp_f<kDppMirror>(t2));
+  if constexpr (S >= 32) top2_merge(t1, t2, __shfl_xor(t1, 16, kWave), __shfl_xor(t2, 16, kWave));
+  if constexpr (S >= 64) top2_merge(t1, t2, __shfl_xor(t1, 32, kWave), __shfl_xor(t2, 32, kWave));
 }
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }

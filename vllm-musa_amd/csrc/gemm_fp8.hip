@@ -3,134 +3,129 @@
 //   B  [N, K] e4m3 (128x128 weight blocks, scales Bs[ceil(N/128), K/128])
 //
 // Two kernels:
-//  * gemm_fp8_bs_kernel  -- tiled BM x BN workgroup tile, 4 waves, K-block of
-//    128 per step, LDS double buffer fed by register prefetch (one barrier per
-//    K-block), XCD-aware tile order.  For M > 64.
+//  * gemm_fp8_dma_kernel -- 128 x 256 workgroup tile, 8 waves, K-block of 128
+//    per step, 3-stage LDS ring fed by direct global->LDS loads (one barrier
+//    per K-block), XCD-aware tile order.  For M > 64.
 //  * gemv_fp8_bs_kernel  -- decode-sized M (<= 64): one wave per 16 weight rows
 //    streams its rows straight from HBM (no LDS), each 16x128 weight fragment
 //    multiplies every 16-row activation tile held in registers, so weights are
 //    read exactly once.  Split-K over blockIdx.y writes fp32 partials that
 //    splitk_reduce_kernel sums in a fixed order (deterministic), one rounding.
 #include "mfma_fp8.h"
+#include "tile_pipe.h"
 
 namespace vmamd {
 
-template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(WM * WN * kWave, 2) void gemm_fp8_bs_kernel(
+// ------------------------------------------- tiled GEMM on the DMA ring ---
+// 128 x 256 output tile per workgroup (8 waves as 2 (m) x 4 (n), 64 x 64 per
+// wave), 3-stage LDS ring fed by direct global->LDS loads: two K steps are in
+// flight while the current one runs on MFMA.  Rows past M / N are clamped to
+// the last row (their results are not stored).
+using DensePipe = TilePipe<true, 128, 256, 2, 4, 3>;
+
+__global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t as_sm, int64_t as_sk,
     const uint8_t* __restrict__ B, const float* __restrict__ Bs, uint16_t* __restrict__ C, int M,
     int N, int K, int TM, int TN) {
-  constexpr int THREADS = WM * WN * kWave;
-  constexpr int WTM = BM / WM, WTN = BN / WN, MT = WTM / 16, NT = WTN / 16;
-  constexpr int ACH = BM * 8 / THREADS, BCH = BN * 8 / THREADS;
-  static_assert(ACH * THREADS == BM * 8 && BCH * THREADS == BN * 8, "tile / thread mismatch");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][(BM + BN) * 128];
-
+  using P = DensePipe;
+  constexpr int NS = 3, BM = 128, BN = 256, WN = 4;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
   int tm, tn;
   if (!xcd_tile(blockIdx.x, TM, TN, tm, tn)) return;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int wm = wave / WN, wn = wave % WN;
   const int li = lane % 16, lg = lane / 16;
-  const int KB = K / 128;
+  const int KS = K / 128, NB = (N + 127) / 128;
 
-  // Thread t copies 16-byte chunk (t % 8) of rows t/8 + c*(THREADS/8); rows
-  // past M / N are clamped to the last row, so loads stay in bounds and their
-  // results are never stored.  Rows 32 apart share (row & 7), hence the same
-  // swizzled chunk slot.
-  constexpr int RSTEP = THREADS / 8;
-  const int crow = tid / 8, cch = tid % 8;
-  const int l0 = lds_off(crow, cch);
-  int64_t goff_a[ACH], goff_b[BCH];
+  P p;
 #pragma unroll
-  for (int c = 0; c < ACH; ++c)
-    goff_a[c] = static_cast<int64_t>(min(m0 + crow + c * RSTEP, M - 1)) * K + cch * 16;
+  for (int j = 0; j < P::kDmaA; ++j) {
+    const int m = min(m0 + P::rowA(wave, lane, j), M - 1);
+    p.srcA[j] = A + static_cast<int64_t>(m) * K + P::chunk(lane);
+    p.ldsA[j] = (wave + j * P::kWaves) * 8 * 128;
+  }
 #pragma unroll
-  for (int c = 0; c < BCH; ++c)
-    goff_b[c] = static_cast<int64_t>(min(n0 + crow + c * RSTEP, N - 1)) * K + cch * 16;
-  const int sa_row0 = m0 + wm * WTM + li;
-  const int sb_col0 = n0 + wn * WTN;
-
-  v4f acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // Scale rows / columns of this lane (clamped like the tile rows).
-  const float* as_row[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-    as_row[mt] = As + static_cast<int64_t>(min(sa_row0 + mt * 16, M - 1)) * as_sm;
-  const float* bs_row[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-    bs_row[nt] = Bs + static_cast<int64_t>(min(sb_col0 + nt * 16, N - 1) / 128) * KB;
-
-  v4i ra[ACH], rb[BCH];
-#pragma unroll
-  for (int c = 0; c < ACH; ++c) ra[c] = ld16(A + goff_a[c]);
-#pragma unroll
-  for (int c = 0; c < BCH; ++c) rb[c] = ld16(B + goff_b[c]);
-#pragma unroll
-  for (int c = 0; c < ACH; ++c) st16(&smem[0][l0 + c * RSTEP * 128], ra[c]);
-#pragma unroll
-  for (int c = 0; c < BCH; ++c) st16(&smem[0][BM * 128 + l0 + c * RSTEP * 128], rb[c]);
-  float sa[MT], sb[NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) sa[mt] = as_row[mt][0];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) sb[nt] = bs_row[nt][0];
-  __syncthreads();
-
-  const v4f zero = {0.f, 0.f, 0.f, 0.f};
-  for (int kb = 0; kb < KB; ++kb) {
-    const int cur = kb & 1;
-    // Prefetch K-block kb+1 (the last iteration re-reads block KB-1; the
-    // copy lands in the idle buffer and is never used).
-    const int kn = min(kb + 1, KB - 1);
-    const int off = kn * 128;
-#pragma unroll
-    for (int c = 0; c < ACH; ++c) ra[c] = ld16(A + goff_a[c] + off);
-#pragma unroll
-    for (int c = 0; c < BCH; ++c) rb[c] = ld16(B + goff_b[c] + off);
-    float san[MT], sbn[NT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) san[mt] = as_row[mt][kn * as_sk];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) sbn[nt] = bs_row[nt][kn];
-
-    const uint8_t* tile = smem[cur];
-    v8i xf[MT], wf[NT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xf[mt] = lds_frag(tile, wm * WTM + mt * 16 + li, lg);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) wf[nt] = lds_frag(tile + BM * 128, wn * WTN + nt * 16 + li, lg);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const v4f p = mfma_fp8(wf[nt], xf[mt], zero);
-        fma4(acc[mt][nt], p, sa[mt] * sb[nt]);
-      }
-#pragma unroll
-    for (int c = 0; c < ACH; ++c) st16(&smem[cur ^ 1][l0 + c * RSTEP * 128], ra[c]);
-#pragma unroll
-    for (int c = 0; c < BCH; ++c) st16(&smem[cur ^ 1][BM * 128 + l0 + c * RSTEP * 128], rb[c]);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) sa[mt] = san[mt];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) sb[nt] = sbn[nt];
-    __syncthreads();
+  for (int j = 0; j < P::kDmaB; ++j) {
+    const int n = min(n0 + P::rowB(wave, lane, j), N - 1);
+    p.srcB[j] = B + static_cast<int64_t>(n) * K + P::chunk(lane);
+    p.ldsB[j] = P::kOffB + (wave + j * P::kWaves) * 8 * 128;
+  }
+  if (wave < BM / 64) {  // activation scales of tile rows 64*wave + lane
+    const int m = min(m0 + 64 * wave + lane, M - 1);
+    p.srcS = reinterpret_cast<const uint8_t*>(As + static_cast<int64_t>(m) * as_sm);
+    p.stepS = static_cast<int>(as_sk * 4);
+    p.ldsS = P::kOffSA + 64 * wave * 4;
+  } else {  // weight-block scales of the tile's two 128-row blocks (slots 0, 1)
+    const int nb = min(n0 / 128 + min(lane, 1), NB - 1);
+    p.srcS = reinterpret_cast<const uint8_t*>(Bs + static_cast<int64_t>(nb) * KS);
+    p.stepS = 4;
+    p.ldsS = P::kOffSB;
   }
 
+  v4f acc[P::MT][P::NT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = m0 + wm * WTM + mt * 16 + li;
+  for (int mt = 0; mt < P::MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < P::NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // Fragments of one K step in registers; the next step's are read from LDS
+  // while this step's MFMAs run.
+  struct Frags {
+    v8i x[P::MT], w[P::NT];
+    float sa[P::MT], sb;
+  };
+  auto read = [&](const uint8_t* st, Frags& f) {
+    f.sb = lds_load<float>(st, P::kOffSB + (wn / 2) * 4);
+#pragma unroll
+    for (int mt = 0; mt < P::MT; ++mt) {
+      f.sa[mt] = lds_load<float>(st, P::kOffSA + (wm * P::WTM + mt * 16 + li) * 4);
+      f.x[mt] = lds_frag(st, wm * P::WTM + mt * 16 + li, lg);
+    }
+#pragma unroll
+    for (int nt = 0; nt < P::NT; ++nt) f.w[nt] = lds_frag(st + P::kOffB, wn * P::WTN + nt * 16 + li, lg);
+  };
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int mt = 0; mt < P::MT; ++mt) {
+      const float sab = f.sa[mt] * f.sb;
+#pragma unroll
+      for (int nt = 0; nt < P::NT; ++nt) fma4(acc[mt][nt], mfma_fp8(f.w[nt], f.x[mt], zero), sab);
+    }
+  };
+  // Step kb: its fragments are in `cur`; buffer kb % NS (already read into
+  // `cur`) is refilled with step kb + NS, step kb + 1 is read into `nxt`.
+  auto step = [&](int kb, const Frags& cur, Frags& nxt) {
+    wait_lgkmcnt0();  // this wave's reads of the buffer refilled below are done
+    wait_vmcnt<(NS - 2) * P::kIPS>();
+    barrier_lds();
+    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
+    read(smem_dyn + ((kb + 1) % NS) * P::kStage, nxt);
+    __builtin_amdgcn_sched_barrier(0);  // the reads issue before the MFMAs they overlap
+    mma(cur);
+  };
+
+#pragma unroll
+  for (int s = 0; s < NS; ++s) p.issue(smem_dyn + s * P::kStage, min(s, KS - 1));
+  wait_vmcnt<(NS - 1) * P::kIPS>();
+  barrier_lds();
+  Frags f0, f1;
+  read(smem_dyn, f0);
+  for (int kb = 0; kb < KS; kb += 2) {
+    step(kb, f0, f1);
+    if (kb + 1 < KS) step(kb + 1, f1, f0);
+  }
+  wait_vmcnt<0>();  // the ring's trailing DMAs must land before the workgroup's LDS is released
+
+#pragma unroll
+  for (int mt = 0; mt < P::MT; ++mt) {
+    const int m = m0 + wm * P::WTM + mt * 16 + li;
     if (m >= M) continue;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int n = n0 + wn * WTN + nt * 16 + 4 * lg;
+    for (int nt = 0; nt < P::NT; ++nt) {
+      const int n = n0 + wn * P::WTN + nt * 16 + 4 * lg;
       if (n >= N) continue;
       const v4f a = acc[mt][nt];
       *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) = pack_bf16x4(a[0], a[1], a[2], a[3]);
@@ -307,9 +302,17 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
     }
     return check_launch("w8a8_block_fp8_matmul(gemv)");
   }
-  constexpr int BM = 128, BN = 128;
-  const int TM = (m + BM - 1) / BM, TN = (n + BN - 1) / BN;
-  gemm_fp8_bs_kernel<BM, BN, 2, 2><<<xcd_grid(TM * TN), 256, 0, st>>>(a, As, as_stride_m, as_stride_k,
-                                                                      b, Bs, c, m, n, k, TM, TN);
+  static bool lds_raised = false;
+  if (!lds_raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_fp8_dma_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, DensePipe::kLds) != hipSuccess) {
+      set_error("w8a8_block_fp8_matmul: cannot raise the LDS limit of the GEMM kernel");
+      return VMAMD_ERR_HIP;
+    }
+    lds_raised = true;
+  }
+  const int TM = (m + 127) / 128, TN = (n + 255) / 256;
+  gemm_fp8_dma_kernel<<<xcd_grid(TM * TN), DensePipe::kThreads, DensePipe::kLds, st>>>(
+      a, As, as_stride_m, as_stride_k, b, Bs, c, m, n, k, TM, TN);
   return check_launch("w8a8_block_fp8_matmul(gemm)");
 }

@@ -63,13 +63,22 @@ __device__ __forceinline__ v4i int4x16_to_fp8(uint2 p) {
              static_cast<int>(int4x4_to_fp8(p.y & 0xFFFFu)), static_cast<int>(int4x4_to_fp8(p.y >> 16))};
 }
 
+// Loads from LDS through address-space-3 pointers, so the compiler knows
+// they touch LDS (a read through a generic pointer makes it wait for every
+// outstanding global->LDS DMA first).
+template <typename T>
+__device__ __forceinline__ T lds_load(const uint8_t* base, int off) {
+  typedef __attribute__((address_space(3))) const T lds_t;
+  return *(lds_t*)((const __attribute__((address_space(3))) uint8_t*)base + off);
+}
+
 // Operand fragment of `row` from an LDS tile.
 __device__ __forceinline__ v8i lds_frag(const uint8_t* tile, int row, int g) {
-  const uint4 lo = *reinterpret_cast<const uint4*>(tile + lds_off(row, g));
-  const uint4 hi = *reinterpret_cast<const uint4*>(tile + lds_off(row, g + 4));
+  const v4i lo = lds_load<v4i>(tile, lds_off(row, g));
+  const v4i hi = lds_load<v4i>(tile, lds_off(row, g + 4));
   v8i f;
-  f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
-  f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+  f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+  f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
   return f;
 }
 

@@ -38,6 +38,7 @@
 #include <type_traits>
 
 #include "mfma_fp8.h"
+#include "tile_pipe.h"
 
 namespace vmamd {
 
@@ -768,6 +769,233 @@ __global__ __launch_bounds__(256, 2) void moe_w2_gemm_kernel(
   }
 }
 
+// ------------------------------------- prefill GEMMs on the DMA ring -------
+// kFp8 / kBf16.  Tile: 128 routes x 256 weight rows, 8 waves as 2 (m) x 4 (n)
+// with 64 x 64 per wave, 3-stage LDS ring fed by direct global->LDS loads
+// (tile_pipe.h); each wave reads the next K step's fragments from LDS while
+// the current step's MFMAs run.  W13: the 256 weight rows are 128 gate + 128
+// up rows interleaved by 16 (epilogue: SiLU-and-mul, and for kFp8 the 1x128
+// a2 quantiser); W2: 256 hidden rows (epilogue: routed weight).  Padding
+// closes each expert's segment, so a 16-route fragment holds only padding iff
+// its first route does; such fragments skip their MFMAs (a wave-uniform test).
+// Padding rows load token 0's activations; their outputs are never used.
+using MoePipeFp8 = TilePipe<true, 128, 256, 2, 4, 3>;
+using MoePipeBf16 = TilePipe<false, 128, 256, 2, 4, 3>;
+template <int KIND>
+using MoePipe = typename std::conditional<KIND == kFp8, MoePipeFp8, MoePipeBf16>::type;
+
+template <int KIND, bool W13>
+__global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
+    const uint8_t* __restrict__ act, const float* __restrict__ act_s, int topk, int K,
+    const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles,
+    const uint8_t* __restrict__ w, const float* __restrict__ ws, int N, int I, float limit,
+    const float* __restrict__ route_w, uint8_t* __restrict__ a2, float* __restrict__ a2s,
+    uint16_t* __restrict__ y) {
+  using P = MoePipe<KIND>;
+  using KB_ = KindBytes<KIND>;
+  constexpr int NS = 3, BM = 128, BN = 256, WN = 4, MT = P::MT, NT = P::NT;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
+  const int TN = W13 ? I / 128 : (N + BN - 1) / BN;
+  int e, mb, tn;
+  if (!moe_tile(blockIdx.x, max_tiles, offsets, ntpp, E, TN, e, mb, tn)) return;
+  const int n0 = W13 ? tn * 128 : tn * BN;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wm = wave / WN, wn = wave % WN, li = lane % 16, lg = lane / 16;
+  const int KS = K / KB_::kElems;
+  const int64_t rowb = static_cast<int64_t>(KS) * 128;
+  const int NB = (N + 127) / 128;
+
+  auto wrow = [&](int j) -> int {  // weight row of local tile row j
+    if constexpr (W13) {
+      const int p = j / 32, q = j % 32;
+      return q < 16 ? n0 + 16 * p + q : I + n0 + 16 * p + (q - 16);
+    } else {
+      return min(n0 + j, N - 1);
+    }
+  };
+  auto arow = [&](int r) -> int64_t {  // activation row of tile row r
+    const int rr = mb * BM + r;
+    if constexpr (W13) {
+      const int s = sorted[rr];
+      return s < numel ? static_cast<int64_t>(s / topk) : 0;
+    } else {
+      return rr;
+    }
+  };
+
+  P p;
+#pragma unroll
+  for (int j = 0; j < P::kDmaA; ++j) {
+    p.srcA[j] = act + arow(P::rowA(wave, lane, j)) * rowb + P::chunk(lane);
+    p.ldsA[j] = (wave + j * P::kWaves) * 8 * 128;
+  }
+#pragma unroll
+  for (int j = 0; j < P::kDmaB; ++j) {
+    p.srcB[j] = w + (static_cast<int64_t>(e) * N + wrow(P::rowB(wave, lane, j))) * rowb + P::chunk(lane);
+    p.ldsB[j] = P::kOffB + (wave + j * P::kWaves) * 8 * 128;
+  }
+  if constexpr (KIND == kFp8) {
+    if (wave < BM / 64) {  // activation group scales of tile rows 64*wave + lane
+      p.srcS = reinterpret_cast<const uint8_t*>(act_s + arow(64 * wave + lane) * KS);
+      p.ldsS = P::kOffSA + 64 * wave * 4;
+    } else {  // weight-block scales: W13 gate / up block, W2 the tile's two 128-row blocks
+      const int slot = min(lane, 1);
+      const int brow = W13 ? (slot ? (I + n0) / 128 : n0 / 128) : min(n0 / 128 + slot, NB - 1);
+      p.srcS = reinterpret_cast<const uint8_t*>(ws + (static_cast<int64_t>(e) * NB + brow) * KS);
+      p.ldsS = P::kOffSB;
+    }
+    p.stepS = 4;
+  }
+  bool live[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) live[mt] = sorted[mb * BM + wm * P::WTM + mt * 16] < numel;
+
+  v4f acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  struct Frags {
+    v8i x[MT], w[NT];
+    float sa[MT], sb0, sb1;
+  };
+  auto read = [&](const uint8_t* st, Frags& f) {
+    if constexpr (KIND == kFp8) {
+      if constexpr (W13) {
+        f.sb0 = lds_load<float>(st, P::kOffSB);
+        f.sb1 = lds_load<float>(st, P::kOffSB + 4);
+      } else {
+        f.sb0 = f.sb1 = lds_load<float>(st, P::kOffSB + (wn / 2) * 4);
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if constexpr (KIND == kFp8)
+        f.sa[mt] = lds_load<float>(st, P::kOffSA + (wm * P::WTM + mt * 16 + li) * 4);
+      f.x[mt] = lds_frag(st, wm * P::WTM + mt * 16 + li, lg);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) f.w[nt] = lds_frag(st + P::kOffB, wn * P::WTN + nt * 16 + li, lg);
+  };
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (!live[mt]) continue;
+      if constexpr (KIND == kFp8) {
+        const float s0 = f.sa[mt] * f.sb0, s1 = f.sa[mt] * f.sb1;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          fma4(acc[mt][nt], mfma_fp8(f.w[nt], f.x[mt], zero), (W13 && (nt & 1)) ? s1 : s0);
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma_bf16x2(f.w[nt], f.x[mt], acc[mt][nt]);
+      }
+    }
+  };
+  auto step = [&](int kb, const Frags& cur, Frags& nxt) {
+    wait_lgkmcnt0();
+    wait_vmcnt<(NS - 2) * P::kIPS>();
+    barrier_lds();
+    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
+    read(smem_dyn + ((kb + 1) % NS) * P::kStage, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(cur);
+  };
+#pragma unroll
+  for (int s = 0; s < NS; ++s) p.issue(smem_dyn + s * P::kStage, min(s, KS - 1));
+  wait_vmcnt<(NS - 1) * P::kIPS>();
+  barrier_lds();
+  Frags f0, f1;
+  read(smem_dyn, f0);
+  for (int kb = 0; kb < KS; kb += 2) {
+    step(kb, f0, f1);
+    if (kb + 1 < KS) step(kb + 1, f1, f0);
+  }
+  wait_lgkmcnt0();
+  wait_vmcnt<0>();  // the ring's trailing DMAs land before LDS is reused or released
+  barrier_lds();
+
+  if constexpr (W13) {
+    if constexpr (KIND == kFp8) {
+      // Activation, row amax across the 4 n-waves through LDS, 1x128 quantiser.
+      float* red = reinterpret_cast<float*>(smem_dyn);  // [WN][BM]
+      float v[MT][2][4];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float amax = 0.f;
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = swiglu_bf16(bf16r(acc[mt][2 * q][r]), bf16r(acc[mt][2 * q + 1][r]), limit);
+            v[mt][q][r] = x;
+            amax = fmaxf(amax, fabsf(x));
+          }
+        amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+        if (lg == 0) red[wn * BM + wm * P::WTM + mt * 16 + li] = amax;
+      }
+      __syncthreads();
+      const int gpr = I / 128;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int ml = wm * P::WTM + mt * 16 + li;
+        float amax = 1e-10f;
+#pragma unroll
+        for (int w4 = 0; w4 < WN; ++w4) amax = fmaxf(amax, red[w4 * BM + ml]);
+        const float scale = amax / 448.0f;
+        const int64_t row = static_cast<int64_t>(mb) * BM + ml;
+        if (wn == 0 && lg == 0) a2s[row * gpr + tn] = scale;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = v[mt][q][r];
+            o[r] = x != x ? -448.0f : fminf(fmaxf(x / scale, -448.0f), 448.0f);
+          }
+          const int col = n0 + (wn * 2 + q) * 16 + 4 * lg;
+          *reinterpret_cast<uint32_t*>(a2 + row * I + col) = f32x4_to_fp8x4(o[0], o[1], o[2], o[3]);
+        }
+      }
+    } else {
+      uint16_t* a2b = reinterpret_cast<uint16_t*>(a2);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int64_t row = static_cast<int64_t>(mb) * BM + wm * P::WTM + mt * 16 + li;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            o[r] = swiglu_bf16(bf16r(acc[mt][2 * q][r]), bf16r(acc[mt][2 * q + 1][r]), limit);
+          const int col = n0 + (wn * 2 + q) * 16 + 4 * lg;
+          *reinterpret_cast<uint2*>(a2b + row * I + col) = pack_bf16x4(o[0], o[1], o[2], o[3]);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = sorted[static_cast<int64_t>(mb) * BM + wm * P::WTM + mt * 16 + li];
+      if (r >= numel) continue;
+      const float rw = route_w ? route_w[r] : 1.0f;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int n = n0 + wn * P::WTN + nt * 16 + 4 * lg;
+        if (n >= N) continue;
+        const v4f a = acc[mt][nt];
+        *reinterpret_cast<uint2*>(y + static_cast<int64_t>(r) * N + n) =
+            pack_bf16x4(a[0] * rw, a[1] * rw, a[2] * rw, a[3] * rw);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------ host side ---
 // Split-K factor of the decode GEMVs: enough waves to cover the chip
 // (>= 4096 over the active experts' n-tiles), at least 4 K steps per split.
@@ -818,6 +1046,19 @@ static int raise_w13_lds() {
   return VMAMD_OK;
 }
 
+template <int KIND, bool W13>
+static int raise_dma_lds() {
+  static bool done = false;
+  if (done) return VMAMD_OK;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_gemm_dma_kernel<KIND, W13>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, MoePipe<KIND>::kLds) != hipSuccess) {
+    set_error("moe gemm: cannot raise the LDS limit of the grouped GEMM kernel");
+    return VMAMD_ERR_HIP;
+  }
+  done = true;
+  return VMAMD_OK;
+}
+
 // Launches of the two stages; arguments are validated by the callers.  kBf16:
 // xa is x itself, xs / w13_s / a2s unused.  kW4: xs are the token row scales,
 // a2 receives the bf16 activation (quantised per row by the caller).
@@ -850,10 +1091,18 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
   }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
   const int tiles = max_blocks * (I / 128);
-  int rc = raise_w13_lds<KIND>();
-  if (rc) return rc;
-  moe_w13_gemm_kernel<KIND><<<xcd_grid(tiles), kW13Threads, 2 * w13_stage_bytes<KIND>(), st>>>(
-      xa, xs, topk, H, sorted, offs, ntpp, E, numel, tiles, w13, w13_s, I, limit, a2, a2s);
+  if constexpr (KIND == kW4) {
+    int rc = raise_w13_lds<KIND>();
+    if (rc) return rc;
+    moe_w13_gemm_kernel<KIND><<<xcd_grid(tiles), kW13Threads, 2 * w13_stage_bytes<KIND>(), st>>>(
+        xa, xs, topk, H, sorted, offs, ntpp, E, numel, tiles, w13, w13_s, I, limit, a2, a2s);
+  } else {
+    int rc = raise_dma_lds<KIND, true>();
+    if (rc) return rc;
+    moe_gemm_dma_kernel<KIND, true><<<xcd_grid(tiles), 512, MoePipe<KIND>::kLds, st>>>(
+        xa, xs, topk, H, sorted, offs, ntpp, E, numel, tiles, w13,
+        static_cast<const float*>(w13_s), 2 * I, I, limit, nullptr, a2, a2s, nullptr);
+  }
   return check_launch("moe w13 (gemm)");
 }
 
@@ -886,9 +1135,19 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
     return check_launch("moe w2 (reduce)");
   }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
-  const int tiles = max_blocks * ((H + 127) / 128);
-  moe_w2_gemm_kernel<KIND><<<xcd_grid(tiles), 256, 0, st>>>(a2, a2s, I, sorted, offs, ntpp, E, numel,
-                                                            tiles, w2, w2_s, H, topk_weights, y);
+  if constexpr (KIND == kW4) {
+    const int tiles = max_blocks * ((H + 127) / 128);
+    moe_w2_gemm_kernel<KIND><<<xcd_grid(tiles), 256, 0, st>>>(a2, a2s, I, sorted, offs, ntpp, E,
+                                                              numel, tiles, w2, w2_s, H,
+                                                              topk_weights, y);
+  } else {
+    const int tiles = max_blocks * ((H + 255) / 256);
+    int rc = raise_dma_lds<KIND, false>();
+    if (rc) return rc;
+    moe_gemm_dma_kernel<KIND, false><<<xcd_grid(tiles), 512, MoePipe<KIND>::kLds, st>>>(
+        a2, a2s, 1, I, sorted, offs, ntpp, E, numel, tiles, w2, static_cast<const float*>(w2_s), H,
+        I, 0.f, topk_weights, nullptr, nullptr, y);
+  }
   return check_launch("moe w2 (gemm)");
 }
 

@@ -2,8 +2,8 @@
 //
 // One wave64 owns one token row.  Expert e lives in lane e % 64, register
 // slot e / 64, so the row is read with fully coalesced loads and every
-// selection round is a 6-step xor-shuffle argmax (ties to the lower expert
-// id).  Selection never depends on the order of a floating-point reduction:
+// selection round is a 6-step wave argmax (ties to the lower expert id) whose
+// first four steps are DPP lane moves and the last two shuffles.  Selection never depends on the order of a floating-point reduction:
 //   - softmax top-k selects on the (biased) logits, which softmax preserves;
 //   - sigmoid/softmax scores that feed a selection together with a bias are
 //     evaluated in double precision and rounded once to float, so they are
@@ -148,6 +148,52 @@ __global__ __launch_bounds__(kRouteWaves * kWave) void topk_sigmoid_kernel(
 }
 
 // ------------------------------------------------------- grouped top-k ----
+// Group g is the S consecutive experts g*S..g*S+S-1.  With S a power of two
+// <= 64 a group occupies S aligned lanes of one register slot (expert e sits
+// in lane e % 64, slot e / 64), so its top-2 is a log2(S)-step reduction; the
+// scores are then gathered so that lane g holds group g's.
+template <int VPT, int S>
+__device__ __forceinline__ float group_scores_pow2(const float (&sel)[VPT], bool sum2, int groups) {
+  constexpr int kSegs = kWave / S;  // groups per register slot
+  const int lane = lane_id();
+  float gs[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    float t1 = sel[i], t2 = -INFINITY;
+    group_top2<S>(t1, t2);
+    gs[i] = sum2 ? t1 + t2 : t1;
+  }
+  float gv = -INFINITY;
+  const int src = (lane % kSegs) * S;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const float v = __shfl(gs[i], src, kWave);
+    if (lane / kSegs == i) gv = v;
+  }
+  return lane < groups ? gv : -INFINITY;
+}
+
+// Any group size: the members of each group are broadcast in turn.
+template <int VPT>
+__device__ __forceinline__ float group_scores_serial(const float (&sel)[VPT], bool sum2, int groups,
+                                                     int gsize) {
+  const int lane = lane_id();
+  float gv = -INFINITY;
+  for (int g = 0; g < groups; ++g) {
+    float t1 = -INFINITY, t2 = -INFINITY;
+    for (int j = 0; j < gsize; ++j) {
+      const int e = g * gsize + j;
+      float mine = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+        if (lane + kWave * i == e) mine = sel[i];
+      top2_merge(t1, t2, __shfl(mine, e % kWave, kWave), -INFINITY);
+    }
+    if (lane == g) gv = sum2 ? t1 + t2 : t1;
+  }
+  return gv;
+}
+
 // Scores per expert (softmax or sigmoid, double-evaluated), sel = score (+
 // bias); group g is the S = experts / groups consecutive experts g*S..g*S+S-1.
 template <int DT, int VPT>
@@ -193,26 +239,18 @@ __global__ __launch_bounds__(kRouteWaves * kWave) void grouped_topk_kernel(
     sel[i] = e < experts ? (bias ? sc[i] + bias[e] : sc[i]) : -INFINITY;
   }
 
-  // Group scores: the members of each group are broadcast in turn, so every
-  // lane holds the same (t1, t2) and lane g keeps the score of group g.
-  float gv = -INFINITY;
-  for (int g = 0; g < groups; ++g) {
-    float t1 = -INFINITY, t2 = -INFINITY;
-    for (int j = 0; j < gsize; ++j) {
-      const int e = g * gsize + j;
-      float mine = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < VPT; ++i)
-        if (lane + kWave * i == e) mine = sel[i];
-      const float x = __shfl(mine, e % kWave, kWave);
-      if (x > t1) {
-        t2 = t1;
-        t1 = x;
-      } else if (x > t2) {
-        t2 = x;
-      }
-    }
-    if (lane == g) gv = bias ? t1 + t2 : t1;
+  // Group scores (sum of the top-2 sel with a bias, else the max), gathered
+  // so that lane g holds the score of group g.
+  float gv;
+  switch (gsize) {
+    case 1: gv = group_scores_pow2<VPT, 1>(sel, bias != nullptr, groups); break;
+    case 2: gv = group_scores_pow2<VPT, 2>(sel, bias != nullptr, groups); break;
+    case 4: gv = group_scores_pow2<VPT, 4>(sel, bias != nullptr, groups); break;
+    case 8: gv = group_scores_pow2<VPT, 8>(sel, bias != nullptr, groups); break;
+    case 16: gv = group_scores_pow2<VPT, 16>(sel, bias != nullptr, groups); break;
+    case 32: gv = group_scores_pow2<VPT, 32>(sel, bias != nullptr, groups); break;
+    case 64: gv = group_scores_pow2<VPT, 64>(sel, bias != nullptr, groups); break;
+    default: gv = group_scores_serial<VPT>(sel, bias != nullptr, groups, gsize); break;
   }
   uint64_t keep = 0;  // bit g set when group g is kept
   {
