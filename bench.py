@@ -12,7 +12,9 @@ Printed (rank 0, one JSON line): value = algorithmic TFLOP/s of the layer at
 T=4096 (2*T*topk*3*H*I flops per call), ms_per_step from HIP events around the
 K timed steps; `sweep` gives us / TFLOP/s / GB/s and roofline fractions at
 T = 1, 16, 256, 4096 (cold weights: a 1 GiB buffer is rewritten between
-iterations); `roofline` is the dominant kernel (W13 grouped GEMM at T=4096)
+iterations; `graph_us` is the same step replayed from a HIP graph, as a
+serving engine runs decode); `roofline` is the dominant kernel (W13 grouped
+GEMM at T=4096)
 timed on its own with HIP events on its launch stream; `cpu_baseline` times
 the CPU oracle on a bounded sample of the same layer.
 
@@ -105,6 +107,26 @@ def time_events(torch, fn, iters: int, flush=None) -> list[float]:
         b.synchronize()
         out.append(a.elapsed_time(b))
     return out
+
+
+def graph_median(torch, fn, iters: int, flush) -> float:
+    """Median ms of one replay of `fn` captured in a HIP graph (how a serving
+    engine runs decode steps: no host work between the kernels)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = statistics.median(time_events(torch, graph.replay, iters, flush))
+    del graph
+    return ms
 
 
 def cpu_baseline(torch, layer: Layer, target_s: float = 15.0) -> dict:
@@ -220,8 +242,12 @@ def main() -> int:
     # ------------------------------------------------------------- sweep ---
     sweep = []
     if not args.no_sweep:
-        flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
-        flush = lambda: flush_buf.fill_(1)
+        # Untimed cache flush before each call: reading 1 GiB evicts the L2s
+        # and the 256 MB memory-side cache without leaving dirty lines (after
+        # a 1 GiB fill the timed kernels would pay for writing those back; in
+        # a model the kernels ahead of a MoE layer mostly read weights).
+        flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+        flush = lambda: flush_buf.max()
         for t in SWEEP_T:
             lay = layer if t == T_HEADLINE else Layer(torch, t, weights)
             u = lay.used_experts()
@@ -230,6 +256,7 @@ def main() -> int:
             torch.cuda.synchronize()
             times = time_events(torch, lay.step, args.sweep_iters, flush)
             med = statistics.median(times)
+            gmed = graph_median(torch, lay.step, args.sweep_iters, flush)
             f = layer_flops(t * TOPK)
             b = layer_bytes(t, u)
             ideal = max(f / (PEAK_FP8_TFLOPS * 1e12), b / (PEAK_HBM_GBS * 1e9))
@@ -238,7 +265,9 @@ def main() -> int:
                           "gbps": round(b / (med * 1e-3) / 1e9, 1),
                           "frac_hbm": round(b / (med * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                           "frac_fp8_peak": round(f / (med * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
-                          "frac_roofline": round(ideal / (med * 1e-3), 4)})
+                          "frac_roofline": round(ideal / (med * 1e-3), 4),
+                          "graph_us": round(gmed * 1e3, 1),
+                          "graph_frac_roofline": round(ideal / (gmed * 1e-3), 4)})
             log(f"bench: sweep {sweep[-1]}")
         del flush_buf
 

@@ -92,29 +92,67 @@ __device__ __forceinline__ v8i weight_frag(const uint8_t* p, int g) {
 // ---------------------------------------------------------- decode GEMV ---
 constexpr int kMoeGemvWaves = 4;
 constexpr int kGemvBlock = 16;  // routes per block (one MFMA column tile)
+// K steps each wave keeps in flight (8 KiB of weights per wave; 4 and 8
+// measured alike, 4 needs fewer registers), and the number of waves the
+// split-K factor aims to launch (16 per CU).
+constexpr int kGemvU = 4;
+constexpr int kGemvTargetWaves = 4096;
 
-// act_s: kFp8 [rows, K/128] group scales (read here); kW4 / kBf16 unused.
+// Raw buffer loads (gfx9 descriptor: base, no stride, num_records bytes):
+// a lane whose byte offset is past num_records reads zeros and fetches
+// nothing, which masks lanes without a branch.
+constexpr int kBufferFlags = 0x00020000;
+constexpr uint32_t kBufferOff = 0x80000000u;  // offset of a masked lane (buffers are < 2 GiB)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferFlags);
+}
+__device__ __forceinline__ v4i buffer_ld16(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, 0));
+}
+// Activation fragment at byte offset off (row + K-block start) of a buffer.
+__device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
+  const v4i lo = buffer_ld16(rs, off + 16u * g);
+  const v4i hi = buffer_ld16(rs, off + 64u + 16u * g);
+  return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// act: [rows, K] activation bytes (rows = numel / act_div), act_bytes its
+// size (< 2^31); act_s: kFp8 [rows, K/128] group scales; kW4 / kBf16 unused.
 // ws: kFp8 f32 block scales; kW4 bf16 row scales.
+//
+// Start-up order: the expert id is the only load the weight stream depends
+// on, so the first K group of weights is requested before the route list is
+// resolved (offsets -> the block's route ids -> activation rows); every wave
+// starts at once, so a serial chain of lookups in front of the stream would
+// leave HBM idle.  The route ids are read with uniform (scalar) loads, which
+// are counted apart from the vector loads, so waiting for them does not wait
+// for the weights.  Columns of padding routes fetch no activation bytes.
+// Four waves per SIMD hold the whole T = 1 grid of a DeepSeek-V3-sized layer
+// at once; the int4 unpacking and the 4-block variant need more registers.
 template <int MAXB, int KIND>
-__global__ __launch_bounds__(kMoeGemvWaves * kWave) void moe_gemv_kernel(
-    const uint8_t* __restrict__ act, const float* __restrict__ act_s, int act_div, int K,
-    const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
+__global__ __launch_bounds__(kMoeGemvWaves * kWave, (MAXB == 1 && KIND != kW4) ? 4 : 2) void
+moe_gemv_kernel(
+    const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_div,
+    int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ active, const int32_t* __restrict__ num_active,
     const uint8_t* __restrict__ w, const void* __restrict__ ws, int N, int numel, int splits,
     float* __restrict__ partial, const float* __restrict__ route_w, uint16_t* __restrict__ y) {
   using KB_ = KindBytes<KIND>;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  constexpr int U = kGemvU;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const int li = lane % 16, lg = lane / 16;
   const int ntile = blockIdx.x * kMoeGemvWaves + wave;
   if (ntile * 16 >= N) return;  // wave-uniform, no barriers in this kernel
   const int slot = blockIdx.y;
-  if (slot >= num_active[0]) return;
+  // The exit test reads both values, so both loads are in flight together;
+  // active[] has one entry per expert and gridDim.y never exceeds the expert
+  // count, so the read is in bounds.
   const int e = active[slot];
-  const int seg0 = offsets[e];
-  const int nblk = (offsets[e + 1] - seg0) / kGemvBlock;
+  const int na = num_active[0];
+  if (slot >= na || e < 0) return;
   const int split = blockIdx.z;
   const int KS = K / KB_::kElems;                    // K steps
-  const int64_t arowb = static_cast<int64_t>(KS) * KB_::kAct;
+  const int arowb = KS * KB_::kAct;
   const int64_t wrowb = static_cast<int64_t>(KS) * KB_::kW;
   const int NB = (N + 127) / 128;
   const int kb0 = split * KS / splits, kb1 = (split + 1) * KS / splits;
@@ -129,62 +167,95 @@ __global__ __launch_bounds__(kMoeGemvWaves * kWave) void moe_gemv_kernel(
     for (int r = 0; r < 4; ++r)
       wsw[r] = static_cast<const uint16_t*>(ws) + (static_cast<int64_t>(e) * N + n + r) * KS;
   }
+  // kFp8 block scales of the wave's rows through a descriptor: uniform values
+  // read by vector loads, which queue behind the weight loads instead of
+  // making the weight stream wait for scalar loads.
+  const __amdgpu_buffer_rsrc_t wsrs = buffer_rsrc(wsr, KIND == kFp8 ? KS * 4 : 0);
+  const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(act, act_bytes);
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(act_s, KIND == kFp8 ? act_bytes / 32 : 0);
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
 
-  for (int b0 = 0; b0 < nblk; b0 += MAXB) {
-    const int nb = min(MAXB, nblk - b0);
-    int rr[MAXB];
-    const uint8_t* arow[MAXB];
-    const float* asr[MAXB];
+  // One K group of weights (U steps from kb, clamped to the split's range).
+  v8i wf[U];
+  float sb[U];
+  v4f sw[U];
+  auto load_w = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = min(kb + u, kb1 - 1);
+      wf[u] = weight_frag<KIND>(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
+      sb[u] = 0.f;
+      sw[u] = zero;
+      if constexpr (KIND == kFp8)
+        sb[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsrs, k * 4, 0, 0));
+      if constexpr (KIND == kW4)
+        sw[u] = v4f{bf16_to_f32(wsw[0][k]), bf16_to_f32(wsw[1][k]), bf16_to_f32(wsw[2][k]),
+                    bf16_to_f32(wsw[3][k])};
+    }
+  };
+  uint32_t aoff[MAXB];  // byte offset of each block's activation row (kBufferOff: padding)
+  v4f acc[MAXB];
+  // Activation loads and MFMAs of the group at kb with the weights in wf.
+  // Steps past the split's end take masked (zero) activations, so the group
+  // has no branches: their products are exactly zero.
+  auto group = [&](int kb, int nb) {
 #pragma unroll
     for (int b = 0; b < MAXB; ++b) {
-      const int r = sorted[seg0 + (b0 + min(b, nb - 1)) * kGemvBlock + li];
-      const bool valid = r < numel;
-      rr[b] = valid ? r : -1;
-      const int64_t row = valid ? r / act_div : 0;
-      arow[b] = act + row * arowb;
-      asr[b] = KIND == kFp8 ? act_s + row * KS : nullptr;
-    }
-    v4f acc[MAXB];
+      if (b < nb) {
+        v8i xf[U];
+        float as[U];
 #pragma unroll
-    for (int b = 0; b < MAXB; ++b) acc[b] = v4f{0.f, 0.f, 0.f, 0.f};
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-
-    constexpr int U = 4;
-    int kb = kb0;
-    for (; kb <= kb1 - 1; kb += U) {
-      const int nu = min(U, kb1 - kb);
-      v8i wf[U];
-      float sb[U];
-      v4f sw[U];
+        for (int u = 0; u < U; ++u) {
+          const bool live = aoff[b] != kBufferOff && kb + u < kb1;
+          const uint32_t off = live ? aoff[b] + static_cast<uint32_t>((kb + u) * KB_::kAct) : kBufferOff;
+          xf[u] = buffer_frag(ars, off, lg);
+          as[u] = 0.f;
+          if constexpr (KIND == kFp8)  // scale byte offset = activation byte offset / 32
+            as[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  srs, static_cast<int>(live ? off / 32 : kBufferOff), 0, 0));
+        }
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int k = kb + min(u, nu - 1);
-        wf[u] = weight_frag<KIND>(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
-        sb[u] = 0.f;
-        sw[u] = zero;
-        if constexpr (KIND == kFp8) sb[u] = wsr[k];
-        if constexpr (KIND == kW4)
-          sw[u] = v4f{bf16_to_f32(wsw[0][k]), bf16_to_f32(wsw[1][k]), bf16_to_f32(wsw[2][k]),
-                      bf16_to_f32(wsw[3][k])};
-      }
-#pragma unroll
-      for (int b = 0; b < MAXB; ++b) {
-        if (b < nb) {
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            if (u < nu) {
-              const v8i xf = global_frag(arow[b] + static_cast<int64_t>(kb + u) * KB_::kAct, lg);
-              if constexpr (KIND == kFp8) {
-                fma4(acc[b], mfma_fp8(wf[u], xf, zero), asr[b][kb + u] * sb[u]);
-              } else if constexpr (KIND == kW4) {
-                fma4v(acc[b], mfma_fp8(wf[u], xf, zero), sw[u]);
-              } else {
-                acc[b] = mfma_bf16x2(wf[u], xf, acc[b]);
-              }
-            }
+        for (int u = 0; u < U; ++u) {
+          if constexpr (KIND == kFp8) {
+            fma4(acc[b], mfma_fp8(wf[u], xf[u], zero), as[u] * sb[u]);
+          } else if constexpr (KIND == kW4) {
+            fma4v(acc[b], mfma_fp8(wf[u], xf[u], zero), sw[u]);
+          } else {
+            acc[b] = mfma_bf16x2(wf[u], xf[u], acc[b]);
           }
         }
       }
+    }
+  };
+
+  const int seg0 = offsets[e];
+  const int nblk = (offsets[e + 1] - seg0) / kGemvBlock;  // >= 1 for an active expert
+  int b0 = 0;
+  do {
+    load_w(kb0);  // first group: in flight while the routes are resolved
+    const int nb = min(MAXB, nblk - b0);
+    int rr[MAXB];
+#pragma unroll
+    for (int b = 0; b < MAXB; ++b) {
+      int r = numel;
+      if (b < nb) {
+        const int32_t* ids = sorted + seg0 + (b0 + b) * kGemvBlock;
+        int sid[kGemvBlock];
+#pragma unroll
+        for (int j = 0; j < kGemvBlock; ++j) sid[j] = ids[j];
+        r = sid[0];
+#pragma unroll
+        for (int j = 1; j < kGemvBlock; ++j) r = li == j ? sid[j] : r;
+      }
+      const bool valid = r >= 0 && r < numel;
+      rr[b] = valid ? r : -1;
+      aoff[b] = valid ? static_cast<uint32_t>((r / act_div) * arowb) : kBufferOff;
+      acc[b] = zero;
+    }
+    group(kb0, nb);
+    for (int kb = kb0 + U; kb < kb1; kb += U) {
+      load_w(kb);
+      group(kb, nb);
     }
 #pragma unroll
     for (int b = 0; b < MAXB; ++b) {
@@ -200,7 +271,8 @@ __global__ __launch_bounds__(kMoeGemvWaves * kWave) void moe_gemv_kernel(
             float4{a[0], a[1], a[2], a[3]};
       }
     }
-  }
+    b0 += MAXB;
+  } while (b0 < nblk);
 }
 
 // Gate/up sums of 8 consecutive columns c0.. of route r: split partials in a
@@ -998,9 +1070,10 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
 
 // ------------------------------------------------------------ host side ---
 // Split-K factor of the decode GEMVs: enough waves to cover the chip
-// (>= 4096 over the active experts' n-tiles), at least 4 K steps per split.
+// (kGemvTargetWaves over the active experts' n-tiles), at least 4 K steps
+// per split.
 static int moe_splits(int64_t waves_per_split, int KS) {
-  int s = static_cast<int>((4096 + waves_per_split - 1) / waves_per_split);
+  int s = static_cast<int>((kGemvTargetWaves + waves_per_split - 1) / waves_per_split);
   return max(1, min(s, max(1, KS / 4)));
 }
 
@@ -1059,6 +1132,25 @@ static int raise_dma_lds() {
   return VMAMD_OK;
 }
 
+// Bytes of a decode GEMV's activation operand ([rows, K]); the GEMV reads it
+// through a buffer descriptor, which the callers keep below 2 GiB.
+template <int KIND>
+static int gemv_act_bytes(int64_t rows, int64_t K) {
+  return static_cast<int>(rows * (K / KindBytes<KIND>::kElems) * KindBytes<KIND>::kAct);
+}
+
+// Decode GEMV launch: an expert holds at most T routes when each token's
+// top-k ids are distinct, so T <= 16 needs one 16-route block per pass
+// (MAXB = 1, fewer registers); more blocks are still handled, by re-streaming
+// the expert's weights once per block.
+template <int KIND, typename... Args>
+static void launch_gemv(dim3 grid, hipStream_t st, int T, Args... args) {
+  if (T <= kGemvBlock)
+    moe_gemv_kernel<1, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
+  else
+    moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
+}
+
 // Launches of the two stages; arguments are validated by the callers.  kBf16:
 // xa is x itself, xs / w13_s / a2s unused.  kW4: xs are the token row scales,
 // a2 receives the bf16 activation (quantised per row by the caller).
@@ -1073,9 +1165,9 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
     const int s13 = w13_splits(numel, E, H, I, KIND);
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s13);
-    moe_gemv_kernel<4, KIND><<<g13, kMoeGemvWaves * kWave, 0, st>>>(
-        xa, xs, topk, H, sorted, offs, active, nact, w13, w13_s, 2 * I, numel, s13, scratch,
-        nullptr, nullptr);
+    launch_gemv<KIND>(g13, st, T, xa, gemv_act_bytes<KIND>(T, H), xs, topk, H, sorted, offs, active,
+                      nact, w13, w13_s, 2 * I, numel, s13, scratch,
+                      static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr));
     int rc = check_launch("moe w13 (gemv)");
     if (rc) return rc;
     if constexpr (KIND == kFp8) {
@@ -1121,12 +1213,13 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g2((H / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s2);
     if (s2 == 1) {
-      moe_gemv_kernel<4, KIND><<<g2, kMoeGemvWaves * kWave, 0, st>>>(
-          a2, a2s, 1, I, sorted, offs, active, nact, w2, w2_s, H, numel, 1, nullptr, yscale, y);
+      launch_gemv<KIND>(g2, st, T, a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs,
+                        active, nact, w2, w2_s, H, numel, 1, static_cast<float*>(nullptr), yscale, y);
       return check_launch("moe w2 (gemv)");
     }
-    moe_gemv_kernel<4, KIND><<<g2, kMoeGemvWaves * kWave, 0, st>>>(
-        a2, a2s, 1, I, sorted, offs, active, nact, w2, w2_s, H, numel, s2, scratch, nullptr, nullptr);
+    launch_gemv<KIND>(g2, st, T, a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs, active,
+                      nact, w2, w2_s, H, numel, s2, scratch, static_cast<const float*>(nullptr),
+                      static_cast<uint16_t*>(nullptr));
     int rc = check_launch("moe w2 (gemv)");
     if (rc) return rc;
     const int64_t mn = static_cast<int64_t>(numel) * H;
@@ -1205,6 +1298,8 @@ static int check_stage_common(const char* who, int64_t T, int topk, int E, int64
   VMAMD_REQUIRE(block_m == kGemvBlock || block_m == kMoeBM, "%s: block_m must be %d or %d (got %d)",
                 who, kGemvBlock, kMoeBM, block_m);
   VMAMD_REQUIRE(T * topk < (1ll << 30) && T * H < (1ll << 40), "%s: problem too large", who);
+  VMAMD_REQUIRE(block_m != kGemvBlock || (T * H * 2 < (1ll << 31) && T * topk * I * 2 < (1ll << 31)),
+                "%s: the decode path (block_m 16) takes activations below 2 GiB", who);
   VMAMD_REQUIRE(cap >= T * topk + static_cast<int64_t>(E) * (block_m - 1) && cap < (1ll << 31),
                 "%s: capacity %lld < T*topk + E*(block_m-1)", who, (long long)cap);
   return VMAMD_OK;
