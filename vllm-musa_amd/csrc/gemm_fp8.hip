@@ -87,12 +87,27 @@ __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
     for (int nt = 0; nt < P::NT; ++nt) f.w[nt] = lds_frag(st + P::kOffB, wn * P::WTN + nt * 16 + li, lg);
   };
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  // The per-K-block scale promotion (acc += p * sa * sb, 4 FMAs) of MFMA i-1
+  // runs while MFMA i executes: products rotate through two registers, and the
+  // schedule is pinned to MFMA, 4 FMAs, MFMA, ... so the matrix core is not
+  // left waiting for the promotion of its own last result.
   auto mma = [&](const Frags& f) {
+    constexpr int NI = P::MT * P::NT;
+    float sab[P::MT];
 #pragma unroll
-    for (int mt = 0; mt < P::MT; ++mt) {
-      const float sab = f.sa[mt] * f.sb;
+    for (int mt = 0; mt < P::MT; ++mt) sab[mt] = f.sa[mt] * f.sb;
+    v4f t[2];
 #pragma unroll
-      for (int nt = 0; nt < P::NT; ++nt) fma4(acc[mt][nt], mfma_fp8(f.w[nt], f.x[mt], zero), sab);
+    for (int i = 0; i <= NI; ++i) {
+      if (i < NI) {
+        t[i & 1] = mfma_fp8(f.w[i % P::NT], f.x[i / P::NT], zero);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      }
+      if (i > 0) {
+        const int j = i - 1;
+        fma4(acc[j / P::NT][j % P::NT], t[j & 1], sab[j / P::NT]);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // its predecessor's 4 FMAs
+      }
     }
   };
   // Step kb: its fragments are in `cur`; buffer kb % NS (already read into

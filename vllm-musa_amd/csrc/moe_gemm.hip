@@ -388,13 +388,19 @@ __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(const float* __restr
 constexpr int kMoeBM = 128;
 
 // Expert-major decode of a logical tile index: all blocks of (expert, tn)
-// are consecutive.  Returns false past the used tiles.
+// are consecutive.  The grid covers the worst case (max_tiles, a multiple of
+// kXcds after xcd_grid); the tiles actually used are split into kXcds
+// contiguous ranges, one per XCD (workgroup wg runs on XCD wg % kXcds), so
+// every XCD gets an equal share whatever the routing.  Returns false for
+// workgroups past the used tiles.
 __device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* __restrict__ offsets,
                                          const int32_t* __restrict__ ntpp, int E, int TN,
                                          int& e_out, int& mb_out, int& tn_out) {
-  const int per = (max_tiles + kXcds - 1) / kXcds;
-  const int L = (wg % kXcds) * per + wg / kXcds;
-  const int used = ntpp[0] / kMoeBM * TN;
+  const int used = min(ntpp[0] / kMoeBM * TN, max_tiles);
+  const int per = (used + kXcds - 1) / kXcds;
+  const int q = wg / kXcds;
+  if (q >= per) return false;
+  const int L = (wg % kXcds) * per + q;
   if (L >= used) return false;
   // largest e with offsets[e] / BM * TN <= L (empty experts collapse onto the next)
   int lo = 0, hi = E - 1;
@@ -848,9 +854,9 @@ __global__ __launch_bounds__(256, 2) void moe_w2_gemm_kernel(
 // the current step's MFMAs run.  W13: the 256 weight rows are 128 gate + 128
 // up rows interleaved by 16 (epilogue: SiLU-and-mul, and for kFp8 the 1x128
 // a2 quantiser); W2: 256 hidden rows (epilogue: routed weight).  Padding
-// closes each expert's segment, so a 16-route fragment holds only padding iff
-// its first route does; such fragments skip their MFMAs (a wave-uniform test).
-// Padding rows load token 0's activations; their outputs are never used.
+// closes each expert's segment, so a wave whose first route is padding holds
+// no route and skips its MFMAs (a wave-uniform test).  Padding rows load
+// token 0's activations; their outputs are never used.
 using MoePipeFp8 = TilePipe<true, 128, 256, 2, 4, 3>;
 using MoePipeBf16 = TilePipe<false, 128, 256, 2, 4, 3>;
 template <int KIND>
@@ -920,9 +926,9 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
     }
     p.stepS = 4;
   }
-  bool live[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) live[mt] = sorted[mb * BM + wm * P::WTM + mt * 16] < numel;
+  // Padding routes close a block, so a wave whose first route is padding
+  // holds none.
+  const bool wave_live = sorted[mb * BM + wm * P::WTM] < numel;
 
   v4f acc[MT][NT];
 #pragma unroll
@@ -953,19 +959,40 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
     for (int nt = 0; nt < NT; ++nt) f.w[nt] = lds_frag(st + P::kOffB, wn * P::WTN + nt * 16 + li, lg);
   };
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  // MFMAs of all the wave's fragments (a partly padded wave computes its
+  // padding too: a second, per-fragment form of this sequence costs register
+  // spills).  kFp8: the scale promotion of MFMA i-1 (acc += p * sa * sb, 4
+  // FMAs) runs while MFMA i executes -- products rotate through two
+  // registers and the schedule is pinned to MFMA, 4 FMAs, MFMA, ... -- so the
+  // matrix core does not wait for the promotion of its own last result.
   auto mma = [&](const Frags& f) {
+    if (!wave_live) return;
+    if constexpr (KIND == kFp8) {
+      constexpr int NI = MT * NT;
+      float sc[MT][2];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if (!live[mt]) continue;
-      if constexpr (KIND == kFp8) {
-        const float s0 = f.sa[mt] * f.sb0, s1 = f.sa[mt] * f.sb1;
+      for (int mt = 0; mt < MT; ++mt) {
+        sc[mt][0] = f.sa[mt] * f.sb0;
+        sc[mt][1] = W13 ? f.sa[mt] * f.sb1 : sc[mt][0];
+      }
+      v4f t[2];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          fma4(acc[mt][nt], mfma_fp8(f.w[nt], f.x[mt], zero), (W13 && (nt & 1)) ? s1 : s0);
-      } else {
+      for (int i = 0; i <= NI; ++i) {
+        if (i < NI) {
+          t[i & 1] = mfma_fp8(f.w[i % NT], f.x[i / NT], zero);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        if (i > 0) {
+          const int j = i - 1, mt = j / NT, nt = j % NT;
+          fma4(acc[mt][nt], t[j & 1], sc[mt][nt & 1]);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma_bf16x2(f.w[nt], f.x[mt], acc[mt][nt]);
-      }
     }
   };
   auto step = [&](int kb, const Frags& cur, Frags& nxt) {
