@@ -102,6 +102,7 @@ __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
       if (i < NI) {
         t[i & 1] = mfma_fp8(f.w[i % P::NT], f.x[i / P::NT], zero);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two of the next step's LDS reads
       }
       if (i > 0) {
         const int j = i - 1;
@@ -110,16 +111,18 @@ __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
       }
     }
   };
-  // Step kb: its fragments are in `cur`; buffer kb % NS (already read into
-  // `cur`) is refilled with step kb + NS, step kb + 1 is read into `nxt`.
+  // Step kb: its fragments are in `cur`; step kb + 1 is read into `nxt`, two
+  // LDS reads after each MFMA, and buffer kb % NS (read into `cur` by every
+  // wave before the barrier) is refilled with step kb + NS after the MFMAs
+  // are issued -- a wave whose DMA issue waits behind the other waves' in the
+  // address unit would otherwise start its MFMAs late.
   auto step = [&](int kb, const Frags& cur, Frags& nxt) {
     wait_lgkmcnt0();  // this wave's reads of the buffer refilled below are done
     wait_vmcnt<(NS - 2) * P::kIPS>();
     barrier_lds();
-    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
     read(smem_dyn + ((kb + 1) % NS) * P::kStage, nxt);
-    __builtin_amdgcn_sched_barrier(0);  // the reads issue before the MFMAs they overlap
     mma(cur);
+    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
   };
 
 #pragma unroll

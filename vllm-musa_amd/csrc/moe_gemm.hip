@@ -981,6 +981,7 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
         if (i < NI) {
           t[i & 1] = mfma_fp8(f.w[i % NT], f.x[i / NT], zero);
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
         if (i > 0) {
           const int j = i - 1, mt = j / NT, nt = j % NT;
@@ -995,14 +996,17 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma_bf16x2(f.w[nt], f.x[mt], acc[mt][nt]);
     }
   };
+  // Step kb: `nxt` is read (two LDS reads after each MFMA) while `cur` runs
+  // on MFMA; buffer kb % NS is refilled with step kb + NS after the MFMAs are
+  // issued, so a wave does not start its MFMAs late behind the DMA issue of
+  // the other waves.
   auto step = [&](int kb, const Frags& cur, Frags& nxt) {
     wait_lgkmcnt0();
     wait_vmcnt<(NS - 2) * P::kIPS>();
     barrier_lds();
-    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
     read(smem_dyn + ((kb + 1) % NS) * P::kStage, nxt);
-    __builtin_amdgcn_sched_barrier(0);
     mma(cur);
+    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
   };
 #pragma unroll
   for (int s = 0; s < NS; ++s) p.issue(smem_dyn + s * P::kStage, min(s, KS - 1));
