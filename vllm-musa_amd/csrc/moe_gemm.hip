@@ -384,6 +384,57 @@ __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(const float* __restr
   *reinterpret_cast<uint2*>(y + i4) = pack_bf16x4(acc.x * rw, acc.y * rw, acc.z * rw, acc.w * rw);
 }
 
+// Decode W2 with split-K partials, reduce and top-k combine in one pass:
+//   out[t, n] = bf16( sum_k y_k ),  y_k = bf16(sum_s partial[s, r, n] * yscale[r])
+// (kW4: sum_k fma(y_k, topk_weights[r], .), yscale being the a2 row scale),
+// r = t * topk + k in slot order -- the same operations, in the same order, as
+// moe_w2_reduce_kernel followed by the top-k sum, without the y round trip.
+// Slots of dropped routes (negative id, or not local through expert_map) are
+// skipped; their partial rows were never written.
+template <bool WEIGHTED>
+__global__ __launch_bounds__(256) void moe_w2_combine_kernel(
+    const float* __restrict__ partial, int splits, int T, int topk, int N,
+    const int32_t* __restrict__ ids, const int32_t* __restrict__ emap, int64_t emap_len,
+    const float* __restrict__ yscale, const float* __restrict__ topk_w, uint16_t* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int cpr = N / 8;
+  if (i >= static_cast<int64_t>(T) * cpr) return;
+  const int t = static_cast<int>(i / cpr);
+  const int n = static_cast<int>(i % cpr) * 8;
+  const int64_t mn = static_cast<int64_t>(T) * topk * N;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < topk; ++k) {
+    const int r = t * topk + k;
+    const int e = ids[r];
+    if (e < 0 || (emap && (e >= emap_len || emap[e] < 0))) continue;
+    const float* src = partial + static_cast<int64_t>(r) * N + n;
+    float4 a = *reinterpret_cast<const float4*>(src);
+    float4 b = *reinterpret_cast<const float4*>(src + 4);
+    for (int sp = 1; sp < splits; ++sp) {
+      const float4 c = *reinterpret_cast<const float4*>(src + sp * mn);
+      const float4 d = *reinterpret_cast<const float4*>(src + sp * mn + 4);
+      a.x += c.x; a.y += c.y; a.z += c.z; a.w += c.w;
+      b.x += d.x; b.y += d.y; b.z += d.z; b.w += d.w;
+    }
+    const float sc = yscale ? yscale[r] : 1.0f;
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    if constexpr (WEIGHTED) {
+      const float wk = topk_w[r];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = fmaf(bf16r(v[j] * sc), wk, acc[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += bf16r(v[j] * sc);
+    }
+  }
+  uint4 o;
+  o.x = static_cast<uint32_t>(f32_to_bf16(acc[0])) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16);
+  o.y = static_cast<uint32_t>(f32_to_bf16(acc[2])) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16);
+  o.z = static_cast<uint32_t>(f32_to_bf16(acc[4])) | (static_cast<uint32_t>(f32_to_bf16(acc[5])) << 16);
+  o.w = static_cast<uint32_t>(f32_to_bf16(acc[6])) | (static_cast<uint32_t>(f32_to_bf16(acc[7])) << 16);
+  *reinterpret_cast<uint4*>(out + static_cast<int64_t>(t) * N + n) = o;
+}
+
 // ------------------------------------------------------ prefill GEMMs -----
 constexpr int kMoeBM = 128;
 
@@ -1230,19 +1281,40 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
 }
 
 // kW4: a2s are the a2 row scales and take the routed weight's place in y.
+// combined_out: when given and the decode path splits K, the reduce and the
+// top-k combine run as one kernel writing the layer output there (y is not
+// written) and *combined is set; otherwise y is written as usual.
 template <int KIND>
 static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const int32_t* sorted,
                      int64_t cap, int block_m, const int32_t* offs, const int32_t* ntpp,
                      const int32_t* active, const int32_t* nact, const uint8_t* w2, const void* w2_s,
                      int E, int H, int I, const float* topk_weights, const int32_t* topk_ids,
                      const int32_t* emap, int64_t emap_len, uint16_t* y, float* scratch,
-                     hipStream_t st) {
+                     hipStream_t st, uint16_t* combined_out = nullptr, bool* combined = nullptr) {
   const int numel = T * topk;
   const float* yscale = KIND == kW4 ? a2s : topk_weights;
+  if (combined) *combined = false;
   if (block_m == kGemvBlock) {
     const int s2 = w2_splits(numel, E, H, I, KIND);
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g2((H / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s2);
+    if (s2 > 1 && combined_out && combined && H % 8 == 0) {
+      launch_gemv<KIND>(g2, st, T, a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs, active,
+                        nact, w2, w2_s, H, numel, s2, scratch, static_cast<const float*>(nullptr),
+                        static_cast<uint16_t*>(nullptr));
+      int rc = check_launch("moe w2 (gemv)");
+      if (rc) return rc;
+      const int64_t chunks = static_cast<int64_t>(T) * (H / 8);
+      const int blocks = static_cast<int>((chunks + 255) / 256);
+      if constexpr (KIND == kW4)
+        moe_w2_combine_kernel<true><<<blocks, 256, 0, st>>>(scratch, s2, T, topk, H, topk_ids, emap,
+                                                            emap_len, yscale, topk_weights, combined_out);
+      else
+        moe_w2_combine_kernel<false><<<blocks, 256, 0, st>>>(scratch, s2, T, topk, H, topk_ids, emap,
+                                                             emap_len, yscale, nullptr, combined_out);
+      *combined = true;
+      return check_launch("moe w2 (combine)");
+    }
     if (s2 == 1) {
       launch_gemv<KIND>(g2, st, T, a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs,
                         active, nact, w2, w2_s, H, numel, 1, static_cast<float*>(nullptr), yscale, y);
@@ -1403,10 +1475,12 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     rc = vmamd_per_token_quant_fp8(act_out, arows, I, I, 1e-4f, -448.f, 448.f, a2, a2s, stream);
     if (rc) return rc;
   }
+  bool combined = false;
   rc = launch_w2<KIND>(a2, a2s, t, topk, sorted, cap, bm, offs, ntpp, active, nact,
                        static_cast<const uint8_t*>(w2), w2_s, E, h, i, topk_weights, topk_ids,
-                       expert_map, expert_map_len, y, scratch, st);
-  if (rc) return rc;
+                       expert_map, expert_map_len, y, scratch, st, static_cast<uint16_t*>(out),
+                       &combined);
+  if (rc || combined) return rc;
   // Slots of dropped routes (negative ids, or non-local experts) hold no
   // expert output and are skipped by the combine.
   if constexpr (KIND == kW4)
