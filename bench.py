@@ -11,14 +11,16 @@ activations ~N(0, 1), logits ~N(0, 1), score bias ~N(0, 0.1).
 Printed (rank 0, one JSON line): value = algorithmic TFLOP/s of the layer at
 T=4096 (2*T*topk*3*H*I flops per call), ms_per_step from HIP events around the
 K timed steps; `sweep` gives us / TFLOP/s / GB/s and roofline fractions at
-T = 1, 16, 256, 4096 (cold weights: a 1 GiB buffer is rewritten between
+T = 1, 16, 256, 4096 (cold weights: a 1 GiB buffer is read between
 iterations; `graph_us` is the same step replayed from a HIP graph, as a
 serving engine runs decode); `roofline` is the dominant kernel (W13 grouped
-GEMM at T=4096)
-timed on its own with HIP events on its launch stream; `cpu_baseline` times
-the CPU oracle on a bounded sample of the same layer.
+GEMM at T=4096) timed on its own with HIP events on its launch stream, its
+`traffic` (HBM bytes per launch) read from the committed rocprofv3 counter
+summary; `cpu_baseline` times the CPU oracle on a bounded sample of the same
+layer.
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-sweep] [--no-cpu]
+  python bench.py --traffic-probe   # the launches profiled for FETCH_SIZE / WRITE_SIZE
 """
 from __future__ import annotations
 
@@ -44,6 +46,21 @@ SWEEP_T = (1, 16, 256, 4096)
 WEIGHT_SEED = 3000
 
 METRIC = "fp8-block MoE layer µs, TFLOPS & HBM GB/s (% roofline) at T=1..4096"
+
+# rocprofv3 counter summary of the W13 kernel at T=4096 (FETCH_SIZE and
+# WRITE_SIZE per dispatch, scaled by a 1 GiB copy); its
+# "traffic_bytes_per_launch:" line fills roofline.traffic.
+TRAFFIC_SUMMARY = os.path.join("profiles", "moe_w13_gemm_fp8_dsv3_T4096_traffic.md")
+
+
+def read_traffic() -> int | None:
+    path = os.path.join(ROOT, TRAFFIC_SUMMARY)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
 
 
 def layer_flops(routes: int) -> float:
@@ -179,6 +196,12 @@ def main() -> int:
     ap.add_argument("--sweep-iters", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the W13 kernel at T=4096 three times, then three "
+                         "1 GiB device copies (the counter calibration), for rocprofv3 --pmc")
+    ap.add_argument("--profile-t", type=int, default=0,
+                    help="only run --steps layer steps at this T (caches flushed by a 1 GiB "
+                         "read before each), for rocprofv3 --kernel-trace; prints no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE layer runs on a single MI355X here "
@@ -197,6 +220,42 @@ def main() -> int:
     log(f"bench: building E={E} H={H} I={I} fp8 expert stack")
     weights = synthetic.moe_fp8_weights(E, H, I, WEIGHT_SEED)
     torch.cuda.synchronize()
+
+    if args.traffic_probe:
+        layer = Layer(torch, T_HEADLINE, weights)
+        w, ids = layer.route()
+        st = Fp8MoeStages(layer.x, *weights, w, ids, path="auto")
+        st.quant()
+        st.align()
+        for _ in range(3):
+            st.w13_stage()
+        torch.cuda.synchronize()
+        del st, layer, weights
+        torch.cuda.empty_cache()
+        # Calibration: a plain 1 GiB device copy whose source was evicted from
+        # the caches by reading another 1 GiB first.
+        src = torch.ones(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        other = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+        for _ in range(3):
+            other.max()
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("bench: traffic probe done (3 W13 launches, 3 x 1 GiB copies)")
+        return 0
+
+    if args.profile_t > 0:
+        layer = Layer(torch, args.profile_t, weights)
+        flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+        for _ in range(args.warmup):
+            layer.step()
+        for _ in range(args.steps):
+            flush_buf.max()
+            torch.cuda.synchronize()
+            layer.step()
+        torch.cuda.synchronize()
+        log(f"bench: profile run done ({args.steps} steps at T={args.profile_t})")
+        return 0
 
     # ---------------------------------------------------------- headline --
     layer = Layer(torch, T_HEADLINE, weights)
@@ -232,8 +291,9 @@ def main() -> int:
     k_bytes = w13_bytes(T_HEADLINE, u_head)
     k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                "kernel": "moe_w13_gemm_fp8_kernel",
+                "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": read_traffic(),
+                "traffic_source": TRAFFIC_SUMMARY,
+                "kernel": "moe_gemm_dma_kernel<kFp8, W13>",
                 "kernel_us": round(k_ms * 1e3, 1),
                 "kernel_tflops": round(2.0 * T_HEADLINE * TOPK * 2 * I * H / (k_ms * 1e-3) / 1e12, 1),
                 "algorithmic_bytes": int(k_bytes)}
