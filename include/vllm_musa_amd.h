@@ -208,8 +208,9 @@ int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64_t as_strid
  * topk_weights f32 / topk_ids i32 [T, topk] (negative ids and experts mapped
  * to a negative local id contribute nothing); out [T, H] bf16.
  * swiglu_limit > 0 selects the clamped activation.  path: AUTO picks the
- * decode (expert-major GEMV, weights streamed once) or the prefill (grouped
- * MFMA GEMM) kernels by T; GEMV / GEMM force one.  Workspace:
+ * decode (expert-major GEMV, weights streamed once) kernels while T*topk <=
+ * 2.5*E (12*E for the bf16 and w4afp8 layers) and the prefill (grouped MFMA
+ * GEMM) kernels above; GEMV / GEMM force one.  Workspace:
  * vmamd_fused_moe_fp8_workspace_size() bytes, 256-byte aligned.
  * Replaces fused_experts_impl / _musa_fused_experts_impl_dispatch
  * (vllm_musa/model_executor/layers/fused_moe/fused_moe.py:1935-2184,

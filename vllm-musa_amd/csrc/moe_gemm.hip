@@ -1382,13 +1382,18 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   return w;
 }
 
-// Decode kernels (GEMV over 16-route blocks) while an expert receives about
-// one block of routes on average (or up to 64 tokens), the grouped GEMM over
-// 128-route blocks above: below that the 128-row tiles are mostly padding.
-static int moe_block_m(int64_t T, int topk, int E, int path) {
+// Path choice of `auto`: the decode kernels (GEMV over 16-route blocks) up to
+// a number of routes per expert measured on MI355X, the grouped GEMMs over
+// 128-route blocks above.  Measured crossovers (graph replay, caches
+// flushed): fp8 DeepSeek-V3 (E=256, H=7168, I=2048, top-8) between 2 and 3
+// routes per expert (T=64 / 96); bf16 (E=128, H=2048, I=768) and w4afp8
+// (E=128, H=4096, I=1536) between 8 and 16 (T=128 / 256).
+static int moe_block_m(int64_t T, int topk, int E, int path, int kind) {
   if (path == VMAMD_MOE_PATH_GEMV) return kGemvBlock;
   if (path == VMAMD_MOE_PATH_GEMM) return kMoeBM;
-  return (T <= 64 || T * topk <= static_cast<int64_t>(kGemvBlock) * E) ? kGemvBlock : kMoeBM;
+  const int64_t routes = T * topk;
+  const int64_t limit = kind == kFp8 ? (5 * static_cast<int64_t>(E)) / 2 : 12 * static_cast<int64_t>(E);
+  return routes <= limit ? kGemvBlock : kMoeBM;
 }
 
 static int check_stage_common(const char* who, int64_t T, int topk, int E, int64_t H, int64_t I,
@@ -1417,7 +1422,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
                        vmamd_stream_t stream) {
   VMAMD_REQUIRE(path >= VMAMD_MOE_PATH_AUTO && path <= VMAMD_MOE_PATH_GEMM, "%s: unknown path %d",
                 who, path);
-  const int bm = moe_block_m(T, topk, E, path);
+  const int bm = moe_block_m(T, topk, E, path, KIND);
   const int64_t cap = T * topk + static_cast<int64_t>(E) * (bm - 1);
   int rc = check_stage_common(who, T, topk, E, H, I, bm, cap);
   if (rc) return rc;
@@ -1582,7 +1587,7 @@ extern "C" int vmamd_moe_fp8_w2(const void* a2q, const float* a2s, int64_t T, in
 
 extern "C" size_t vmamd_fused_moe_fp8_workspace_size(int64_t T, int topk, int num_experts,
                                                      int64_t H, int64_t I, int path) {
-  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path), kFp8).total;
+  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path, kFp8), kFp8).total;
 }
 
 extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H,
@@ -1633,7 +1638,7 @@ extern "C" int vmamd_moe_bf16_w2(const void* a2, int64_t T, int topk,
 
 extern "C" size_t vmamd_fused_moe_bf16_workspace_size(int64_t T, int topk, int num_experts,
                                                       int64_t H, int64_t I, int path) {
-  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path), kBf16).total;
+  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path, kBf16), kBf16).total;
 }
 
 extern "C" int vmamd_fused_moe_bf16(const void* x, int64_t T, int64_t H, const void* w13,
@@ -1650,7 +1655,7 @@ extern "C" int vmamd_fused_moe_bf16(const void* x, int64_t T, int64_t H, const v
 // --------------------------------------------------------------- w4afp8 ---
 extern "C" size_t vmamd_w4afp8_moe_workspace_size(int64_t T, int topk, int num_experts, int64_t H,
                                                   int64_t I, int path) {
-  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path), kW4).total;
+  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path, kW4), kW4).total;
 }
 
 extern "C" int vmamd_w4afp8_moe(const void* x, int64_t T, int64_t H, const void* w13,

@@ -183,7 +183,10 @@ class MoeStages:
         self.topk = topk_ids.shape[1]
         self.t = t
         numel = t * self.topk
-        gemv = path == "gemv" or (path == "auto" and (t <= 64 or numel <= 16 * self.e))
+        # `auto`: the rule of moe_block_m (csrc/moe_gemm.hip) -- decode kernels up to
+        # 2.5 routes per expert for fp8, 12 for bf16 (measured crossovers).
+        limit = (5 * self.e) // 2 if self.fp8 else 12 * self.e
+        gemv = path == "gemv" or (path == "auto" and numel <= limit)
         self.block_m = 16 if gemv else 128
         self.w13, self.w2 = w13.contiguous(), w2.contiguous()
         if self.fp8:
