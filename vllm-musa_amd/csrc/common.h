@@ -92,24 +92,6 @@ __device__ __forceinline__ float fp8_to_f32(uint32_t byte) {
 }
 
 // ----------------------------------------------------------- wave utils ---
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
-}
-// Max over aligned groups of `W` lanes (W a power of two <= 64).
-template <int W>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int m = W / 2; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
-}
-
 // Cross-lane moves in DPP form (a VALU operand modifier: no LDS round trip).
 constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]: lane ^ 1
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]: lane ^ 2
@@ -125,6 +107,41 @@ __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
 
+// Value of lane `src` (wave-uniform) in every lane.  A readlane reads the
+// lane's register whether or not that lane is still active, so the 32- and
+// 64-lane forms below need every lane of the wave live.
+__device__ __forceinline__ float lane_value(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+__device__ __forceinline__ int lane_value(int v, int src) { return __builtin_amdgcn_readlane(v, src); }
+
+// Max over aligned groups of `W` lanes (W a power of two <= 64), every lane of
+// a group ending with it.  Max is order-independent, so the first four steps
+// pair lanes with DPP moves inside each 16-lane row (quad swaps, then the 8-
+// and 16-lane mirrors) and wider groups merge the rows' results read with
+// v_readlane -- no LDS round trip.
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (W >= 2) v = fmaxf(v, dpp_f<kDppXor1>(v));
+  if constexpr (W >= 4) v = fmaxf(v, dpp_f<kDppXor2>(v));
+  if constexpr (W >= 8) v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  if constexpr (W >= 16) v = fmaxf(v, dpp_f<kDppMirror>(v));
+  if constexpr (W == 32) {
+    const float lo = fmaxf(lane_value(v, 0), lane_value(v, 16));
+    const float hi = fmaxf(lane_value(v, 32), lane_value(v, 48));
+    v = __lane_id() < 32 ? lo : hi;
+  }
+  if constexpr (W == 64)
+    v = fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) { return group_max<kWave>(v); }
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
 // Merge (v, idx) with a partner's under the order (value desc, index asc).
 __device__ __forceinline__ void argmax_merge(float& v, int& idx, float ov, int oi) {
   if (ov > v || (ov == v && oi < idx)) {
@@ -134,16 +151,23 @@ __device__ __forceinline__ void argmax_merge(float& v, int& idx, float ov, int o
 }
 
 // Argmax over the wave with ties broken towards the lower index; every lane
-// ends with the result.  The merge is a maximum under a total order, so any
-// pairing that joins disjoint lane sets works: quad swaps and the 8- and
-// 16-lane mirrors run as DPP moves, the 32- and 64-lane steps as shuffles.
+// ends with the result (every lane of the wave must be active).  The merge is
+// a maximum under a total order, so any pairing that joins disjoint lane sets
+// works: quad swaps and the 8- and 16-lane mirrors run as DPP moves inside
+// each 16-lane row, then the four rows' results are read with v_readlane and
+// merged as wave-uniform values.
 __device__ __forceinline__ void wave_argmax(float& v, int& idx) {
   argmax_merge(v, idx, dpp_f<kDppXor1>(v), dpp_i<kDppXor1>(idx));
   argmax_merge(v, idx, dpp_f<kDppXor2>(v), dpp_i<kDppXor2>(idx));
   argmax_merge(v, idx, dpp_f<kDppHalfMirror>(v), dpp_i<kDppHalfMirror>(idx));
   argmax_merge(v, idx, dpp_f<kDppMirror>(v), dpp_i<kDppMirror>(idx));
-  argmax_merge(v, idx, __shfl_xor(v, 16, kWave), __shfl_xor(idx, 16, kWave));
-  argmax_merge(v, idx, __shfl_xor(v, 32, kWave), __shfl_xor(idx, 32, kWave));
+  float v0 = lane_value(v, 0), v1 = lane_value(v, 16), v2 = lane_value(v, 32), v3 = lane_value(v, 48);
+  int i0 = lane_value(idx, 0), i1 = lane_value(idx, 16), i2 = lane_value(idx, 32), i3 = lane_value(idx, 48);
+  argmax_merge(v0, i0, v1, i1);
+  argmax_merge(v2, i2, v3, i3);
+  argmax_merge(v0, i0, v2, i2);
+  v = v0;
+  idx = i0;
 }
 
 // Top-2 (t1 >= t2) of the union of two disjoint value sets.
@@ -154,15 +178,34 @@ __device__ __forceinline__ void top2_merge(float& t1, float& t2, float o1, float
 }
 
 // Top-2 over aligned groups of S lanes (S a power of two <= 64), every lane
-// of a group ending with its group's (t1, t2).
+// of a group ending with its group's (t1, t2); the top-2 of a set does not
+// depend on the merge order, so rows of 16 merge by DPP and wider groups
+// through v_readlane (every lane of the wave must be active).
 template <int S>
 __device__ __forceinline__ void group_top2(float& t1, float& t2) {
   if constexpr (S >= 2) top2_merge(t1, t2, dpp_f<kDppXor1>(t1), dpp_f<kDppXor1>(t2));
   if constexpr (S >= 4) top2_merge(t1, t2, dpp_f<kDppXor2>(t1), dpp_f<kDppXor2>(t2));
   if constexpr (S >= 8) top2_merge(t1, t2, dpp_f<kDppHalfMirror>(t1), dpp_f<kDppHalfMirror>(t2));
   if constexpr (S >= 16) top2_merge(t1, t2, dpp_f<kDppMirror>(t1), dpp_f<kDppMirror>(t2));
-  if constexpr (S >= 32) top2_merge(t1, t2, __shfl_xor(t1, 16, kWave), __shfl_xor(t2, 16, kWave));
-  if constexpr (S >= 64) top2_merge(t1, t2, __shfl_xor(t1, 32, kWave), __shfl_xor(t2, 32, kWave));
+  if constexpr (S >= 32) {
+    float r1[4], r2[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      r1[r] = lane_value(t1, 16 * r);
+      r2[r] = lane_value(t2, 16 * r);
+    }
+    top2_merge(r1[0], r2[0], r1[1], r2[1]);
+    top2_merge(r1[2], r2[2], r1[3], r2[3]);
+    if constexpr (S == 64) {
+      top2_merge(r1[0], r2[0], r1[2], r2[2]);
+      t1 = r1[0];
+      t2 = r2[0];
+    } else {
+      const bool lo = __lane_id() < 32;
+      t1 = lo ? r1[0] : r1[2];
+      t2 = lo ? r2[0] : r2[2];
+    }
+  }
 }
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }

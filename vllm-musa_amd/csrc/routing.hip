@@ -134,7 +134,7 @@ __global__ __launch_bounds__(kRouteWaves * kWave) void topk_sigmoid_kernel(
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
       if (lane + kWave * i == bi) s_local = sc[i];
-    const float s = __shfl(s_local, bi % kWave, kWave);
+    const float s = lane_value(s_local, bi % kWave);  // bi is wave-uniform
     sum += s;
     if (lane == k) {
       my_w = s;
@@ -163,12 +163,20 @@ __device__ __forceinline__ float group_scores_pow2(const float (&sel)[VPT], bool
     group_top2<S>(t1, t2);
     gs[i] = sum2 ? t1 + t2 : t1;
   }
+  // Group j of slot i (score in lanes j*S .. j*S+S-1) goes to lane i*kSegs + j.
   float gv = -INFINITY;
-  const int src = (lane % kSegs) * S;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const float v = __shfl(gs[i], src, kWave);
-    if (lane / kSegs == i) gv = v;
+    if constexpr (kSegs <= 4) {
+#pragma unroll
+      for (int j = 0; j < kSegs; ++j) {
+        const float v = lane_value(gs[i], j * S);
+        if (lane == i * kSegs + j) gv = v;
+      }
+    } else {
+      const float v = __shfl(gs[i], (lane % kSegs) * S, kWave);
+      if (lane / kSegs == i) gv = v;
+    }
   }
   return lane < groups ? gv : -INFINITY;
 }
@@ -277,7 +285,7 @@ __global__ __launch_bounds__(kRouteWaves * kWave) void grouped_topk_kernel(
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
       if (lane + kWave * i == bi) s_local = sc[i];
-    const float s = __shfl(s_local, bi % kWave, kWave);
+    const float s = lane_value(s_local, bi % kWave);  // bi is wave-uniform
     sum += s;
     if (lane == k) {
       my_w = s;
