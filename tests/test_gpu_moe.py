@@ -206,3 +206,22 @@ def test_fp8_moe_graph_replay_matches_eager(path):
     graph.replay()
     torch.cuda.synchronize()
     assert torch.equal(out, _run(x, w13, s13, w2, s2, w, ids2, path))
+
+
+@pytest.mark.parametrize("path", ["gemv", "gemm"])
+def test_fp8_moe_padded_intermediate_is_exact(path):
+    # The intermediate partition padded to the block grid with zero weights
+    # (Fp8MoEMethod.create_weights / load_expert) gives the unpadded layer's
+    # output bit for bit.
+    import types
+    from vllm_musa_amd.quant_methods import Fp8MoEMethod
+    E, H, I0, I = 8, 512, 256, 384
+    x, w13, s13, w2, s2, w, ids = _case(24, E, H, I0, 4, seed=91)
+    m = Fp8MoEMethod()
+    layer = types.SimpleNamespace()
+    m.create_weights(layer, E, H, I, intermediate_size_unpadded=I0)
+    for e in range(E):
+        m.load_expert(layer, e, w13[e], s13[e], w2[e], s2[e])
+    padded = _run(x, layer.w13_weight, layer.w13_weight_scale_inv, layer.w2_weight,
+                  layer.w2_weight_scale_inv, w, ids, path)
+    assert torch.equal(padded, _run(x, w13, s13, w2, s2, w, ids, path))

@@ -14,8 +14,15 @@ Shared experts that the caller delegates (shared_experts with an input) are
 added to the routed output, as the reference does when the runner hands them
 to the quant method.  Expert-parallel all-to-all managers are not part of this
 single-GPU path; layer.expert_map selects the local experts.
+
+Fp8MoEMethod also carries the block-grid padding of the intermediate
+partition (maybe_roundup_sizes / create_weights, quantization/fp8.py:27-115):
+the kernels take I in multiples of 128, and zero-filled padding rows / columns
+contribute nothing to the layer output.
 """
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -35,12 +42,72 @@ def _activation(layer) -> str:
     return getattr(act, "value", act) if not isinstance(act, str) else act
 
 
+def _round_up(value: int, multiple: int) -> int:
+    return (value + multiple - 1) // multiple * multiple
+
+
 class Fp8MoEMethod:
     """Block-fp8 (128x128 weight blocks, dynamic 1x128 activations) experts."""
 
-    def __init__(self, block_shape=(128, 128), swiglu_limit: float | None = None):
+    def __init__(self, block_shape=(128, 128), swiglu_limit: float | None = None,
+                 block_quant: bool = True):
         self.block_shape = list(block_shape)
         self.swiglu_limit = swiglu_limit
+        self.block_quant = block_quant
+
+    def maybe_roundup_sizes(self, hidden_size: int, intermediate_size_per_partition: int,
+                            act_dtype: torch.dtype, moe_parallel_config) -> tuple[int, int]:
+        """Pads a tensor-parallel shard's intermediate size up to the block grid
+        (lcm of the weight block sides), as the reference does for block-quantised
+        experts with tp_size > 1 (quantization/fp8.py:27-72)."""
+        if not (self.block_quant and getattr(moe_parallel_config, "tp_size", 1) > 1):
+            return hidden_size, intermediate_size_per_partition
+        block_n, block_k = (int(b) for b in self.block_shape)
+        return hidden_size, _round_up(intermediate_size_per_partition, math.lcm(block_n, block_k))
+
+    def create_weights(self, layer, num_experts: int, hidden_size: int,
+                       intermediate_size_per_partition: int, params_dtype=None,
+                       intermediate_size_unpadded: int | None = None, device="cuda"):
+        """Allocates the expert stack on `layer`: w13_weight [E, 2I, H] and
+        w2_weight [E, H, I] in e4m3fn, w13_weight_scale_inv / w2_weight_scale_inv
+        on the block grid.  When the partition was padded
+        (intermediate_size_unpadded < I) the weights are zero-filled, so the
+        padding rows and columns contribute nothing (quantization/fp8.py:75-115);
+        padding-only scale blocks hold 1.0."""
+        e, h, i = num_experts, hidden_size, intermediate_size_per_partition
+        bn, bk = (int(b) for b in self.block_shape)
+        fp8 = torch.float8_e4m3fn
+        padded = intermediate_size_unpadded is not None and intermediate_size_unpadded != i
+        alloc = torch.zeros if padded else torch.empty
+        layer.w13_weight = alloc(e, 2 * i, h, dtype=fp8, device=device)
+        layer.w2_weight = alloc(e, h, i, dtype=fp8, device=device)
+        layer.w13_weight_scale_inv = torch.ones(e, -(-2 * i // bn), -(-h // bk), dtype=torch.float32,
+                                                device=device)
+        layer.w2_weight_scale_inv = torch.ones(e, -(-h // bn), -(-i // bk), dtype=torch.float32,
+                                               device=device)
+        layer.intermediate_size_per_partition = i
+        layer.intermediate_size_unpadded = intermediate_size_unpadded or i
+
+    @staticmethod
+    def load_expert(layer, expert: int, w13, w13_scale, w2, w2_scale):
+        """Copies one expert's unpadded checkpoint tensors (w13 [2*I0, H] gate
+        then up, w2 [H, I0], block scales on their own grid) into the padded
+        stack: gate rows at [0, I0), up rows at [I, I + I0), w2 columns
+        [0, I0).  I0 must be a multiple of the block side, as the checkpoint's
+        blocks do not straddle the shard boundary then."""
+        i = layer.intermediate_size_per_partition
+        i0 = w2.shape[1]
+        bn = -(-layer.w13_weight.shape[1] // layer.w13_weight_scale_inv.shape[1])
+        bk = -(-layer.w2_weight.shape[2] // layer.w2_weight_scale_inv.shape[2])
+        if i0 % bn or i0 % bk:
+            raise ValueError(f"unpadded intermediate size {i0} is not on the {bn}x{bk} block grid")
+        layer.w13_weight[expert, :i0] = w13[:i0]
+        layer.w13_weight[expert, i:i + i0] = w13[i0:]
+        layer.w2_weight[expert, :, :i0] = w2
+        nb0 = i0 // bn
+        layer.w13_weight_scale_inv[expert, :nb0] = w13_scale[:nb0]
+        layer.w13_weight_scale_inv[expert, i // bn:i // bn + nb0] = w13_scale[nb0:]
+        layer.w2_weight_scale_inv[expert, :, :i0 // bk] = w2_scale
 
     def apply(self, layer, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
               shared_experts=None, shared_experts_input: torch.Tensor | None = None):
