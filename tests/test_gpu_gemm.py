@@ -79,6 +79,29 @@ def test_block_fp8_matmul_full_small():
     _check(out, ref)
 
 
+@pytest.mark.parametrize("M", [1, 7, 40])
+@pytest.mark.parametrize("K", [640, 1152])
+def test_block_fp8_gemv_k_not_multiple_of_512(M, K):
+    """Decode-sized M with K / 128 not a multiple of 4: the K-groups of the
+    GEMV's waves end part-way through the last group (masked blocks), and the
+    scales take the per-block load path.  Every output element is checked,
+    and a second call must give identical bits (fixed summation order)."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    N = 400
+    w, ws = synthetic.dense_fp8_weight(N, K, 11)
+    x = synthetic.activations(M, K, 12 + M)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    out = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    again = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    assert torch.equal(out, again)
+    ref = block_fp8_matmul_sampled(xq.view(torch.uint8).cpu().numpy(), xs.cpu().numpy(),
+                                   w.view(torch.uint8).cpu().numpy(), ws.cpu().numpy(),
+                                   np.arange(M), np.arange(N))
+    _check(out.float().cpu().numpy(), ref)
+
+
 def test_block_fp8_column_major_scales():
     from vllm_musa_amd import synthetic
     from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul

@@ -6,11 +6,12 @@
 //  * gemm_fp8_dma_kernel -- 128 x 256 workgroup tile, 8 waves, K-block of 128
 //    per step, 3-stage LDS ring fed by direct global->LDS loads (one barrier
 //    per K-block), XCD-aware tile order.  For M > 64.
-//  * gemv_fp8_bs_kernel  -- decode-sized M (<= 64): one wave per 16 weight rows
-//    streams its rows straight from HBM (no LDS), each 16x128 weight fragment
-//    multiplies every 16-row activation tile held in registers, so weights are
-//    read exactly once.  Split-K over blockIdx.y writes fp32 partials that
-//    splitk_reduce_kernel sums in a fixed order (deterministic), one rounding.
+//  * gemv_fp8_bs_kernel  -- decode-sized M (<= 64): one workgroup per 16
+//    weight rows, its waves split K and stream the rows straight from HBM
+//    into registers; each 16x128 weight fragment multiplies every 16-row
+//    activation tile, so weights are read exactly once.  The waves' partial
+//    sums meet in LDS and are added in wave order (deterministic), one
+//    rounding, in the same kernel.
 #include "mfma_fp8.h"
 #include "tile_pipe.h"
 
@@ -152,112 +153,184 @@ __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
 }
 
 // ------------------------------------------------------------ split-K GEMV --
-constexpr int kGemvWaves = 4;
+constexpr int kGemvU = 4;  // K-blocks of weights per pass (8 KiB per wave)
 
-template <int MT>
-__global__ __launch_bounds__(kGemvWaves * kWave) void gemv_fp8_bs_kernel(
-    const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t as_sm, int64_t as_sk,
-    const uint8_t* __restrict__ B, const float* __restrict__ Bs, int M, int N, int K, int splits,
-    float* __restrict__ partial, uint16_t* __restrict__ C) {
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+// Raw buffer loads (gfx9 descriptor: base, no stride, num_records bytes); a
+// lane whose byte offset is past num_records reads zeros and fetches nothing,
+// which masks rows past M and K-blocks past a split without branches.
+constexpr int kGemvBufferFlags = 0x00020000;
+constexpr uint32_t kGemvMasked = 0x80000000u;  // offset of a masked lane (buffers are < 2 GiB)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemv_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kGemvBufferFlags);
+}
+__device__ __forceinline__ v8i gemv_buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
+  const v4i lo = __builtin_bit_cast(
+      v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off + 16u * g), 0, 0));
+  const v4i hi = __builtin_bit_cast(
+      v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off + 64u + 16u * g), 0, 0));
+  return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+// U consecutive f32 scales at byte offset off (U = 2 or 4, 8- or 16-byte aligned).
+template <int U>
+__device__ __forceinline__ void gemv_buffer_scales(__amdgpu_buffer_rsrc_t rs, uint32_t off, float (&out)[U]) {
+  static_assert(U == 2 || U == 4, "scale vector width");
+  if constexpr (U == 4) {
+    const v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, 0));
+    for (int u = 0; u < 4; ++u) out[u] = v[u];
+  } else {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, static_cast<int>(off), 0, 0));
+    out[0] = v[0];
+    out[1] = v[1];
+  }
+}
+__device__ __forceinline__ float gemv_buffer_f32(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(off), 0, 0));
+}
+
+// One workgroup per 16 weight rows; its W waves (W = blockDim.x / 64) split
+// K by interleaved groups of U K-blocks: at pass r wave w reads blocks
+// [(r*W + w)*U, +U), so the workgroup streams W*U*128 contiguous bytes of
+// each of its rows per pass.  Each 16x128 weight fragment multiplies every
+// 16-row activation tile (MT of them, M <= 16 * MT), so the weights are read
+// exactly once.  Weights, both scale sets and activations are raw buffer
+// loads: blocks past K and activation rows past M are masked lanes (zeros,
+// no fetch), so the loop has no tail and no branches, and the first pass's
+// weights are requested before anything else.  The W partial sums meet in
+// LDS and wave 0 adds them in wave order (deterministic) and rounds once.
+// a_bytes = M * K and as_bytes cover A and As (both < 2 GiB); 16 * K < 2 GiB.
+template <int MT, bool VS>
+__global__ __launch_bounds__(MT == 1 ? 1024 : 512) void gemv_fp8_bs_kernel(
+    const uint8_t* __restrict__ A, int a_bytes, const float* __restrict__ As, int as_bytes,
+    int64_t as_sm, int64_t as_sk, const uint8_t* __restrict__ B, const float* __restrict__ Bs,
+    int M, int N, int K, uint16_t* __restrict__ C) {
+  constexpr int U = kGemvU;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
+  const int W = blockDim.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const int li = lane % 16, lg = lane / 16;
-  const int ntile = blockIdx.x * kGemvWaves + wave;
-  if (ntile * 16 >= N) return;  // wave-uniform; this kernel has no barriers
-  const int split = blockIdx.y;
+  const int ntile = blockIdx.x;  // the grid is exactly N / 16 workgroups
   const int KB = K / 128;
-  const int kb0 = static_cast<int>(static_cast<int64_t>(split) * KB / splits);
-  const int kb1 = static_cast<int>(static_cast<int64_t>(split + 1) * KB / splits);
-  const uint8_t* wrow = B + static_cast<int64_t>(ntile * 16 + li) * K;
-  const float* bs = Bs + static_cast<int64_t>((ntile * 16) / 128) * KB;
-  const uint8_t* xrow[MT];
-  const float* as[MT];
+  const __amdgpu_buffer_rsrc_t wrs = gemv_rsrc(B + static_cast<int64_t>(ntile) * 16 * K, 16 * K);
+  const __amdgpu_buffer_rsrc_t bsrs = gemv_rsrc(Bs + static_cast<int64_t>((ntile * 16) / 128) * KB, KB * 4);
+  const __amdgpu_buffer_rsrc_t ars = gemv_rsrc(A, a_bytes);
+  const __amdgpu_buffer_rsrc_t asrs = gemv_rsrc(As, as_bytes);
+  const uint32_t woff = static_cast<uint32_t>(li) * static_cast<uint32_t>(K);
+  uint32_t aoff[MT], soff[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int m = min(mt * 16 + li, M - 1);
-    xrow[mt] = A + static_cast<int64_t>(m) * K;
-    as[mt] = As + static_cast<int64_t>(m) * as_sm;
+    const int m = mt * 16 + li;
+    aoff[mt] = m < M ? static_cast<uint32_t>(m) * static_cast<uint32_t>(K) : kGemvMasked;
+    soff[mt] = m < M ? static_cast<uint32_t>(m * as_sm * 4) : kGemvMasked;
   }
   v4f acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
 
-  constexpr int U = 4;  // K-blocks in flight per wave
-  int kb = kb0;
-  for (; kb + U <= kb1; kb += U) {
-    v8i w[U];
+  // One pass: U K-blocks of the 16 weight rows and of every activation tile,
+  // with their scales.  VS: the U scales of a group are contiguous in both
+  // scale arrays (As rows with unit K stride, K / 128 a multiple of U,
+  // 16-byte aligned rows), so each set is one 16-byte load instead of U
+  // scattered ones; a group is then entirely inside or entirely past K.
+  struct Pass {
+    v8i wf[U];
+    float sb[U];
+    v8i xf[MT][U];
+    float sa[MT][U];
+  };
+  auto load = [&](Pass& p, int kb) {
+    if constexpr (VS) gemv_buffer_scales<U>(bsrs, kb < KB ? static_cast<uint32_t>(kb * 4) : kGemvMasked, p.sb);
 #pragma unroll
-    for (int u = 0; u < U; ++u) w[u] = global_frag(wrow + (kb + u) * 128, lg);
-    float sbv[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) sbv[u] = bs[kb + u];
+    for (int u = 0; u < U; ++u) {
+      const bool live = kb + u < KB;
+      p.wf[u] = gemv_buffer_frag(wrs, live ? woff + static_cast<uint32_t>((kb + u) * 128) : kGemvMasked, lg);
+      if constexpr (!VS) p.sb[u] = gemv_buffer_f32(bsrs, live ? static_cast<uint32_t>(kb + u) * 4u : kGemvMasked);
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      v8i x[U];
-      float sav[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        x[u] = global_frag(xrow[mt] + (kb + u) * 128, lg);
-        sav[u] = as[mt][(kb + u) * as_sk];
+      if constexpr (VS) {
+        const bool live = aoff[mt] != kGemvMasked && kb < KB;
+        gemv_buffer_scales<U>(asrs, live ? soff[mt] + static_cast<uint32_t>(kb * 4) : kGemvMasked, p.sa[mt]);
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u) fma4(acc[mt], mfma_fp8(w[u], x[u], zero), sav[u] * sbv[u]);
+      for (int u = 0; u < U; ++u) {
+        const bool live = aoff[mt] != kGemvMasked && kb + u < KB;
+        p.xf[mt][u] =
+            gemv_buffer_frag(ars, live ? aoff[mt] + static_cast<uint32_t>((kb + u) * 128) : kGemvMasked, lg);
+        if constexpr (!VS)
+          p.sa[mt][u] = gemv_buffer_f32(asrs, live ? soff[mt] + static_cast<uint32_t>((kb + u) * as_sk * 4)
+                                                   : kGemvMasked);
+      }
     }
-  }
-  for (; kb < kb1; ++kb) {
-    const v8i w = global_frag(wrow + kb * 128, lg);
-    const float sb = bs[kb];
+  };
+  auto compute = [&](const Pass& p) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
-      fma4(acc[mt], mfma_fp8(w, global_frag(xrow[mt] + kb * 128, lg), zero), as[mt][kb * as_sk] * sb);
-  }
+#pragma unroll
+      for (int u = 0; u < U; ++u) fma4(acc[mt], mfma_fp8(p.wf[u], p.xf[mt][u], zero), p.sa[mt][u] * p.sb[u]);
+  };
+  // Every load of a pass ahead of its first MFMA (the group barriers), so a
+  // pass costs one memory round trip.  Measured: two passes in flight per
+  // wave (half-size passes, double-buffered registers) is slower; there are
+  // enough waves per CU to cover the latency.  The host sizes
+  // W <= ceil(KB / U), so every wave owns at least one pass.
+  constexpr int kLoads = (2 * U + (VS ? 1 : U)) * (1 + MT), kMfmas = U * MT;
+  const int step = W * U;
+  int kb = wave * U;
+  do {
+    Pass p;
+    load(p, kb);
+    compute(p);
+    __builtin_amdgcn_sched_group_barrier(0x020, kLoads, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, kMfmas, 0);
+    kb += step;
+  } while (kb < KB);
 
+  if (W > 1) {  // uniform over the grid
+    float4* red = reinterpret_cast<float4*>(smem_dyn);
+    if (wave > 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        red[((wave - 1) * MT + mt) * kWave + lane] = float4{acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]};
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    for (int w = 1; w < W; ++w) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const float4 v = red[((w - 1) * MT + mt) * kWave + lane];
+        acc[mt][0] += v.x; acc[mt][1] += v.y; acc[mt][2] += v.z; acc[mt][3] += v.w;
+      }
+    }
+  }
   const int n = ntile * 16 + 4 * lg;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + li;
-    if (m >= M) continue;
-    const v4f a = acc[mt];
-    if (splits == 1) {
-      *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) = pack_bf16x4(a[0], a[1], a[2], a[3]);
-    } else {
-      float4 v = {a[0], a[1], a[2], a[3]};
-      *reinterpret_cast<float4*>(partial + (static_cast<int64_t>(split) * M + m) * N + n) = v;
-    }
+    if (m < M)
+      *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) =
+          pack_bf16x4(acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]);
   }
-}
-
-// C[m, n] = bf16(sum_{s < splits} partial[s, m, n]) in split order.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial,
-                                                            int splits, int64_t mn,
-                                                            uint16_t* __restrict__ C) {
-  const int64_t i4 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
-  if (i4 >= mn) return;
-  float4 acc = *reinterpret_cast<const float4*>(partial + i4);
-  for (int s = 1; s < splits; ++s) {
-    const float4 v = *reinterpret_cast<const float4*>(partial + s * mn + i4);
-    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-  }
-  *reinterpret_cast<uint2*>(C + i4) = pack_bf16x4(acc.x, acc.y, acc.z, acc.w);
 }
 
 // ------------------------------------------------------------ dispatch ------
 constexpr int kGemvMaxM = 64;
 
-static int gemv_splits(int M, int N, int K) {
+// Waves per GEMV workgroup: enough for about 4096 waves in all (16 per CU),
+// then as few as keep the same number of passes per wave (fewer partial sums
+// to add); at most 16 (8 for M > 16, whose waves need more registers) and
+// at most one per group of U K-blocks.
+static int gemv_waves(int M, int N, int K) {
   const int tiles = N / 16;
-  const int KB = K / 128;
-  int s = (2048 + tiles - 1) / tiles;  // aim for >= 2048 waves (8 per CU)
-  s = max(1, min(s, KB / 2 > 0 ? KB / 2 : 1));
-  (void)M;
-  return s;
+  const int groups = (K / 128 + kGemvU - 1) / kGemvU;
+  const int wmax = min(M > 16 ? 8 : 16, groups);
+  const int w0 = max(1, min(wmax, (4096 + tiles - 1) / tiles));
+  const int passes = (groups + w0 - 1) / w0;
+  return (groups + passes - 1) / passes;
 }
 
-size_t w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M > kGemvMaxM || M <= 0) return 0;
-  const int s = gemv_splits(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
-  return s > 1 ? static_cast<size_t>(s) * M * N * sizeof(float) : 0;
-}
+size_t w8a8_workspace_bytes(int64_t, int64_t, int64_t) { return 0; }
 
 }  // namespace vmamd
 
@@ -293,31 +366,30 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
   const uint8_t* a = static_cast<const uint8_t*>(A);
   const uint8_t* b = static_cast<const uint8_t*>(B);
   if (m <= kGemvMaxM) {
-    const int splits = gemv_splits(m, n, k);
-    float* part = nullptr;
-    if (splits > 1) {
-      const size_t need = static_cast<size_t>(splits) * m * n * sizeof(float);
-      VMAMD_REQUIRE(workspace && workspace_bytes >= need,
-                    "w8a8_block_fp8_matmul: workspace of %zu bytes required (got %zu)", need,
-                    workspace_bytes);
-      VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
-                    "w8a8_block_fp8_matmul: workspace must be 16-byte aligned");
-      part = static_cast<float*>(workspace);
-    }
-    dim3 grid((n / 16 + kGemvWaves - 1) / kGemvWaves, splits);
-    if (m <= 16)
-      gemv_fp8_bs_kernel<1><<<grid, kGemvWaves * kWave, 0, st>>>(a, As, as_stride_m, as_stride_k, b, Bs,
-                                                                m, n, k, splits, part, c);
-    else if (m <= 32)
-      gemv_fp8_bs_kernel<2><<<grid, kGemvWaves * kWave, 0, st>>>(a, As, as_stride_m, as_stride_k, b, Bs,
-                                                                m, n, k, splits, part, c);
+    // A, As and each 16-row weight tile are read through buffer descriptors:
+    // all must stay below 2 GiB.
+    const int64_t as_elems = (m - 1) * as_stride_m + (k / 128 - 1) * as_stride_k + 1;
+    VMAMD_REQUIRE(as_stride_m >= 0 && as_stride_k >= 0 && static_cast<int64_t>(m) * k < (1ll << 31) &&
+                      as_elems * 4 < (1ll << 31) && 16ll * k < (1ll << 31),
+                  "w8a8_block_fp8_matmul: activations, their scales and 16 weight rows must stay "
+                  "below 2 GiB");
+    const int a_bytes = m * k, as_bytes = static_cast<int>(as_elems * 4);
+    const int w = gemv_waves(m, n, k);
+    const int mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
+    const bool vs = as_stride_k == 1 && as_stride_m % kGemvU == 0 && (k / 128) % kGemvU == 0 &&
+                    reinterpret_cast<uintptr_t>(As) % (4 * kGemvU) == 0 &&
+                    reinterpret_cast<uintptr_t>(Bs) % (4 * kGemvU) == 0;
+    const size_t lds = static_cast<size_t>(w - 1) * mt * kWave * sizeof(float4);
+    auto launch = [&](auto kernel) {
+      kernel<<<n / 16, w * kWave, lds, st>>>(a, a_bytes, As, as_bytes, as_stride_m, as_stride_k, b, Bs, m, n,
+                                             k, c);
+    };
+    if (mt == 1)
+      vs ? launch(gemv_fp8_bs_kernel<1, true>) : launch(gemv_fp8_bs_kernel<1, false>);
+    else if (mt == 2)
+      vs ? launch(gemv_fp8_bs_kernel<2, true>) : launch(gemv_fp8_bs_kernel<2, false>);
     else
-      gemv_fp8_bs_kernel<4><<<grid, kGemvWaves * kWave, 0, st>>>(a, As, as_stride_m, as_stride_k, b, Bs,
-                                                                m, n, k, splits, part, c);
-    if (splits > 1) {
-      const int64_t mn = static_cast<int64_t>(m) * n;
-      splitk_reduce_kernel<<<static_cast<int>((mn / 4 + 255) / 256), 256, 0, st>>>(part, splits, mn, c);
-    }
+      vs ? launch(gemv_fp8_bs_kernel<4, true>) : launch(gemv_fp8_bs_kernel<4, false>);
     return check_launch("w8a8_block_fp8_matmul(gemv)");
   }
   static bool lds_raised = false;
