@@ -129,7 +129,12 @@ __device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t o
 // for the weights.  Columns of padding routes fetch no activation bytes.
 // Four waves per SIMD hold the whole T = 1 grid of a DeepSeek-V3-sized layer
 // at once; the int4 unpacking and the 4-block variant need more registers.
-template <int MAXB, int KIND>
+//
+// VS (kFp8 with K/128 a multiple of U and 16-byte aligned scale rows): the U
+// block scales of a group, and each route's U activation scales, are one
+// 16-byte load each instead of U scattered ones.  Splits start on group
+// boundaries, so with VS every group lies entirely inside its split.
+template <int MAXB, int KIND, bool VS = false>
 __global__ __launch_bounds__(kMoeGemvWaves * kWave, (MAXB == 1 && KIND != kW4) ? 4 : 2) void
 moe_gemv_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_div,
@@ -155,7 +160,9 @@ moe_gemv_kernel(
   const int arowb = KS * KB_::kAct;
   const int64_t wrowb = static_cast<int64_t>(KS) * KB_::kW;
   const int NB = (N + 127) / 128;
-  const int kb0 = split * KS / splits, kb1 = (split + 1) * KS / splits;
+  const int groups = (KS + kGemvU - 1) / kGemvU;  // splits start on group boundaries
+  const int kb0 = split * groups / splits * kGemvU;
+  const int kb1 = min((split + 1) * groups / splits * kGemvU, KS);
   const int n = ntile * 16 + 4 * lg;
   const uint8_t* wrow = w + (static_cast<int64_t>(e) * N + ntile * 16 + li) * wrowb;
   const float* wsr = nullptr;                        // kFp8: block scales of the 16 rows
@@ -180,13 +187,18 @@ moe_gemv_kernel(
   float sb[U];
   v4f sw[U];
   auto load_w = [&](int kb) {
+    if constexpr (VS) {
+      const v4f s4 = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(wsrs, kb * 4, 0, 0));
+#pragma unroll
+      for (int u = 0; u < U; ++u) sb[u] = s4[u];
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = min(kb + u, kb1 - 1);
       wf[u] = weight_frag<KIND>(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
-      sb[u] = 0.f;
+      if constexpr (!VS) sb[u] = 0.f;
       sw[u] = zero;
-      if constexpr (KIND == kFp8)
+      if constexpr (KIND == kFp8 && !VS)
         sb[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsrs, k * 4, 0, 0));
       if constexpr (KIND == kW4)
         sw[u] = v4f{bf16_to_f32(wsw[0][k]), bf16_to_f32(wsw[1][k]), bf16_to_f32(wsw[2][k]),
@@ -204,13 +216,20 @@ moe_gemv_kernel(
       if (b < nb) {
         v8i xf[U];
         float as[U];
+        if constexpr (VS) {  // scale byte offset = activation byte offset / 32
+          const uint32_t off = aoff[b] != kBufferOff ? aoff[b] / 32 + static_cast<uint32_t>(kb * 4) : kBufferOff;
+          const v4f s4 = __builtin_bit_cast(
+              v4f, __builtin_amdgcn_raw_buffer_load_b128(srs, static_cast<int>(off), 0, 0));
+#pragma unroll
+          for (int u = 0; u < U; ++u) as[u] = s4[u];
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const bool live = aoff[b] != kBufferOff && kb + u < kb1;
           const uint32_t off = live ? aoff[b] + static_cast<uint32_t>((kb + u) * KB_::kAct) : kBufferOff;
           xf[u] = buffer_frag(ars, off, lg);
-          as[u] = 0.f;
-          if constexpr (KIND == kFp8)  // scale byte offset = activation byte offset / 32
+          if constexpr (!VS) as[u] = 0.f;
+          if constexpr (KIND == kFp8 && !VS)  // scale byte offset = activation byte offset / 32
             as[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                   srs, static_cast<int>(live ? off / 32 : kBufferOff), 0, 0));
         }
@@ -1225,12 +1244,30 @@ static int gemv_act_bytes(int64_t rows, int64_t K) {
 // top-k ids are distinct, so T <= 16 needs one 16-route block per pass
 // (MAXB = 1, fewer registers); more blocks are still handled, by re-streaming
 // the expert's weights once per block.
+// vs: the kFp8 scale layout allows one 16-byte load per group of scales.
 template <int KIND, typename... Args>
-static void launch_gemv(dim3 grid, hipStream_t st, int T, Args... args) {
+static void launch_gemv(dim3 grid, hipStream_t st, int T, bool vs, Args... args) {
+  if constexpr (KIND == kFp8) {
+    if (vs) {
+      if (T <= kGemvBlock)
+        moe_gemv_kernel<1, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
+      else
+        moe_gemv_kernel<4, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
+      return;
+    }
+  }
   if (T <= kGemvBlock)
     moe_gemv_kernel<1, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
   else
     moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
+}
+
+// True when a kFp8 GEMV over K may read its scales U at a time: K/128 a
+// multiple of U and both scale arrays 16-byte aligned (rows then are too).
+template <int KIND>
+static bool gemv_vector_scales(int64_t K, const void* act_s, const void* w_s) {
+  return KIND == kFp8 && (K / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(act_s) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(w_s) % 16 == 0;
 }
 
 // Launches of the two stages; arguments are validated by the callers.  kBf16:
@@ -1247,7 +1284,8 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
     const int s13 = w13_splits(numel, E, H, I, KIND);
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s13);
-    launch_gemv<KIND>(g13, st, T, xa, gemv_act_bytes<KIND>(T, H), xs, topk, H, sorted, offs, active,
+    launch_gemv<KIND>(g13, st, T, gemv_vector_scales<KIND>(H, xs, w13_s), xa, gemv_act_bytes<KIND>(T, H),
+                      xs, topk, H, sorted, offs, active,
                       nact, w13, w13_s, 2 * I, numel, s13, scratch,
                       static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr));
     int rc = check_launch("moe w13 (gemv)");
@@ -1299,7 +1337,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g2((H / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s2);
     if (s2 > 1 && combined_out && combined && H % 8 == 0) {
-      launch_gemv<KIND>(g2, st, T, a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs, active,
+      launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, a2s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs, active,
                         nact, w2, w2_s, H, numel, s2, scratch, static_cast<const float*>(nullptr),
                         static_cast<uint16_t*>(nullptr));
       int rc = check_launch("moe w2 (gemv)");
@@ -1316,11 +1354,11 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
       return check_launch("moe w2 (combine)");
     }
     if (s2 == 1) {
-      launch_gemv<KIND>(g2, st, T, a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs,
+      launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, a2s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs,
                         active, nact, w2, w2_s, H, numel, 1, static_cast<float*>(nullptr), yscale, y);
       return check_launch("moe w2 (gemv)");
     }
-    launch_gemv<KIND>(g2, st, T, a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs, active,
+    launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, a2s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs, active,
                       nact, w2, w2_s, H, numel, s2, scratch, static_cast<const float*>(nullptr),
                       static_cast<uint16_t*>(nullptr));
     int rc = check_launch("moe w2 (gemv)");
