@@ -207,6 +207,34 @@ def test_moe_align_skewed_expert_map_and_scatter():
         np.testing.assert_array_equal(got.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("T,K,E,bs", [(2000, 8, 256, 128), (1537, 3, 40, 16), (4096, 8, 256, 16)])
+def test_moe_align_multi_workgroup_all_outputs(T, K, E, bs):
+    """Inputs above 1024 routes are placed by one workgroup per chunk: every
+    output (sorted ids, expert ids, padded count, offsets, scatter index,
+    active experts) equals the oracle's, with a hot expert spanning chunks."""
+    from vllm_musa_amd import _custom_ops as ops
+    g = np.random.Generator(np.random.PCG64(T * K + E))
+    ids = np.stack([g.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    ids[::2, 0] = 3
+    ids[T // 3, :] = np.arange(K)
+    cap = oalign.capacity_for(T * K, E, bs)
+    s = torch.empty(cap, dtype=torch.int32, device=DEV)
+    eids = torch.empty(-(-cap // bs), dtype=torch.int32, device=DEV)
+    ntpp = torch.empty(1, dtype=torch.int32, device=DEV)
+    offs = torch.empty(E + 1, dtype=torch.int32, device=DEV)
+    scat = torch.empty(T * K, dtype=torch.int32, device=DEV)
+    act = torch.full((E,), -7, dtype=torch.int32, device=DEV)
+    nact = torch.empty(1, dtype=torch.int32, device=DEV)
+    ops.moe_align_block_size(torch.from_numpy(ids).to(DEV), E, bs, s, eids, ntpp, None, scat, offs,
+                             act, nact)
+    r = oalign.moe_align_block_size(ids, E, bs)
+    for got, ref in zip((s, eids, ntpp, offs, scat), r):
+        np.testing.assert_array_equal(got.cpu().numpy(), ref)
+    used = np.flatnonzero(np.bincount(ids.reshape(-1), minlength=E))
+    assert int(nact.item()) == used.size
+    np.testing.assert_array_equal(act.cpu().numpy()[:used.size], used)
+
+
 # --------------------------------------------------------------- combine --
 @pytest.mark.parametrize("T,K,H", [(1, 8, 7168), (33, 2, 1024), (300, 8, 2048), (5, 3, 100)])
 def test_moe_sum_bit_exact(T, K, H):

@@ -2,16 +2,22 @@
 // a multiple of the block size, and keep ascending route order inside each
 // segment (a stable counting sort), so the result is deterministic.
 //
-// One 1024-thread workgroup does the whole job:
-//   1. LDS histogram of the (mapped) expert ids;
+// Each 1024-thread workgroup places one contiguous chunk of 1024 routes (more
+// per workgroup only beyond 256 workgroups):
+//   1. LDS histogram of all the (mapped) expert ids, and of those before the
+//      chunk (every workgroup reads all ids: no global scratch and no second
+//      launch, at numel * 4 bytes of L2 reads per workgroup);
 //   2. block-wide exclusive scan of the padded counts -> segment bases;
-//   3. stable placement, 1024 routes per step: the rank of a route among the
-//      same-expert routes of its wave comes from bit-sliced ballots (one
-//      64-bit ballot per expert-id bit, no loops over lanes), the rank across
-//      the 16 waves of the step from a [wave][expert] count table in LDS, and
-//      the rank across steps from a running per-expert counter.
-// Every position of sorted_token_ids that no route takes is written with the
-// sentinel `numel` exactly once, so no ordering between writers is needed.
+//   3. stable placement of the chunk, 1024 routes per step: the rank of a
+//      route among the same-expert routes of its wave comes from bit-sliced
+//      ballots (one 64-bit ballot per expert-id bit, no loops over lanes), the
+//      rank across the 16 waves of the step from a [wave][expert] count table
+//      in LDS, and the rank across steps and earlier chunks from a running
+//      per-expert counter that starts at the count before the chunk.
+// Workgroup 0 also writes the per-call outputs (num_tokens_post_pad, offsets,
+// active experts, expert_ids) and the sentinel `numel` at every position of
+// sorted_token_ids that no route takes, exactly once, so no ordering between
+// writers is needed.
 #include "common.h"
 
 namespace vmamd {
@@ -30,11 +36,16 @@ __device__ __forceinline__ int mapped_expert(const int32_t* __restrict__ ids, in
   return (e >= 0 && e < E) ? e : -1;
 }
 
+// Routes placed per workgroup: one placement step (several steps per
+// workgroup only beyond 256 workgroups).
+constexpr int64_t kAlignChunk = kAlignThreads;
+
 __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
-    const int32_t* __restrict__ ids, int64_t numel, int E, int bs, const int32_t* __restrict__ map,
-    int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity, int32_t* __restrict__ expert_ids,
-    int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out, int32_t* __restrict__ scatter_idx,
-    int32_t* __restrict__ active_out, int32_t* __restrict__ num_active_out) {
+    const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int E, int bs,
+    const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
+    int32_t* __restrict__ scatter_idx, int32_t* __restrict__ active_out,
+    int32_t* __restrict__ num_active_out) {
   __shared__ int cnt[kMaxAlignExperts];
   __shared__ int base[kMaxAlignExperts + 1];
   __shared__ int run[kMaxAlignExperts];
@@ -51,12 +62,18 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
   __syncthreads();
 
-  // 1. histogram
+  // 1. histograms: all routes (cnt) and the routes before this chunk (run)
+  const int64_t c_begin = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t c_end = min(numel, c_begin + chunk);
   for (int64_t r = tid; r < numel; r += kAlignThreads) {
     const int e = mapped_expert(ids, r, E, map, map_len);
-    if (e >= 0) atomicAdd(&cnt[e], 1);
+    if (e >= 0) {
+      atomicAdd(&cnt[e], 1);
+      if (r < c_begin) atomicAdd(&run[e], 1);
+    }
   }
   __syncthreads();
+  const bool lead = blockIdx.x == 0;  // writes the per-call outputs
 
   // 2. exclusive scan of padded counts (E <= 1024: one expert per thread)
   int padded = 0;
@@ -75,12 +92,12 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   if (tid == kAlignThreads - 1) base[E] = wave_off + incl;  // last thread sees the total
   __syncthreads();
   const int total = base[E];
-  if (tid == 0) ntpp[0] = total;
-  if (offsets_out)
+  if (lead && tid == 0) ntpp[0] = total;
+  if (lead && offsets_out)
     for (int e = tid; e <= E; e += kAlignThreads) offsets_out[e] = base[e];
 
   // compact list of the experts that received routes (ascending ids)
-  if (active_out) {
+  if (lead && active_out) {
     const bool act = tid < E && cnt[tid] > 0;
     const uint64_t m = ballot(act);
     const int below = __popcll(m & ((lane == 0) ? 0ull : (~0ull >> (kWave - lane))));
@@ -95,7 +112,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
 
   // expert_ids: binary search of the segment holding each block
-  const int64_t nblocks = (capacity + bs - 1) / bs;
+  const int64_t nblocks = lead ? (capacity + bs - 1) / bs : 0;
   for (int64_t b = tid; b < nblocks; b += kAlignThreads) {
     int out = -1;
     const int64_t pos = b * bs;
@@ -111,18 +128,20 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
   // sentinel for the padding of each segment and the unused tail
   const int32_t sentinel = static_cast<int32_t>(numel);
-  for (int e = tid; e < E; e += kAlignThreads)
-    for (int p = base[e] + cnt[e]; p < base[e + 1]; ++p) sorted[p] = sentinel;
-  for (int64_t p = total + tid; p < capacity; p += kAlignThreads) sorted[p] = sentinel;
+  if (lead) {
+    for (int e = tid; e < E; e += kAlignThreads)
+      for (int p = base[e] + cnt[e]; p < base[e + 1]; ++p) sorted[p] = sentinel;
+    for (int64_t p = total + tid; p < capacity; p += kAlignThreads) sorted[p] = sentinel;
+  }
 
   // 3. stable placement
   int nbits = 1;
   while ((1 << nbits) < E) ++nbits;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-  for (int64_t c0 = 0; c0 < numel; c0 += kAlignThreads) {
+  for (int64_t c0 = c_begin; c0 < c_end; c0 += kAlignThreads) {
     for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) wcnt[i / E][i % E] = 0;
     const int64_t r = c0 + tid;
-    const int e = r < numel ? mapped_expert(ids, r, E, map, map_len) : -1;
+    const int e = r < c_end ? mapped_expert(ids, r, E, map, map_len) : -1;
     const bool valid = e >= 0;
     uint64_t same = ballot(valid);
 #pragma unroll 1
@@ -142,7 +161,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
         sorted[pos] = static_cast<int32_t>(r);
         if (scatter_idx) scatter_idx[r] = pos;
       }
-    } else if (r < numel && scatter_idx) {
+    } else if (r < c_end && scatter_idx) {
       scatter_idx[r] = -1;
     }
     __syncthreads();
@@ -182,8 +201,11 @@ extern "C" int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel
                 "moe_align_block_size: active_experts and num_active go together");
   VMAMD_REQUIRE((topk_ids || numel == 0) && sorted_token_ids && expert_ids && num_tokens_post_pad,
                 "moe_align_block_size: null pointer");
-  moe_align_kernel<<<1, kAlignThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      topk_ids, numel, num_experts, block_size, expert_map, expert_map_len, sorted_token_ids,
+  // One workgroup per chunk of 1024 routes, at most 256 workgroups.
+  const int64_t chunk = kAlignChunk * std::max<int64_t>(1, (numel + kAlignChunk * 256 - 1) / (kAlignChunk * 256));
+  const int groups = static_cast<int>((numel + chunk - 1) / chunk);
+  moe_align_kernel<<<groups > 0 ? groups : 1, kAlignThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      topk_ids, numel, chunk, num_experts, block_size, expert_map, expert_map_len, sorted_token_ids,
       capacity, expert_ids, num_tokens_post_pad, expert_offsets, scatter_idx, active_experts,
       num_active);
   return check_launch("moe_align_block_size");
