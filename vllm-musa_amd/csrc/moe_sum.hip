@@ -20,6 +20,9 @@ __device__ __forceinline__ bool slot_live(const int32_t* __restrict__ ids, const
   return e < map_len && map[e] >= 0;
 }
 
+// Slots a thread loads up front (DeepSeek-V3 and most MoE layers use top-8).
+constexpr int kSumSlots = 8;
+
 template <int DT, bool VEC>
 __global__ __launch_bounds__(256) void moe_sum_kernel(const typename Elem<DT>::T* __restrict__ x,
                                                       int64_t tokens, int topk, int64_t hidden,
@@ -36,6 +39,43 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const typename Elem<DT>::T
     const int64_t t = i / chunks;
     const int64_t h = (i - t * chunks) * 8;
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if constexpr (VEC && sizeof(T) == 2) {
+      if (topk <= kSumSlots) {
+        // All slot rows are requested before the first add (one memory round
+        // trip instead of topk), unconditionally (slots past topk re-read the
+        // last row: a branch around a load would make it wait on its own);
+        // dead slots are read too (their rows exist) and dropped by a select,
+        // and the adds stay in slot order.
+        uint4 raw[kSumSlots];
+#pragma unroll
+        for (int k = 0; k < kSumSlots; ++k) {
+          const int kk = k < topk ? k : topk - 1;
+          raw[k] = *reinterpret_cast<const uint4*>(x + (t * topk + kk) * hidden + h);
+        }
+#pragma unroll
+        for (int k = 0; k < kSumSlots; ++k) {
+          if (k >= topk) continue;
+          const bool live = slot_live(ids, map, map_len, t * topk + k);
+          const float wk = wts ? wts[t * topk + k] : 1.0f;
+          const uint16_t* p = reinterpret_cast<const uint16_t*>(&raw[k]);
+          // One fused multiply-add per weighted slot (one rounding, as the
+          // weighted combine is defined); a dead slot leaves acc untouched.
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float v = E::to_f(p[j]);
+            const float a = wts ? __builtin_fmaf(v, wk, acc[j]) : acc[j] + v;
+            acc[j] = live ? a : acc[j];
+          }
+        }
+        T* dst = out + t * hidden + h;
+        uint4 o;
+        uint16_t* q = reinterpret_cast<uint16_t*>(&o);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = E::from_f(acc[j]);
+        *reinterpret_cast<uint4*>(dst) = o;
+        continue;
+      }
+    }
     for (int k = 0; k < topk; ++k) {
       if (!slot_live(ids, map, map_len, t * topk + k)) continue;
       const T* src = x + (t * topk + k) * hidden + h;
