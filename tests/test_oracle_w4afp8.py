@@ -136,25 +136,51 @@ def test_e4m3_of_int4_values():
 
 
 def _perm(s0: int, s1: int, sel: int) -> int:
-    """v_perm_b32: byte i of the result is byte sel_i (0..7) of {s0:s1}, s1 low."""
+    """v_perm_b32: byte i of the result from selector byte sel_i over the 8
+    bytes of {s0:s1} (s1 low): 0..7 pick a byte; 8, 9, 10, 11 replicate bit 7
+    of byte 1, 3, 5, 7; 12 gives 0x00 and 13..255 give 0xFF."""
     data = (s0 << 32) | s1
-    return sum(((data >> (8 * ((sel >> (8 * i)) & 0xFF))) & 0xFF) << (8 * i) for i in range(4))
+    out = 0
+    for i in range(4):
+        k = (sel >> (8 * i)) & 0xFF
+        if k < 8:
+            b = (data >> (8 * k)) & 0xFF
+        elif k < 12:
+            b = 0xFF * ((data >> (8 * (2 * (k - 8) + 1) + 7)) & 1)
+        else:
+            b = 0x00 if k == 12 else 0xFF
+        out |= b << (8 * i)
+    return out
 
 
-def _int4x4_to_fp8(t: int) -> int:
-    """Host restatement of the kernels' nibble -> e4m3 conversion (mfma_fp8.h)."""
-    s = (t & 0xF) | ((t & 0xF0) << 4) | ((t & 0xF00) << 8) | ((t & 0xF000) << 12)
-    sel = s & 0x07070707
-    neg = ((s >> 3) & 0x01010101) * 0xFF
-    pos = _perm(0x4E4C4A48, 0x44403800, sel)
-    ngv = _perm(0xB8C0C4C8, 0xCACCCED0, sel)
-    return (pos & ~neg & 0xFFFFFFFF) | (ngv & neg)
+def _int4x8_to_fp8(x: int) -> int:
+    """Host restatement of the kernels' nibble -> e4m3 conversion (mfma_fp8.h):
+    8 packed int4 in a dword -> 8 e4m3 codes (64 bits, element order)."""
+    m32 = 0xFFFFFFFF
+    se, so = x & 0x07070707, (x >> 4) & 0x07070707
+    qe = (x << 4) & m32
+    me = _perm((qe << 8) & m32, qe, 0x090B080A)
+    mo = _perm((x << 8) & m32, x, 0x090B080A)
+    ce = (_perm(0xB8C0C4C8, 0xCACCCED0, se) & me) | (_perm(0x4E4C4A48, 0x44403800, se) & ~me & m32)
+    co = (_perm(0xB8C0C4C8, 0xCACCCED0, so) & mo) | (_perm(0x4E4C4A48, 0x44403800, so) & ~mo & m32)
+    return _perm(co, ce, 0x05010400) | (_perm(co, ce, 0x07030602) << 32)
+
+
+def test_perm_emulation_known_selectors():
+    """The emulated v_perm_b32 on selectors whose results the ISA fixes."""
+    assert _perm(0x07060504, 0x03020100, 0x07050301) == 0x07050301
+    assert _perm(0, 0x00008000, 0x08080808) == 0xFFFFFFFF  # bit 15 -> selector 8
+    assert _perm(0x80000000, 0, 0x0B0B0B0B) == 0xFFFFFFFF  # bit 63 -> selector 11
+    assert _perm(0xFFFFFFFF, 0xFFFFFFFF, 0x0D0C0D0C) == 0xFF00FF00
 
 
 def test_kernel_nibble_table_is_e4m3_of_the_int4_value():
-    for t in range(0, 1 << 16, 7):  # every nibble value in every position, many combinations
-        out = _int4x4_to_fp8(t)
-        for i in range(4):
+    g = np.random.Generator(np.random.PCG64(5))
+    words = list(range(0, 1 << 16, 7)) + [int(w) for w in g.integers(0, 1 << 32, 4000, dtype=np.uint64)]
+    words += [0x88888888, 0x77777777, 0xF0F0F0F0, 0x0F0F0F0F, 0x80808080, 0x08080808]
+    for t in words:  # every nibble value in every position, many combinations
+        out = _int4x8_to_fp8(t)
+        for i in range(8):
             v = (t >> (4 * i)) & 0xF
             v = v - 16 if v >= 8 else v
-            assert (out >> (8 * i)) & 0xFF == int(e4m3_encode(np.float32(v))), (t, i)
+            assert (out >> (8 * i)) & 0xFF == int(e4m3_encode(np.float32(v))), (hex(t), i)

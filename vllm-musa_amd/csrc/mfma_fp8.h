@@ -44,23 +44,34 @@ __device__ __forceinline__ v4f mfma_bf16x2(const v8i& a, const v8i& b, v4f c) {
   return c;
 }
 
-// 16 signed int4 values (element 2j in the low nibble of byte j of `p`) ->
-// their 16 e4m3 codes, in element order.  Every integer in [-8, 7] is exact in
-// e4m3; the codes come from two byte-permute lookups (nibble & 7 indexes a
-// table of the non-negative codes 0..7 and one of the codes of -8..-1) and a
-// per-byte select on the nibble's sign bit.
-__device__ __forceinline__ uint32_t int4x4_to_fp8(uint32_t t) {
-  // t: 4 nibbles in its low 16 bits -> one nibble per byte
-  const uint32_t s = (t & 0xFu) | ((t & 0xF0u) << 4) | ((t & 0xF00u) << 8) | ((t & 0xF000u) << 12);
-  const uint32_t sel = s & 0x07070707u;
-  const uint32_t neg = ((s >> 3) & 0x01010101u) * 0xFFu;
-  const uint32_t pos = __builtin_amdgcn_perm(0x4E4C4A48u, 0x44403800u, sel);  // 0..7
-  const uint32_t ngv = __builtin_amdgcn_perm(0xB8C0C4C8u, 0xCACCCED0u, sel);  // -8..-1
-  return (pos & ~neg) | (ngv & neg);
+// 8 signed int4 values (element 2j in the low nibble of byte j of `x`, 2j+1
+// in the high nibble) -> their 8 e4m3 codes, in element order.  Every integer
+// in [-8, 7] is exact in e4m3.  The even and the odd elements are taken as
+// two byte planes; in each, a byte-permute lookup on the nibble's low three
+// bits reads the codes of 0..7 and another those of -8..-1, and the nibble's
+// sign (bit 3) selects between them through a per-byte mask that v_perm_b32
+// itself builds (selectors 8..11 replicate bit 7 of bytes 1 and 3 of either
+// source dword: the mask of x needs the sign bits at bit 7 of every byte,
+// which x has for the odd plane and x << 4 for the even one, and x << 8 moves
+// bytes 0 and 2 into the positions the selectors read).  Two more permutes
+// re-interleave the planes.  16 VALU operations per 8 elements.
+__device__ __forceinline__ uint2 int4x8_to_fp8(uint32_t x) {
+  constexpr uint32_t kPosLo = 0x44403800u, kPosHi = 0x4E4C4A48u;  // e4m3 of 0..7
+  constexpr uint32_t kNegLo = 0xCACCCED0u, kNegHi = 0xB8C0C4C8u;  // e4m3 of -8..-1
+  constexpr uint32_t kSignSel = 0x090B080Au;  // byte i <- bit 7 of byte i of q, from {q << 8, q}
+  const uint32_t se = x & 0x07070707u, so = (x >> 4) & 0x07070707u;
+  const uint32_t qe = x << 4;  // bit 7 of byte i: sign of the even element i
+  const uint32_t me = __builtin_amdgcn_perm(qe << 8, qe, kSignSel);
+  const uint32_t mo = __builtin_amdgcn_perm(x << 8, x, kSignSel);
+  const uint32_t ce = (__builtin_amdgcn_perm(kNegHi, kNegLo, se) & me) |
+                      (__builtin_amdgcn_perm(kPosHi, kPosLo, se) & ~me);
+  const uint32_t co = (__builtin_amdgcn_perm(kNegHi, kNegLo, so) & mo) |
+                      (__builtin_amdgcn_perm(kPosHi, kPosLo, so) & ~mo);
+  return uint2{__builtin_amdgcn_perm(co, ce, 0x05010400u), __builtin_amdgcn_perm(co, ce, 0x07030602u)};
 }
 __device__ __forceinline__ v4i int4x16_to_fp8(uint2 p) {
-  return v4i{static_cast<int>(int4x4_to_fp8(p.x & 0xFFFFu)), static_cast<int>(int4x4_to_fp8(p.x >> 16)),
-             static_cast<int>(int4x4_to_fp8(p.y & 0xFFFFu)), static_cast<int>(int4x4_to_fp8(p.y >> 16))};
+  const uint2 a = int4x8_to_fp8(p.x), b = int4x8_to_fp8(p.y);
+  return v4i{static_cast<int>(a.x), static_cast<int>(a.y), static_cast<int>(b.x), static_cast<int>(b.y)};
 }
 
 // Loads from LDS through address-space-3 pointers, so the compiler knows
@@ -101,14 +112,22 @@ __device__ __forceinline__ void st16(uint8_t* p, const v4i& v) { *reinterpret_ca
 // Operand fragment of one 128-element K-block of a packed int4 row (64 bytes
 // at p), converted to e4m3 in the same K order as global_frag: lane group g
 // takes elements [16g, 16g+16) and [64+16g, 64+16g+16).
-__device__ __forceinline__ v8i global_frag_int4(const uint8_t* p, int g) {
+// The packed bytes of such a fragment (16 bytes per lane, kept packed until
+// the MFMA needs them), and their conversion.
+__device__ __forceinline__ uint4 global_frag_int4_raw(const uint8_t* p, int g) {
   const uint2 lo = *reinterpret_cast<const uint2*>(p + 8 * g);
   const uint2 hi = *reinterpret_cast<const uint2*>(p + 32 + 8 * g);
-  const v4i a = int4x16_to_fp8(lo), b = int4x16_to_fp8(hi);
+  return uint4{lo.x, lo.y, hi.x, hi.y};
+}
+__device__ __forceinline__ v8i int4_frag_to_fp8(const uint4& raw) {
+  const v4i a = int4x16_to_fp8(uint2{raw.x, raw.y}), b = int4x16_to_fp8(uint2{raw.z, raw.w});
   v8i f;
   f[0] = a[0]; f[1] = a[1]; f[2] = a[2]; f[3] = a[3];
   f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
   return f;
+}
+__device__ __forceinline__ v8i global_frag_int4(const uint8_t* p, int g) {
+  return int4_frag_to_fp8(global_frag_int4_raw(p, g));
 }
 
 // acc += p * s, element-wise (the per-K-block scale promotion).

@@ -128,14 +128,16 @@ __device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t o
 // are counted apart from the vector loads, so waiting for them does not wait
 // for the weights.  Columns of padding routes fetch no activation bytes.
 // Four waves per SIMD hold the whole T = 1 grid of a DeepSeek-V3-sized layer
-// at once; the int4 unpacking and the 4-block variant need more registers.
+// at once; the int4 variant fits three and the 4-block variant two.
 //
-// VS (kFp8 with K/128 a multiple of U and 16-byte aligned scale rows): the U
-// block scales of a group, and each route's U activation scales, are one
-// 16-byte load each instead of U scattered ones.  Splits start on group
-// boundaries, so with VS every group lies entirely inside its split.
+// VS (K/128 a multiple of U and aligned scale rows): kFp8 reads the U block
+// scales of a group, and each route's U activation scales, with one 16-byte
+// load each instead of U scattered ones; kW4 reads each of the lane's four
+// rows' U bf16 scales with one 8-byte load instead of U 2-byte ones.  Splits
+// start on group boundaries, so with VS every group lies entirely inside its
+// split.
 template <int MAXB, int KIND, bool VS = false>
-__global__ __launch_bounds__(kMoeGemvWaves * kWave, (MAXB == 1 && KIND != kW4) ? 4 : 2) void
+__global__ __launch_bounds__(kMoeGemvWaves * kWave, MAXB == 1 ? (KIND == kW4 ? 3 : 4) : 2) void
 moe_gemv_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_div,
     int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
@@ -183,7 +185,13 @@ moe_gemv_kernel(
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
 
   // One K group of weights (U steps from kb, clamped to the split's range).
-  v8i wf[U];
+  // kW4 with one route block keeps the weights packed (half the registers:
+  // more waves, more bytes in flight) and converts each fragment right before
+  // its MFMA; with several blocks a fragment is converted once per group.
+  constexpr bool kRawW4 = KIND == kW4 && MAXB == 1;
+  v8i wf[kRawW4 ? 1 : U];
+  uint4 wraw[kRawW4 ? U : 1];
+  uint2 swr[4];  // kW4 + VS: packed bf16 scales, U per row
   float sb[U];
   v4f sw[U];
   auto load_w = [&](int kb) {
@@ -195,14 +203,33 @@ moe_gemv_kernel(
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = min(kb + u, kb1 - 1);
-      wf[u] = weight_frag<KIND>(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
+      if constexpr (kRawW4)
+        wraw[u] = global_frag_int4_raw(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
+      else
+        wf[u] = weight_frag<KIND>(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
       if constexpr (!VS) sb[u] = 0.f;
       sw[u] = zero;
       if constexpr (KIND == kFp8 && !VS)
         sb[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsrs, k * 4, 0, 0));
-      if constexpr (KIND == kW4)
+      if constexpr (KIND == kW4 && !VS)
         sw[u] = v4f{bf16_to_f32(wsw[0][k]), bf16_to_f32(wsw[1][k]), bf16_to_f32(wsw[2][k]),
                     bf16_to_f32(wsw[3][k])};
+    }
+    if constexpr (KIND == kW4 && VS) {  // each row's U scales: one 8-byte load
+#pragma unroll
+      for (int r = 0; r < 4; ++r) swr[r] = *reinterpret_cast<const uint2*>(wsw[r] + kb);
+    }
+  };
+  // Scales of step u of the group for the lane's four rows (kW4).
+  auto w4_scales = [&](int u) -> v4f {
+    if constexpr (KIND == kW4 && VS) {
+      auto pick = [u](const uint2& v) {
+        const uint32_t w = u < 2 ? v.x : v.y;
+        return __uint_as_float((u & 1) ? (w & 0xFFFF0000u) : (w << 16));
+      };
+      return v4f{pick(swr[0]), pick(swr[1]), pick(swr[2]), pick(swr[3])};
+    } else {
+      return sw[u];
     }
   };
   uint32_t aoff[MAXB];  // byte offset of each block's activation row (kBufferOff: padding)
@@ -238,7 +265,10 @@ moe_gemv_kernel(
           if constexpr (KIND == kFp8) {
             fma4(acc[b], mfma_fp8(wf[u], xf[u], zero), as[u] * sb[u]);
           } else if constexpr (KIND == kW4) {
-            fma4v(acc[b], mfma_fp8(wf[u], xf[u], zero), sw[u]);
+            if constexpr (kRawW4)
+              fma4v(acc[b], mfma_fp8(int4_frag_to_fp8(wraw[u]), xf[u], zero), w4_scales(u));
+            else
+              fma4v(acc[b], mfma_fp8(wf[u], xf[u], zero), w4_scales(u));
           } else {
             acc[b] = mfma_bf16x2(wf[u], xf[u], acc[b]);
           }
@@ -1247,7 +1277,7 @@ static int gemv_act_bytes(int64_t rows, int64_t K) {
 // vs: the kFp8 scale layout allows one 16-byte load per group of scales.
 template <int KIND, typename... Args>
 static void launch_gemv(dim3 grid, hipStream_t st, int T, bool vs, Args... args) {
-  if constexpr (KIND == kFp8) {
+  if constexpr (KIND != kBf16) {
     if (vs) {
       if (T <= kGemvBlock)
         moe_gemv_kernel<1, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
@@ -1262,12 +1292,16 @@ static void launch_gemv(dim3 grid, hipStream_t st, int T, bool vs, Args... args)
     moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
 }
 
-// True when a kFp8 GEMV over K may read its scales U at a time: K/128 a
-// multiple of U and both scale arrays 16-byte aligned (rows then are too).
+// True when a GEMV over K may read its scales U at a time: K/128 a multiple
+// of U and the scale arrays aligned so that every row is (kFp8: 16 bytes for
+// both scale sets; kW4: 8 bytes for the bf16 weight scales).
 template <int KIND>
 static bool gemv_vector_scales(int64_t K, const void* act_s, const void* w_s) {
-  return KIND == kFp8 && (K / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(act_s) % 16 == 0 &&
-         reinterpret_cast<uintptr_t>(w_s) % 16 == 0;
+  if constexpr (KIND == kFp8)
+    return (K / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(act_s) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(w_s) % 16 == 0;
+  if constexpr (KIND == kW4) return (K / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(w_s) % 8 == 0;
+  return false;
 }
 
 // Launches of the two stages; arguments are validated by the callers.  kBf16:
