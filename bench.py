@@ -21,6 +21,8 @@ layer.
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-sweep] [--no-cpu]
   python bench.py --traffic-probe   # the launches profiled for FETCH_SIZE / WRITE_SIZE
+  python bench.py --dense           # dense block-fp8 linear shapes, M = 1 .. 4096 (JSON lines)
+  python bench.py --w4              # w4afp8 MoE layer, T = 1 .. 1024 (JSON lines)
 """
 from __future__ import annotations
 
@@ -188,6 +190,72 @@ def cpu_baseline(torch, layer: Layer, target_s: float = 15.0) -> dict:
                       f"{layer_flops(layer.t * TOPK) / (tflops * 1e12):.0f} s"}
 
 
+# DeepSeek-V3 linear layers as [N, K] (fused q_a + kv_a, q_b, kv_b, o_proj,
+# shared-expert gate_up and down, dense-FFN gate_up and down).
+DENSE_SHAPES = ((2112, 7168), (24576, 1536), (32768, 512), (7168, 16384), (4096, 7168),
+                (7168, 2048), (36864, 7168), (7168, 18432))
+DENSE_M = (1, 4, 16, 32, 64, 4096)
+
+
+def dense_sweep(torch, iters: int, log) -> int:
+    """HIP-event medians of w8a8_block_fp8_matmul (caches flushed by a 1 GiB
+    read before each call); bytes = weights + scales + activations + output."""
+    from vllm_musa_amd import per_token_group_quant_fp8, synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    for n, k in DENSE_SHAPES:
+        w, ws = synthetic.dense_fp8_weight(n, k, 7)
+        row = {"N": n, "K": k}
+        for m in DENSE_M:
+            x = synthetic.activations(m, k, 8)
+            q, s = per_token_group_quant_fp8(x, 128)
+            f = lambda: w8a8_block_fp8_matmul(q, w, s, ws, [128, 128])
+            for _ in range(3):
+                f()
+            torch.cuda.synchronize()
+            us = statistics.median(time_events(torch, f, iters, lambda: flush_buf.max())) * 1e3
+            by = n * k + 4 * ((n + 127) // 128) * (k // 128) + m * k + 4 * m * (k // 128) + 2 * m * n
+            fl = 2.0 * m * n * k
+            row[f"M{m}"] = {"us": round(us, 1), "frac_hbm": round(by / (us * 1e-6) / (PEAK_HBM_GBS * 1e9), 3),
+                            "frac_fp8_peak": round(fl / (us * 1e-6) / (PEAK_FP8_TFLOPS * 1e12), 3)}
+        print(json.dumps(row), flush=True)
+        del w, ws
+    log("bench: dense sweep done")
+    return 0
+
+
+W4_E, W4_H, W4_I = 128, 4096, 1536
+
+
+def w4_sweep(torch, iters: int, log) -> int:
+    """HIP-event medians of routing + w4afp8_moe (caches flushed by a 1 GiB read
+    before each call); bytes = touched experts' int4 weights and bf16 scales +
+    activations + output."""
+    from vllm_musa_amd import fused_topk, synthetic, w4afp8_moe
+    w13, w2, s13, s2 = synthetic.moe_w4a8_weights(W4_E, W4_H, W4_I, 12)
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    per_expert = 3 * W4_I * W4_H // 2 + 2 * 3 * W4_I * (W4_H // 128)
+    for t in (1, 16, 256, 1024):
+        x = synthetic.activations(t, W4_H, 100 + t)
+        logits = synthetic.router_logits(t, W4_E, 200 + t)
+        def f():
+            w, ids, _ = fused_topk(x, logits, TOPK, True)
+            return w4afp8_moe(x, w13, w2, s13, s2, w, ids)
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        _, ids, _ = fused_topk(x, logits, TOPK, True)
+        used = int(torch.unique(ids).numel())
+        us = statistics.median(time_events(torch, f, iters, lambda: flush_buf.max())) * 1e3
+        by = used * per_expert + 2 * t * W4_H * 2
+        fl = 2.0 * t * TOPK * 3 * W4_H * W4_I
+        print(json.dumps({"T": t, "experts_touched": used, "us": round(us, 1),
+                          "frac_hbm": round(by / (us * 1e-6) / (PEAK_HBM_GBS * 1e9), 3),
+                          "tflops": round(fl / (us * 1e-6) / 1e12, 2)}), flush=True)
+    log("bench: w4afp8 sweep done")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -202,6 +270,12 @@ def main() -> int:
     ap.add_argument("--profile-t", type=int, default=0,
                     help="only run --steps layer steps at this T (caches flushed by a 1 GiB "
                          "read before each), for rocprofv3 --kernel-trace; prints no JSON")
+    ap.add_argument("--dense", action="store_true",
+                    help="only time the dense w8a8 block-fp8 GEMM / GEMV at the DeepSeek-V3 "
+                         "linear shapes (one JSON line per shape)")
+    ap.add_argument("--w4", action="store_true",
+                    help="only time the w4afp8 MoE layer (E=128, top-8, H=4096, I=1536) at "
+                         "T = 1, 16, 256, 1024 (one JSON line per T)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE layer runs on a single MI355X here "
@@ -216,6 +290,11 @@ def main() -> int:
     vllm_musa_amd.load()
     torch.cuda.set_device(0)
     log = lambda *a: print(*a, file=sys.stderr, flush=True)
+
+    if args.dense:
+        return dense_sweep(torch, args.sweep_iters, log)
+    if args.w4:
+        return w4_sweep(torch, args.sweep_iters, log)
 
     log(f"bench: building E={E} H={H} I={I} fp8 expert stack")
     weights = synthetic.moe_fp8_weights(E, H, I, WEIGHT_SEED)
