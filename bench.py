@@ -23,6 +23,7 @@ layer.
   python bench.py --traffic-probe   # the launches profiled for FETCH_SIZE / WRITE_SIZE
   python bench.py --dense           # dense block-fp8 linear shapes, M = 1 .. 4096 (JSON lines)
   python bench.py --w4              # w4afp8 MoE layer, T = 1 .. 1024 (JSON lines)
+  python bench.py --swiglu          # clamped SwiGLU + block-fp8 down projection (JSON lines)
 """
 from __future__ import annotations
 
@@ -224,6 +225,39 @@ def dense_sweep(torch, iters: int, log) -> int:
     return 0
 
 
+# Down projections after a clamped SwiGLU, as [N, D] (gate_up is [M, 2D]):
+# the dense MLP and the shared expert of a DeepSeek-V3-sized model.
+SWIGLU_SHAPES = ((7168, 18432), (7168, 2048))
+SWIGLU_M = (1, 16, 64, 4096)
+
+
+def swiglu_sweep(torch, iters: int, log) -> int:
+    """HIP-event medians of silu_clamp_block_fp8_matmul (quantiser + GEMM,
+    caches flushed by a 1 GiB read before each call); algorithmic bytes = the
+    bf16 gate_up read + weights and scales + the bf16 output."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import silu_clamp_block_fp8_matmul
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    for n, d in SWIGLU_SHAPES:
+        w, ws = synthetic.dense_fp8_weight(n, d, 7)
+        row = {"N": n, "D": d}
+        for m in SWIGLU_M:
+            gate_up = synthetic.activations(m, 2 * d, 9)
+            f = lambda: silu_clamp_block_fp8_matmul(gate_up, w, ws, 128, False, 10.0)
+            for _ in range(3):
+                f()
+            torch.cuda.synchronize()
+            us = statistics.median(time_events(torch, f, iters, lambda: flush_buf.max())) * 1e3
+            by = 4 * m * d + n * d + 4 * ((n + 127) // 128) * (d // 128) + 2 * m * n
+            fl = 2.0 * m * n * d
+            row[f"M{m}"] = {"us": round(us, 1), "frac_hbm": round(by / (us * 1e-6) / (PEAK_HBM_GBS * 1e9), 3),
+                            "frac_fp8_peak": round(fl / (us * 1e-6) / (PEAK_FP8_TFLOPS * 1e12), 3)}
+        print(json.dumps(row), flush=True)
+        del w, ws
+    log("bench: swiglu sweep done")
+    return 0
+
+
 W4_E, W4_H, W4_I = 128, 4096, 1536
 
 
@@ -276,6 +310,9 @@ def main() -> int:
     ap.add_argument("--w4", action="store_true",
                     help="only time the w4afp8 MoE layer (E=128, top-8, H=4096, I=1536) at "
                          "T = 1, 16, 256, 1024 (one JSON line per T)")
+    ap.add_argument("--swiglu", action="store_true",
+                    help="only time the clamp-aware SwiGLU + block-fp8 down projection at the "
+                         "DeepSeek-V3 dense-MLP and shared-expert shapes (one JSON line per shape)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE layer runs on a single MI355X here "
@@ -295,6 +332,8 @@ def main() -> int:
         return dense_sweep(torch, args.sweep_iters, log)
     if args.w4:
         return w4_sweep(torch, args.sweep_iters, log)
+    if args.swiglu:
+        return swiglu_sweep(torch, args.sweep_iters, log)
 
     log(f"bench: building E={E} H={H} I={I} fp8 expert stack")
     weights = synthetic.moe_fp8_weights(E, H, I, WEIGHT_SEED)

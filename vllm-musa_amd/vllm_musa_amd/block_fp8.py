@@ -8,6 +8,10 @@
       (_musa_deepgemm_fp8_op, model_executor/kernels/linear/scaled_mm/deep_gemm.py:233-262)
   Fp8BlockScaledMMKernel.apply_block_scaled_mm(A, B, As, Bs, **kwargs)
       MUSADeepGemmFp8BlockScaledMMKernel.apply_block_scaled_mm (deep_gemm.py:177-197)
+  silu_clamp_block_fp8_matmul(input, weight, weight_scale, group_size, use_deep_gemm_e8m0,
+                              swiglu_limit)
+      clamp-aware SwiGLU + 1x128 fp8 quantisation + block-fp8 down projection
+      (_musa_silu_clamp_deepgemm_fp8_op, deep_gemm.py:336-409)
 """
 from __future__ import annotations
 
@@ -79,3 +83,40 @@ class Fp8BlockScaledMMKernel:
             dst.copy_(out)
             return dst
         return out
+
+
+def silu_clamp_block_fp8_matmul(input: torch.Tensor, weight: torch.Tensor,
+                                weight_scale: torch.Tensor, group_size: int = 128,
+                                use_deep_gemm_e8m0: bool = False,
+                                swiglu_limit: float = 10.0) -> torch.Tensor:
+    """down = block_fp8( quant1x128( silu(min(gate, L)) * clamp(up, -L, L) ) ) for
+    input = [gate | up] of shape [M, 2D] (bf16 / f16) and weight [N, D] e4m3fn with
+    128x128 block scales; returns [M, N] bf16.
+
+    The activation is rounded to the input dtype before its group absmax, as the
+    materialised activation of the ordinary path is (the quantiser is bit-exact
+    to torch's clamp / sigmoid / multiply in bf16 followed by the 1x128
+    quantiser).  Shapes the fused quantiser does not take run the reference's
+    fallback: the activation in torch, then the quantiser and the block GEMM.
+    Reference: _musa_silu_clamp_deepgemm_fp8_op (scaled_mm/deep_gemm.py:336-409)."""
+    if use_deep_gemm_e8m0:
+        raise NotImplementedError("power-of-two (ue8m0) activation scales are not supported")
+    hidden = input.shape[-1] // 2 if input.dim() == 2 else 0
+    supported = (group_size == 128 and input.dim() == 2
+                 and input.shape[-1] % (2 * group_size) == 0 and hidden == weight.shape[-1]
+                 and input.dtype in (torch.bfloat16, torch.float16) and input.is_contiguous()
+                 and swiglu_limit > 0.0)
+    if not supported:
+        d = input.shape[-1] // 2
+        gate = torch.clamp(input[..., :d], max=swiglu_limit)
+        up = torch.clamp(input[..., d:], min=-swiglu_limit, max=swiglu_limit)
+        activated = gate * torch.sigmoid(gate) * up
+        return apply_w8a8_block_fp8_linear(activated, weight, weight_scale, [group_size, group_size])
+    from . import _custom_ops as ops
+    check_cuda(input, weight, weight_scale)
+    m = input.shape[0]
+    q = torch.empty((m, hidden), dtype=FP8_DTYPE, device=input.device)
+    s = torch.empty((m, hidden // group_size), dtype=torch.float32, device=input.device)
+    ops.silu_and_mul_clamp_per_token_group_fp8_quant(input, q, s, group_size, 1e-10, -448.0, 448.0,
+                                                     swiglu_limit)
+    return w8a8_block_fp8_matmul(q, weight, s, weight_scale, [128, 128])
