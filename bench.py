@@ -24,6 +24,7 @@ layer.
   python bench.py --dense           # dense block-fp8 linear shapes, M = 1 .. 4096 (JSON lines)
   python bench.py --w4              # w4afp8 MoE layer, T = 1 .. 1024 (JSON lines)
   python bench.py --swiglu          # clamped SwiGLU + block-fp8 down projection (JSON lines)
+  python bench.py --fold            # shared expert folded into the MoE vs run as dense GEMMs
 """
 from __future__ import annotations
 
@@ -225,6 +226,61 @@ def dense_sweep(torch, iters: int, log) -> int:
     return 0
 
 
+def fold_sweep(torch, weights, iters: int, log) -> int:
+    """The headline layer plus one shared expert of the routed experts' shape:
+    folded (Fp8MoEMethod.fold_shared_expert: expert E of the stack, one more
+    slot per token weighted by sigmoid of the shared gate) vs the shared MLP as
+    its own dense block-fp8 GEMMs (gate_up, SiLU-and-mul + quantiser, down) added
+    to the routed output.  HIP-event medians, caches flushed before each call."""
+    from types import SimpleNamespace
+
+    from vllm_musa_amd import silu_mul_per_token_group_quant_fp8, synthetic
+    from vllm_musa_amd.block_fp8 import apply_w8a8_block_fp8_linear, w8a8_block_fp8_matmul
+    from vllm_musa_amd.fused_moe import fused_experts_impl
+    from vllm_musa_amd.quant_methods import Fp8MoEMethod
+    sw13, ss13, sw2, ss2 = synthetic.moe_fp8_weights(1, H, I, WEIGHT_SEED + 5)
+    gate_vec = synthetic.activations(1, H, WEIGHT_SEED + 6).view(-1) * 0.02
+    w13, s13, w2, s2 = weights
+    layer = SimpleNamespace(w13_weight=w13, w2_weight=w2, w13_weight_scale_inv=s13,
+                            w2_weight_scale_inv=s2, expert_map=None, activation="silu",
+                            apply_router_weight_on_input=False,
+                            moe_config=SimpleNamespace(experts_per_token=TOPK))
+    layer._musa_shared_gate = lambda h: ((h @ gate_vec).view(-1, 1), None)
+    mlp = SimpleNamespace(gate_up_proj=SimpleNamespace(weight=sw13[0].clone(), weight_scale_inv=ss13[0].clone()),
+                          down_proj=SimpleNamespace(weight=sw2[0].clone(), weight_scale_inv=ss2[0].clone()))
+    method = Fp8MoEMethod()
+    method.fold_shared_expert(layer, mlp)
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    for t in SWEEP_T:
+        lay = Layer(torch, t, weights)
+
+        def folded():
+            w, ids = lay.route()
+            return method.apply(layer, lay.x, w, ids)
+
+        def separate():
+            w, ids = lay.route()
+            routed = fused_experts_impl(lay.x, w13, w2, w, ids, use_fp8_w8a8=True, w1_scale=s13,
+                                        w2_scale=s2, block_shape=[128, 128])
+            sig = torch.sigmoid(lay.x @ gate_vec).view(-1, 1)
+            h = apply_w8a8_block_fp8_linear(lay.x, sw13[0], ss13[0])
+            q, s = silu_mul_per_token_group_quant_fp8(h, 128)
+            down = w8a8_block_fp8_matmul(q, sw2[0], s, ss2[0], [128, 128])
+            return routed + down * sig
+
+        row = {"T": t}
+        for name, fn in (("folded_us", folded), ("separate_us", separate)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            row[name] = round(statistics.median(time_events(torch, fn, iters, lambda: flush_buf.max())) * 1e3, 1)
+        row["speedup"] = round(row["separate_us"] / row["folded_us"], 3)
+        print(json.dumps(row), flush=True)
+        del lay
+    log("bench: fold sweep done")
+    return 0
+
+
 # Down projections after a clamped SwiGLU, as [N, D] (gate_up is [M, 2D]):
 # the dense MLP and the shared expert of a DeepSeek-V3-sized model.
 SWIGLU_SHAPES = ((7168, 18432), (7168, 2048))
@@ -313,6 +369,10 @@ def main() -> int:
     ap.add_argument("--swiglu", action="store_true",
                     help="only time the clamp-aware SwiGLU + block-fp8 down projection at the "
                          "DeepSeek-V3 dense-MLP and shared-expert shapes (one JSON line per shape)")
+    ap.add_argument("--fold", action="store_true",
+                    help="only time the headline layer with one shared expert, folded into the "
+                         "grouped GEMMs (E+1 experts, top-8 + 1) vs run as separate dense "
+                         "GEMMs, at T = 1, 16, 256, 4096 (one JSON line per T)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE layer runs on a single MI355X here "
@@ -338,6 +398,9 @@ def main() -> int:
     log(f"bench: building E={E} H={H} I={I} fp8 expert stack")
     weights = synthetic.moe_fp8_weights(E, H, I, WEIGHT_SEED)
     torch.cuda.synchronize()
+
+    if args.fold:
+        return fold_sweep(torch, weights, args.sweep_iters, log)
 
     if args.traffic_probe:
         layer = Layer(torch, T_HEADLINE, weights)

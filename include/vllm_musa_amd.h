@@ -109,6 +109,18 @@ int vmamd_topk_sigmoid(const void* gating, int dtype, int64_t tokens, int expert
                        int renormalize, const float* bias, float* topk_weights,
                        int32_t* topk_ids, vmamd_stream_t stream);
 
+/* Folded shared expert: out = [topk_weights | w_s], [topk_ids | shared_expert_id]
+ * ([tokens, topk + 1]) with w_s = sigmoid(shared_logits[t]) computed in fp32
+ * and rounded to the logit dtype (VMAMD_DTYPE_*).  The routed weights are
+ * copied unchanged (no renormalisation with the shared weight).  Replaces
+ * extend_topk_with_shared (vllm_musa/jit_kernel/extend_topk_shared.py:17-73)
+ * and the shared column of the fused-shared top-k
+ * (vllm_musa/jit_kernel/csrc/topk/topk_gating.mu:369-456). */
+int vmamd_extend_topk_with_shared(const float* topk_weights, const int32_t* topk_ids,
+                                  int64_t tokens, int topk, const void* shared_logits, int dtype,
+                                  int32_t shared_expert_id, float* out_weights, int32_t* out_ids,
+                                  vmamd_stream_t stream);
+
 #define VMAMD_SCORING_SOFTMAX 0
 #define VMAMD_SCORING_SIGMOID 1
 

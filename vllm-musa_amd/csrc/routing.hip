@@ -337,6 +337,65 @@ using namespace vmamd;
     }                                                                                         \
   } while (0)
 
+namespace vmamd {
+// Folded shared expert: the [T, K] routing plus one always-selected column
+// (weight = sigmoid(shared gate logit) in fp32, rounded to the logit dtype;
+// id = the shared expert's id).  One thread per output element.
+template <int DT>
+__global__ __launch_bounds__(256) void extend_topk_shared_kernel(
+    const float* __restrict__ w_in, const int32_t* __restrict__ ids_in, int64_t tokens, int topk,
+    const typename Elem<DT>::T* __restrict__ logits, int32_t shared_id, float* __restrict__ w_out,
+    int32_t* __restrict__ ids_out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int k1 = topk + 1;
+  if (i >= tokens * k1) return;
+  const int64_t t = i / k1;
+  const int k = static_cast<int>(i - t * k1);
+  if (k < topk) {
+    w_out[i] = w_in[t * topk + k];
+    ids_out[i] = ids_in[t * topk + k];
+  } else {
+    const float s = 1.0f / (1.0f + expf(-Elem<DT>::load(logits, t)));
+    w_out[i] = Elem<DT>::to_f(Elem<DT>::from_f(s));
+    ids_out[i] = shared_id;
+  }
+}
+}  // namespace vmamd
+
+extern "C" int vmamd_extend_topk_with_shared(const float* topk_weights, const int32_t* topk_ids,
+                                             int64_t tokens, int topk, const void* shared_logits,
+                                             int dtype, int32_t shared_expert_id, float* out_weights,
+                                             int32_t* out_ids, vmamd_stream_t stream) {
+  using namespace vmamd;
+  VMAMD_REQUIRE(tokens >= 0 && topk >= 0, "extend_topk_with_shared: bad sizes");
+  if (tokens == 0) return VMAMD_OK;
+  VMAMD_REQUIRE((topk_weights && topk_ids) || topk == 0, "extend_topk_with_shared: null routing");
+  VMAMD_REQUIRE(shared_logits && out_weights && out_ids, "extend_topk_with_shared: null pointer");
+  const int64_t n = tokens * (topk + 1);
+  const int blocks = static_cast<int>((n + 255) / 256);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case kF32:
+      extend_topk_shared_kernel<kF32><<<blocks, 256, 0, st>>>(
+          topk_weights, topk_ids, tokens, topk, static_cast<const float*>(shared_logits),
+          shared_expert_id, out_weights, out_ids);
+      break;
+    case kF16:
+      extend_topk_shared_kernel<kF16><<<blocks, 256, 0, st>>>(
+          topk_weights, topk_ids, tokens, topk, static_cast<const uint16_t*>(shared_logits),
+          shared_expert_id, out_weights, out_ids);
+      break;
+    case kBF16:
+      extend_topk_shared_kernel<kBF16><<<blocks, 256, 0, st>>>(
+          topk_weights, topk_ids, tokens, topk, static_cast<const uint16_t*>(shared_logits),
+          shared_expert_id, out_weights, out_ids);
+      break;
+    default:
+      VMAMD_REQUIRE(false, "extend_topk_with_shared: unsupported logit dtype %d", dtype);
+  }
+  return check_launch("extend_topk_with_shared");
+}
+
 extern "C" int vmamd_topk_softmax(const void* gating, int dtype, int64_t tokens, int experts,
                                   int topk, int renormalize, float softcap, const float* bias,
                                   float* topk_weights, int32_t* topk_ids, vmamd_stream_t stream) {

@@ -104,33 +104,92 @@ def _check_routing_out(topk_weights, topk_ids, gating_output):
         raise ValueError("routing shapes do not match")
 
 
+def extend_topk_with_shared(topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                            shared_logits: torch.Tensor, shared_expert_id: int,
+                            out_weights: torch.Tensor | None = None,
+                            out_ids: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """[T, K] routing -> [T, K + 1]: the folded shared expert as one more
+    always-selected slot, weight sigmoid(shared logit) rounded to the logit
+    dtype, id shared_expert_id; routed weights unchanged.
+    Reference: extend_topk_with_shared (vllm_musa/jit_kernel/extend_topk_shared.py:49-73)."""
+    check_cuda(topk_weights, topk_ids, shared_logits, out_weights, out_ids)
+    t, k = topk_weights.shape
+    if topk_ids.shape != (t, k) or topk_weights.dtype != torch.float32 or topk_ids.dtype != torch.int32:
+        raise ValueError("topk_weights must be float32 and topk_ids int32, both [T, K]")
+    logits = shared_logits.reshape(-1)
+    if logits.numel() != t:
+        raise ValueError(f"shared_logits must hold one logit per token ({t}), got {logits.numel()}")
+    logits = logits.contiguous()
+    if out_weights is None:
+        out_weights = torch.empty((t, k + 1), dtype=torch.float32, device=topk_weights.device)
+    if out_ids is None:
+        out_ids = torch.empty((t, k + 1), dtype=torch.int32, device=topk_ids.device)
+    if tuple(out_weights.shape) != (t, k + 1) or tuple(out_ids.shape) != (t, k + 1):
+        raise ValueError("outputs must be [T, K + 1]")
+    _contig(out_weights, "out_weights")
+    _contig(out_ids, "out_ids")
+    call("vmamd_extend_topk_with_shared", ptr(topk_weights.contiguous()), ptr(topk_ids.contiguous()),
+         t, k, ptr(logits), dtype_code(logits.dtype), int(shared_expert_id), ptr(out_weights),
+         ptr(out_ids), stream_of(topk_weights))
+    return out_weights, out_ids
+
+
+def _shared_columns(topk_weights, shared_expert_gate_output, num_fused_shared_experts):
+    """Number of routed columns when the top-k also appends the fused shared
+    expert (the reference's shared1 kernels take exactly one)."""
+    if shared_expert_gate_output is None or num_fused_shared_experts <= 0:
+        return topk_weights.shape[1], False
+    if num_fused_shared_experts != 1:
+        raise NotImplementedError("only one fused shared expert is supported")
+    return topk_weights.shape[1] - 1, True
+
+
 def topk_softmax(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_output: torch.Tensor,
                  renormalize: bool = False, moe_softcapping: float = 0.0,
-                 correction_bias: torch.Tensor | None = None) -> None:
-    """Reference: topk_softmax (vllm_musa/jit_kernel/csrc/topk.py:211-242)."""
+                 correction_bias: torch.Tensor | None = None,
+                 shared_expert_gate_output: torch.Tensor | None = None,
+                 num_fused_shared_experts: int = 0) -> None:
+    """Reference: topk_softmax (vllm_musa/jit_kernel/csrc/topk.py:211-242).  With a
+    shared gate output and one fused shared expert, the last of the
+    topk_weights.shape[1] columns is that expert (id = number of routed experts,
+    weight = sigmoid of its gate, outside the renormalisation), as the fused-shared
+    kernel writes it (csrc/topk/topk_gating.mu:369-456)."""
     _check_routing_out(topk_weights, topk_ids, gating_output)
     if correction_bias is not None:
         check_cuda(correction_bias)
         if correction_bias.dtype != torch.float32 or correction_bias.numel() != gating_output.shape[1]:
             raise ValueError("correction_bias must be float32 [num_experts]")
     t, e = gating_output.shape
+    k, shared = _shared_columns(topk_weights, shared_expert_gate_output, num_fused_shared_experts)
+    w = torch.empty(t, k, dtype=torch.float32, device=gating_output.device) if shared else topk_weights
+    ids = torch.empty(t, k, dtype=torch.int32, device=gating_output.device) if shared else topk_ids
     call("vmamd_topk_softmax", ptr(gating_output), dtype_code(gating_output.dtype), t, e,
-         topk_weights.shape[1], int(bool(renormalize)), float(moe_softcapping),
-         ptr(correction_bias), ptr(topk_weights), ptr(topk_ids), stream_of(gating_output))
+         k, int(bool(renormalize)), float(moe_softcapping),
+         ptr(correction_bias), ptr(w), ptr(ids), stream_of(gating_output))
+    if shared:
+        extend_topk_with_shared(w, ids, shared_expert_gate_output, e, topk_weights, topk_ids)
 
 
 def topk_sigmoid(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_output: torch.Tensor,
-                 renormalize: bool = False, correction_bias: torch.Tensor | None = None) -> None:
-    """Reference: topk_sigmoid (vllm_musa/jit_kernel/csrc/topk.py:245-275)."""
+                 renormalize: bool = False, correction_bias: torch.Tensor | None = None,
+                 shared_expert_gate_output: torch.Tensor | None = None,
+                 num_fused_shared_experts: int = 0) -> None:
+    """Reference: topk_sigmoid (vllm_musa/jit_kernel/csrc/topk.py:245-275); the fused
+    shared expert as for topk_softmax."""
     _check_routing_out(topk_weights, topk_ids, gating_output)
     if correction_bias is not None:
         check_cuda(correction_bias)
         if correction_bias.dtype != torch.float32 or correction_bias.numel() != gating_output.shape[1]:
             raise ValueError("correction_bias must be float32 [num_experts]")
     t, e = gating_output.shape
+    k, shared = _shared_columns(topk_weights, shared_expert_gate_output, num_fused_shared_experts)
+    w = torch.empty(t, k, dtype=torch.float32, device=gating_output.device) if shared else topk_weights
+    ids = torch.empty(t, k, dtype=torch.int32, device=gating_output.device) if shared else topk_ids
     call("vmamd_topk_sigmoid", ptr(gating_output), dtype_code(gating_output.dtype), t, e,
-         topk_weights.shape[1], int(bool(renormalize)), ptr(correction_bias), ptr(topk_weights),
-         ptr(topk_ids), stream_of(gating_output))
+         k, int(bool(renormalize)), ptr(correction_bias), ptr(w),
+         ptr(ids), stream_of(gating_output))
+    if shared:
+        extend_topk_with_shared(w, ids, shared_expert_gate_output, e, topk_weights, topk_ids)
 
 
 def grouped_topk_into(topk_weights: torch.Tensor, topk_ids: torch.Tensor,

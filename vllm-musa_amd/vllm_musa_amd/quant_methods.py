@@ -18,7 +18,11 @@ single-GPU path; layer.expert_map selects the local experts.
 Fp8MoEMethod also carries the block-grid padding of the intermediate
 partition (maybe_roundup_sizes / create_weights, quantization/fp8.py:27-115):
 the kernels take I in multiples of 128, and zero-filled padding rows / columns
-contribute nothing to the layer output.
+contribute nothing to the layer output; and the shared-expert fold
+(fold_shared_expert, quantization/fp8.py:118-185, 191-244): a shared MLP with
+the routed experts' shapes and block format is appended as expert E, and apply
+gives every token one more slot on it, weighted by sigmoid of the shared gate,
+so routed and shared work run as one grouped GEMM chain.
 """
 from __future__ import annotations
 
@@ -26,6 +30,7 @@ import math
 
 import torch
 
+from . import _custom_ops as ops
 from .fused_moe import fused_experts_impl
 from .w4afp8_moe import w4afp8_moe
 
@@ -109,8 +114,63 @@ class Fp8MoEMethod:
         layer.w13_weight_scale_inv[expert, i // bn:i // bn + nb0] = w13_scale[nb0:]
         layer.w2_weight_scale_inv[expert, :, :i0 // bk] = w2_scale
 
+    weight_scale_name = "weight_scale_inv"
+
+    def fold_shared_expert(self, layer, mlp) -> None:
+        """Append the shared MLP (mlp.gate_up_proj [2I, H] gate-then-up rows and
+        mlp.down_proj [H, I], each with its weight_scale_inv block scales) to the
+        routed stack as expert E, release the shared projections, and mark the
+        layer folded (layer._musa_shared_expert_id = E).  The shared expert must
+        have a routed expert's shapes, dtypes and scale grid; once per layer,
+        after loading.  Reference: _fold_shared_expert_weights
+        (quantization/fp8.py:118-185)."""
+        if mlp is None or getattr(layer, "_musa_shared_folded", False):
+            return
+        if getattr(layer, "expert_map", None) is not None:
+            raise RuntimeError("shared-expert fold: expert parallelism is not folded")
+        name = self.weight_scale_name
+        parts = (("w13_weight", f"w13_{name}", mlp.gate_up_proj),
+                 ("w2_weight", f"w2_{name}", mlp.down_proj))
+        folded = {}
+        for weight_attr, scale_attr, proj in parts:
+            routed_w, routed_s = getattr(layer, weight_attr), getattr(layer, scale_attr)
+            shared_w, shared_s = proj.weight, getattr(proj, name)
+            if tuple(shared_w.shape) != tuple(routed_w.shape[1:]) or shared_w.dtype != routed_w.dtype:
+                raise RuntimeError(f"shared-expert fold: {weight_attr} expects "
+                                   f"{tuple(routed_w.shape[1:])}/{routed_w.dtype}, shared expert has "
+                                   f"{tuple(shared_w.shape)}/{shared_w.dtype}")
+            if tuple(shared_s.shape) != tuple(routed_s.shape[1:]) or shared_s.dtype != routed_s.dtype:
+                raise RuntimeError(f"shared-expert fold: {scale_attr} expects "
+                                   f"{tuple(routed_s.shape[1:])}/{routed_s.dtype}, shared expert has "
+                                   f"{tuple(shared_s.shape)}/{shared_s.dtype}")
+            folded[weight_attr] = torch.cat([routed_w, shared_w.unsqueeze(0)], dim=0).contiguous()
+            folded[scale_attr] = torch.cat([routed_s, shared_s.unsqueeze(0)], dim=0).contiguous()
+        num_routed = int(layer.w13_weight.shape[0])
+        for attr, t in folded.items():
+            setattr(layer, attr, t)
+        for _, _, proj in parts:  # the shared projections now live in the stack
+            proj.weight = None
+            setattr(proj, name, None)
+        layer._musa_shared_expert_id = num_routed
+        layer._musa_shared_folded = True
+
     def apply(self, layer, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
               shared_experts=None, shared_experts_input: torch.Tensor | None = None):
+        if getattr(layer, "_musa_shared_folded", False):
+            # The folded shared expert is one more always-selected slot; a router
+            # that already appended it (top-k + 1 columns) is taken as is
+            # (reference: apply, quantization/fp8.py:222-244).
+            if shared_experts is not None or shared_experts_input is not None:
+                raise ValueError("a folded shared expert expects shared_experts=None")
+            routed_topk = int(getattr(getattr(layer, "moe_config", None), "experts_per_token",
+                                      topk_ids.shape[1]))
+            if topk_ids.shape[1] == routed_topk:
+                shared_logits, _ = layer._musa_shared_gate(x)
+                topk_weights, topk_ids = ops.extend_topk_with_shared(
+                    topk_weights, topk_ids, shared_logits.reshape(-1), layer._musa_shared_expert_id)
+            elif topk_ids.shape[1] != routed_topk + 1 or topk_weights.shape[1] != routed_topk + 1:
+                raise ValueError(f"routing has {topk_ids.shape[1]} columns; expected {routed_topk} "
+                                 f"or {routed_topk + 1} with the shared slot")
         routed = fused_experts_impl(
             x, layer.w13_weight, layer.w2_weight, topk_weights, topk_ids,
             activation=_activation(layer),

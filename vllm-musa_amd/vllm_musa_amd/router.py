@@ -4,6 +4,7 @@
   fused_topk                    upstream fused_topk as called from
                                 model_executor/layers/fused_moe/router/grouped_topk_router.py:219-225
   grouped_topk                  grouped_topk_router.py:388-469 (and _grouped_topk_general 257-357)
+  extend_topk_with_shared       vllm_musa/jit_kernel/extend_topk_shared.py:49-73
 """
 from __future__ import annotations
 
@@ -13,6 +14,15 @@ from . import _custom_ops as ops
 
 topk_softmax = ops.topk_softmax
 topk_sigmoid = ops.topk_sigmoid
+
+
+def extend_topk_with_shared(topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                            shared_logits: torch.Tensor,
+                            shared_expert_id: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """[T, K] routing -> new [T, K + 1] tensors with the folded shared expert's
+    always-selected slot (weight sigmoid(shared logit), rounded to the logit
+    dtype; routed weights unchanged)."""
+    return ops.extend_topk_with_shared(topk_weights, topk_ids, shared_logits, shared_expert_id)
 
 
 def fused_topk(hidden_states: torch.Tensor, gating_output: torch.Tensor, topk: int,
