@@ -346,6 +346,41 @@ def w4_sweep(torch, iters: int, log) -> int:
     return 0
 
 
+def scales_sweep(torch, iters: int, log) -> int:
+    """HIP-event medians of vmamd_convert_scales on checkpoint-load workloads
+    (caches flushed by a 1 GiB read before each call): the e8m0 -> f32 upcast of
+    every MoE block scale of DeepSeek-V3 (58 MoE layers x 256 experts x (32 x 56
+    + 56 x 16) blocks) and the bf16 cast + check of one w4afp8 layer's group
+    scales (E=128, H=4096, I=1536: w13 [128, 3072, 32], w2 [128, 4096, 12]).
+    Bytes = elements x (source + destination element size)."""
+    from vllm_musa_amd import _custom_ops as ops
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    work = []
+    n = 58 * 256 * (32 * 56 + 56 * 16)
+    src = torch.randint(100, 130, (n,), dtype=torch.uint8, device="cuda", generator=g)
+    work.append(("e8m0->f32 DeepSeek-V3 MoE block scales", src,
+                 torch.empty(n, dtype=torch.float32, device="cuda"), None))
+    for name, shape in (("w13", (W4_E, 2 * W4_I, W4_H // 128)), ("w2", (W4_E, W4_H, W4_I // 128))):
+        src = torch.rand(shape, device="cuda", generator=g) * 0.01 + 0.001
+        work.append((f"f32->bf16+check w4afp8 {name} scales {list(shape)}", src,
+                     torch.empty(shape, dtype=torch.bfloat16, device="cuda"),
+                     torch.zeros(1, dtype=torch.int32, device="cuda")))
+    for name, src, dst, bad in work:
+        f = lambda: ops.convert_scales(src, dst, bad)
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        us = statistics.median(time_events(torch, f, iters, lambda: flush_buf.max())) * 1e3
+        by = src.numel() * (src.element_size() + dst.element_size())
+        print(json.dumps({"workload": name, "elements": src.numel(), "us": round(us, 1),
+                          "GBps": round(by / (us * 1e-6) / 1e9, 1),
+                          "frac_hbm": round(by / (us * 1e-6) / (PEAK_HBM_GBS * 1e9), 3)}),
+              flush=True)
+    log("bench: checkpoint scale conversion sweep done")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -373,6 +408,10 @@ def main() -> int:
                     help="only time the headline layer with one shared expert, folded into the "
                          "grouped GEMMs (E+1 experts, top-8 + 1) vs run as separate dense "
                          "GEMMs, at T = 1, 16, 256, 4096 (one JSON line per T)")
+    ap.add_argument("--scales", action="store_true",
+                    help="only time the checkpoint scale conversions (e8m0 -> f32 of the "
+                         "DeepSeek-V3 MoE block scales, f32 -> bf16 + check of a w4afp8 layer's "
+                         "group scales), one JSON line per workload")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE layer runs on a single MI355X here "
@@ -394,6 +433,8 @@ def main() -> int:
         return w4_sweep(torch, args.sweep_iters, log)
     if args.swiglu:
         return swiglu_sweep(torch, args.sweep_iters, log)
+    if args.scales:
+        return scales_sweep(torch, args.sweep_iters, log)
 
     log(f"bench: building E={E} H={H} I={I} fp8 expert stack")
     weights = synthetic.moe_fp8_weights(E, H, I, WEIGHT_SEED)

@@ -36,6 +36,7 @@ typedef struct ihipStream_t* vmamd_stream_t; /* == hipStream_t */
 #define VMAMD_DTYPE_F32 0
 #define VMAMD_DTYPE_F16 1
 #define VMAMD_DTYPE_BF16 2
+#define VMAMD_DTYPE_E8M0 3 /* unsigned power-of-two exponent byte (scales only) */
 
 /* Message of the last error on this thread ("" if none). */
 const char* vmamd_last_error(void);
@@ -339,6 +340,21 @@ int vmamd_w4afp8_moe(const void* x, int64_t T, int64_t H, const void* w13, const
                      const int32_t* expert_map, int64_t expert_map_len, float swiglu_limit,
                      int path, void* out, void* workspace, size_t workspace_bytes,
                      vmamd_stream_t stream);
+
+/* ------------------------------------------------------ checkpoint scales --
+ * Converts n weight scales from src_dtype (E8M0, F32 or BF16) to dst_dtype
+ * (F32 or BF16), element for element:
+ *   e8m0 -> f32 : bits = b << 23 (b = 0 gives +0.0, b = 255 gives +inf)
+ *   f32 -> bf16 : round to nearest even, NaN -> 0x7fc0
+ * When invalid_count is not null, the number of destination values that are
+ * not finite and positive is ADDED to *invalid_count (the caller clears it).
+ * src and dst are either the same buffer (equal element sizes) or disjoint.
+ * Replaces _upcast_e8m0_to_fp32 / deepgemm_post_process_fp8_weight_block
+ * (vllm_musa/model_executor/layers/quantization/utils/fp8_utils.py:13-30)
+ * and the cast + check of MusaW4AFp8MoEMethod.process_weights_after_loading
+ * (model_executor/layers/quantization/w4afp8.py:126-135). */
+int vmamd_convert_scales(const void* src, int src_dtype, int64_t n, void* dst, int dst_dtype,
+                         int32_t* invalid_count, vmamd_stream_t stream);
 
 #ifdef __cplusplus
 }

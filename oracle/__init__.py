@@ -16,6 +16,7 @@ Modules:
   gemm      -- w8a8 block-fp8 GEMM (fp64 closed form)
   moe       -- fused experts (bf16 and fp8-block), moe_sum
   w4afp8    -- the w4afp8 MoE reference
+  scales    -- checkpoint scale conversion (e8m0 upcast, bf16 cast + check)
 
 How each function is pinned (golden vectors, closed forms, brute force,
 library cross-checks) is listed in tests/test_oracle_*.py.

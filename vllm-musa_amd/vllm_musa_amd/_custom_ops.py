@@ -16,6 +16,14 @@ from ._lib import call, check_cuda, dtype_code, ptr, stream_of
 FP8_DTYPE = torch.float8_e4m3fn
 FP8_MAX = float(torch.finfo(FP8_DTYPE).max)  # 448
 FP8_MIN = -FP8_MAX
+E8M0_DTYPE = getattr(torch, "float8_e8m0fnu", None)
+
+# Scale encodings of vmamd_convert_scales (VMAMD_DTYPE_*): raw uint8 bytes are
+# taken as e8m0 exponents, like torch.float8_e8m0fnu.
+_SCALE_SRC = {torch.float32: 0, torch.bfloat16: 2, torch.uint8: 3}
+if E8M0_DTYPE is not None:
+    _SCALE_SRC[E8M0_DTYPE] = 3
+_SCALE_DST = {torch.float32: 0, torch.bfloat16: 2}
 
 
 def _contig(t: torch.Tensor, name: str) -> None:
@@ -299,3 +307,30 @@ def moe_weighted_sum(input: torch.Tensor, topk_weights: torch.Tensor, output: to
     t, k, h = input.shape
     call("vmamd_moe_weighted_sum", ptr(input), dtype_code(input.dtype), t, k, h, ptr(w), ptr(ids),
          ptr(emap), 0 if emap is None else emap.numel(), ptr(output), stream_of(input))
+
+
+# ------------------------------------------------------ checkpoint scales --
+def convert_scales(src: torch.Tensor, dst: torch.Tensor,
+                   invalid_count: torch.Tensor | None = None) -> None:
+    """dst = src converted element for element (e8m0 / f32 / bf16 -> f32 / bf16;
+    e8m0 byte b -> float bits b << 23, f32 -> bf16 round to nearest even).  When
+    given, invalid_count (one int32) is increased by the number of dst values
+    that are not finite and positive.  References: _upcast_e8m0_to_fp32
+    (quantization/utils/fp8_utils.py:13-15) and the cast + check of
+    MusaW4AFp8MoEMethod.process_weights_after_loading
+    (quantization/w4afp8.py:126-131)."""
+    check_cuda(src, dst, invalid_count)
+    _contig(src, "src")
+    _contig(dst, "dst")
+    if src.dtype not in _SCALE_SRC:
+        raise ValueError(f"convert_scales: unsupported source dtype {src.dtype}")
+    if dst.dtype not in _SCALE_DST:
+        raise ValueError(f"convert_scales: unsupported destination dtype {dst.dtype}")
+    if src.numel() != dst.numel():
+        raise ValueError(f"convert_scales: {src.numel()} source and {dst.numel()} destination "
+                         "elements")
+    if invalid_count is not None and (invalid_count.dtype != torch.int32
+                                      or invalid_count.numel() != 1):
+        raise ValueError("invalid_count must be a single int32")
+    call("vmamd_convert_scales", ptr(src), _SCALE_SRC[src.dtype], src.numel(), ptr(dst),
+         _SCALE_DST[dst.dtype], ptr(invalid_count), stream_of(dst))

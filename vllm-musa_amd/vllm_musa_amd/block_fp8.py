@@ -19,7 +19,8 @@ import torch
 
 from . import _lib
 from ._lib import call, check_cuda, ptr, stream_of
-from .fp8_utils import FP8_DTYPE, per_token_group_quant_fp8
+from .fp8_utils import (FP8_DTYPE, deepgemm_post_process_fp8_weight_block,
+                        per_token_group_quant_fp8)
 
 
 def w8a8_block_fp8_matmul(A: torch.Tensor, B: torch.Tensor, As: torch.Tensor, Bs: torch.Tensor,
@@ -74,6 +75,24 @@ class Fp8BlockScaledMMKernel:
 
     def __init__(self, weight_group_shape=(128, 128)):
         self.weight_group_shape = tuple(weight_group_shape)
+        self.use_deep_gemm_e8m0 = False
+
+    def process_weights_after_loading(self, layer) -> None:
+        """Once after loading: block scales stored as e8m0 (weight_scale_inv, else
+        weight_scale) are replaced by their float32 values, which the GEMM reads.
+        Reference: MUSADeepGemmFp8BlockScaledMMKernel.process_weights_after_loading
+        (model_executor/kernels/linear/scaled_mm/deep_gemm.py:112-146)."""
+        name = ("weight_scale_inv" if getattr(layer, "weight_scale_inv", None) is not None
+                else "weight_scale")
+        block = tuple(getattr(layer, "weight_block_size", None) or self.weight_group_shape)
+        old = getattr(layer, name)
+        weight, scale = deepgemm_post_process_fp8_weight_block(
+            layer.weight, old, block, self.use_deep_gemm_e8m0,
+            getattr(layer, "is_bmm", False), getattr(layer, "bmm_batch_size", 0))
+        if scale is not old:
+            if isinstance(old, torch.nn.Parameter):
+                scale = torch.nn.Parameter(scale, requires_grad=False)
+            setattr(layer, name, scale)
 
     def apply_block_scaled_mm(self, A: torch.Tensor, B: torch.Tensor, As: torch.Tensor | None,
                               Bs: torch.Tensor, **kwargs) -> torch.Tensor:

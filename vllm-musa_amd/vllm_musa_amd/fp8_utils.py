@@ -1,7 +1,10 @@
-"""Activation quantisation with the reference's Python signature.
+"""Activation quantisation and checkpoint scale handling with the
+reference's Python signatures.
 
-Reference: per_token_group_quant_fp8
-(vllm_musa/model_executor/layers/quantization/utils/fp8_utils.py:33-152).
+References (vllm_musa/model_executor/layers/quantization/utils/fp8_utils.py):
+  per_token_group_quant_fp8                33-152
+  _upcast_e8m0_to_fp32                     13-15
+  deepgemm_post_process_fp8_weight_block   18-30
 """
 from __future__ import annotations
 
@@ -10,6 +13,31 @@ import torch
 from . import _custom_ops as ops
 
 FP8_DTYPE = ops.FP8_DTYPE
+E8M0_DTYPE = ops.E8M0_DTYPE
+
+
+def upcast_e8m0_to_fp32(scale: torch.Tensor) -> torch.Tensor:
+    """e8m0 exponent bytes -> float32 with the byte as the exponent field and a
+    zero mantissa (0 -> +0.0, 255 -> +inf), on the GPU.  Reference:
+    _upcast_e8m0_to_fp32 (fp8_utils.py:13-15)."""
+    out = torch.empty(scale.shape, dtype=torch.float32, device=scale.device)
+    ops.convert_scales(scale.contiguous(), out)
+    return out
+
+
+_upcast_e8m0_to_fp32 = upcast_e8m0_to_fp32
+
+
+def deepgemm_post_process_fp8_weight_block(wq: torch.Tensor, ws: torch.Tensor,
+                                           quant_block_shape: tuple[int, ...], use_e8m0: bool,
+                                           is_bmm: bool = False, bmm_batch_size: int = 0
+                                           ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Weights are kept as they are; e8m0 block scales become float32 unless the
+    GEMM consumes e8m0 itself (use_e8m0).  Reference: fp8_utils.py:18-30."""
+    del quant_block_shape, is_bmm, bmm_batch_size
+    if E8M0_DTYPE is not None and ws.dtype == E8M0_DTYPE and not use_e8m0:
+        return wq, upcast_e8m0_to_fp32(ws)
+    return wq, ws
 
 
 def per_token_group_quant_fp8(x: torch.Tensor, group_size: int, eps: float = 1e-10,

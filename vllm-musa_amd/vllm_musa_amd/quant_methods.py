@@ -9,6 +9,7 @@ method does and runs this package's fused layer:
   UnquantizedFusedMoEMethod.forward_oot
                                    model_executor/layers/fused_moe/unquantized_fused_moe_method.py:81-130
   W4AFp8MoEMethod.apply            model_executor/layers/quantization/w4afp8.py:147-170
+  W4AFp8MoEMethod loading          model_executor/layers/quantization/w4afp8.py:74-140
 
 Shared experts that the caller delegates (shared_experts with an input) are
 added to the routed output, as the reference does when the runner hands them
@@ -202,10 +203,108 @@ class UnquantizedFusedMoEMethod:
 
 class W4AFp8MoEMethod:
     """Packed int4 experts with bf16 group-128 scales and dynamic per-row fp8
-    activations."""
+    activations.
+
+    Loading follows the reference method (quantization/w4afp8.py:74-140):
+    create_weights allocates w13_weight [E, 2I, H/2] and w2_weight [E, H, I/2]
+    int8 (two int4 per byte), float32 group-128 scales w13_weight_scale_inv
+    [E, 2I, H/128] / w2_weight_scale_inv [E, H, I/128] and unused bf16
+    input-scale placeholders; load_weight copies a tensor-parallel rank's shard
+    of one checkpoint tensor; process_weights_after_loading casts the scales
+    to bf16 on the GPU and rejects any that is not finite and positive."""
+
+    GROUP = 128
 
     def __init__(self, swiglu_limit: float | None = None):
         self.swiglu_limit = swiglu_limit
+
+    def maybe_roundup_sizes(self, hidden_size: int, intermediate_size_per_partition: int,
+                            act_dtype: torch.dtype, moe_parallel_config) -> tuple[int, int]:
+        """No padding: the int4 scale groups must not straddle a shard, so H and
+        the partition's I must be multiples of 128 (quantization/w4afp8.py:74-87)."""
+        if hidden_size % self.GROUP or intermediate_size_per_partition % self.GROUP:
+            raise ValueError(
+                f"W4AFP8 experts need H and I per partition in multiples of {self.GROUP} "
+                f"(got H={hidden_size}, I={intermediate_size_per_partition}); a tensor-parallel "
+                "split that breaks the groups needs --enable-expert-parallel instead")
+        return hidden_size, intermediate_size_per_partition
+
+    def create_weights(self, layer, num_experts: int, hidden_size: int,
+                       intermediate_size_per_partition: int, params_dtype=None, device="cuda",
+                       **extra_weight_attrs) -> None:
+        """Registers the packed weights, float32 scales and input-scale
+        placeholders on `layer` (quantization/w4afp8.py:89-124); extra
+        attributes (weight_loader, ...) are set on every parameter and the scales
+        carry quant_method = "group"."""
+        e, h, i, g = num_experts, hidden_size, intermediate_size_per_partition, self.GROUP
+        shapes = {"w13_weight": (e, 2 * i, h // 2), "w2_weight": (e, h, i // 2),
+                  "w13_weight_scale_inv": (e, 2 * i, h // g), "w2_weight_scale_inv": (e, h, i // g),
+                  "w13_input_scale": (e,), "w2_input_scale": (e,)}
+        for name, shape in shapes.items():
+            if name.endswith("weight"):
+                value, attrs = torch.empty(shape, dtype=torch.int8, device=device), extra_weight_attrs
+            else:
+                fill = torch.ones if name.endswith("input_scale") else torch.empty
+                dtype = torch.bfloat16 if name.endswith("input_scale") else torch.float32
+                value = fill(shape, dtype=dtype, device=device)
+                attrs = {**extra_weight_attrs, "quant_method": "group"}
+            param = torch.nn.Parameter(value, requires_grad=False)
+            for key, attr in attrs.items():
+                setattr(param, key, attr)
+            if isinstance(layer, torch.nn.Module):
+                layer.register_parameter(name, param)
+            else:
+                setattr(layer, name, param)
+        layer.intermediate_size_per_partition = i
+
+    @staticmethod
+    def load_weight(layer, name: str, loaded_weight: torch.Tensor, expert_id: int, shard_id: str,
+                    tp_rank: int = 0, tp_size: int = 1) -> None:
+        """Copies tensor-parallel rank tp_rank's shard of one expert's checkpoint
+        tensor into `layer`.  w1 / w3 (gate / up: [I, H/2] packed weights, [I,
+        H/128] scales) are split along dim 0 and land in the first / second half
+        of the w13 rows; w2 ([H, I/2], [H, I/128]) is split along dim 1.  The
+        input-scale placeholders are ignored: activations are quantised
+        dynamically.  Same shards as vLLM's fused-MoE loader
+        (_load_w13 / _load_w2, exercised by tests/test_w4afp8_quantization.py:228-293)."""
+        if name.endswith("input_scale"):
+            return
+        if not 0 <= tp_rank < tp_size:
+            raise ValueError(f"tp_rank {tp_rank} is outside tp_size {tp_size}")
+        dest = getattr(layer, name).data[expert_id]
+        if shard_id in ("w1", "w3"):
+            if not name.startswith("w13"):
+                raise ValueError(f"shard {shard_id} belongs to w13, not {name}")
+            half = dest.shape[0] // 2
+            if tuple(loaded_weight.shape) != (half * tp_size, dest.shape[1]):
+                raise ValueError(f"{name}/{shard_id}: checkpoint shape {tuple(loaded_weight.shape)}, "
+                                 f"expected {(half * tp_size, dest.shape[1])}")
+            src = loaded_weight.narrow(0, half * tp_rank, half)
+            dest = dest.narrow(0, half if shard_id == "w3" else 0, half)
+        elif shard_id == "w2":
+            if not name.startswith("w2"):
+                raise ValueError(f"shard w2 belongs to w2, not {name}")
+            cols = dest.shape[1]
+            if tuple(loaded_weight.shape) != (dest.shape[0], cols * tp_size):
+                raise ValueError(f"{name}/w2: checkpoint shape {tuple(loaded_weight.shape)}, "
+                                 f"expected {(dest.shape[0], cols * tp_size)}")
+            src = loaded_weight.narrow(1, cols * tp_rank, cols)
+        else:
+            raise ValueError(f"unknown shard id {shard_id!r}")
+        dest.copy_(src)
+
+    def process_weights_after_loading(self, layer) -> None:
+        """Scales -> bf16 (round to nearest even) on the GPU; a scale that is not
+        finite and positive after the cast raises ValueError naming its tensor
+        (quantization/w4afp8.py:126-135)."""
+        for name in ("w13_weight_scale_inv", "w2_weight_scale_inv"):
+            src = getattr(layer, name).data.contiguous()
+            dst = torch.empty(src.shape, dtype=torch.bfloat16, device=src.device)
+            bad = torch.zeros(1, dtype=torch.int32, device=src.device)
+            ops.convert_scales(src, dst, bad)
+            if int(bad.item()):
+                raise ValueError(f"Invalid W4AFP8 weight scale in {name}")
+            setattr(layer, name, torch.nn.Parameter(dst, requires_grad=False))
 
     def apply(self, layer, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
               shared_experts=None, shared_experts_input: torch.Tensor | None = None):
