@@ -381,6 +381,43 @@ def scales_sweep(torch, iters: int, log) -> int:
     return 0
 
 
+def router_sweep(torch, iters: int, log) -> int:
+    """The fp32 router gate of Nemotron-H (x [M, 2688] bf16 . W [128, 2688]^T fp32)
+    at M = 1, 7, 115, 512: vmamd_router_gate_fp32 against the platform's fp32
+    GEMM on the same operands (F.linear(x.float(), W), the caller's own path),
+    eager and as HIP-graph replays, caches flushed by a 1 GiB read before each
+    call.  Bytes = W + x + logits."""
+    import torch.nn.functional as F
+    from vllm_musa_amd import _custom_ops as ops
+    k, e = 2688, 128
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    flush = lambda: flush_buf.max()
+    g = torch.Generator(device="cuda").manual_seed(11)
+    w = torch.randn((e, k), device="cuda", generator=g)
+    for m in (1, 7, 115, 512):
+        x = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+        out = torch.empty((m, e), device="cuda")
+        ours = lambda: ops.router_gate_fp32(x, w, out)
+        plat = lambda: F.linear(x.float(), w)
+        for _ in range(3):
+            ours(), plat()
+        torch.cuda.synchronize()
+        t_ours = statistics.median(time_events(torch, ours, iters, flush)) * 1e3
+        t_plat = statistics.median(time_events(torch, plat, iters, flush)) * 1e3
+        g_ours = graph_median(torch, ours, iters, flush) * 1e3
+        g_plat = graph_median(torch, plat, iters, flush) * 1e3
+        by = e * k * 4 + m * k * 2 + m * e * 4
+        print(json.dumps({"M": m, "us": round(t_ours, 2), "graph_us": round(g_ours, 2),
+                          "platform_fp32_us": round(t_plat, 2),
+                          "platform_fp32_graph_us": round(g_plat, 2),
+                          "speedup_graph": round(g_plat / g_ours, 2),
+                          "frac_hbm_graph": round(by / (g_ours * 1e-6) / (PEAK_HBM_GBS * 1e9), 3),
+                          "gflops_graph": round(2.0 * m * k * e / (g_ours * 1e-6) / 1e9, 1)}),
+              flush=True)
+    log("bench: router gate sweep done")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -412,6 +449,9 @@ def main() -> int:
                     help="only time the checkpoint scale conversions (e8m0 -> f32 of the "
                          "DeepSeek-V3 MoE block scales, f32 -> bf16 + check of a w4afp8 layer's "
                          "group scales), one JSON line per workload")
+    ap.add_argument("--router", action="store_true",
+                    help="only time the fp32 router gate (Nemotron-H, [M, 2688] x [128, 2688]^T) "
+                         "against the platform fp32 GEMM at M = 1, 7, 115, 512")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE layer runs on a single MI355X here "
@@ -435,6 +475,8 @@ def main() -> int:
         return swiglu_sweep(torch, args.sweep_iters, log)
     if args.scales:
         return scales_sweep(torch, args.sweep_iters, log)
+    if args.router:
+        return router_sweep(torch, args.sweep_iters, log)
 
     log(f"bench: building E={E} H={H} I={I} fp8 expert stack")
     weights = synthetic.moe_fp8_weights(E, H, I, WEIGHT_SEED)

@@ -356,6 +356,19 @@ int vmamd_w4afp8_moe(const void* x, int64_t T, int64_t H, const void* w13, const
 int vmamd_convert_scales(const void* src, int src_dtype, int64_t n, void* dst, int dst_dtype,
                          int32_t* invalid_count, vmamd_stream_t stream);
 
+/* ------------------------------------------------------ router-gate GEMM --
+ * logits[M, E] = x[M, K] . w[E, K]^T in IEEE fp32, with one fixed summation
+ * order per logit (independent of M and of the launch): lane l of 64 runs a
+ * fused-multiply-add chain over k = 2l + 128i + j (i ascending, j = 0, 1),
+ * starting from +0, and the 64 partials are added by an xor butterfly
+ * (p_l += p_{l^s}, s = 32, 16, 8, 4, 2, 1).  x: bf16 or f32, rows contiguous
+ * (stride K); w: f32 [E, K] contiguous; y: f32 [M, E] contiguous.
+ * K % 128 == 0, E <= 65535.  M = 0 is a no-op.
+ * Replaces router_gate_fp32 / _router_gate_fp32_kernel
+ * (vllm_musa/model_executor/layers/fused_moe/router/musa_router_gemm.py:140-266). */
+int vmamd_router_gate_fp32(const void* x, int x_dtype, int64_t M, int64_t K, const float* w,
+                           int64_t E, float* y, vmamd_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,6 +17,7 @@ Modules:
   moe       -- fused experts (bf16 and fp8-block), moe_sum
   w4afp8    -- the w4afp8 MoE reference
   scales    -- checkpoint scale conversion (e8m0 upcast, bf16 cast + check)
+  router_gate -- fp32 router-gate GEMM in its fixed summation order
 
 How each function is pinned (golden vectors, closed forms, brute force,
 library cross-checks) is listed in tests/test_oracle_*.py.

@@ -334,3 +334,26 @@ def convert_scales(src: torch.Tensor, dst: torch.Tensor,
         raise ValueError("invalid_count must be a single int32")
     call("vmamd_convert_scales", ptr(src), _SCALE_SRC[src.dtype], src.numel(), ptr(dst),
          _SCALE_DST[dst.dtype], ptr(invalid_count), stream_of(dst))
+
+
+# ------------------------------------------------------- router-gate GEMM --
+def router_gate_fp32(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor) -> None:
+    """out[M, E] = x[M, K] . weight[E, K]^T in fp32 with a fixed, batch-invariant
+    summation order (x bf16 or f32, weight f32, K % 128 == 0).  Reference:
+    _router_gate_fp32_kernel (fused_moe/router/musa_router_gemm.py:140-226)."""
+    check_cuda(x, weight, out)
+    if x.dim() != 2 or weight.dim() != 2 or out.dim() != 2:
+        raise ValueError("router_gate_fp32 expects 2-D x, weight and out")
+    for t, name in ((x, "x"), (weight, "weight"), (out, "out")):
+        _contig(t, name)
+    m, k = x.shape
+    e = weight.shape[0]
+    if weight.shape[1] != k or tuple(out.shape) != (m, e):
+        raise ValueError(f"router_gate_fp32: x {tuple(x.shape)}, weight {tuple(weight.shape)}, "
+                         f"out {tuple(out.shape)} do not match")
+    if weight.dtype != torch.float32 or out.dtype != torch.float32:
+        raise ValueError("router_gate_fp32: weight and out must be float32")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("router_gate_fp32: x must be float32 or bfloat16")
+    call("vmamd_router_gate_fp32", ptr(x), dtype_code(x.dtype), m, k, ptr(weight), e, ptr(out),
+         stream_of(x))
