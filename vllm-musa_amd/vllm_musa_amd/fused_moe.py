@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 
 from . import _custom_ops as ops
-from . import _lib
+from . import _lib, dispatch_policy
 from ._lib import call, ptr, stream_of
 
 
@@ -85,7 +85,9 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
     rounding points.  Supported: bf16 weights, and fp8 weights with 128x128
     block scales (use_fp8_w8a8, block_shape=[128, 128]) and dynamic 1x128
     activation quantisation.  ``path`` forces the decode ("gemv") or prefill
-    ("gemm") kernels; "auto" picks by routes per expert."""
+    ("gemm") kernels; "auto" asks the dispatch policy (the calibrated per-shape
+    table, the VLLM_MUSA_FUSED_MOE_DISPATCH override) and otherwise picks by
+    routes per expert."""
     if activation != "silu":
         raise NotImplementedError(f"activation {activation!r}: only silu (SwiGLU) is on this path")
     if use_int8_w8a8 or use_int8_w8a16 or use_int4_w4a16 or ocp_mx_scheme or per_channel_quant:
@@ -117,6 +119,11 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
     wts = topk_weights.to(torch.float32).contiguous()
     emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
     limit = 0.0 if gemm1_clamp_limit is None else float(gemm1_clamp_limit)
+    if path == "auto":
+        path = dispatch_policy.resolve_path(hidden_states, w1, w2,
+                                            w1_scale if use_fp8_w8a8 else None,
+                                            w2_scale if use_fp8_w8a8 else None, topk,
+                                            block_shape, expert_map)
     code = PATHS[path]
     if use_fp8_w8a8:
         if block_shape is None or list(block_shape) != [128, 128]:
