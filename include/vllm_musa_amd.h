@@ -125,6 +125,23 @@ int vmamd_extend_topk_with_shared(const float* topk_weights, const int32_t* topk
 #define VMAMD_SCORING_SOFTMAX 0
 #define VMAMD_SCORING_SIGMOID 1
 
+/* Softmax / sigmoid top-k with the fused shared expert: as vmamd_topk_softmax
+ * / vmamd_topk_sigmoid for the topk routed columns, plus column topk of each
+ * [tokens, topk + 1] output row = the shared expert (weight = sigmoid of
+ * shared_logits[t] in fp32, rounded to shared_dtype; id = shared_expert_id;
+ * outside the renormalisation), written by the same kernel.  topk <= 63.
+ * Replaces the shared1 variants of topk_softmax / topk_sigmoid
+ * (vllm_musa/jit_kernel/csrc/topk/topk_gating.mu:369-456, jit_kernel/csrc/topk.py:35-100). */
+int vmamd_topk_softmax_shared(const void* gating, int dtype, int64_t tokens, int experts, int topk,
+                              int renormalize, float softcap, const float* bias,
+                              const void* shared_logits, int shared_dtype,
+                              int32_t shared_expert_id, float* topk_weights, int32_t* topk_ids,
+                              vmamd_stream_t stream);
+int vmamd_topk_sigmoid_shared(const void* gating, int dtype, int64_t tokens, int experts, int topk,
+                              int renormalize, const float* bias, const void* shared_logits,
+                              int shared_dtype, int32_t shared_expert_id, float* topk_weights,
+                              int32_t* topk_ids, vmamd_stream_t stream);
+
 /* Grouped top-k (DeepSeek-V3 routing).  scores = softmax or sigmoid of the
  * gating row; sel = scores + bias (bias may be NULL); group score = sum of
  * the top-2 sel in the group when bias != NULL, else the group max; keep the

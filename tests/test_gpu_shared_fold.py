@@ -120,3 +120,23 @@ def test_folded_apply_accepts_router_with_shared_column():
     a = method.apply(layer, x, w, ids)
     b = method.apply(layer, x, we, ie)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("kind", ["softmax", "sigmoid"])
+@pytest.mark.parametrize("gate_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("experts,topk,tokens", [(256, 8, 37), (64, 6, 1), (128, 63, 5)])
+def test_fused_shared_column_equals_two_launch_composition(kind, gate_dtype, experts, topk, tokens):
+    from vllm_musa_amd import _custom_ops as ops
+    g = torch.Generator().manual_seed(experts + topk + tokens)
+    logits = torch.randn(tokens, experts, generator=g).to(gate_dtype).cuda()
+    shared = (torch.randn(tokens, 1, generator=g) * 3).to(gate_dtype).cuda()
+    fn = ops.topk_softmax if kind == "softmax" else ops.topk_sigmoid
+    w1 = torch.full((tokens, topk + 1), float("nan"), device="cuda")
+    i1 = torch.full((tokens, topk + 1), -1, dtype=torch.int32, device="cuda")
+    fn(w1, i1, logits, True, shared_expert_gate_output=shared, num_fused_shared_experts=1)
+    w0 = torch.empty(tokens, topk, device="cuda")
+    i0 = torch.empty(tokens, topk, dtype=torch.int32, device="cuda")
+    fn(w0, i0, logits, True)
+    w2, i2 = ops.extend_topk_with_shared(w0, i0, shared.reshape(-1), experts)
+    assert torch.equal(i1, i2) and torch.equal(w1, w2)
+    assert (i1[:, topk] == experts).all()

@@ -49,12 +49,46 @@ __device__ __forceinline__ int select_round(const float (&v)[VPT], uint32_t& ali
   return bi;
 }
 
+// Fused shared expert: one more output column per token, weight = sigmoid of
+// the token's shared gate logit computed in fp32 and rounded to the logit
+// dtype, id = the shared expert's id (topk_gating.mu:369-456 writes it in the
+// same kernel as the routed top-k).  logits == nullptr: no shared column.
+struct SharedCol {
+  const void* logits;
+  int dtype;
+  int32_t id;
+};
+
+template <int DT>
+__device__ __forceinline__ float shared_weight(const typename Elem<DT>::T* logits, int64_t t) {
+  const float s = 1.0f / (1.0f + expf(-Elem<DT>::load(logits, t)));
+  return Elem<DT>::to_f(Elem<DT>::from_f(s));
+}
+
+__device__ __forceinline__ float shared_weight_rt(const SharedCol& sh, int64_t t) {
+  switch (sh.dtype) {
+    case kF32: return shared_weight<kF32>(static_cast<const float*>(sh.logits), t);
+    case kF16: return shared_weight<kF16>(static_cast<const uint16_t*>(sh.logits), t);
+    default: return shared_weight<kBF16>(static_cast<const uint16_t*>(sh.logits), t);
+  }
+}
+
+// Output row r holds the routed top-k in columns [0, topk) and, with a shared
+// column, that expert in column topk (row stride topk + 1).
+__device__ __forceinline__ void write_shared(const SharedCol& sh, int lane, int topk, int64_t row,
+                                             float* w_out, int32_t* id_out) {
+  if (sh.logits && lane == topk) {
+    w_out[row * (topk + 1) + topk] = shared_weight_rt(sh, row);
+    id_out[row * (topk + 1) + topk] = sh.id;
+  }
+}
+
 // ------------------------------------------------------- softmax top-k ----
 template <int DT, int VPT>
 __global__ __launch_bounds__(kRouteWaves * kWave) void topk_softmax_kernel(
     const void* __restrict__ gating, int64_t tokens, int experts, int topk, bool renorm,
     float softcap, const float* __restrict__ bias, float* __restrict__ w_out,
-    int32_t* __restrict__ id_out) {
+    int32_t* __restrict__ id_out, SharedCol sh) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRouteWaves + threadIdx.x / kWave;
   if (row >= tokens) return;
   const int lane = lane_id();
@@ -96,17 +130,20 @@ __global__ __launch_bounds__(kRouteWaves * kWave) void topk_softmax_kernel(
     // Retired entries still hold their logits in v[], so the sum is complete.
     denom = wave_sum(part);
   }
+  const int64_t ostride = sh.logits ? topk + 1 : topk;
   if (lane < topk) {
-    w_out[row * topk + lane] = my_w / denom;
-    id_out[row * topk + lane] = my_id;
+    w_out[row * ostride + lane] = my_w / denom;
+    id_out[row * ostride + lane] = my_id;
   }
+  write_shared(sh, lane, topk, row, w_out, id_out);
 }
 
 // ------------------------------------------------------- sigmoid top-k ----
 template <int DT, int VPT>
 __global__ __launch_bounds__(kRouteWaves * kWave) void topk_sigmoid_kernel(
     const void* __restrict__ gating, int64_t tokens, int experts, int topk, bool renorm,
-    const float* __restrict__ bias, float* __restrict__ w_out, int32_t* __restrict__ id_out) {
+    const float* __restrict__ bias, float* __restrict__ w_out, int32_t* __restrict__ id_out,
+    SharedCol sh) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRouteWaves + threadIdx.x / kWave;
   if (row >= tokens) return;
   const int lane = lane_id();
@@ -141,10 +178,12 @@ __global__ __launch_bounds__(kRouteWaves * kWave) void topk_sigmoid_kernel(
       my_id = bi;
     }
   }
+  const int64_t ostride = sh.logits ? topk + 1 : topk;
   if (lane < topk) {
-    w_out[row * topk + lane] = renorm ? my_w / sum : my_w;
-    id_out[row * topk + lane] = my_id;
+    w_out[row * ostride + lane] = renorm ? my_w / sum : my_w;
+    id_out[row * ostride + lane] = my_id;
   }
+  write_shared(sh, lane, topk, row, w_out, id_out);
 }
 
 // ------------------------------------------------------- grouped top-k ----
@@ -355,8 +394,7 @@ __global__ __launch_bounds__(256) void extend_topk_shared_kernel(
     w_out[i] = w_in[t * topk + k];
     ids_out[i] = ids_in[t * topk + k];
   } else {
-    const float s = 1.0f / (1.0f + expf(-Elem<DT>::load(logits, t)));
-    w_out[i] = Elem<DT>::to_f(Elem<DT>::from_f(s));
+    w_out[i] = shared_weight<DT>(logits, t);
     ids_out[i] = shared_id;
   }
 }
@@ -407,8 +445,30 @@ extern "C" int vmamd_topk_softmax(const void* gating, int dtype, int64_t tokens,
   if (tokens == 0) return VMAMD_OK;
   VMAMD_REQUIRE(gating && topk_weights && topk_ids, "topk_softmax: null pointer");
   VMAMD_ROUTE_DISPATCH(topk_softmax_kernel, gating, tokens, experts, topk, renormalize != 0, softcap,
-                       bias, topk_weights, topk_ids);
+                       bias, topk_weights, topk_ids, SharedCol{nullptr, 0, 0});
   return check_launch("topk_softmax");
+}
+
+extern "C" int vmamd_topk_softmax_shared(const void* gating, int dtype, int64_t tokens,
+                                         int experts, int topk, int renormalize, float softcap,
+                                         const float* bias, const void* shared_logits,
+                                         int shared_dtype, int32_t shared_expert_id,
+                                         float* topk_weights, int32_t* topk_ids,
+                                         vmamd_stream_t stream) {
+  VMAMD_REQUIRE(experts > 0 && experts <= 1024,
+                "topk_softmax_shared: experts must be in [1, 1024] (got %d)", experts);
+  VMAMD_REQUIRE(topk > 0 && topk <= experts && topk < 64,
+                "topk_softmax_shared: topk must be in [1, min(experts, 63)] (got %d)", topk);
+  VMAMD_REQUIRE(shared_dtype == kF32 || shared_dtype == kF16 || shared_dtype == kBF16,
+                "topk_softmax_shared: unsupported shared logit dtype %d", shared_dtype);
+  VMAMD_REQUIRE(tokens >= 0, "topk_softmax_shared: negative token count");
+  if (tokens == 0) return VMAMD_OK;
+  VMAMD_REQUIRE(gating && shared_logits && topk_weights && topk_ids,
+                "topk_softmax_shared: null pointer");
+  VMAMD_ROUTE_DISPATCH(topk_softmax_kernel, gating, tokens, experts, topk, renormalize != 0, softcap,
+                       bias, topk_weights, topk_ids,
+                       SharedCol{shared_logits, shared_dtype, shared_expert_id});
+  return check_launch("topk_softmax_shared");
 }
 
 extern "C" int vmamd_topk_sigmoid(const void* gating, int dtype, int64_t tokens, int experts,
@@ -422,8 +482,29 @@ extern "C" int vmamd_topk_sigmoid(const void* gating, int dtype, int64_t tokens,
   if (tokens == 0) return VMAMD_OK;
   VMAMD_REQUIRE(gating && topk_weights && topk_ids, "topk_sigmoid: null pointer");
   VMAMD_ROUTE_DISPATCH(topk_sigmoid_kernel, gating, tokens, experts, topk, renormalize != 0, bias,
-                       topk_weights, topk_ids);
+                       topk_weights, topk_ids, SharedCol{nullptr, 0, 0});
   return check_launch("topk_sigmoid");
+}
+
+extern "C" int vmamd_topk_sigmoid_shared(const void* gating, int dtype, int64_t tokens,
+                                         int experts, int topk, int renormalize, const float* bias,
+                                         const void* shared_logits, int shared_dtype,
+                                         int32_t shared_expert_id, float* topk_weights,
+                                         int32_t* topk_ids, vmamd_stream_t stream) {
+  VMAMD_REQUIRE(experts > 0 && experts <= 1024,
+                "topk_sigmoid_shared: experts must be in [1, 1024] (got %d)", experts);
+  VMAMD_REQUIRE(topk > 0 && topk <= experts && topk < 64,
+                "topk_sigmoid_shared: topk must be in [1, min(experts, 63)] (got %d)", topk);
+  VMAMD_REQUIRE(shared_dtype == kF32 || shared_dtype == kF16 || shared_dtype == kBF16,
+                "topk_sigmoid_shared: unsupported shared logit dtype %d", shared_dtype);
+  VMAMD_REQUIRE(tokens >= 0, "topk_sigmoid_shared: negative token count");
+  if (tokens == 0) return VMAMD_OK;
+  VMAMD_REQUIRE(gating && shared_logits && topk_weights && topk_ids,
+                "topk_sigmoid_shared: null pointer");
+  VMAMD_ROUTE_DISPATCH(topk_sigmoid_kernel, gating, tokens, experts, topk, renormalize != 0, bias,
+                       topk_weights, topk_ids,
+                       SharedCol{shared_logits, shared_dtype, shared_expert_id});
+  return check_launch("topk_sigmoid_shared");
 }
 
 extern "C" int vmamd_grouped_topk(const void* gating, int dtype, int64_t tokens, int experts,

@@ -142,6 +142,15 @@ def extend_topk_with_shared(topk_weights: torch.Tensor, topk_ids: torch.Tensor,
     return out_weights, out_ids
 
 
+def _shared_logits(shared_expert_gate_output, tokens):
+    """The shared gate logits as a contiguous [T] vector of the gate's dtype."""
+    check_cuda(shared_expert_gate_output)
+    logits = shared_expert_gate_output.reshape(-1)
+    if logits.numel() != tokens:
+        raise ValueError(f"shared_expert_gate_output has {logits.numel()} logits for {tokens} tokens")
+    return logits.contiguous()
+
+
 def _shared_columns(topk_weights, shared_expert_gate_output, num_fused_shared_experts):
     """Number of routed columns when the top-k also appends the fused shared
     expert (the reference's shared1 kernels take exactly one)."""
@@ -169,13 +178,16 @@ def topk_softmax(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_outp
             raise ValueError("correction_bias must be float32 [num_experts]")
     t, e = gating_output.shape
     k, shared = _shared_columns(topk_weights, shared_expert_gate_output, num_fused_shared_experts)
-    w = torch.empty(t, k, dtype=torch.float32, device=gating_output.device) if shared else topk_weights
-    ids = torch.empty(t, k, dtype=torch.int32, device=gating_output.device) if shared else topk_ids
+    if shared:
+        logits = _shared_logits(shared_expert_gate_output, t)
+        call("vmamd_topk_softmax_shared", ptr(gating_output), dtype_code(gating_output.dtype), t,
+             e, k, int(bool(renormalize)), float(moe_softcapping), ptr(correction_bias),
+             ptr(logits), dtype_code(logits.dtype), e, ptr(topk_weights), ptr(topk_ids),
+             stream_of(gating_output))
+        return
     call("vmamd_topk_softmax", ptr(gating_output), dtype_code(gating_output.dtype), t, e,
          k, int(bool(renormalize)), float(moe_softcapping),
-         ptr(correction_bias), ptr(w), ptr(ids), stream_of(gating_output))
-    if shared:
-        extend_topk_with_shared(w, ids, shared_expert_gate_output, e, topk_weights, topk_ids)
+         ptr(correction_bias), ptr(topk_weights), ptr(topk_ids), stream_of(gating_output))
 
 
 def topk_sigmoid(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_output: torch.Tensor,
@@ -191,13 +203,16 @@ def topk_sigmoid(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_outp
             raise ValueError("correction_bias must be float32 [num_experts]")
     t, e = gating_output.shape
     k, shared = _shared_columns(topk_weights, shared_expert_gate_output, num_fused_shared_experts)
-    w = torch.empty(t, k, dtype=torch.float32, device=gating_output.device) if shared else topk_weights
-    ids = torch.empty(t, k, dtype=torch.int32, device=gating_output.device) if shared else topk_ids
-    call("vmamd_topk_sigmoid", ptr(gating_output), dtype_code(gating_output.dtype), t, e,
-         k, int(bool(renormalize)), ptr(correction_bias), ptr(w),
-         ptr(ids), stream_of(gating_output))
     if shared:
-        extend_topk_with_shared(w, ids, shared_expert_gate_output, e, topk_weights, topk_ids)
+        logits = _shared_logits(shared_expert_gate_output, t)
+        call("vmamd_topk_sigmoid_shared", ptr(gating_output), dtype_code(gating_output.dtype), t,
+             e, k, int(bool(renormalize)), ptr(correction_bias), ptr(logits),
+             dtype_code(logits.dtype), e, ptr(topk_weights), ptr(topk_ids),
+             stream_of(gating_output))
+        return
+    call("vmamd_topk_sigmoid", ptr(gating_output), dtype_code(gating_output.dtype), t, e, k,
+         int(bool(renormalize)), ptr(correction_bias), ptr(topk_weights), ptr(topk_ids),
+         stream_of(gating_output))
 
 
 def grouped_topk_into(topk_weights: torch.Tensor, topk_ids: torch.Tensor,
