@@ -346,9 +346,38 @@ __device__ __forceinline__ void gate_up8(const float* __restrict__ partial, int 
   }
 }
 
+// gate_up8 with the split count fixed (SPL <= 4): all loads are issued before
+// the first add, which keeps the same summation order.
+template <int SPL>
+__device__ __forceinline__ void gate_up8_fixed(const float* __restrict__ partial, int numel, int I,
+                                               int r, int c0, float (&g)[8], float (&u)[8]) {
+  const int64_t plane = static_cast<int64_t>(numel) * 2 * I;
+  const float* src = partial + static_cast<int64_t>(r) * 2 * I + c0;
+  float4 gs[2][SPL], us[2][SPL];
+#pragma unroll
+  for (int s = 0; s < SPL; ++s)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      gs[h][s] = *reinterpret_cast<const float4*>(src + s * plane + 4 * h);
+      us[h][s] = *reinterpret_cast<const float4*>(src + s * plane + I + 4 * h);
+    }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float4 a = gs[h][0], b = us[h][0];
+#pragma unroll
+    for (int s = 1; s < SPL; ++s) {
+      a.x += gs[h][s].x; a.y += gs[h][s].y; a.z += gs[h][s].z; a.w += gs[h][s].w;
+      b.x += us[h][s].x; b.y += us[h][s].y; b.z += us[h][s].z; b.w += us[h][s].w;
+    }
+    g[4 * h + 0] = a.x; g[4 * h + 1] = a.y; g[4 * h + 2] = a.z; g[4 * h + 3] = a.w;
+    u[4 * h + 0] = b.x; u[4 * h + 1] = b.y; u[4 * h + 2] = b.z; u[4 * h + 3] = b.w;
+  }
+}
+
 // kFp8: activation then a2 quantisation per 1x128 group (one 16-lane segment
 // per group, 8 columns per lane).  NaN activations (clamped variant) quantise
-// to fp8_min.
+// to fp8_min.  SPL > 0: the split count, fixed at compile time; 0: runtime.
+template <int SPL>
 __global__ __launch_bounds__(256) void moe_act_quant_kernel(const float* __restrict__ partial,
                                                             int splits, int numel, int I,
                                                             float limit, uint8_t* __restrict__ a2q,
@@ -360,7 +389,10 @@ __global__ __launch_bounds__(256) void moe_act_quant_kernel(const float* __restr
   const int r = static_cast<int>(g / gpr);
   const int c0 = static_cast<int>(g % gpr) * 128 + sub * 8;
   float gv[8], uv[8], v[8];
-  gate_up8(partial, splits, numel, I, r, c0, 1.0f, gv, uv);
+  if constexpr (SPL > 0)
+    gate_up8_fixed<SPL>(partial, numel, I, r, c0, gv, uv);
+  else
+    gate_up8(partial, splits, numel, I, r, c0, 1.0f, gv, uv);
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] = swiglu_bf16(bf16r(gv[j]), bf16r(uv[j]), limit);
   float amax = 1e-10f;
@@ -482,6 +514,86 @@ __global__ __launch_bounds__(256) void moe_w2_combine_kernel(
   o.z = static_cast<uint32_t>(f32_to_bf16(acc[4])) | (static_cast<uint32_t>(f32_to_bf16(acc[5])) << 16);
   o.w = static_cast<uint32_t>(f32_to_bf16(acc[6])) | (static_cast<uint32_t>(f32_to_bf16(acc[7])) << 16);
   *reinterpret_cast<uint4*>(out + static_cast<int64_t>(t) * N + n) = o;
+}
+
+// moe_w2_combine_kernel for topk <= 8 and SPL = splits <= 4, with every
+// load of a thread issued before its first add: dead slots read their own
+// (in-bounds) rows and are dropped by a select, so no branch orders the
+// loads.  Four columns per thread.  Same arithmetic, in the same order, as
+// moe_w2_combine_kernel.
+template <bool WEIGHTED, int SPL>
+__global__ __launch_bounds__(256) void moe_w2_combine_fast_kernel(
+    const float* __restrict__ partial, int T, int topk, int N, const int32_t* __restrict__ ids,
+    const int32_t* __restrict__ emap, int64_t emap_len, const float* __restrict__ yscale,
+    const float* __restrict__ topk_w, uint16_t* __restrict__ out) {
+  constexpr int KM = 8;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int cpr = N / 4;
+  if (i >= static_cast<int64_t>(T) * cpr) return;
+  const int t = static_cast<int>(i / cpr);
+  const int n = static_cast<int>(i % cpr) * 4;
+  const int64_t mn = static_cast<int64_t>(T) * topk * N;
+  bool live[KM];
+  float sc[KM], wk[KM];
+  float4 p[KM][SPL];
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    const int kk = k < topk ? k : topk - 1;
+    const int r = t * topk + kk;
+    const int e = ids[r];
+    live[k] = k < topk && e >= 0 && !(emap && (e >= emap_len || emap[e] < 0));
+    sc[k] = yscale ? yscale[r] : 1.0f;
+    wk[k] = WEIGHTED ? topk_w[r] : 1.0f;
+    const float* src = partial + static_cast<int64_t>(r) * N + n;
+#pragma unroll
+    for (int sp = 0; sp < SPL; ++sp) p[k][sp] = *reinterpret_cast<const float4*>(src + sp * mn);
+  }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    float4 a = p[k][0];
+#pragma unroll
+    for (int sp = 1; sp < SPL; ++sp) {
+      a.x += p[k][sp].x; a.y += p[k][sp].y; a.z += p[k][sp].z; a.w += p[k][sp].w;
+    }
+    const float v[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float q = bf16r(v[j] * sc[k]);
+      const float nx = WEIGHTED ? __builtin_fmaf(q, wk[k], acc[j]) : acc[j] + q;
+      acc[j] = live[k] ? nx : acc[j];
+    }
+  }
+  uint2 o;
+  o.x = static_cast<uint32_t>(f32_to_bf16(acc[0])) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16);
+  o.y = static_cast<uint32_t>(f32_to_bf16(acc[2])) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16);
+  *reinterpret_cast<uint2*>(out + static_cast<int64_t>(t) * N + n) = o;
+}
+
+template <bool WEIGHTED>
+static void launch_w2_combine(const float* partial, int splits, int T, int topk, int N,
+                              const int32_t* ids, const int32_t* emap, int64_t emap_len,
+                              const float* yscale, const float* topk_w, uint16_t* out,
+                              hipStream_t st) {
+  if (topk <= 8 && splits >= 1 && splits <= 4 && N % 4 == 0) {
+    const int64_t threads = static_cast<int64_t>(T) * (N / 4);
+    const int blocks = static_cast<int>((threads + 255) / 256);
+#define VMAMD_COMBINE(S)                                                                        \
+  moe_w2_combine_fast_kernel<WEIGHTED, S><<<blocks, 256, 0, st>>>(partial, T, topk, N, ids, emap, \
+                                                                  emap_len, yscale, topk_w, out)
+    switch (splits) {
+      case 1: VMAMD_COMBINE(1); break;
+      case 2: VMAMD_COMBINE(2); break;
+      case 3: VMAMD_COMBINE(3); break;
+      default: VMAMD_COMBINE(4); break;
+    }
+#undef VMAMD_COMBINE
+    return;
+  }
+  const int64_t chunks = static_cast<int64_t>(T) * (N / 8);
+  const int blocks = static_cast<int>((chunks + 255) / 256);
+  moe_w2_combine_kernel<WEIGHTED><<<blocks, 256, 0, st>>>(partial, splits, T, topk, N, ids, emap,
+                                                          emap_len, yscale, topk_w, out);
 }
 
 // ------------------------------------------------------ prefill GEMMs -----
@@ -1326,8 +1438,17 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
     if (rc) return rc;
     if constexpr (KIND == kFp8) {
       const int64_t groups = static_cast<int64_t>(numel) * (I / 128);
-      moe_act_quant_kernel<<<static_cast<int>((groups + 15) / 16), 256, 0, st>>>(
-          scratch, s13, numel, I, limit, a2, a2s);
+      const int blocks = static_cast<int>((groups + 15) / 16);
+#define VMAMD_ACTQ(S) \
+  moe_act_quant_kernel<S><<<blocks, 256, 0, st>>>(scratch, s13, numel, I, limit, a2, a2s)
+      switch (s13) {
+        case 1: VMAMD_ACTQ(1); break;
+        case 2: VMAMD_ACTQ(2); break;
+        case 3: VMAMD_ACTQ(3); break;
+        case 4: VMAMD_ACTQ(4); break;
+        default: VMAMD_ACTQ(0); break;
+      }
+#undef VMAMD_ACTQ
     } else {
       const int64_t chunks = static_cast<int64_t>(numel) * (I / 8);
       moe_act_bf16_kernel<KIND><<<static_cast<int>((chunks + 255) / 256), 256, 0, st>>>(
@@ -1376,14 +1497,12 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
                         static_cast<uint16_t*>(nullptr));
       int rc = check_launch("moe w2 (gemv)");
       if (rc) return rc;
-      const int64_t chunks = static_cast<int64_t>(T) * (H / 8);
-      const int blocks = static_cast<int>((chunks + 255) / 256);
       if constexpr (KIND == kW4)
-        moe_w2_combine_kernel<true><<<blocks, 256, 0, st>>>(scratch, s2, T, topk, H, topk_ids, emap,
-                                                            emap_len, yscale, topk_weights, combined_out);
+        launch_w2_combine<true>(scratch, s2, T, topk, H, topk_ids, emap, emap_len, yscale,
+                                topk_weights, combined_out, st);
       else
-        moe_w2_combine_kernel<false><<<blocks, 256, 0, st>>>(scratch, s2, T, topk, H, topk_ids, emap,
-                                                             emap_len, yscale, nullptr, combined_out);
+        launch_w2_combine<false>(scratch, s2, T, topk, H, topk_ids, emap, emap_len, yscale,
+                                 nullptr, combined_out, st);
       *combined = true;
       return check_launch("moe w2 (combine)");
     }
