@@ -18,7 +18,7 @@
 // active experts, expert_ids) and the sentinel `numel` at every position of
 // sorted_token_ids that no route takes, exactly once, so no ordering between
 // writers is needed.
-#include "common.h"
+#include "quant_dev.h"
 
 namespace vmamd {
 
@@ -40,8 +40,8 @@ __device__ __forceinline__ int mapped_expert(const int32_t* __restrict__ ids, in
 // workgroup only beyond 256 workgroups).
 constexpr int64_t kAlignChunk = kAlignThreads;
 
-__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
-    const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int E, int bs,
+__device__ __forceinline__ void align_body(
+    int blk, const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int E, int bs,
     const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ scatter_idx, int32_t* __restrict__ active_out,
@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   __syncthreads();
 
   // 1. histograms: all routes (cnt) and the routes before this chunk (run)
-  const int64_t c_begin = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t c_begin = static_cast<int64_t>(blk) * chunk;
   const int64_t c_end = min(numel, c_begin + chunk);
   for (int64_t r = tid; r < numel; r += kAlignThreads) {
     const int e = mapped_expert(ids, r, E, map, map_len);
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     }
   }
   __syncthreads();
-  const bool lead = blockIdx.x == 0;  // writes the per-call outputs
+  const bool lead = blk == 0;  // writes the per-call outputs
 
   // 2. exclusive scan of padded counts (E <= 1024: one expert per thread)
   int padded = 0;
@@ -174,9 +174,85 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
 }
 
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int E, int bs,
+    const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
+    int32_t* __restrict__ scatter_idx, int32_t* __restrict__ active_out,
+    int32_t* __restrict__ num_active_out) {
+  align_body(blockIdx.x, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids, ntpp,
+             offsets_out, scatter_idx, active_out, num_active_out);
+}
+
+// The MoE layer's two independent first steps in one launch: workgroups
+// [0, align_groups) run moe_align_block_size, the others the 1x128 fp8
+// quantiser of the bf16 activations (kAlignThreads / 16 groups each).
+__global__ __launch_bounds__(kAlignThreads) void moe_align_quant_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int align_groups, int E, int bs,
+    const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
+    int32_t* __restrict__ active_out, int32_t* __restrict__ num_active_out,
+    const uint16_t* __restrict__ x, int64_t groups_per_row, int64_t num_groups, bool vec,
+    uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  if (static_cast<int>(blockIdx.x) < align_groups) {
+    align_body(blockIdx.x, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids,
+               ntpp, offsets_out, nullptr, active_out, num_active_out);
+    return;
+  }
+  constexpr int kGroupsPerAlignBlock = kAlignThreads / kLanesPerGroup;
+  const int64_t g = static_cast<int64_t>(blockIdx.x - align_groups) * kGroupsPerAlignBlock +
+                    threadIdx.x / kLanesPerGroup;
+  if (g >= num_groups) return;
+  const int64_t cols = groups_per_row * kGroup;
+  group_quant_group<kBF16>(x, cols, groups_per_row, g, threadIdx.x % kLanesPerGroup, vec, 1e-10f,
+                           -448.f, 448.f, xq, cols, xs, groups_per_row, 1);
+}
+
 }  // namespace vmamd
 
 using namespace vmamd;
+
+namespace vmamd {
+// Work split of moe_align_block_size: one workgroup per chunk of 1024 routes,
+// at most 256 workgroups.
+static void align_grid(int64_t numel, int64_t& chunk, int& groups) {
+  chunk = kAlignChunk * std::max<int64_t>(1, (numel + kAlignChunk * 256 - 1) / (kAlignChunk * 256));
+  groups = static_cast<int>((numel + chunk - 1) / chunk);
+}
+
+int align_and_group_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_experts,
+                              int block_size, const int32_t* expert_map, int64_t expert_map_len,
+                              int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
+                              int32_t* offsets, int32_t* active, int32_t* num_active,
+                              const void* x, int64_t rows, int64_t cols, uint8_t* xq, float* xs,
+                              hipStream_t st) {
+  const char* who = "moe align + quant";
+  VMAMD_REQUIRE(num_experts > 0 && num_experts <= kMaxAlignExperts && block_size > 0, "%s: bad sizes",
+                who);
+  VMAMD_REQUIRE(numel >= 0 && numel < (1ll << 31) - 1 && capacity < (1ll << 31) &&
+                    capacity >= numel + static_cast<int64_t>(num_experts) * (block_size - 1),
+                "%s: bad route count or capacity", who);
+  VMAMD_REQUIRE(!expert_map || expert_map_len > 0, "%s: empty expert_map", who);
+  VMAMD_REQUIRE(rows >= 0 && cols > 0 && cols % kGroup == 0, "%s: cols must be a multiple of 128", who);
+  VMAMD_REQUIRE((topk_ids || numel == 0) && sorted && expert_ids && ntpp && (x || rows == 0) &&
+                    (reinterpret_cast<uintptr_t>(xq) & 7) == 0,
+                "%s: null or misaligned pointer", who);
+  int64_t chunk;
+  int groups;
+  align_grid(numel, chunk, groups);
+  groups = std::max(groups, 1);
+  const int64_t groups_per_row = cols / kGroup;
+  const int64_t num_groups = rows * groups_per_row;
+  const int64_t qblocks = (num_groups + kAlignThreads / kLanesPerGroup - 1) / (kAlignThreads / kLanesPerGroup);
+  const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;  // rows of cols % 128 == 0 bf16 stay aligned
+  moe_align_quant_kernel<<<static_cast<int>(groups + qblocks), kAlignThreads, 0, st>>>(
+      topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted,
+      capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),
+      groups_per_row, num_groups, vec, xq, xs);
+  return check_launch(who);
+}
+}  // namespace vmamd
 
 extern "C" int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int num_experts,
                                           int block_size, const int32_t* expert_map,
@@ -201,9 +277,9 @@ extern "C" int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel
                 "moe_align_block_size: active_experts and num_active go together");
   VMAMD_REQUIRE((topk_ids || numel == 0) && sorted_token_ids && expert_ids && num_tokens_post_pad,
                 "moe_align_block_size: null pointer");
-  // One workgroup per chunk of 1024 routes, at most 256 workgroups.
-  const int64_t chunk = kAlignChunk * std::max<int64_t>(1, (numel + kAlignChunk * 256 - 1) / (kAlignChunk * 256));
-  const int groups = static_cast<int>((numel + chunk - 1) / chunk);
+  int64_t chunk;
+  int groups;
+  align_grid(numel, chunk, groups);
   moe_align_kernel<<<groups > 0 ? groups : 1, kAlignThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
       topk_ids, numel, chunk, num_experts, block_size, expert_map, expert_map_len, sorted_token_ids,
       capacity, expert_ids, num_tokens_post_pad, expert_offsets, scatter_idx, active_experts,

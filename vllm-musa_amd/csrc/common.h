@@ -25,6 +25,16 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
 
+// moe_align_block_size and the 1x128 fp8 quantiser of bf16 activations
+// x [rows, cols] (into xq [rows, cols], xs [rows, cols / 128]) as one launch
+// (align.hip).
+int align_and_group_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_experts,
+                              int block_size, const int32_t* expert_map, int64_t expert_map_len,
+                              int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
+                              int32_t* offsets, int32_t* active, int32_t* num_active,
+                              const void* x, int64_t rows, int64_t cols, uint8_t* xq, float* xs,
+                              hipStream_t st);
+
 #define VMAMD_REQUIRE(cond, ...)                \
   do {                                          \
     if (!(cond)) {                              \

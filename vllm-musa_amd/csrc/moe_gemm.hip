@@ -1646,21 +1646,27 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
 
   const uint8_t* xa = static_cast<const uint8_t*>(x);
   const float* xs = nullptr;
-  if constexpr (KIND != kBf16) {
+  if constexpr (KIND == kFp8) {  // quantiser and alignment in one launch
     uint8_t* xq = ws + L.xq;
     float* xsw = reinterpret_cast<float*>(ws + L.xs);
-    if constexpr (KIND == kFp8)
-      rc = vmamd_per_token_group_quant_fp8(x, kBF16, T, H, H, 128, 1e-10f, -448.f, 448.f, xq, xsw,
-                                           H / 128, 1, stream);
-    else
-      rc = vmamd_per_token_quant_fp8(x, T, H, H, 1e-4f, -448.f, 448.f, xq, xsw, stream);
+    rc = align_and_group_quant_fp8(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
+                                   eids, ntpp, offs, active, nact, x, T, H, xq, xsw, st);
     if (rc) return rc;
     xa = xq;
     xs = xsw;
+  } else {
+    if constexpr (KIND == kW4) {
+      uint8_t* xq = ws + L.xq;
+      float* xsw = reinterpret_cast<float*>(ws + L.xs);
+      rc = vmamd_per_token_quant_fp8(x, T, H, H, 1e-4f, -448.f, 448.f, xq, xsw, stream);
+      if (rc) return rc;
+      xa = xq;
+      xs = xsw;
+    }
+    rc = vmamd_moe_align_block_size(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
+                                    eids, ntpp, offs, nullptr, active, nact, stream);
+    if (rc) return rc;
   }
-  rc = vmamd_moe_align_block_size(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
-                                  eids, ntpp, offs, nullptr, active, nact, stream);
-  if (rc) return rc;
   uint8_t* act_out = KIND == kW4 ? ws + L.abf : a2;  // kW4: bf16 activation, quantised below
   rc = launch_w13<KIND>(xa, xs, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
                         static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, act_out, a2s,

@@ -5,49 +5,9 @@
 // wave64 quantises 4 groups and a 256-thread block 16 groups.  The group
 // absmax is a 4-step xor-shuffle inside the 16-lane segment; scales and fp8
 // bytes are written straight from registers (8 bytes per lane).
-#include "common.h"
+#include "quant_dev.h"
 
 namespace vmamd {
-
-constexpr int kGroup = 128;
-constexpr int kLanesPerGroup = 16;
-constexpr int kElemsPerLane = kGroup / kLanesPerGroup;  // 8
-constexpr int kQuantThreads = 256;
-constexpr int kGroupsPerBlock = kQuantThreads / kLanesPerGroup;  // 16
-
-template <int DT>
-__device__ __forceinline__ void load8(const typename Elem<DT>::T* p, bool vec, float (&v)[8]) {
-  using T = typename Elem<DT>::T;
-  if constexpr (sizeof(T) == 2) {
-    if (vec) {
-      uint4 raw = *reinterpret_cast<const uint4*>(p);
-      const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = Elem<DT>::to_f(h[i]);
-      return;
-    }
-  } else {
-    if (vec) {
-      float4 a = reinterpret_cast<const float4*>(p)[0];
-      float4 b = reinterpret_cast<const float4*>(p)[1];
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-      return;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = Elem<DT>::load(p, i);
-}
-
-__device__ __forceinline__ uint2 quant8(const float (&v)[8], float s, float qmin, float qmax) {
-  float q[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = fminf(fmaxf(v[i] / s, qmin), qmax);
-  uint2 out;
-  out.x = f32x4_to_fp8x4(q[0], q[1], q[2], q[3]);
-  out.y = f32x4_to_fp8x4(q[4], q[5], q[6], q[7]);
-  return out;
-}
 
 // ----------------------------------------------------- group quantiser ---
 template <int DT>
@@ -58,19 +18,8 @@ __global__ __launch_bounds__(kQuantThreads) void group_quant_fp8_kernel(
   const int64_t g = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kLanesPerGroup;
   const int sub = threadIdx.x % kLanesPerGroup;
   if (g >= num_groups) return;
-  const int64_t row = g / groups_per_row;
-  const int64_t grp = g - row * groups_per_row;
-  const int64_t col = grp * kGroup + sub * kElemsPerLane;
-
-  float v[8];
-  load8<DT>(x + row * x_row_stride + col, vec, v);
-  float amax = eps;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = group_max<kLanesPerGroup>(amax);
-  const float scale = amax / qmax;
-  if (sub == 0) s[row * s_stride_row + grp * s_stride_group] = scale;
-  *reinterpret_cast<uint2*>(q + row * q_row_stride + col) = quant8(v, scale, qmin, qmax);
+  group_quant_group<DT>(x, x_row_stride, groups_per_row, g, sub, vec, eps, qmin, qmax, q,
+                        q_row_stride, s, s_stride_row, s_stride_group);
 }
 
 // -------------------------------------------------- SiLU and multiply -----

@@ -1,0 +1,73 @@
+// Device parts of the 1x128 group quantiser, shared by its own kernel and by
+// the fused align + quantise launch of the MoE layer:
+//   s = max(eps, amax of the group) / qmax,  q = e4m3fn(clamp(x / s, qmin, qmax)),
+// one 16-lane segment per 128-column group, 8 columns per lane.
+#pragma once
+
+#include "common.h"
+
+namespace vmamd {
+
+constexpr int kGroup = 128;
+constexpr int kLanesPerGroup = 16;
+constexpr int kElemsPerLane = kGroup / kLanesPerGroup;  // 8
+constexpr int kQuantThreads = 256;
+constexpr int kGroupsPerBlock = kQuantThreads / kLanesPerGroup;  // 16
+
+template <int DT>
+__device__ __forceinline__ void load8(const typename Elem<DT>::T* p, bool vec, float (&v)[8]) {
+  using T = typename Elem<DT>::T;
+  if constexpr (sizeof(T) == 2) {
+    if (vec) {
+      uint4 raw = *reinterpret_cast<const uint4*>(p);
+      const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = Elem<DT>::to_f(h[i]);
+      return;
+    }
+  } else {
+    if (vec) {
+      float4 a = reinterpret_cast<const float4*>(p)[0];
+      float4 b = reinterpret_cast<const float4*>(p)[1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      return;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = Elem<DT>::load(p, i);
+}
+
+__device__ __forceinline__ uint2 quant8(const float (&v)[8], float s, float qmin, float qmax) {
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = fminf(fmaxf(v[i] / s, qmin), qmax);
+  uint2 out;
+  out.x = f32x4_to_fp8x4(q[0], q[1], q[2], q[3]);
+  out.y = f32x4_to_fp8x4(q[4], q[5], q[6], q[7]);
+  return out;
+}
+
+// Group g (row g / groups_per_row) by the 16 lanes of one segment; sub is
+// the lane's index in the segment.  Every lane of the segment must call it.
+template <int DT>
+__device__ __forceinline__ void group_quant_group(
+    const typename Elem<DT>::T* __restrict__ x, int64_t x_row_stride, int64_t groups_per_row,
+    int64_t g, int sub, bool vec, float eps, float qmin, float qmax, uint8_t* __restrict__ q,
+    int64_t q_row_stride, float* __restrict__ s, int64_t s_stride_row, int64_t s_stride_group) {
+  const int64_t row = g / groups_per_row;
+  const int64_t grp = g - row * groups_per_row;
+  const int64_t col = grp * kGroup + sub * kElemsPerLane;
+
+  float v[8];
+  load8<DT>(x + row * x_row_stride + col, vec, v);
+  float amax = eps;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = group_max<kLanesPerGroup>(amax);
+  const float scale = amax / qmax;
+  if (sub == 0) s[row * s_stride_row + grp * s_stride_group] = scale;
+  *reinterpret_cast<uint2*>(q + row * q_row_stride + col) = quant8(v, scale, qmin, qmax);
+}
+
+}  // namespace vmamd
