@@ -37,6 +37,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "quant_dev.h"
 #include "mfma_fp8.h"
 #include "tile_pipe.h"
 
@@ -437,6 +438,50 @@ __global__ __launch_bounds__(256) void moe_act_bf16_kernel(const float* __restri
   o.z = static_cast<uint32_t>(f32_to_bf16(v[4])) | (static_cast<uint32_t>(f32_to_bf16(v[5])) << 16);
   o.w = static_cast<uint32_t>(f32_to_bf16(v[6])) | (static_cast<uint32_t>(f32_to_bf16(v[7])) << 16);
   *reinterpret_cast<uint4*>(a2 + static_cast<int64_t>(r) * I + c0) = o;
+}
+
+// kW4 decode: moe_act_bf16_kernel<kW4> and the per-row a2 quantiser in one
+// pass, one kRowThreads block per route row: the bf16-rounded activations stay
+// in registers for the row maximum and the quantiser (the values the separate
+// quantiser would read back), so neither the bf16 activation nor a second
+// launch is needed.  I <= kRowThreads * 8 * kRowChunks.
+__global__ __launch_bounds__(kRowThreads) void moe_act_rowquant_w4_kernel(
+    const float* __restrict__ partial, int splits, int numel, int I, float limit,
+    const float* __restrict__ xs, int topk, uint8_t* __restrict__ a2q, float* __restrict__ a2s) {
+  __shared__ float red[kRowThreads / kWave];
+  const int r = blockIdx.x;
+  const int nchunk = I / 8;
+  const float scale = xs[r / topk];
+  float v[kRowChunks][8];
+  float amax = 1e-4f;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int ch = threadIdx.x + c * kRowThreads;
+    if (ch < nchunk) {
+      float gv[8], uv[8];
+      gate_up8(partial, splits, numel, I, r, ch * 8, scale, gv, uv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[c][j] = bf16r(swiglu_w4(bf16r(gv[j]), bf16r(uv[j]), limit));
+        amax = fmaxf(amax, fabsf(v[c][j]));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  if (lane_id() == 0) red[threadIdx.x / kWave] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kRowThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
+  const float s = amax / 448.0f;
+  if (threadIdx.x == 0) a2s[r] = s;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int ch = threadIdx.x + c * kRowThreads;
+    if (ch < nchunk)
+      *reinterpret_cast<uint2*>(a2q + static_cast<int64_t>(r) * I + ch * 8) =
+          quant8(v[c], s, -448.0f, 448.0f);
+  }
 }
 
 // y[r, n] = bf16(sum_s partial[s, r, n] * w_r) for the W2 split path (kW4:
@@ -1449,6 +1494,9 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
         default: VMAMD_ACTQ(0); break;
       }
 #undef VMAMD_ACTQ
+    } else if constexpr (KIND == kW4) {  // a2: fp8 [numel, I], a2s: row scales
+      moe_act_rowquant_w4_kernel<<<numel, kRowThreads, 0, st>>>(scratch, s13, numel, I, limit, xs,
+                                                                topk, a2, a2s);
     } else {
       const int64_t chunks = static_cast<int64_t>(numel) * (I / 8);
       moe_act_bf16_kernel<KIND><<<static_cast<int>((chunks + 255) / 256), 256, 0, st>>>(
@@ -1654,28 +1702,31 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     if (rc) return rc;
     xa = xq;
     xs = xsw;
+  } else if constexpr (KIND == kW4) {  // per-row quantiser and alignment in one launch
+    uint8_t* xq = ws + L.xq;
+    float* xsw = reinterpret_cast<float*>(ws + L.xs);
+    rc = align_and_row_quant_fp8(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
+                                 eids, ntpp, offs, active, nact, x, T, H, xq, xsw, st);
+    if (rc) return rc;
+    xa = xq;
+    xs = xsw;
   } else {
-    if constexpr (KIND == kW4) {
-      uint8_t* xq = ws + L.xq;
-      float* xsw = reinterpret_cast<float*>(ws + L.xs);
-      rc = vmamd_per_token_quant_fp8(x, T, H, H, 1e-4f, -448.f, 448.f, xq, xsw, stream);
-      if (rc) return rc;
-      xa = xq;
-      xs = xsw;
-    }
     rc = vmamd_moe_align_block_size(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
                                     eids, ntpp, offs, nullptr, active, nact, stream);
     if (rc) return rc;
   }
-  uint8_t* act_out = KIND == kW4 ? ws + L.abf : a2;  // kW4: bf16 activation, quantised below
+  // kW4 prefill: bf16 activation, quantised per row below (the decode path
+  // writes the quantised a2 directly).
+  uint8_t* act_out = KIND == kW4 && bm != kGemvBlock ? ws + L.abf : a2;
   rc = launch_w13<KIND>(xa, xs, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
                         static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, act_out, a2s,
                         scratch, st);
   if (rc) return rc;
   if constexpr (KIND == kW4) {
-    const int64_t arows = bm == kGemvBlock ? numel : cap;
-    rc = vmamd_per_token_quant_fp8(act_out, arows, I, I, 1e-4f, -448.f, 448.f, a2, a2s, stream);
-    if (rc) return rc;
+    if (bm != kGemvBlock) {
+      rc = vmamd_per_token_quant_fp8(act_out, cap, I, I, 1e-4f, -448.f, 448.f, a2, a2s, stream);
+      if (rc) return rc;
+    }
   }
   bool combined = false;
   rc = launch_w2<KIND>(a2, a2s, t, topk, sorted, cap, bm, offs, ntpp, active, nact,

@@ -92,46 +92,12 @@ __global__ __launch_bounds__(kQuantThreads) void silu_mul_quant_fp8_kernel(
 }
 
 
-// ------------------------------------------------- per-row quantiser -----
-// s[r] = max(eps, max_c |x[r,c]|) / qmax over the whole row,
-// q[r,c] = e4m3(clamp(x[r,c] / s[r], qmin, qmax)).  One 256-thread block per
-// row, 8 columns per thread per pass; up to kRowChunks passes stay in
-// registers between the amax and the quantise steps.
-constexpr int kRowThreads = 256;
-constexpr int kRowChunks = 8;  // rows of up to 256 * 8 * 8 = 16384 columns
 
 __global__ __launch_bounds__(kRowThreads) void row_quant_fp8_kernel(
     const uint16_t* __restrict__ x, int64_t x_row_stride, int cols, float eps, float qmin,
     float qmax, uint8_t* __restrict__ q, float* __restrict__ s) {
   __shared__ float red[kRowThreads / kWave];
-  const int64_t row = blockIdx.x;
-  const uint16_t* xr = x + row * x_row_stride;
-  const int nchunk = cols / 8;
-  float v[kRowChunks][8];
-  float amax = eps;
-#pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int ch = threadIdx.x + c * kRowThreads;
-    if (ch < nchunk) {
-      load8<kBF16>(xr + ch * 8, true, v[c]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
-    }
-  }
-  amax = wave_max(amax);
-  if (lane_id() == 0) red[threadIdx.x / kWave] = amax;
-  __syncthreads();
-  amax = red[0];
-#pragma unroll
-  for (int w = 1; w < kRowThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
-  const float scale = amax / qmax;
-  if (threadIdx.x == 0) s[row] = scale;
-#pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    const int ch = threadIdx.x + c * kRowThreads;
-    if (ch < nchunk)
-      *reinterpret_cast<uint2*>(q + row * cols + ch * 8) = quant8(v[c], scale, qmin, qmax);
-  }
+  row_quant_part(x, x_row_stride, cols, eps, qmin, qmax, q, s, blockIdx.x, true, threadIdx.x, red);
 }
 
 }  // namespace vmamd

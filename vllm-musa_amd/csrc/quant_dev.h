@@ -70,4 +70,51 @@ __device__ __forceinline__ void group_quant_group(
   *reinterpret_cast<uint2*>(q + row * q_row_stride + col) = quant8(v, scale, qmin, qmax);
 }
 
+// ------------------------------------------------- per-row quantiser -----
+// s[r] = max(eps, max_c |x[r,c]|) / qmax over the whole row,
+// q[r,c] = e4m3(clamp(x[r,c] / s[r], qmin, qmax)).  One 256-thread block per
+// row, 8 columns per thread per pass; up to kRowChunks passes stay in
+// registers between the amax and the quantise steps.
+constexpr int kRowThreads = 256;
+constexpr int kRowChunks = 8;  // rows of up to 256 * 8 * 8 = 16384 columns
+
+// Per-row quantiser (w4afp8 activations): s = max(eps, amax of the row) /
+// qmax, q = e4m3fn(clamp(x / s, qmin, qmax)).  A part of kRowThreads threads
+// (t = 0 .. kRowThreads - 1 within it) handles one bf16 row; red holds the
+// part's kRowThreads / 64 wave maxima.  Every thread of the block must call
+// it (it synchronises the block); live = false parts only take part in the
+// barrier.
+__device__ __forceinline__ void row_quant_part(const uint16_t* __restrict__ x, int64_t x_row_stride,
+                                               int cols, float eps, float qmin, float qmax,
+                                               uint8_t* __restrict__ q, float* __restrict__ s,
+                                               int64_t row, bool live, int t, float* red) {
+  const uint16_t* xr = x + row * x_row_stride;
+  const int nchunk = live ? cols / 8 : 0;
+  float v[kRowChunks][8];
+  float amax = eps;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int ch = t + c * kRowThreads;
+    if (ch < nchunk) {
+      load8<kBF16>(xr + ch * 8, true, v[c]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
+    }
+  }
+  amax = wave_max(amax);
+  if (lane_id() == 0) red[t / kWave] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kRowThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
+  const float scale = amax / qmax;
+  if (live && t == 0) s[row] = scale;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int ch = t + c * kRowThreads;
+    if (ch < nchunk)
+      *reinterpret_cast<uint2*>(q + row * cols + ch * 8) = quant8(v[c], scale, qmin, qmax);
+  }
+}
+
 }  // namespace vmamd
