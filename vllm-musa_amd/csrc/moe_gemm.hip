@@ -1369,11 +1369,32 @@ static int64_t moe_umax(int64_t numel, int E) { return std::min<int64_t>(E, nume
 
 static int ksteps(int64_t K, int kind) { return static_cast<int>(K / (kind == kBf16 ? 64 : 128)); }
 
+// kW4 decode GEMVs run 3 waves per SIMD (1024 SIMDs on an MI355X): among
+// s = 1 .. KS / 4 the split with the fewest wave rounds x K steps per wave,
+// the smallest on ties, so the last round is not a partial one (no split
+// once one split's waves fill the GPU).
+static int w4_splits(int64_t waves_per_split, int KS) {
+  constexpr int64_t kSlots = 1024 * 3;
+  if (waves_per_split >= kSlots) return 1;  // one split already fills the GPU
+  int best = 1;
+  int64_t cost = -1;
+  for (int sp = 1; sp <= std::max(1, KS / 4); ++sp) {
+    const int64_t rounds = (waves_per_split * sp + kSlots - 1) / kSlots;
+    const int64_t c = rounds * ((KS + sp - 1) / sp);
+    if (cost < 0 || c < cost) {
+      cost = c;
+      best = sp;
+    }
+  }
+  return best;
+}
 static int w13_splits(int64_t numel, int E, int64_t H, int64_t I, int kind) {
-  return moe_splits(moe_umax(numel, E) * (2 * I / 16), ksteps(H, kind));
+  const int64_t wps = moe_umax(numel, E) * (2 * I / 16);
+  return kind == kW4 ? w4_splits(wps, ksteps(H, kind)) : moe_splits(wps, ksteps(H, kind));
 }
 static int w2_splits(int64_t numel, int E, int64_t H, int64_t I, int kind) {
-  return moe_splits(moe_umax(numel, E) * (H / 16), ksteps(I, kind));
+  const int64_t wps = moe_umax(numel, E) * (H / 16);
+  return kind == kW4 ? w4_splits(wps, ksteps(I, kind)) : moe_splits(wps, ksteps(I, kind));
 }
 
 static size_t al256(size_t x) { return (x + 255) / 256 * 256; }
