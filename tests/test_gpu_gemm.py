@@ -114,3 +114,62 @@ def test_block_fp8_column_major_scales():
     a = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
     b = w8a8_block_fp8_matmul(xq2, w, xs2, ws, [128, 128])
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("M", [1, 17, 33, 64])
+def test_block_fp8_gemv_wide_weight_tiles(M):
+    """N = 12288, K = 4096: the GEMV gives each wave two (M <= 16) or four
+    (M > 16) 16-row weight tiles, so every activation fragment is reused
+    across them; sampled outputs against the oracle and a repeat call with
+    identical bits."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    N, K = 12288, 4096
+    w, ws = synthetic.dense_fp8_weight(N, K, 21)
+    x = synthetic.activations(M, K, 22 + M)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    out = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    assert torch.equal(out, w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128]))
+    g = np.random.Generator(np.random.PCG64(M))
+    cols = np.unique(np.concatenate([[0, 63, 64, N - 1], g.integers(0, N, 1024)]))
+    ref = block_fp8_matmul_sampled(xq.view(torch.uint8).cpu().numpy(), xs.cpu().numpy(),
+                                   w.view(torch.uint8).cpu().numpy(), ws.cpu().numpy(),
+                                   np.arange(M), cols)
+    _check(out.float().cpu().numpy()[:, cols], ref)
+
+
+@pytest.mark.parametrize("M", [1, 7, 40])
+def test_block_fp8_gemv_wide_tiles_ragged_k(M):
+    """N = 7168 (two weight tiles per wave, passes of 2 K-blocks) with
+    K / 128 = 9: the last pass of a wave is half masked and the scales take
+    the per-block path.  Every output element is checked."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    N, K = 7168, 1152
+    w, ws = synthetic.dense_fp8_weight(N, K, 31)
+    x = synthetic.activations(M, K, 32 + M)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    out = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    ref = block_fp8_matmul_sampled(xq.view(torch.uint8).cpu().numpy(), xs.cpu().numpy(),
+                                   w.view(torch.uint8).cpu().numpy(), ws.cpu().numpy(),
+                                   np.arange(M), np.arange(N))
+    _check(out.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M", [8, 24, 64])
+def test_block_fp8_wide_tiles_column_major_scales(M):
+    """Row-major and column-major activation scales take different scale
+    loads but the same tiles, passes and waves: identical bits."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    N, K = 12288, 4096
+    w, ws = synthetic.dense_fp8_weight(N, K, 41)
+    x = synthetic.activations(M, K, 42)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    xq2, xs2 = per_token_group_quant_fp8(x, 128, column_major_scales=True)
+    a = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    b = w8a8_block_fp8_matmul(xq2, w, xs2, ws, [128, 128])
+    assert torch.equal(a, b)

@@ -6,14 +6,17 @@
 //  * gemm_fp8_dma_kernel -- 128 x 256 workgroup tile, 8 waves, K-block of 128
 //    per step, 3-stage LDS ring fed by direct global->LDS loads (one barrier
 //    per K-block), XCD-aware tile order.  For M > 64.
-//  * gemv_fp8_bs_kernel  -- decode-sized M (<= 64): one workgroup per 16
+//  * gemv_fp8_bs_kernel  -- decode-sized M (<= 64): one workgroup per NT x 16
 //    weight rows, its waves split K and stream the rows straight from HBM
 //    into registers; each 16x128 weight fragment multiplies every 16-row
-//    activation tile, so weights are read exactly once.  The waves' partial
-//    sums meet in LDS and are added in wave order (deterministic), one
-//    rounding, in the same kernel.
+//    activation tile and each activation fragment the NT weight tiles, so
+//    weights are read exactly once and activations once per NT x 16 rows.
+//    The waves' partial sums meet in LDS and are added in wave order
+//    (deterministic), one rounding, in the same kernel.
 #include "mfma_fp8.h"
 #include "tile_pipe.h"
+
+#include <atomic>
 
 namespace vmamd {
 
@@ -188,34 +191,44 @@ __device__ __forceinline__ float gemv_buffer_f32(__amdgpu_buffer_rsrc_t rs, uint
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(off), 0, 0));
 }
 
-// One workgroup per 16 weight rows; its W waves (W = blockDim.x / 64) split
-// K by interleaved groups of U K-blocks: at pass r wave w reads blocks
+// One workgroup per NT x 16 weight rows; its W waves (W = blockDim.x / 64)
+// split K by interleaved groups of U K-blocks: at pass r wave w reads blocks
 // [(r*W + w)*U, +U), so the workgroup streams W*U*128 contiguous bytes of
-// each of its rows per pass.  Each 16x128 weight fragment multiplies every
-// 16-row activation tile (MT of them, M <= 16 * MT), so the weights are read
-// exactly once.  Weights, both scale sets and activations are raw buffer
-// loads: blocks past K and activation rows past M are masked lanes (zeros,
-// no fetch), so the loop has no tail and no branches, and the first pass's
-// weights are requested before anything else.  The W partial sums meet in
-// LDS and wave 0 adds them in wave order (deterministic) and rounds once.
-// a_bytes = M * K and as_bytes cover A and As (both < 2 GiB); 16 * K < 2 GiB.
-template <int MT, bool VS>
-__global__ __launch_bounds__(MT == 1 ? 1024 : 512) void gemv_fp8_bs_kernel(
+// each of its rows per pass.  Every 16x128 weight fragment multiplies every
+// 16-row activation tile (MT of them, M <= 16 * MT) and every activation
+// fragment multiplies the NT weight fragments of its K-block, so the weights
+// are read exactly once and the activations once per NT x 16 weight rows.
+// Weights, both scale sets and activations are raw buffer loads: blocks past
+// K and activation rows past M are masked lanes (zeros, no fetch), so the
+// loop has no tail and no branches, and the first pass's weights are
+// requested before anything else.  The W partial sums meet in LDS and wave 0
+// adds them in wave order (deterministic) and rounds once.
+// a_bytes = M * K and as_bytes cover A and As (both < 2 GiB);
+// NT * 16 * K < 2 GiB; NT * 16 divides 128, so a workgroup's rows share one
+// row of weight-block scales.
+constexpr int gemv_max_threads(int MT, int NT, int U) {
+  // 1024 threads (16 waves) only where the pass fits 128 VGPRs
+  return 8 * U * (MT + NT) + 4 * MT * NT + U * (MT + 1) + 24 <= 128 ? 1024 : 512;
+}
+
+template <int MT, int NT, int U, bool VS>
+__global__ __launch_bounds__(gemv_max_threads(MT, NT, U)) void gemv_fp8_bs_kernel(
     const uint8_t* __restrict__ A, int a_bytes, const float* __restrict__ As, int as_bytes,
     int64_t as_sm, int64_t as_sk, const uint8_t* __restrict__ B, const float* __restrict__ Bs,
     int M, int N, int K, uint16_t* __restrict__ C) {
-  constexpr int U = kGemvU;
+  static_assert(128 % (16 * NT) == 0, "a workgroup's rows must share one weight-scale row");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
   const int W = blockDim.x / kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const int li = lane % 16, lg = lane / 16;
-  const int ntile = blockIdx.x;  // the grid is exactly N / 16 workgroups
+  const int n0 = blockIdx.x * NT * 16;  // the grid is exactly N / (NT * 16) workgroups
   const int KB = K / 128;
-  const __amdgpu_buffer_rsrc_t wrs = gemv_rsrc(B + static_cast<int64_t>(ntile) * 16 * K, 16 * K);
-  const __amdgpu_buffer_rsrc_t bsrs = gemv_rsrc(Bs + static_cast<int64_t>((ntile * 16) / 128) * KB, KB * 4);
+  const __amdgpu_buffer_rsrc_t wrs = gemv_rsrc(B + static_cast<int64_t>(n0) * K, NT * 16 * K);
+  const __amdgpu_buffer_rsrc_t bsrs = gemv_rsrc(Bs + static_cast<int64_t>(n0 / 128) * KB, KB * 4);
   const __amdgpu_buffer_rsrc_t ars = gemv_rsrc(A, a_bytes);
   const __amdgpu_buffer_rsrc_t asrs = gemv_rsrc(As, as_bytes);
   const uint32_t woff = static_cast<uint32_t>(li) * static_cast<uint32_t>(K);
+  const uint32_t wtile = 16u * static_cast<uint32_t>(K);  // bytes between weight tiles
   uint32_t aoff[MT], soff[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -223,18 +236,20 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void gemv_fp8_bs_kernel(
     aoff[mt] = m < M ? static_cast<uint32_t>(m) * static_cast<uint32_t>(K) : kGemvMasked;
     soff[mt] = m < M ? static_cast<uint32_t>(m * as_sm * 4) : kGemvMasked;
   }
-  v4f acc[MT];
+  v4f acc[MT][NT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
 
-  // One pass: U K-blocks of the 16 weight rows and of every activation tile,
-  // with their scales.  VS: the U scales of a group are contiguous in both
-  // scale arrays (As rows with unit K stride, K / 128 a multiple of U,
-  // 16-byte aligned rows), so each set is one 16-byte load instead of U
+  // One pass: U K-blocks of the NT weight tiles and of every activation
+  // tile, with their scales.  VS: the U scales of a group are contiguous in
+  // both scale arrays (As rows with unit K stride, K / 128 a multiple of U,
+  // 8- or 16-byte aligned rows), so each set is one wide load instead of U
   // scattered ones; a group is then entirely inside or entirely past K.
   struct Pass {
-    v8i wf[U];
+    v8i wf[NT][U];
     float sb[U];
     v8i xf[MT][U];
     float sa[MT][U];
@@ -244,7 +259,10 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void gemv_fp8_bs_kernel(
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool live = kb + u < KB;
-      p.wf[u] = gemv_buffer_frag(wrs, live ? woff + static_cast<uint32_t>((kb + u) * 128) : kGemvMasked, lg);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        p.wf[nt][u] = gemv_buffer_frag(
+            wrs, live ? nt * wtile + woff + static_cast<uint32_t>((kb + u) * 128) : kGemvMasked, lg);
       if constexpr (!VS) p.sb[u] = gemv_buffer_f32(bsrs, live ? static_cast<uint32_t>(kb + u) * 4u : kGemvMasked);
     }
 #pragma unroll
@@ -268,14 +286,18 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void gemv_fp8_bs_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int u = 0; u < U; ++u) fma4(acc[mt], mfma_fp8(p.wf[u], p.xf[mt][u], zero), p.sa[mt][u] * p.sb[u]);
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          fma4(acc[mt][nt], mfma_fp8(p.wf[nt][u], p.xf[mt][u], zero), p.sa[mt][u] * p.sb[u]);
   };
   // Every load of a pass ahead of its first MFMA (the group barriers), so a
   // pass costs one memory round trip.  Measured: two passes in flight per
   // wave (half-size passes, double-buffered registers) is slower; there are
   // enough waves per CU to cover the latency.  The host sizes
   // W <= ceil(KB / U), so every wave owns at least one pass.
-  constexpr int kLoads = (2 * U + (VS ? 1 : U)) * (1 + MT), kMfmas = U * MT;
+  constexpr int kScaleLoads = VS ? 1 : U;
+  constexpr int kLoads = (2 * U * NT + kScaleLoads) + MT * (2 * U + kScaleLoads), kMfmas = U * MT * NT;
   const int step = W * U;
   int kb = wave * U;
   do {
@@ -292,42 +314,137 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void gemv_fp8_bs_kernel(
     if (wave > 0) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        red[((wave - 1) * MT + mt) * kWave + lane] = float4{acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]};
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const v4f& a = acc[mt][nt];
+          red[(((wave - 1) * MT + mt) * NT + nt) * kWave + lane] = float4{a[0], a[1], a[2], a[3]};
+        }
     }
     __syncthreads();
     if (wave > 0) return;
     for (int w = 1; w < W; ++w) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const float4 v = red[((w - 1) * MT + mt) * kWave + lane];
-        acc[mt][0] += v.x; acc[mt][1] += v.y; acc[mt][2] += v.z; acc[mt][3] += v.w;
-      }
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const float4 v = red[(((w - 1) * MT + mt) * NT + nt) * kWave + lane];
+          acc[mt][nt][0] += v.x; acc[mt][nt][1] += v.y; acc[mt][nt][2] += v.z; acc[mt][nt][3] += v.w;
+        }
     }
   }
-  const int n = ntile * 16 + 4 * lg;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + li;
-    if (m < M)
-      *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) =
-          pack_bf16x4(acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]);
+    if (m < M) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int n = n0 + nt * 16 + 4 * lg;
+        const v4f& a = acc[mt][nt];
+        *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) = pack_bf16x4(a[0], a[1], a[2], a[3]);
+      }
+    }
   }
 }
 
 // ------------------------------------------------------------ dispatch ------
 constexpr int kGemvMaxM = 64;
 
-// Waves per GEMV workgroup: enough for about 4096 waves in all (16 per CU),
-// then as few as keep the same number of passes per wave (fewer partial sums
-// to add); at most 16 (8 for M > 16, whose waves need more registers) and
-// at most one per group of U K-blocks.
-static int gemv_waves(int M, int N, int K) {
-  const int tiles = N / 16;
-  const int groups = (K / 128 + kGemvU - 1) / kGemvU;
-  const int wmax = min(M > 16 ? 8 : 16, groups);
-  const int w0 = max(1, min(wmax, (4096 + tiles - 1) / tiles));
-  const int passes = (groups + w0 - 1) / w0;
-  return (groups + passes - 1) / passes;
+// The (MT, NT, U) instances gemv_shape can pick.
+#define VMAMD_GEMV_SHAPES(X) \
+  X(1, 1, 4) X(1, 2, 2) X(2, 1, 4) X(2, 2, 2) X(2, 4, 2) X(4, 1, 4) X(4, 2, 2) X(4, 4, 2)
+
+struct GemvShape {
+  int mt, nt, u, w;  // activation tiles, weight tiles per wave, K-blocks per pass, waves
+};
+
+// Workgroups of `kernel` resident per CU at W waves (register, LDS and wave
+// limits), cached per W; every instance is built for the same gfx950.
+template <int MT, int NT, int U>
+static int gemv_blocks_per_cu(int w) {
+  static std::atomic<int> cache[17];
+  int v = cache[w].load(std::memory_order_relaxed);
+  if (v == 0) {
+    const size_t lds = static_cast<size_t>(w - 1) * MT * NT * kWave * sizeof(float4);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &v, reinterpret_cast<const void*>(gemv_fp8_bs_kernel<MT, NT, U, true>), w * kWave, lds) != hipSuccess ||
+        v < 1)
+      v = 1;
+    cache[w].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
+static int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
+// Waves per workgroup: the fewest that minimise rounds x passes, where a
+// round is one set of workgroups resident together on every CU and a wave
+// makes ceil(groups / W) passes of U K-blocks.  At most 16 (the kernel's
+// thread limit may say 8), at most one per group, and the reduction buffer
+// within 64 KiB of LDS.  The VS = true instance sizes both scale layouts, so
+// the summation order never depends on the scale layout.
+template <int MT, int NT, int U>
+static int gemv_waves(int tiles, int groups) {
+  const int wmax = min(min(gemv_max_threads(MT, NT, U) / kWave, groups), 1 + 64 / (MT * NT));
+  const int64_t cus = device_cus();
+  int best = 1;
+  int64_t cost = -1;
+  for (int w = 1; w <= wmax; ++w) {
+    const int64_t resident = cus * gemv_blocks_per_cu<MT, NT, U>(w);
+    const int64_t c = (tiles + resident - 1) / resident * ((groups + w - 1) / w);
+    if (cost < 0 || c < cost) {
+      cost = c;
+      best = w;
+    }
+  }
+  return best;
+}
+
+// Activation tiles cover M; each wave takes NT weight tiles, reusing every
+// activation fragment NT times, where the weight matrix has enough 16-row
+// tiles to keep every CU busy with fewer, wider workgroups: two from
+// N = 7168, four for M > 16 from N = 12288 with K >= 4096 (shorter rows
+// leave too few passes to hide the wider pass).  Wider tiles take passes of
+// 2 K-blocks (their registers; measured no slower at M <= 16).  Measured on
+// MI355X over the DeepSeek-V3 linear shapes and 12288 x 4096,
+// 16384 x 7168 at M = 1..64.
+static GemvShape gemv_shape(int M, int N, int K) {
+  GemvShape g;
+  g.mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  g.nt = 1;
+  if (N >= 7168 && N % 32 == 0) g.nt = 2;
+  if (g.mt >= 2 && N >= 12288 && K >= 4096 && N % 64 == 0) g.nt = 4;
+  g.u = g.nt > 1 ? 2 : kGemvU;
+  const int tiles = N / (16 * g.nt), groups = (K / 128 + g.u - 1) / g.u;
+  g.w = 0;
+#define VMAMD_GEMV(MT, NT, U) \
+  if (g.mt == MT && g.nt == NT && g.u == U) g.w = gemv_waves<MT, NT, U>(tiles, groups);
+  VMAMD_GEMV_SHAPES(VMAMD_GEMV)
+#undef VMAMD_GEMV
+  return g;
+}
+
+template <int MT, int NT, int U>
+static void launch_gemv(bool vs, int w, const uint8_t* a, int a_bytes, const float* As, int as_bytes,
+                        int64_t as_sm, int64_t as_sk, const uint8_t* b, const float* Bs, int m, int n,
+                        int k, uint16_t* c, hipStream_t st) {
+  const size_t lds = static_cast<size_t>(w - 1) * MT * NT * kWave * sizeof(float4);
+  const int grid = n / (16 * NT);
+  if (vs)
+    gemv_fp8_bs_kernel<MT, NT, U, true><<<grid, w * kWave, lds, st>>>(a, a_bytes, As, as_bytes, as_sm, as_sk, b,
+                                                                     Bs, m, n, k, c);
+  else
+    gemv_fp8_bs_kernel<MT, NT, U, false><<<grid, w * kWave, lds, st>>>(a, a_bytes, As, as_bytes, as_sm, as_sk, b,
+                                                                      Bs, m, n, k, c);
 }
 
 size_t w8a8_workspace_bytes(int64_t, int64_t, int64_t) { return 0; }
@@ -374,22 +491,21 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
                   "w8a8_block_fp8_matmul: activations, their scales and 16 weight rows must stay "
                   "below 2 GiB");
     const int a_bytes = m * k, as_bytes = static_cast<int>(as_elems * 4);
-    const int w = gemv_waves(m, n, k);
-    const int mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
-    const bool vs = as_stride_k == 1 && as_stride_m % kGemvU == 0 && (k / 128) % kGemvU == 0 &&
-                    reinterpret_cast<uintptr_t>(As) % (4 * kGemvU) == 0 &&
-                    reinterpret_cast<uintptr_t>(Bs) % (4 * kGemvU) == 0;
-    const size_t lds = static_cast<size_t>(w - 1) * mt * kWave * sizeof(float4);
-    auto launch = [&](auto kernel) {
-      kernel<<<n / 16, w * kWave, lds, st>>>(a, a_bytes, As, as_bytes, as_stride_m, as_stride_k, b, Bs, m, n,
-                                             k, c);
-    };
-    if (mt == 1)
-      vs ? launch(gemv_fp8_bs_kernel<1, true>) : launch(gemv_fp8_bs_kernel<1, false>);
-    else if (mt == 2)
-      vs ? launch(gemv_fp8_bs_kernel<2, true>) : launch(gemv_fp8_bs_kernel<2, false>);
-    else
-      vs ? launch(gemv_fp8_bs_kernel<4, true>) : launch(gemv_fp8_bs_kernel<4, false>);
+    const GemvShape g = gemv_shape(m, n, k);
+    VMAMD_REQUIRE(16ll * g.nt * k < (1ll << 31), "w8a8_block_fp8_matmul: weight tile of %d rows past 2 GiB",
+                  16 * g.nt);
+    const bool vs = as_stride_k == 1 && as_stride_m % g.u == 0 && (k / 128) % g.u == 0 &&
+                    reinterpret_cast<uintptr_t>(As) % (4 * g.u) == 0 &&
+                    reinterpret_cast<uintptr_t>(Bs) % (4 * g.u) == 0;
+    VMAMD_REQUIRE(g.w >= 1, "w8a8_block_fp8_matmul: no GEMV instance for %d x %d x %d", g.mt, g.nt, g.u);
+#define VMAMD_GEMV(MT, NT, U)                                                                   \
+  if (g.mt == MT && g.nt == NT && g.u == U)                                                     \
+    launch_gemv<MT, NT, U>(vs, g.w, a, a_bytes, As, as_bytes, as_stride_m, as_stride_k, b, Bs, m, n, k, c, \
+                           st);                                                                 \
+  else
+    VMAMD_GEMV_SHAPES(VMAMD_GEMV)
+    VMAMD_REQUIRE(false, "w8a8_block_fp8_matmul: no GEMV instance for %d x %d x %d", g.mt, g.nt, g.u);
+#undef VMAMD_GEMV
     return check_launch("w8a8_block_fp8_matmul(gemv)");
   }
   static bool lds_raised = false;
