@@ -196,7 +196,7 @@ def cpu_baseline(torch, layer: Layer, target_s: float = 15.0) -> dict:
 # shared-expert gate_up and down, dense-FFN gate_up and down).
 DENSE_SHAPES = ((2112, 7168), (24576, 1536), (32768, 512), (7168, 16384), (4096, 7168),
                 (7168, 2048), (36864, 7168), (7168, 18432))
-DENSE_M = (1, 4, 16, 32, 64, 4096)
+DENSE_M = (1, 4, 16, 32, 64, 128, 512, 4096)
 
 
 def dense_sweep(torch, iters: int, log) -> int:

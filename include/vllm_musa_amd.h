@@ -211,11 +211,16 @@ int vmamd_moe_weighted_sum(const void* x, int dtype, int64_t tokens, int topk, i
  * C[M, N] = bf16( sum_kb (sum_{k in kb} A[m,k] B[n,k]) * As[m,kb] * Bs[n/128, kb] )
  * A [M, K] fp8 with As[m*as_stride_m + kb*as_stride_k] (1x128 groups),
  * B [N, K] fp8 with Bs [ceil(N/128), K/128] f32 (128x128 blocks), C [M, N]
- * bf16.  K % 128 == 0, N % 16 == 0, block_n == block_k == 128.  M <= 64
+ * bf16.  K % 128 == 0, N % 16 == 0, block_n == block_k == 128.  Small M
  * runs the split-K GEMV (weights read once, K split over the waves of a
- * workgroup and reduced in LDS), larger M the tiled MFMA GEMM.  Neither needs
- * a workspace: vmamd_w8a8_block_fp8_matmul_workspace_size() returns 0 and the
- * workspace arguments are accepted for interface stability.  Replaces
+ * workgroup and reduced in LDS), larger M the tiled MFMA GEMM; where its
+ * tiles are too few to fill the GPU the GEMM splits K over workgroups into
+ * fp32 partials held in `workspace` and adds them in split order (a second
+ * kernel).  vmamd_w8a8_block_fp8_matmul_workspace_size() gives the bytes the
+ * shape's plan needs (0 when it needs none; 16-byte aligned).  With a smaller
+ * or NULL workspace the call still succeeds: M <= 64 then takes the GEMV
+ * and larger M the unsplit GEMM, whose fp32 sums run in another order.
+ * Results are deterministic for a given shape and workspace.  Replaces
  * w8a8_triton_block_scaled_mm(A, B, As, Bs, block_size, output_dtype) as
  * called at vllm_musa/deepseek_v4_jit/fp8_einsum.py:399-406, fp8_gemm_nt in
  * _musa_deepgemm_fp8_op (model_executor/kernels/linear/scaled_mm/deep_gemm.py:233-262)

@@ -49,3 +49,18 @@ def test_argument_errors_are_reported_without_a_gpu():
                   None, None, None, None, None)
     msg = _lib.load().vmamd_last_error().decode()
     assert "capacity" in msg
+
+
+def test_dense_workspace_query():
+    """vmamd_w8a8_block_fp8_matmul_workspace_size is host arithmetic (no GPU
+    needed): nothing for the GEMV (M <= 16) or for a GEMM whose tiles fill
+    the GPU; for a split plan, a whole number (2..16) of fp32 M x N partials
+    within 256 MiB."""
+    from vllm_musa_amd import _lib
+    q = _lib.load().vmamd_w8a8_block_fp8_matmul_workspace_size
+    for m, n, k in [(1, 2112, 7168), (16, 7168, 18432), (64, 7168, 2048), (4096, 7168, 18432),
+                    (2048, 36864, 7168), (0, 7168, 2048)]:
+        assert q(m, n, k) == 0, (m, n, k)
+    for m, n, k in [(40, 2112, 7168), (65, 7168, 18432), (512, 2112, 7168), (130, 7168, 2048)]:
+        b = q(m, n, k)
+        assert b > 0 and b % (m * n * 4) == 0 and 2 <= b // (m * n * 4) <= 16 and b <= 256 << 20, (m, n, k, b)

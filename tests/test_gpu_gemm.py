@@ -173,3 +173,55 @@ def test_block_fp8_wide_tiles_column_major_scales(M):
     a = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
     b = w8a8_block_fp8_matmul(xq2, w, xs2, ws, [128, 128])
     assert torch.equal(a, b)
+
+
+SPLIT_CASES = [(40, 2112, 7168), (65, 576, 7168), (130, 7168, 2048), (200, 2112, 7168), (512, 1536, 7168)]
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_CASES)
+def test_block_fp8_splitk_gemm(M, N, K):
+    """Shapes whose 128 x 256 GEMM tiles are too few for the GPU: the GEMM
+    splits K over workgroups into fp32 partials (the workspace) and adds them
+    in split order.  M = 40 at K = 7168 takes the split GEMM instead of the
+    GEMV.  Sampled outputs against the oracle; a repeat call gives identical
+    bits."""
+    from vllm_musa_amd import _lib, synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    assert _lib.load().vmamd_w8a8_block_fp8_matmul_workspace_size(M, N, K) > 0
+    w, ws = synthetic.dense_fp8_weight(N, K, 51)
+    x = synthetic.activations(M, K, 52 + M)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    out = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    assert torch.equal(out, w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128]))
+    g = np.random.Generator(np.random.PCG64(M + N))
+    rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 48)]))
+    cols = np.unique(np.concatenate([[0, N - 1], g.integers(0, N, 512)]))
+    ref = block_fp8_matmul_sampled(xq.view(torch.uint8).cpu().numpy(), xs.cpu().numpy(),
+                                   w.view(torch.uint8).cpu().numpy(), ws.cpu().numpy(), rows, cols)
+    _check(out.float().cpu().numpy()[np.ix_(rows, cols)], ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(40, 2112, 7168), (200, 2112, 7168)])
+def test_block_fp8_gemm_without_workspace(M, N, K):
+    """Through the C ABI with a NULL workspace where the plan wants one: the
+    call succeeds on the unsplit path (the GEMV at M <= 64) and matches the
+    oracle; the split result agrees with it to the fp32 summation order."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd._lib import call, ptr, stream_of
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    w, ws = synthetic.dense_fp8_weight(N, K, 61)
+    x = synthetic.activations(M, K, 62)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=xq.device)
+    call("vmamd_w8a8_block_fp8_matmul", ptr(xq), ptr(xs), xs.stride(0), xs.stride(1), ptr(w), ptr(ws),
+         ptr(out), M, N, K, 128, 128, None, 0, stream_of(xq))
+    split = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    ref = block_fp8_matmul_sampled(xq.view(torch.uint8).cpu().numpy(), xs.cpu().numpy(),
+                                   w.view(torch.uint8).cpu().numpy(), ws.cpu().numpy(),
+                                   np.arange(M), np.arange(N))
+    _check(out.float().cpu().numpy(), ref)
+    _check(split.float().cpu().numpy(), ref)
+    d = (out.float() - split.float()).abs().max().item()
+    assert d <= 2 ** -7 * split.float().abs().max().item()

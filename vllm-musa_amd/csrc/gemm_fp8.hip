@@ -24,13 +24,16 @@ namespace vmamd {
 // 128 x 256 output tile per workgroup (8 waves as 2 (m) x 4 (n), 64 x 64 per
 // wave), 3-stage LDS ring fed by direct global->LDS loads: two K steps are in
 // flight while the current one runs on MFMA.  Rows past M / N are clamped to
-// the last row (their results are not stored).
+// the last row (their results are not stored).  Split K: workgroup row
+// blockIdx.y takes K steps [blockIdx.y * kper, +kper) and, with `partial`
+// set, stores its fp32 tile at partial[blockIdx.y][M][N] for
+// splitk_reduce_kernel; without it, the bf16 tile at C.
 using DensePipe = TilePipe<true, 128, 256, 2, 4, 3>;
 
 __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t as_sm, int64_t as_sk,
     const uint8_t* __restrict__ B, const float* __restrict__ Bs, uint16_t* __restrict__ C, int M,
-    int N, int K, int TM, int TN) {
+    int N, int K, int TM, int TN, int kper, float* __restrict__ partial) {
   using P = DensePipe;
   constexpr int NS = 3, BM = 128, BN = 256, WN = 4;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
@@ -42,6 +45,7 @@ __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
   const int wm = wave / WN, wn = wave % WN;
   const int li = lane % 16, lg = lane / 16;
   const int KS = K / 128, NB = (N + 127) / 128;
+  const int kb0 = blockIdx.y * kper, KL = min(kper, KS - kb0);  // the host keeps KL >= 1
 
   P p;
 #pragma unroll
@@ -66,6 +70,13 @@ __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
     p.srcS = reinterpret_cast<const uint8_t*>(Bs + static_cast<int64_t>(nb) * KS);
     p.stepS = 4;
     p.ldsS = P::kOffSB;
+  }
+  if (kb0 > 0) {  // this split's first K step becomes step 0 of the ring
+#pragma unroll
+    for (int j = 0; j < P::kDmaA; ++j) p.srcA[j] += static_cast<int64_t>(kb0) * 128;
+#pragma unroll
+    for (int j = 0; j < P::kDmaB; ++j) p.srcB[j] += static_cast<int64_t>(kb0) * 128;
+    p.srcS += static_cast<int64_t>(kb0) * p.stepS;
   }
 
   v4f acc[P::MT][P::NT];
@@ -126,18 +137,18 @@ __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
     barrier_lds();
     read(smem_dyn + ((kb + 1) % NS) * P::kStage, nxt);
     mma(cur);
-    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
+    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KL - 1));
   };
 
 #pragma unroll
-  for (int s = 0; s < NS; ++s) p.issue(smem_dyn + s * P::kStage, min(s, KS - 1));
+  for (int s = 0; s < NS; ++s) p.issue(smem_dyn + s * P::kStage, min(s, KL - 1));
   wait_vmcnt<(NS - 1) * P::kIPS>();
   barrier_lds();
   Frags f0, f1;
   read(smem_dyn, f0);
-  for (int kb = 0; kb < KS; kb += 2) {
+  for (int kb = 0; kb < KL; kb += 2) {
     step(kb, f0, f1);
-    if (kb + 1 < KS) step(kb + 1, f1, f0);
+    if (kb + 1 < KL) step(kb + 1, f1, f0);
   }
   wait_vmcnt<0>();  // the ring's trailing DMAs must land before the workgroup's LDS is released
 
@@ -150,8 +161,51 @@ __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
       const int n = n0 + wn * P::WTN + nt * 16 + 4 * lg;
       if (n >= N) continue;
       const v4f a = acc[mt][nt];
-      *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) = pack_bf16x4(a[0], a[1], a[2], a[3]);
+      if (partial)
+        *reinterpret_cast<float4*>(partial + (static_cast<int64_t>(blockIdx.y) * M + m) * N + n) =
+            float4{a[0], a[1], a[2], a[3]};
+      else
+        *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) = pack_bf16x4(a[0], a[1], a[2], a[3]);
     }
+  }
+}
+
+// C = bf16(sum_s partial[s]) over the S split-K partials of an M x N output,
+// added in split order (deterministic), 4 elements per lane (M * N is a
+// multiple of 16).  All S loads of a lane are issued before its first add,
+// so a lane costs one memory round trip.
+template <int S>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial, int64_t mn,
+                                                            uint16_t* __restrict__ C) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x * 4;
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4; i < mn; i += stride) {
+    float4 v[S];
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) v[sp] = *reinterpret_cast<const float4*>(partial + sp * mn + i);
+    float4 a = v[0];
+#pragma unroll
+    for (int sp = 1; sp < S; ++sp) {
+      a.x += v[sp].x; a.y += v[sp].y; a.z += v[sp].z; a.w += v[sp].w;
+    }
+    *reinterpret_cast<uint2*>(C + i) = pack_bf16x4(a.x, a.y, a.z, a.w);
+  }
+}
+
+template <int S>
+static void launch_splitk_reduce(const float* partial, int64_t mn, uint16_t* c, hipStream_t st) {
+  const int64_t blocks = (mn / 4 + 255) / 256;
+  splitk_reduce_kernel<S><<<static_cast<int>(blocks < 8192 ? blocks : 8192), 256, 0, st>>>(partial, mn, c);
+}
+
+static void splitk_reduce(const float* partial, int splits, int64_t mn, uint16_t* c, hipStream_t st) {
+  switch (splits) {
+#define VMAMD_RED(S) \
+  case S: launch_splitk_reduce<S>(partial, mn, c, st); break;
+    VMAMD_RED(2) VMAMD_RED(3) VMAMD_RED(4) VMAMD_RED(5) VMAMD_RED(6) VMAMD_RED(7) VMAMD_RED(8)
+    VMAMD_RED(9) VMAMD_RED(10) VMAMD_RED(11) VMAMD_RED(12) VMAMD_RED(13) VMAMD_RED(14) VMAMD_RED(15)
+    VMAMD_RED(16)
+#undef VMAMD_RED
+    default: break;  // gemm_kper plans 2..16 splits
   }
 }
 
@@ -386,6 +440,67 @@ static int device_cus() {
   return v;
 }
 
+// K splits of the tiled GEMM: where its 128 x 256 tiles are too few to give
+// every CU a workgroup (small N, M of a few hundred), workgroups of one tile
+// take disjoint K ranges, write fp32 partials and a second kernel adds them.
+// Chosen by a time model fitted on MI355X: rounds x K steps per workgroup x
+// a step time that grows with the workgroups streaming at once (they share
+// HBM: 1.08 us for 28 workgroups, 1.87 us for 224 at 7168 x 18432), plus,
+// when split, the partials' round trip at 4 TB/s and 3 us for the extra
+// launch.  A round is what one XCD holds at one workgroup per CU; each split
+// row of the grid spreads its tiles over the XCDs in blocks of
+// ceil(tiles / 8) (xcd_tile).  At most 16 splits of at least 4 K steps each
+// and 256 MiB of partials.  Over 80 measured cases (10 shapes, M = 65..2048)
+// the picks sum to 5595 us (the nearest measured split count where the pick
+// was not measured), the best split of each case to 5573 us, no split to
+// 8091 us.  Returns the K steps per split.
+constexpr int64_t kSplitKMaxBytes = 256ll << 20;
+static int gemm_kper(int M, int N, int K) {
+  const int64_t T = static_cast<int64_t>((M + 127) / 128) * ((N + 255) / 256), KS = K / 128;
+  const int64_t cus = device_cus(), xcd_cus = max(1, static_cast<int>(cus / kXcds));
+  const int64_t per_xcd = (T + kXcds - 1) / kXcds;
+  // Tiles that alone occupy more than half the CUs: splitting gained at most
+  // 5 % in the fit and lost up to 16 % where the model missed.
+  if (2 * T > cus) return static_cast<int>(KS);
+  auto gemm_us = [&](int64_t se, int64_t per) {
+    const double active = static_cast<double>(min(T * se, cus));
+    return static_cast<double>((per_xcd * se + xcd_cus - 1) / xcd_cus * per) * (1.0 + 0.004 * active);
+  };
+  int best = static_cast<int>(KS);
+  double cost = gemm_us(1, KS);
+  for (int64_t s = 2; s <= 16 && s * 4 <= KS; ++s) {
+    const int64_t per = (KS + s - 1) / s, se = (KS + per - 1) / per;
+    const int64_t bytes = se * static_cast<int64_t>(M) * N * 4;
+    if (bytes > kSplitKMaxBytes) break;
+    const double c = gemm_us(se, per) + (bytes + 2.0 * M * N) / 4e6 + 3.0;
+    if (c < cost) {
+      cost = c;
+      best = static_cast<int>(per);
+    }
+  }
+  return best;
+}
+
+// The dense path for an M x N x K product: the GEMV up to M = 16, and up to
+// M = 32 / 64 unless the split GEMM is faster there -- weights of 96 MiB and
+// more from M = 17, rows of K >= 4096 from M = 33 (measured on MI355X over
+// the DeepSeek-V3 linear shapes: e.g. 7168 x 18432 at M = 64, 61 us GEMV,
+// 39 us split GEMM).  `splits` > 1 needs splits * M * N * 4 bytes of
+// workspace.
+struct DensePlan {
+  bool gemv;
+  int kper, splits;
+};
+static DensePlan dense_plan(int M, int N, int K) {
+  DensePlan d;
+  const int KS = K / 128;
+  const bool heavy = static_cast<int64_t>(N) * K >= (96ll << 20);
+  d.gemv = M <= 16 || (M <= 32 && !heavy) || (M <= kGemvMaxM && K < 4096 && !heavy);
+  d.kper = d.gemv ? KS : gemm_kper(M, N, K);
+  d.splits = (KS + d.kper - 1) / d.kper;
+  return d;
+}
+
 // Waves per workgroup: the fewest that minimise rounds x passes, where a
 // round is one set of workgroups resident together on every CU and a wave
 // makes ceil(groups / W) passes of U K-blocks.  At most 16 (the kernel's
@@ -447,7 +562,12 @@ static void launch_gemv(bool vs, int w, const uint8_t* a, int a_bytes, const flo
                                                                       Bs, m, n, k, c);
 }
 
-size_t w8a8_workspace_bytes(int64_t, int64_t, int64_t) { return 0; }
+// The GEMM's split-K partials (none for the GEMV or an unsplit GEMM).
+size_t w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K < 128 || M >= (1ll << 31) || N >= (1ll << 31) || K >= (1ll << 31)) return 0;
+  const DensePlan d = dense_plan(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+  return d.splits > 1 ? static_cast<size_t>(d.splits * M * N * 4) : 0;
+}
 
 }  // namespace vmamd
 
@@ -482,7 +602,17 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
   uint16_t* c = static_cast<uint16_t*>(C);
   const uint8_t* a = static_cast<const uint8_t*>(A);
   const uint8_t* b = static_cast<const uint8_t*>(B);
-  if (m <= kGemvMaxM) {
+  // Without the workspace a split plan needs, M <= 64 takes the GEMV and
+  // larger M the unsplit GEMM (same result up to the order of the fp32 sums).
+  DensePlan plan = dense_plan(m, n, k);
+  if (plan.splits > 1 && (workspace == nullptr ||
+                          workspace_bytes < static_cast<size_t>(plan.splits) * m * n * 4 ||
+                          reinterpret_cast<uintptr_t>(workspace) % 16 != 0)) {
+    plan.gemv = m <= kGemvMaxM;
+    plan.kper = k / 128;
+    plan.splits = 1;
+  }
+  if (plan.gemv) {
     // A, As and each 16-row weight tile are read through buffer descriptors:
     // all must stay below 2 GiB.
     const int64_t as_elems = (m - 1) * as_stride_m + (k / 128 - 1) * as_stride_k + 1;
@@ -518,7 +648,11 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
     lds_raised = true;
   }
   const int TM = (m + 127) / 128, TN = (n + 255) / 256;
-  gemm_fp8_dma_kernel<<<xcd_grid(TM * TN), DensePipe::kThreads, DensePipe::kLds, st>>>(
-      a, As, as_stride_m, as_stride_k, b, Bs, c, m, n, k, TM, TN);
+  const int kper = plan.kper, splits = plan.splits;
+  VMAMD_REQUIRE(splits >= 1 && splits <= 16, "w8a8_block_fp8_matmul: %d K splits planned", splits);
+  float* partial = splits > 1 ? static_cast<float*>(workspace) : nullptr;
+  gemm_fp8_dma_kernel<<<dim3(xcd_grid(TM * TN), splits), DensePipe::kThreads, DensePipe::kLds, st>>>(
+      a, As, as_stride_m, as_stride_k, b, Bs, c, m, n, k, TM, TN, kper, partial);
+  if (splits > 1) splitk_reduce(partial, splits, static_cast<int64_t>(m) * n, c, st);
   return check_launch("w8a8_block_fp8_matmul(gemm)");
 }
