@@ -225,3 +225,23 @@ def test_block_fp8_gemm_without_workspace(M, N, K):
     _check(split.float().cpu().numpy(), ref)
     d = (out.float() - split.float()).abs().max().item()
     assert d <= 2 ** -7 * split.float().abs().max().item()
+
+
+@pytest.mark.parametrize("M", [40, 200])
+def test_block_fp8_splitk_column_major_scales(M):
+    """Split-K plans (N = 2112, K = 7168) with column-major activation
+    scales: each split starts its scale reads K-blocks into the strided
+    layout; same plan and same values as row-major scales, so identical
+    bits."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    N, K = 2112, 7168
+    w, ws = synthetic.dense_fp8_weight(N, K, 71)
+    x = synthetic.activations(M, K, 72)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    xq2, xs2 = per_token_group_quant_fp8(x, 128, column_major_scales=True)
+    assert xs2.stride(0) == 1
+    a = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    b = w8a8_block_fp8_matmul(xq2, w, xs2, ws, [128, 128])
+    assert torch.equal(a, b)
