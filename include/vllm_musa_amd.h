@@ -241,9 +241,12 @@ int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64_t as_strid
  *   h = bf16(W13[e] . q(x[t])),  e = (expert_map ? expert_map[id] : id)
  * x [T, H] bf16; w13 [E, 2I, H] fp8 (rows [0, I) gate, [I, 2I) up) with
  * w13_s [E, 2I/128, H/128] f32; w2 [E, H, I] fp8 with w2_s [E, H/128, I/128];
- * topk_weights f32 / topk_ids i32 [T, topk] (negative ids and experts mapped
- * to a negative local id contribute nothing); out [T, H] bf16.
- * swiglu_limit > 0 selects the clamped activation.  path: AUTO picks the
+ * topk_weights f32 / topk_ids i32 [T, topk] (negative ids, ids mapped to a
+ * negative local id, and local ids >= num_experts contribute nothing); out
+ * [T, H] bf16.  swiglu_limit > 0 selects the clamped activation.
+ * apply_router_weight_on_input != 0 moves the routed weight to the W13 output
+ * (h = bf16((W13[e] . q(x[t])) * w[t,k]), y unweighted), as upstream
+ * fused_experts_impl does with MUL_ROUTED_WEIGHT on its first GEMM.  path: AUTO picks the
  * decode (expert-major GEMV, weights streamed once) kernels while T*topk <=
  * 2.5*E (12*E for the bf16 and w4afp8 layers) and the prefill (grouped MFMA
  * GEMM) kernels above; GEMV / GEMM force one.  Workspace:
@@ -262,8 +265,8 @@ int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H, const 
                         const float* w13_s, const void* w2, const float* w2_s, int num_experts,
                         int64_t I, const float* topk_weights, const int32_t* topk_ids, int topk,
                         const int32_t* expert_map, int64_t expert_map_len, float swiglu_limit,
-                        int path, void* out, void* workspace, size_t workspace_bytes,
-                        vmamd_stream_t stream);
+                        int apply_router_weight_on_input, int path, void* out, void* workspace,
+                        size_t workspace_bytes, vmamd_stream_t stream);
 
 /* ------------------------------------------------ fused-MoE fp8 stages --
  * The two grouped expert GEMMs of vmamd_fused_moe_fp8, callable one by one
@@ -321,8 +324,9 @@ size_t vmamd_fused_moe_bf16_workspace_size(int64_t T, int topk, int num_experts,
 int vmamd_fused_moe_bf16(const void* x, int64_t T, int64_t H, const void* w13, const void* w2,
                          int num_experts, int64_t I, const float* topk_weights,
                          const int32_t* topk_ids, int topk, const int32_t* expert_map,
-                         int64_t expert_map_len, float swiglu_limit, int path, void* out,
-                         void* workspace, size_t workspace_bytes, vmamd_stream_t stream);
+                         int64_t expert_map_len, float swiglu_limit,
+                         int apply_router_weight_on_input, int path, void* out, void* workspace,
+                         size_t workspace_bytes, vmamd_stream_t stream);
 size_t vmamd_moe_bf16_stage_workspace_size(int64_t T, int topk, int num_experts, int64_t H,
                                            int64_t I, int block_m);
 int vmamd_moe_bf16_w13(const void* x, int64_t T, int64_t H, int topk,

@@ -18,7 +18,15 @@ DeepGEMM prefill path, which agree (Appendix of the path's numerics):
   combine:        out[t] = bf16(sum_k f32(y[t, k]))   (slot order)
 
 Routes whose expert maps to a negative local id (expert_map) contribute
-nothing; with apply_router_weight_on_input the weight scales x instead of y.
+nothing.  With apply_router_weight_on_input the routed weight multiplies the
+W13 output (gate and up, fp32) before its bf16 rounding and y is not weighted:
+the reference's native GEMV-MoE driver passes mul_routed_weight =
+apply_router_weight_on_input to its first GEMV and the negation to its second
+(fused_moe.py:2148-2177; the multiply, csrc/musa/gemv.mu:472-475, precedes the
+SwiGLU at 477-487), and upstream's Triton fused_moe_kernel does the same
+through MUL_ROUTED_WEIGHT on the first GEMM:
+
+  h = bf16(W13[e] . x * w);  y = bf16(W2[e] . q(act(h)))
 """
 from __future__ import annotations
 
@@ -60,10 +68,10 @@ def fused_experts_bf16(x, w13, w2, topk_weights, topk_ids, expert_map=None,
     y = np.zeros((t, k, h), dtype=np.float32)
     for e in np.unique(loc[loc >= 0]):
         tt, kk = np.nonzero(loc == e)
-        xa = x[tt]
+        hh = (x[tt].astype(np.float64) @ np.asarray(w13[e], np.float64).T).astype(np.float32)
         if apply_router_weight_on_input:
-            xa = bf16_round(xa * w[tt, kk][:, None])
-        hh = bf16_round((xa.astype(np.float64) @ np.asarray(w13[e], np.float64).T).astype(np.float32))
+            hh = (hh * w[tt, kk][:, None]).astype(np.float32)
+        hh = bf16_round(hh)
         a = silu_and_mul(hh, "bf16")
         acc = (a.astype(np.float64) @ np.asarray(w2[e], np.float64).T).astype(np.float32)
         if not apply_router_weight_on_input:
@@ -93,14 +101,13 @@ def fused_experts_fp8(x, w13_q, w13_s, w2_q, w2_s, topk_weights, topk_ids, exper
         tt, kk = np.nonzero(loc == e)
         if tt.size == 0:
             continue
-        if apply_router_weight_on_input:
-            xa = bf16_round(x[tt] * w[tt, kk][:, None])
-            aq_, as_ = group_quant_fp8(xa)
-        else:
-            aq_, as_ = xq[tt], xs[tt]
+        aq_, as_ = xq[tt], xs[tt]
         a_deq = e4m3_decode(aq_).astype(np.float64) * np.repeat(as_.astype(np.float64), bk, axis=-1)
         w1 = _dequant64(w13_q[e], w13_s[e], bn, bk)
-        hh = bf16_round((a_deq @ w1.T).astype(np.float32))
+        hh = (a_deq @ w1.T).astype(np.float32)
+        if apply_router_weight_on_input:
+            hh = (hh * w[tt, kk][:, None]).astype(np.float32)
+        hh = bf16_round(hh)
         a = silu_and_mul(hh, "bf16")
         a_q, a_s = group_quant_fp8(a)
         a2 = e4m3_decode(a_q).astype(np.float64) * np.repeat(a_s.astype(np.float64), bk, axis=-1)

@@ -30,7 +30,7 @@ def paths(monkeypatch):
 
     def spy(name, *args):
         if name == "vmamd_fused_moe_fp8":
-            seen.append(args[16])
+            seen.append(args[17])
         return real(name, *args)
 
     monkeypatch.setattr(fused_moe, "call", spy)

@@ -53,8 +53,9 @@ def test_block_fp8_gemm_shapes(M, N, K):
     _run(M, N, K, seed=1000 + M + N // 16 + K // 128)
 
 
-@pytest.mark.parametrize("N,K", [(2112, 7168), (24576, 1536)])
+@pytest.mark.parametrize("N,K", SHAPES)
 def test_block_fp8_gemm_m4096(N, K):
+    """M = 4096 at every dense DeepSeek-V3 shape (the compute-bound point)."""
     _run(4096, N, K, seed=77, sample_rows=24, sample_cols=512)
 
 
@@ -118,10 +119,11 @@ def test_block_fp8_column_major_scales():
 
 @pytest.mark.parametrize("M", [1, 17, 33, 64])
 def test_block_fp8_gemv_wide_weight_tiles(M):
-    """N = 12288, K = 4096: the GEMV gives each wave two (M <= 16) or four
-    (M > 16) 16-row weight tiles, so every activation fragment is reused
-    across them; sampled outputs against the oracle and a repeat call with
-    identical bits."""
+    """N = 12288, K = 4096 with a workspace: M <= 32 runs the GEMV, whose
+    waves hold two (M <= 16) or four (M > 16) 16-row weight tiles so every
+    activation fragment is reused across them; M = 33 and 64 run the split-K
+    GEMM (K >= 4096 from M = 33).  Sampled outputs against the oracle and a
+    repeat call with identical bits."""
     from vllm_musa_amd import synthetic
     from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
     from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
@@ -160,8 +162,9 @@ def test_block_fp8_gemv_wide_tiles_ragged_k(M):
 
 @pytest.mark.parametrize("M", [8, 24, 64])
 def test_block_fp8_wide_tiles_column_major_scales(M):
-    """Row-major and column-major activation scales take different scale
-    loads but the same tiles, passes and waves: identical bits."""
+    """N = 12288, K = 4096 (GEMV with wide weight tiles at M = 8 and 24, the
+    split GEMM at M = 64): row-major and column-major activation scales take
+    different scale loads but the same tiles and plan: identical bits."""
     from vllm_musa_amd import synthetic
     from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
     from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
@@ -245,3 +248,43 @@ def test_block_fp8_splitk_column_major_scales(M):
     a = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
     b = w8a8_block_fp8_matmul(xq2, w, xs2, ws, [128, 128])
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("M,N,K", [(33, 12288, 4096), (48, 12288, 4096), (64, 12288, 4096)])
+def test_block_fp8_gemv_fallback_without_workspace(M, N, K):
+    """M = 33..64 on a weight the plan sends to the split GEMM, called through
+    the C ABI with a NULL workspace: the call falls back to the GEMV with four
+    16-row weight tiles per wave (gemv_fp8_bs_kernel<4, 4, 2>).  Every output
+    element against the oracle, and a repeat call gives identical bits."""
+    from vllm_musa_amd import _lib, synthetic
+    from vllm_musa_amd._lib import call, ptr, stream_of
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    assert _lib.load().vmamd_w8a8_block_fp8_matmul_workspace_size(M, N, K) > 0
+    w, ws = synthetic.dense_fp8_weight(N, K, 81)
+    x = synthetic.activations(M, K, 82 + M)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    outs = []
+    for _ in range(2):
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=xq.device)
+        call("vmamd_w8a8_block_fp8_matmul", ptr(xq), ptr(xs), xs.stride(0), xs.stride(1), ptr(w),
+             ptr(ws), ptr(out), M, N, K, 128, 128, None, 0, stream_of(xq))
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    ref = block_fp8_matmul_sampled(xq.view(torch.uint8).cpu().numpy(), xs.cpu().numpy(),
+                                   w.view(torch.uint8).cpu().numpy(), ws.cpu().numpy(),
+                                   np.arange(M), np.arange(N))
+    _check(outs[0].float().cpu().numpy(), ref)
+
+
+def test_block_fp8_matmul_rejects_bad_out():
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    M, N, K = 8, 256, 512
+    w, ws = synthetic.dense_fp8_weight(N, K, 9)
+    xq, xs = per_token_group_quant_fp8(synthetic.activations(M, K, 10), 128)
+    for bad in (torch.empty(M, N - 1, dtype=torch.bfloat16, device=xq.device),
+                torch.empty(M, N, dtype=torch.float16, device=xq.device),
+                torch.empty(N, M, dtype=torch.bfloat16, device=xq.device).t()):
+        with pytest.raises(ValueError, match="out must be"):
+            w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128], out=bad)

@@ -128,3 +128,38 @@ def test_fp8_codes_used_by_the_oracle_are_exact(rng):
     from oracle.numerics import e4m3_decode
     codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
     np.testing.assert_array_equal(e4m3_encode(e4m3_decode(codes)), codes)
+
+
+def test_weight_on_input_equals_scaling_x_bf16(rng):
+    """apply_router_weight_on_input with a power-of-two routed weight equals the
+    default layer on x scaled by that weight with weight 1: the weight enters
+    once, on the W13 side, before the SiLU.  On the W2 side instead (or twice)
+    the SiLU would break the equality."""
+    x, w13, w2 = _mlp_case(rng, t=9, e=4)
+    ids = rng.integers(0, 4, (9, 1)).astype(np.int32)
+    half = np.full((9, 1), 0.5, np.float32)
+    got = omoe.fused_experts_bf16(x, w13, w2, half, ids, apply_router_weight_on_input=True)
+    ref = omoe.fused_experts_bf16(x * np.float32(0.5), w13, w2, np.ones((9, 1), np.float32), ids)
+    np.testing.assert_array_equal(got, ref)
+    assert not np.array_equal(got, omoe.fused_experts_bf16(x, w13, w2, half, ids))
+
+
+def test_weight_on_input_equals_scaling_x_fp8(rng):
+    # halving x halves every 1x128 scale exactly and keeps the codes
+    x, w13, s13, w2, s2 = _fp8_case(rng)
+    ids = rng.integers(0, 4, (7, 1)).astype(np.int32)
+    quarter = np.full((7, 1), 0.25, np.float32)
+    got = omoe.fused_experts_fp8(x, w13, s13, w2, s2, quarter, ids,
+                                 apply_router_weight_on_input=True)
+    ref = omoe.fused_experts_fp8(x * np.float32(0.25), w13, s13, w2, s2,
+                                 np.ones((7, 1), np.float32), ids)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_weight_on_input_unit_weights_match_default(rng):
+    x, w13, s13, w2, s2 = _fp8_case(rng)
+    ids = np.stack([rng.permutation(4)[:2] for _ in range(7)]).astype(np.int32)
+    ones = np.ones((7, 2), np.float32)
+    np.testing.assert_array_equal(
+        omoe.fused_experts_fp8(x, w13, s13, w2, s2, ones, ids, apply_router_weight_on_input=True),
+        omoe.fused_experts_fp8(x, w13, s13, w2, s2, ones, ids))

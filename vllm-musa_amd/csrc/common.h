@@ -41,6 +41,13 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
                             int32_t* offsets, int32_t* active, int32_t* num_active, const void* x,
                             int64_t rows, int64_t cols, uint8_t* xq, float* xs, hipStream_t st);
 
+// Top-k combine (moe_sum.hip): out[t] = round(sum_k x[t, k] (* wts[t, k])) over
+// the live slots; num_experts > 0 also drops slots whose local id is >= it.
+int moe_sum_impl(const char* who, const void* x, int dtype, int64_t tokens, int topk,
+                 int64_t hidden, const int32_t* topk_ids, const int32_t* expert_map,
+                 int64_t expert_map_len, int num_experts, const float* wts, void* out,
+                 vmamd_stream_t stream);
+
 #define VMAMD_REQUIRE(cond, ...)                \
   do {                                          \
     if (!(cond)) {                              \

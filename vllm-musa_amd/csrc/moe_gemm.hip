@@ -378,10 +378,13 @@ __device__ __forceinline__ void gate_up8_fixed(const float* __restrict__ partial
 // kFp8: activation then a2 quantisation per 1x128 group (one 16-lane segment
 // per group, 8 columns per lane).  NaN activations (clamped variant) quantise
 // to fp8_min.  SPL > 0: the split count, fixed at compile time; 0: runtime.
+// route_w (apply_router_weight_on_input): gate/up sums times the route's
+// weight before their bf16 rounding (null: times 1, which is exact).
 template <int SPL>
 __global__ __launch_bounds__(256) void moe_act_quant_kernel(const float* __restrict__ partial,
                                                             int splits, int numel, int I,
-                                                            float limit, uint8_t* __restrict__ a2q,
+                                                            float limit, const float* __restrict__ route_w,
+                                                            uint8_t* __restrict__ a2q,
                                                             float* __restrict__ a2s) {
   const int64_t g = static_cast<int64_t>(blockIdx.x) * 16 + threadIdx.x / 16;
   const int sub = threadIdx.x % 16;
@@ -390,12 +393,13 @@ __global__ __launch_bounds__(256) void moe_act_quant_kernel(const float* __restr
   const int r = static_cast<int>(g / gpr);
   const int c0 = static_cast<int>(g % gpr) * 128 + sub * 8;
   float gv[8], uv[8], v[8];
+  const float rw = route_w ? route_w[r] : 1.0f;
   if constexpr (SPL > 0)
     gate_up8_fixed<SPL>(partial, numel, I, r, c0, gv, uv);
   else
     gate_up8(partial, splits, numel, I, r, c0, 1.0f, gv, uv);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = swiglu_bf16(bf16r(gv[j]), bf16r(uv[j]), limit);
+  for (int j = 0; j < 8; ++j) v[j] = swiglu_bf16(bf16r(gv[j] * rw), bf16r(uv[j] * rw), limit);
   float amax = 1e-10f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
@@ -414,18 +418,20 @@ __global__ __launch_bounds__(256) void moe_act_quant_kernel(const float* __restr
 // kBf16 / kW4: a[r, c] = the bf16 activation, 8 columns per thread (16-byte
 // store).  kW4 first scales the sums by the token's activation scale
 // xs[r / topk] and rounds gate/up to bf16, then applies swiglu_w4; its a2
-// quantiser (one scale per row) runs as a separate row kernel.
+// quantiser (one scale per row) runs as a separate row kernel.  kBf16 scales
+// the sums by route_w[r] when given (apply_router_weight_on_input).
 template <int KIND>
 __global__ __launch_bounds__(256) void moe_act_bf16_kernel(const float* __restrict__ partial,
                                                            int splits, int numel, int I,
                                                            float limit, const float* __restrict__ xs,
-                                                           int topk, uint16_t* __restrict__ a2) {
+                                                           int topk, const float* __restrict__ route_w,
+                                                           uint16_t* __restrict__ a2) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int cpr = I / 8;
   if (idx >= static_cast<int64_t>(numel) * cpr) return;
   const int r = static_cast<int>(idx / cpr);
   const int c0 = static_cast<int>(idx % cpr) * 8;
-  const float scale = KIND == kW4 ? xs[r / topk] : 1.0f;
+  const float scale = KIND == kW4 ? xs[r / topk] : (route_w ? route_w[r] : 1.0f);
   float gv[8], uv[8], v[8];
   gate_up8(partial, splits, numel, I, r, c0, scale, gv, uv);
 #pragma unroll
@@ -484,23 +490,33 @@ __global__ __launch_bounds__(kRowThreads) void moe_act_rowquant_w4_kernel(
   }
 }
 
+// A route's slot is live when its expert id is >= 0 and its local id
+// (through expert_map when given) lies in [0, E): the rule of the alignment,
+// which places no other route, so no other partial row is ever written.
+__device__ __forceinline__ bool route_live(const int32_t* __restrict__ emap, int64_t emap_len, int E,
+                                           int e) {
+  if (e < 0) return false;
+  if (emap) {
+    if (e >= emap_len) return false;
+    e = emap[e];
+  }
+  return e >= 0 && e < E;
+}
+
 // y[r, n] = bf16(sum_s partial[s, r, n] * w_r) for the W2 split path (kW4:
 // w_r is the a2 row scale).
 __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(const float* __restrict__ partial,
                                                             int splits, int numel, int N,
                                                             const int32_t* __restrict__ ids,
                                                             const int32_t* __restrict__ emap,
-                                                            int64_t emap_len,
+                                                            int64_t emap_len, int E,
                                                             const float* __restrict__ route_w,
                                                             uint16_t* __restrict__ y) {
   const int64_t i4 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   const int64_t mn = static_cast<int64_t>(numel) * N;
   if (i4 >= mn) return;
   const int r = static_cast<int>(i4 / N);
-  if (emap) {
-    const int e = ids[r];
-    if (e < 0 || e >= emap_len || emap[e] < 0) return;
-  }
+  if (!route_live(emap, emap_len, E, ids[r])) return;
   float4 acc = *reinterpret_cast<const float4*>(partial + i4);
   for (int s = 1; s < splits; ++s) {
     const float4 v = *reinterpret_cast<const float4*>(partial + s * mn + i4);
@@ -520,7 +536,7 @@ __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(const float* __restr
 template <bool WEIGHTED>
 __global__ __launch_bounds__(256) void moe_w2_combine_kernel(
     const float* __restrict__ partial, int splits, int T, int topk, int N,
-    const int32_t* __restrict__ ids, const int32_t* __restrict__ emap, int64_t emap_len,
+    const int32_t* __restrict__ ids, const int32_t* __restrict__ emap, int64_t emap_len, int E,
     const float* __restrict__ yscale, const float* __restrict__ topk_w, uint16_t* __restrict__ out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int cpr = N / 8;
@@ -531,8 +547,7 @@ __global__ __launch_bounds__(256) void moe_w2_combine_kernel(
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int k = 0; k < topk; ++k) {
     const int r = t * topk + k;
-    const int e = ids[r];
-    if (e < 0 || (emap && (e >= emap_len || emap[e] < 0))) continue;
+    if (!route_live(emap, emap_len, E, ids[r])) continue;
     const float* src = partial + static_cast<int64_t>(r) * N + n;
     float4 a = *reinterpret_cast<const float4*>(src);
     float4 b = *reinterpret_cast<const float4*>(src + 4);
@@ -569,7 +584,7 @@ __global__ __launch_bounds__(256) void moe_w2_combine_kernel(
 template <bool WEIGHTED, int SPL>
 __global__ __launch_bounds__(256) void moe_w2_combine_fast_kernel(
     const float* __restrict__ partial, int T, int topk, int N, const int32_t* __restrict__ ids,
-    const int32_t* __restrict__ emap, int64_t emap_len, const float* __restrict__ yscale,
+    const int32_t* __restrict__ emap, int64_t emap_len, int E, const float* __restrict__ yscale,
     const float* __restrict__ topk_w, uint16_t* __restrict__ out) {
   constexpr int KM = 8;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -585,8 +600,7 @@ __global__ __launch_bounds__(256) void moe_w2_combine_fast_kernel(
   for (int k = 0; k < KM; ++k) {
     const int kk = k < topk ? k : topk - 1;
     const int r = t * topk + kk;
-    const int e = ids[r];
-    live[k] = k < topk && e >= 0 && !(emap && (e >= emap_len || emap[e] < 0));
+    live[k] = k < topk && route_live(emap, emap_len, E, ids[r]);
     sc[k] = yscale ? yscale[r] : 1.0f;
     wk[k] = WEIGHTED ? topk_w[r] : 1.0f;
     const float* src = partial + static_cast<int64_t>(r) * N + n;
@@ -617,7 +631,7 @@ __global__ __launch_bounds__(256) void moe_w2_combine_fast_kernel(
 
 template <bool WEIGHTED>
 static void launch_w2_combine(const float* partial, int splits, int T, int topk, int N,
-                              const int32_t* ids, const int32_t* emap, int64_t emap_len,
+                              const int32_t* ids, const int32_t* emap, int64_t emap_len, int E,
                               const float* yscale, const float* topk_w, uint16_t* out,
                               hipStream_t st) {
   if (topk <= 8 && splits >= 1 && splits <= 4 && N % 4 == 0) {
@@ -625,7 +639,7 @@ static void launch_w2_combine(const float* partial, int splits, int T, int topk,
     const int blocks = static_cast<int>((threads + 255) / 256);
 #define VMAMD_COMBINE(S)                                                                        \
   moe_w2_combine_fast_kernel<WEIGHTED, S><<<blocks, 256, 0, st>>>(partial, T, topk, N, ids, emap, \
-                                                                  emap_len, yscale, topk_w, out)
+                                                                  emap_len, E, yscale, topk_w, out)
     switch (splits) {
       case 1: VMAMD_COMBINE(1); break;
       case 2: VMAMD_COMBINE(2); break;
@@ -638,7 +652,7 @@ static void launch_w2_combine(const float* partial, int splits, int T, int topk,
   const int64_t chunks = static_cast<int64_t>(T) * (N / 8);
   const int blocks = static_cast<int>((chunks + 255) / 256);
   moe_w2_combine_kernel<WEIGHTED><<<blocks, 256, 0, st>>>(partial, splits, T, topk, N, ids, emap,
-                                                          emap_len, yscale, topk_w, out);
+                                                          emap_len, E, yscale, topk_w, out);
 }
 
 // ------------------------------------------------------ prefill GEMMs -----
@@ -1280,6 +1294,17 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
   barrier_lds();
 
   if constexpr (W13) {
+    // route_w (apply_router_weight_on_input): gate/up times the route's weight
+    // before their bf16 rounding; without it the factor is 1 (exact).
+    float rw[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      rw[mt] = 1.0f;
+      if (route_w) {
+        const int r = sorted[static_cast<int64_t>(mb) * BM + wm * P::WTM + mt * 16 + li];
+        rw[mt] = r < numel ? route_w[r] : 0.0f;
+      }
+    }
     if constexpr (KIND == kFp8) {
       // Activation, row amax across the 4 n-waves through LDS, 1x128 quantiser.
       float* red = reinterpret_cast<float*>(smem_dyn);  // [WN][BM]
@@ -1291,7 +1316,8 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
         for (int q = 0; q < 2; ++q)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float x = swiglu_bf16(bf16r(acc[mt][2 * q][r]), bf16r(acc[mt][2 * q + 1][r]), limit);
+            const float x = swiglu_bf16(bf16r(acc[mt][2 * q][r] * rw[mt]),
+                                        bf16r(acc[mt][2 * q + 1][r] * rw[mt]), limit);
             v[mt][q][r] = x;
             amax = fmaxf(amax, fabsf(x));
           }
@@ -1332,7 +1358,8 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
           float o[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            o[r] = swiglu_bf16(bf16r(acc[mt][2 * q][r]), bf16r(acc[mt][2 * q + 1][r]), limit);
+            o[r] = swiglu_bf16(bf16r(acc[mt][2 * q][r] * rw[mt]), bf16r(acc[mt][2 * q + 1][r] * rw[mt]),
+                               limit);
           const int col = n0 + (wn * 2 + q) * 16 + 4 * lg;
           *reinterpret_cast<uint2*>(a2b + row * I + col) = pack_bf16x4(o[0], o[1], o[2], o[3]);
         }
@@ -1490,7 +1517,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
                       const int32_t* sorted, int64_t cap, int block_m, const int32_t* offs,
                       const int32_t* ntpp, const int32_t* active, const int32_t* nact,
                       const uint8_t* w13, const void* w13_s, int E, int I, float limit,
-                      uint8_t* a2, float* a2s, float* scratch, hipStream_t st) {
+                      const float* route_w, uint8_t* a2, float* a2s, float* scratch, hipStream_t st) {
   const int numel = T * topk;
   if (block_m == kGemvBlock) {
     const int s13 = w13_splits(numel, E, H, I, KIND);
@@ -1506,7 +1533,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
       const int64_t groups = static_cast<int64_t>(numel) * (I / 128);
       const int blocks = static_cast<int>((groups + 15) / 16);
 #define VMAMD_ACTQ(S) \
-  moe_act_quant_kernel<S><<<blocks, 256, 0, st>>>(scratch, s13, numel, I, limit, a2, a2s)
+  moe_act_quant_kernel<S><<<blocks, 256, 0, st>>>(scratch, s13, numel, I, limit, route_w, a2, a2s)
       switch (s13) {
         case 1: VMAMD_ACTQ(1); break;
         case 2: VMAMD_ACTQ(2); break;
@@ -1521,7 +1548,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
     } else {
       const int64_t chunks = static_cast<int64_t>(numel) * (I / 8);
       moe_act_bf16_kernel<KIND><<<static_cast<int>((chunks + 255) / 256), 256, 0, st>>>(
-          scratch, s13, numel, I, limit, xs, topk, reinterpret_cast<uint16_t*>(a2));
+          scratch, s13, numel, I, limit, xs, topk, route_w, reinterpret_cast<uint16_t*>(a2));
     }
     return check_launch("moe w13 (activation)");
   }
@@ -1537,7 +1564,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
     if (rc) return rc;
     moe_gemm_dma_kernel<KIND, true><<<xcd_grid(tiles), 512, MoePipe<KIND>::kLds, st>>>(
         xa, xs, topk, H, sorted, offs, ntpp, E, numel, tiles, w13,
-        static_cast<const float*>(w13_s), 2 * I, I, limit, nullptr, a2, a2s, nullptr);
+        static_cast<const float*>(w13_s), 2 * I, I, limit, route_w, a2, a2s, nullptr);
   }
   return check_launch("moe w13 (gemm)");
 }
@@ -1550,11 +1577,12 @@ template <int KIND>
 static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const int32_t* sorted,
                      int64_t cap, int block_m, const int32_t* offs, const int32_t* ntpp,
                      const int32_t* active, const int32_t* nact, const uint8_t* w2, const void* w2_s,
-                     int E, int H, int I, const float* topk_weights, const int32_t* topk_ids,
-                     const int32_t* emap, int64_t emap_len, uint16_t* y, float* scratch,
-                     hipStream_t st, uint16_t* combined_out = nullptr, bool* combined = nullptr) {
+                     int E, int H, int I, const float* topk_weights, const float* route_w,
+                     const int32_t* topk_ids, const int32_t* emap, int64_t emap_len, uint16_t* y,
+                     float* scratch, hipStream_t st, uint16_t* combined_out = nullptr,
+                     bool* combined = nullptr) {
   const int numel = T * topk;
-  const float* yscale = KIND == kW4 ? a2s : topk_weights;
+  const float* yscale = KIND == kW4 ? a2s : route_w;
   if (combined) *combined = false;
   if (block_m == kGemvBlock) {
     const int s2 = w2_splits(numel, E, H, I, KIND);
@@ -1567,10 +1595,10 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
       int rc = check_launch("moe w2 (gemv)");
       if (rc) return rc;
       if constexpr (KIND == kW4)
-        launch_w2_combine<true>(scratch, s2, T, topk, H, topk_ids, emap, emap_len, yscale,
+        launch_w2_combine<true>(scratch, s2, T, topk, H, topk_ids, emap, emap_len, E, yscale,
                                 topk_weights, combined_out, st);
       else
-        launch_w2_combine<false>(scratch, s2, T, topk, H, topk_ids, emap, emap_len, yscale,
+        launch_w2_combine<false>(scratch, s2, T, topk, H, topk_ids, emap, emap_len, E, yscale,
                                  nullptr, combined_out, st);
       *combined = true;
       return check_launch("moe w2 (combine)");
@@ -1587,7 +1615,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
     if (rc) return rc;
     const int64_t mn = static_cast<int64_t>(numel) * H;
     moe_w2_reduce_kernel<<<static_cast<int>((mn / 4 + 255) / 256), 256, 0, st>>>(
-        scratch, s2, numel, H, topk_ids, emap, emap_len, yscale, y);
+        scratch, s2, numel, H, topk_ids, emap, emap_len, E, yscale, y);
     return check_launch("moe w2 (reduce)");
   }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
@@ -1602,7 +1630,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
     if (rc) return rc;
     moe_gemm_dma_kernel<KIND, false><<<xcd_grid(tiles), 512, MoePipe<KIND>::kLds, st>>>(
         a2, a2s, 1, I, sorted, offs, ntpp, E, numel, tiles, w2, static_cast<const float*>(w2_s), H,
-        I, 0.f, topk_weights, nullptr, nullptr, y);
+        I, 0.f, route_w, nullptr, nullptr, y);
   }
   return check_launch("moe w2 (gemm)");
 }
@@ -1678,10 +1706,12 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
                        const void* w13_s, const void* w2, const void* w2_s, int E, int64_t I,
                        const float* topk_weights, const int32_t* topk_ids, int topk,
                        const int32_t* expert_map, int64_t expert_map_len, float swiglu_limit,
-                       int path, void* out, void* workspace, size_t workspace_bytes,
-                       vmamd_stream_t stream) {
+                       bool weight_on_input, int path, void* out, void* workspace,
+                       size_t workspace_bytes, vmamd_stream_t stream) {
   VMAMD_REQUIRE(path >= VMAMD_MOE_PATH_AUTO && path <= VMAMD_MOE_PATH_GEMM, "%s: unknown path %d",
                 who, path);
+  VMAMD_REQUIRE(KIND != kW4 || !weight_on_input, "%s: apply_router_weight_on_input is not supported",
+                who);
   const int bm = moe_block_m(T, topk, E, path, KIND);
   const int64_t cap = T * topk + static_cast<int64_t>(E) * (bm - 1);
   int rc = check_stage_common(who, T, topk, E, H, I, bm, cap);
@@ -1739,9 +1769,13 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   // kW4 prefill: bf16 activation, quantised per row below (the decode path
   // writes the quantised a2 directly).
   uint8_t* act_out = KIND == kW4 && bm != kGemvBlock ? ws + L.abf : a2;
+  // The routed weight is applied once: on the W13 output before the
+  // activation (apply_router_weight_on_input), otherwise in the W2 epilogue.
+  const float* w13_rw = weight_on_input ? topk_weights : nullptr;
+  const float* w2_rw = weight_on_input ? nullptr : topk_weights;
   rc = launch_w13<KIND>(xa, xs, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
-                        static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, act_out, a2s,
-                        scratch, st);
+                        static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, w13_rw, act_out,
+                        a2s, scratch, st);
   if (rc) return rc;
   if constexpr (KIND == kW4) {
     if (bm != kGemvBlock) {
@@ -1751,16 +1785,15 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   }
   bool combined = false;
   rc = launch_w2<KIND>(a2, a2s, t, topk, sorted, cap, bm, offs, ntpp, active, nact,
-                       static_cast<const uint8_t*>(w2), w2_s, E, h, i, topk_weights, topk_ids,
+                       static_cast<const uint8_t*>(w2), w2_s, E, h, i, topk_weights, w2_rw, topk_ids,
                        expert_map, expert_map_len, y, scratch, st, static_cast<uint16_t*>(out),
                        &combined);
   if (rc || combined) return rc;
   // Slots of dropped routes (negative ids, or non-local experts) hold no
   // expert output and are skipped by the combine.
-  if constexpr (KIND == kW4)
-    return vmamd_moe_weighted_sum(y, kBF16, T, topk, H, topk_weights, topk_ids, expert_map,
-                                  expert_map_len, out, stream);
-  return vmamd_moe_sum(y, kBF16, T, topk, H, topk_ids, expert_map, expert_map_len, out, stream);
+  return moe_sum_impl(KIND == kW4 ? "w4afp8_moe (combine)" : "fused_moe (combine)", y, kBF16, T, topk,
+                      H, topk_ids, expert_map, expert_map_len, E,
+                      KIND == kW4 ? topk_weights : nullptr, out, stream);
 }
 
 template <int KIND>
@@ -1786,7 +1819,7 @@ static int stage_w13(const char* who, const void* xa, const float* xs, int64_t T
   return launch_w13<KIND>(static_cast<const uint8_t*>(xa), xs, static_cast<int>(T), static_cast<int>(H),
                           topk, sorted, capacity, block_m, offs, ntpp, active, nact,
                           static_cast<const uint8_t*>(w13), w13_s, E, static_cast<int>(I), limit,
-                          static_cast<uint8_t*>(a2), a2s, static_cast<float*>(workspace),
+                          nullptr, static_cast<uint8_t*>(a2), a2s, static_cast<float*>(workspace),
                           reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -1813,7 +1846,8 @@ static int stage_w2(const char* who, const void* a2, const float* a2s, int64_t T
                 "%s: a2 and workspace must be 16-byte and y 8-byte aligned", who);
   return launch_w2<KIND>(static_cast<const uint8_t*>(a2), a2s, static_cast<int>(T), topk, sorted,
                          capacity, block_m, offs, ntpp, active, nact, static_cast<const uint8_t*>(w2),
-                         w2_s, E, static_cast<int>(H), static_cast<int>(I), topk_weights, topk_ids,
+                         w2_s, E, static_cast<int>(H), static_cast<int>(I), topk_weights,
+                         KIND == kW4 ? nullptr : topk_weights, topk_ids,
                          emap, emap_len, static_cast<uint16_t*>(y), static_cast<float*>(workspace),
                          reinterpret_cast<hipStream_t>(stream));
 }
@@ -1864,12 +1898,14 @@ extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_
                                    const float* w2_s, int num_experts, int64_t I,
                                    const float* topk_weights, const int32_t* topk_ids, int topk,
                                    const int32_t* expert_map, int64_t expert_map_len,
-                                   float swiglu_limit, int path, void* out, void* workspace,
-                                   size_t workspace_bytes, vmamd_stream_t stream) {
+                                   float swiglu_limit, int apply_router_weight_on_input, int path,
+                                   void* out, void* workspace, size_t workspace_bytes,
+                                   vmamd_stream_t stream) {
   VMAMD_REQUIRE(x_dtype == kBF16, "fused_moe_fp8: hidden states must be bf16");
   return fused_layer<kFp8>("fused_moe_fp8", x, T, H, w13, w13_s, w2, w2_s, num_experts, I,
                            topk_weights, topk_ids, topk, expert_map, expert_map_len, swiglu_limit,
-                           path, out, workspace, workspace_bytes, stream);
+                           apply_router_weight_on_input != 0, path, out, workspace,
+                           workspace_bytes, stream);
 }
 
 // ----------------------------------------------------------------- bf16 ---
@@ -1914,11 +1950,13 @@ extern "C" int vmamd_fused_moe_bf16(const void* x, int64_t T, int64_t H, const v
                                     const void* w2, int num_experts, int64_t I,
                                     const float* topk_weights, const int32_t* topk_ids, int topk,
                                     const int32_t* expert_map, int64_t expert_map_len,
-                                    float swiglu_limit, int path, void* out, void* workspace,
-                                    size_t workspace_bytes, vmamd_stream_t stream) {
+                                    float swiglu_limit, int apply_router_weight_on_input, int path,
+                                    void* out, void* workspace, size_t workspace_bytes,
+                                    vmamd_stream_t stream) {
   return fused_layer<kBf16>("fused_moe_bf16", x, T, H, w13, nullptr, w2, nullptr, num_experts, I,
                             topk_weights, topk_ids, topk, expert_map, expert_map_len, swiglu_limit,
-                            path, out, workspace, workspace_bytes, stream);
+                            apply_router_weight_on_input != 0, path, out, workspace,
+                            workspace_bytes, stream);
 }
 
 // --------------------------------------------------------------- w4afp8 ---
@@ -1934,6 +1972,6 @@ extern "C" int vmamd_w4afp8_moe(const void* x, int64_t T, int64_t H, const void*
                                 int64_t expert_map_len, float swiglu_limit, int path, void* out,
                                 void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
   return fused_layer<kW4>("w4afp8_moe", x, T, H, w13, w13_s, w2, w2_s, num_experts, I, topk_weights,
-                          topk_ids, topk, expert_map, expert_map_len, swiglu_limit, path, out,
-                          workspace, workspace_bytes, stream);
+                          topk_ids, topk, expert_map, expert_map_len, swiglu_limit, false, path,
+                          out, workspace, workspace_bytes, stream);
 }

@@ -3,7 +3,9 @@
 // the routed weights w are applied here only when given (otherwise the expert
 // outputs already carry them).  With topk_ids
 // given, slots whose expert id is negative, or maps to a negative local id
-// through expert_map, are skipped (their rows hold no expert output).
+// through expert_map, are skipped (their rows hold no expert output); the
+// fused layers also pass their expert count, so that a slot whose (local) id
+// is past the last expert -- a route the alignment drops -- is skipped too.
 //
 // Each thread owns 8 consecutive hidden elements of one token (16-byte loads
 // for 2-byte types), so a wave streams 1 KiB contiguous per slot.
@@ -11,13 +13,18 @@
 
 namespace vmamd {
 
+// num_experts <= 0: no upper bound on the (local) id.
 __device__ __forceinline__ bool slot_live(const int32_t* __restrict__ ids, const int32_t* __restrict__ map,
-                                          int64_t map_len, int64_t route) {
+                                          int64_t map_len, int num_experts, int64_t route) {
   if (!ids) return true;
-  const int e = ids[route];
+  int e = ids[route];
   if (e < 0) return false;
-  if (!map) return true;
-  return e < map_len && map[e] >= 0;
+  if (map) {
+    if (e >= map_len) return false;
+    e = map[e];
+    if (e < 0) return false;
+  }
+  return num_experts <= 0 || e < num_experts;
 }
 
 // Slots a thread loads up front (DeepSeek-V3 and most MoE layers use top-8).
@@ -29,7 +36,7 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const typename Elem<DT>::T
                                                       typename Elem<DT>::T* __restrict__ out,
                                                       const int32_t* __restrict__ ids,
                                                       const int32_t* __restrict__ map, int64_t map_len,
-                                                      const float* __restrict__ wts) {
+                                                      int num_experts, const float* __restrict__ wts) {
   using E = Elem<DT>;
   using T = typename E::T;
   const int64_t chunks = hidden / 8;
@@ -55,7 +62,7 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const typename Elem<DT>::T
 #pragma unroll
         for (int k = 0; k < kSumSlots; ++k) {
           if (k >= topk) continue;
-          const bool live = slot_live(ids, map, map_len, t * topk + k);
+          const bool live = slot_live(ids, map, map_len, num_experts, t * topk + k);
           const float wk = wts ? wts[t * topk + k] : 1.0f;
           const uint16_t* p = reinterpret_cast<const uint16_t*>(&raw[k]);
           // One fused multiply-add per weighted slot (one rounding, as the
@@ -77,7 +84,7 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const typename Elem<DT>::T
       }
     }
     for (int k = 0; k < topk; ++k) {
-      if (!slot_live(ids, map, map_len, t * topk + k)) continue;
+      if (!slot_live(ids, map, map_len, num_experts, t * topk + k)) continue;
       const T* src = x + (t * topk + k) * hidden + h;
       if constexpr (VEC && sizeof(T) == 2) {
         const uint4 raw = *reinterpret_cast<const uint4*>(src);
@@ -117,7 +124,7 @@ __global__ __launch_bounds__(256) void moe_sum_scalar_kernel(const typename Elem
                                                              typename Elem<DT>::T* __restrict__ out,
                                                              const int32_t* __restrict__ ids,
                                                              const int32_t* __restrict__ map,
-                                                             int64_t map_len,
+                                                             int64_t map_len, int num_experts,
                                                              const float* __restrict__ wts) {
   using E = Elem<DT>;
   const int64_t total = tokens * hidden;
@@ -126,7 +133,7 @@ __global__ __launch_bounds__(256) void moe_sum_scalar_kernel(const typename Elem
     const int64_t t = i / hidden, h = i - t * hidden;
     float acc = 0.f;
     for (int k = 0; k < topk; ++k)
-      if (slot_live(ids, map, map_len, t * topk + k)) {
+      if (slot_live(ids, map, map_len, num_experts, t * topk + k)) {
         const float v = E::to_f(x[(t * topk + k) * hidden + h]);
         acc += wts ? v * wts[t * topk + k] : v;
       }
@@ -138,9 +145,12 @@ __global__ __launch_bounds__(256) void moe_sum_scalar_kernel(const typename Elem
 
 using namespace vmamd;
 
-static int moe_sum_impl(const char* who, const void* x, int dtype, int64_t tokens, int topk,
-                        int64_t hidden, const int32_t* topk_ids, const int32_t* expert_map,
-                        int64_t expert_map_len, const float* wts, void* out, vmamd_stream_t stream) {
+namespace vmamd {
+
+int moe_sum_impl(const char* who, const void* x, int dtype, int64_t tokens, int topk,
+                 int64_t hidden, const int32_t* topk_ids, const int32_t* expert_map,
+                 int64_t expert_map_len, int num_experts, const float* wts, void* out,
+                 vmamd_stream_t stream) {
   VMAMD_REQUIRE(tokens >= 0 && topk > 0 && hidden >= 0, "%s: bad sizes", who);
   VMAMD_REQUIRE(!expert_map || topk_ids, "%s: expert_map needs topk_ids", who);
   if (tokens * hidden == 0) return VMAMD_OK;
@@ -157,13 +167,16 @@ static int moe_sum_impl(const char* who, const void* x, int dtype, int64_t token
     TY* oi = static_cast<TY*>(out);                                                             \
     if (hidden % 8 != 0)                                                                        \
       moe_sum_scalar_kernel<DT><<<blocks, 256, 0, st>>>(xi, tokens, topk, hidden, oi, topk_ids, \
-                                                        expert_map, expert_map_len, wts);       \
+                                                        expert_map, expert_map_len, num_experts,    \
+                                                        wts);                                   \
     else if (vec)                                                                               \
       moe_sum_kernel<DT, true><<<blocks, 256, 0, st>>>(xi, tokens, topk, hidden, oi, topk_ids,  \
-                                                       expert_map, expert_map_len, wts);        \
+                                                       expert_map, expert_map_len, num_experts,     \
+                                                       wts);                                    \
     else                                                                                        \
       moe_sum_kernel<DT, false><<<blocks, 256, 0, st>>>(xi, tokens, topk, hidden, oi, topk_ids, \
-                                                        expert_map, expert_map_len, wts);       \
+                                                        expert_map, expert_map_len, num_experts,    \
+                                                        wts);                                   \
   } while (0)
   switch (dtype) {
     case kBF16: VMAMD_SUM(kBF16, uint16_t); break;
@@ -175,11 +188,13 @@ static int moe_sum_impl(const char* who, const void* x, int dtype, int64_t token
   return check_launch(who);
 }
 
+}  // namespace vmamd
+
 extern "C" int vmamd_moe_sum(const void* x, int dtype, int64_t tokens, int topk, int64_t hidden,
                              const int32_t* topk_ids, const int32_t* expert_map,
                              int64_t expert_map_len, void* out, vmamd_stream_t stream) {
   return moe_sum_impl("moe_sum", x, dtype, tokens, topk, hidden, topk_ids, expert_map,
-                      expert_map_len, nullptr, out, stream);
+                      expert_map_len, 0, nullptr, out, stream);
 }
 
 extern "C" int vmamd_moe_weighted_sum(const void* x, int dtype, int64_t tokens, int topk,
@@ -188,5 +203,5 @@ extern "C" int vmamd_moe_weighted_sum(const void* x, int dtype, int64_t tokens, 
                                       int64_t expert_map_len, void* out, vmamd_stream_t stream) {
   VMAMD_REQUIRE(topk_weights || tokens * hidden == 0, "moe_weighted_sum: null topk_weights");
   return moe_sum_impl("moe_weighted_sum", x, dtype, tokens, topk, hidden, topk_ids, expert_map,
-                      expert_map_len, topk_weights, out, stream);
+                      expert_map_len, 0, topk_weights, out, stream);
 }

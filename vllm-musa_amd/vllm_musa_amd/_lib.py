@@ -54,7 +54,7 @@ SIGNATURES: dict[str, list] = {
                                     _p, _sz, _p],
     "vmamd_fused_moe_fp8_workspace_size": [_i64, _i32, _i32, _i64, _i64, _i32],
     "vmamd_fused_moe_fp8": [_p, _i32, _i64, _i64, _p, _p, _p, _p, _i32, _i64, _p, _p, _i32, _p,
-                            _i64, _f32, _i32, _p, _p, _sz, _p],
+                            _i64, _f32, _i32, _i32, _p, _p, _sz, _p],
     "vmamd_moe_fp8_stage_workspace_size": [_i64, _i32, _i32, _i64, _i64, _i32],
     "vmamd_moe_fp8_w13": [_p, _p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _p, _p, _i32,
                           _i64, _f32, _p, _p, _p, _sz, _p],
@@ -62,7 +62,7 @@ SIGNATURES: dict[str, list] = {
                          _i64, _p, _p, _p, _i64, _p, _p, _sz, _p],
     "vmamd_fused_moe_bf16_workspace_size": [_i64, _i32, _i32, _i64, _i64, _i32],
     "vmamd_fused_moe_bf16": [_p, _i64, _i64, _p, _p, _i32, _i64, _p, _p, _i32, _p, _i64, _f32,
-                             _i32, _p, _p, _sz, _p],
+                             _i32, _i32, _p, _p, _sz, _p],
     "vmamd_moe_bf16_stage_workspace_size": [_i64, _i32, _i32, _i64, _i64, _i32],
     "vmamd_moe_bf16_w13": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _p, _i32, _i64,
                            _f32, _p, _p, _sz, _p],

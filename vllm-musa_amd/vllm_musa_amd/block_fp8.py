@@ -50,6 +50,10 @@ def w8a8_block_fp8_matmul(A: torch.Tensor, B: torch.Tensor, As: torch.Tensor, Bs
     Bs = Bs.contiguous()
     if out is None:
         out = torch.empty((m, n), dtype=torch.bfloat16, device=A.device)
+    elif (tuple(out.shape) != (m, n) or out.dtype != torch.bfloat16 or not out.is_contiguous()
+          or out.device != A.device):
+        raise ValueError(f"out must be a contiguous bfloat16 [M, N] = {(m, n)} tensor on "
+                         f"{A.device}, got {tuple(out.shape)} {out.dtype} on {out.device}")
     ws_bytes = _lib.load().vmamd_w8a8_block_fp8_matmul_workspace_size(m, n, k)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=A.device) if ws_bytes else None
     call("vmamd_w8a8_block_fp8_matmul", ptr(a2), ptr(as2), as2.stride(0), as2.stride(1), ptr(B),

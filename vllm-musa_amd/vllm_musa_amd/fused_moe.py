@@ -49,20 +49,54 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: i
 PATHS = {"auto": 0, "gemv": 1, "gemm": 2}
 
 
+def _per_expert_scale(scale: torch.Tensor, e: int) -> torch.Tensor | None:
+    """The [E] per-expert view of a per-tensor / per-expert scale layout (0-d,
+    one element, [E] or [E, 1]), or None for any other layout."""
+    if scale.dim() == 0 or (scale.dim() == 1 and scale.numel() == 1):
+        return scale.reshape(1).expand(e)
+    if scale.dim() == 1 and scale.numel() == e:
+        return scale
+    if scale.dim() == 2 and tuple(scale.shape) == (e, 1):
+        return scale[:, 0]
+    return None
+
+
+def fp8_moe_scale_layout_is_supported(scale: torch.Tensor | None, weight: torch.Tensor) -> bool:
+    """True when this path takes ``scale`` for the fp8 expert stack ``weight``
+    [E, N, K]: f32 and contiguous, K a multiple of 128, and either one of the
+    per-tensor layouts (0-d, [1], [E], [E, 1]) or the 128x128 block grid
+    [E, ceil(N/128), K/128].  Mirrors the reference's guard
+    _musa_fp8_moe_scale_layout_is_supported (fused_moe.py:1262-1302) for the
+    128-wide grid; its 64-wide grid (a 128x128 block holding four different
+    scales) has no 128x128 view and is declined."""
+    if scale is None or scale.dtype != torch.float32 or not scale.is_contiguous():
+        return False
+    e, n, k = weight.shape
+    if k % 128 != 0:
+        return False
+    if _per_expert_scale(scale, e) is not None:
+        return True
+    return tuple(scale.shape) == (e, (n + 127) // 128, k // 128)
+
+
 def _expand_fp8_scale(scale: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """Per-tensor / per-expert fp8 scales -> the [E, ceil(N/128), K/128] block
-    view (reference: _maybe_expand_fp8_moe_per_tensor_scale, fused_moe.py:1212-1259)."""
+    view; a scale already on that grid passes through (reference:
+    _maybe_expand_fp8_moe_per_tensor_scale, fused_moe.py:1212-1259, applied by
+    fused_experts_impl at 2006-2008 whatever block_shape says)."""
     e, n, k = w.shape
+    if k % 128 != 0:
+        raise ValueError(f"fp8 MoE weights need an input size divisible by 128, got {k}")
     want = (e, (n + 127) // 128, k // 128)
     s = scale.to(torch.float32)
     if tuple(s.shape) == want:
         return s.contiguous()
-    if s.numel() == 1:
-        return s.reshape(1, 1, 1).expand(want).contiguous()
-    if s.numel() == e:
-        return s.reshape(e, 1, 1).expand(want).contiguous()
-    raise ValueError(f"fp8 MoE scale of shape {tuple(scale.shape)} does not match the "
-                     f"128x128 block grid {want}")
+    per_expert = _per_expert_scale(s, e)
+    if per_expert is not None:
+        return per_expert.reshape(e, 1, 1).expand(want).contiguous()
+    raise ValueError(f"fp8 MoE scale of shape {tuple(scale.shape)} is neither per-tensor, "
+                     f"per-expert nor the 128x128 block grid {want} (64-wide block scales "
+                     "are not on this path)")
 
 
 def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
@@ -82,9 +116,14 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
     """Drop-in for the reference's fused_experts_impl
     (vllm_musa/model_executor/layers/fused_moe/fused_moe.py:1935-1965, 2214-2240):
     out[t] = sum_k w[t,k] * W2[e] . act(W13[e] . x[t]) with the reference's
-    rounding points.  Supported: bf16 weights, and fp8 weights with 128x128
-    block scales (use_fp8_w8a8, block_shape=[128, 128]) and dynamic 1x128
-    activation quantisation.  ``path`` forces the decode ("gemv") or prefill
+    rounding points.  Supported: bf16 weights, and fp8 weights (use_fp8_w8a8)
+    with 128x128 block scales (block_shape=[128, 128]) or per-tensor /
+    per-expert scales (any block_shape; expanded to the 128x128 grid as the
+    reference's fused_experts_impl does, fused_moe.py:2006-2008), with dynamic
+    1x128 activation quantisation.  apply_router_weight_on_input multiplies
+    the W13 output by the routed weight before the activation and leaves the
+    W2 output unweighted (the reference's mul_routed_weight on its first GEMV,
+    fused_moe.py:2148-2177).  ``path`` forces the decode ("gemv") or prefill
     ("gemm") kernels; "auto" asks the dispatch policy (the calibrated per-shape
     table, the VLLM_MUSA_FUSED_MOE_DISPATCH override) and otherwise picks by
     routes per expert."""
@@ -92,8 +131,6 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
         raise NotImplementedError(f"activation {activation!r}: only silu (SwiGLU) is on this path")
     if use_int8_w8a8 or use_int8_w8a16 or use_int4_w4a16 or ocp_mx_scheme or per_channel_quant:
         raise NotImplementedError("int8 / int4-w4a16 / MX / per-channel MoE are not on this path")
-    if apply_router_weight_on_input:
-        raise NotImplementedError("apply_router_weight_on_input is not on this path")
     if w1_bias is not None or w2_bias is not None or w1_zp is not None or w2_zp is not None:
         raise NotImplementedError("expert biases / zero points are not on this path")
     if a1_scale is not None or a2_scale is not None:
@@ -119,6 +156,16 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
     wts = topk_weights.to(torch.float32).contiguous()
     emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
     limit = 0.0 if gemm1_clamp_limit is None else float(gemm1_clamp_limit)
+    on_input = int(bool(apply_router_weight_on_input))
+    if use_fp8_w8a8:
+        if block_shape is not None and list(block_shape) != [128, 128]:
+            raise NotImplementedError("fp8 MoE on this path takes block_shape [128, 128] "
+                                      "or per-tensor / per-expert scales")
+        if w1_scale is None or w2_scale is None:
+            raise ValueError("fp8 MoE needs w1_scale and w2_scale")
+        w1_scale = _expand_fp8_scale(w1_scale, w1)
+        w2_scale = _expand_fp8_scale(w2_scale, w2)
+        block_shape = [128, 128]
     if path == "auto":
         path = dispatch_policy.resolve_path(hidden_states, w1, w2,
                                             w1_scale if use_fp8_w8a8 else None,
@@ -126,14 +173,9 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
                                             block_shape, expert_map)
     code = PATHS[path]
     if use_fp8_w8a8:
-        if block_shape is None or list(block_shape) != [128, 128]:
-            raise NotImplementedError("fp8 MoE on this path needs block_shape=[128, 128]")
         if w1.dtype != torch.float8_e4m3fn or w2.dtype != torch.float8_e4m3fn:
             raise ValueError("fp8 MoE weights must be float8_e4m3fn")
-        if w1_scale is None or w2_scale is None:
-            raise ValueError("fp8 MoE needs w1_scale and w2_scale")
-        s1 = _expand_fp8_scale(w1_scale, w1)
-        s2 = _expand_fp8_scale(w2_scale, w2)
+        s1, s2 = w1_scale, w2_scale
         w1c, w2c = w1.contiguous(), w2.contiguous()
         _lib.check_cuda(hidden_states, w1c, w2c, s1, s2, wts, ids, emap)
         lib = _lib.load()
@@ -141,17 +183,17 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
         ws = torch.empty(nbytes, dtype=torch.uint8, device=hidden_states.device)
         call("vmamd_fused_moe_fp8", ptr(hidden_states), _lib.DTYPE_BF16, t, h, ptr(w1c), ptr(s1),
              ptr(w2c), ptr(s2), e, i, ptr(wts), ptr(ids), topk, ptr(emap),
-             0 if emap is None else emap.numel(), limit, code, ptr(out), ptr(ws), nbytes,
+             0 if emap is None else emap.numel(), limit, on_input, code, ptr(out), ptr(ws), nbytes,
              stream_of(hidden_states))
         return out
     if w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16:
         if w1_scale is not None or w2_scale is not None:
             raise ValueError("bf16 MoE weights take no scales")
-        return _fused_experts_bf16(hidden_states, w1, w2, wts, ids, emap, limit, code, out)
+        return _fused_experts_bf16(hidden_states, w1, w2, wts, ids, emap, limit, on_input, code, out)
     raise NotImplementedError(f"MoE weights of dtype {w1.dtype} are not on this path")
 
 
-def _fused_experts_bf16(x, w1, w2, wts, ids, emap, limit, code, out):
+def _fused_experts_bf16(x, w1, w2, wts, ids, emap, limit, on_input, code, out):
     e, n2, h = w1.shape
     i = n2 // 2
     t, topk = ids.shape
@@ -160,8 +202,8 @@ def _fused_experts_bf16(x, w1, w2, wts, ids, emap, limit, code, out):
     nbytes = _lib.load().vmamd_fused_moe_bf16_workspace_size(t, topk, e, h, i, code)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
     call("vmamd_fused_moe_bf16", ptr(x), t, h, ptr(w1c), ptr(w2c), e, i, ptr(wts), ptr(ids), topk,
-         ptr(emap), 0 if emap is None else emap.numel(), limit, code, ptr(out), ptr(ws), nbytes,
-         stream_of(x))
+         ptr(emap), 0 if emap is None else emap.numel(), limit, on_input, code, ptr(out), ptr(ws),
+         nbytes, stream_of(x))
     return out
 
 
