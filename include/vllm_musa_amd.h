@@ -231,6 +231,23 @@ int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64_t as_strid
                                 int64_t M, int64_t N, int64_t K, int block_n, int block_k,
                                 void* workspace, size_t workspace_bytes, vmamd_stream_t stream);
 
+/* vmamd_w8a8_block_fp8_matmul for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  It has no counterpart in the reference.  The same plan and
+ * kernels, with the split-K partials in a fixed device-resident scratch array
+ * of VMAMD_W8A8_NOALLOC_SCRATCH_BYTES per GPU (held by each GPU the library
+ * runs on until the process ends) instead of a workspace; the call allocates
+ * nothing.  A shape whose plan needs more partial bytes than that
+ * (vmamd_w8a8_block_fp8_matmul_workspace_size) is rejected with
+ * VMAMD_ERR_INVALID.  Results equal vmamd_w8a8_block_fp8_matmul's with a
+ * sufficient workspace, bit for bit.  All calls on one GPU share its array:
+ * calls that overlap on one GPU (different streams, or host threads) race. */
+#define VMAMD_W8A8_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int vmamd_w8a8_block_fp8_matmul_noalloc(const void* A, const float* As, int64_t as_stride_m,
+                                        int64_t as_stride_k, const void* B, const float* Bs,
+                                        void* C, int64_t M, int64_t N, int64_t K, int block_n,
+                                        int block_k, vmamd_stream_t stream);
+
 /* ------------------------------------------------------------ fused MoE --
  * One fused-experts layer with 128x128 block-fp8 weights, the whole pipeline
  * on `stream`: 1x128 quantisation of x, moe_align_block_size, W13 grouped

@@ -17,6 +17,7 @@
 #include "tile_pipe.h"
 
 #include <atomic>
+#include <mutex>
 
 namespace vmamd {
 
@@ -655,4 +656,62 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
       a, As, as_stride_m, as_stride_k, b, Bs, c, m, n, k, TM, TN, kper, partial);
   if (splits > 1) splitk_reduce(partial, splits, static_cast<int64_t>(m) * n, c, st);
   return check_launch("w8a8_block_fp8_matmul(gemm)");
+}
+
+// ------------------------------------------------- allocation-free variant --
+// vmamd_w8a8_block_fp8_matmul_noalloc keeps the split-K partials in one fixed
+// device-resident array per GPU instead of a caller workspace.  In host code
+// the array's name denotes a host-side stand-in, not device memory, so it is
+// never handed to a kernel: its device address comes from
+// hipGetSymbolAddress, taken once per device with that device current, and
+// only that address is used.  Every split writes its whole partial slab
+// before the reduce reads it, so nothing needs clearing between calls.
+namespace vmamd {
+
+constexpr size_t kNoAllocScratchBytes = VMAMD_W8A8_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+static int noalloc_scratch(void** out) {
+  static std::mutex mu;
+  static void* per_device[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("w8a8_block_fp8_matmul_noalloc: no current device below 64");
+    return VMAMD_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (per_device[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("w8a8_block_fp8_matmul_noalloc: hipGetSymbolAddress of the scratch array failed: %s",
+                hipGetErrorString(e));
+      return VMAMD_ERR_HIP;
+    }
+    per_device[dev] = p;
+  }
+  *out = per_device[dev];
+  return VMAMD_OK;
+}
+
+}  // namespace vmamd
+
+extern "C" int vmamd_w8a8_block_fp8_matmul_noalloc(const void* A, const float* As,
+                                                   int64_t as_stride_m, int64_t as_stride_k,
+                                                   const void* B, const float* Bs, void* C,
+                                                   int64_t M, int64_t N, int64_t K, int block_n,
+                                                   int block_k, vmamd_stream_t stream) {
+  const size_t need = w8a8_workspace_bytes(M, N, K);
+  VMAMD_REQUIRE(need <= kNoAllocScratchBytes,
+                "w8a8_block_fp8_matmul_noalloc: the plan for %lld x %lld x %lld needs %zu bytes of "
+                "split-K partials; the fixed scratch holds %zu (call vmamd_w8a8_block_fp8_matmul "
+                "with a workspace)",
+                (long long)M, (long long)N, (long long)K, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = noalloc_scratch(&ws);
+    if (rc) return rc;
+  }
+  return vmamd_w8a8_block_fp8_matmul(A, As, as_stride_m, as_stride_k, B, Bs, C, M, N, K, block_n,
+                                     block_k, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
 }

@@ -52,6 +52,8 @@ SIGNATURES: dict[str, list] = {
     "vmamd_w8a8_block_fp8_matmul_workspace_size": [_i64, _i64, _i64],
     "vmamd_w8a8_block_fp8_matmul": [_p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32,
                                     _p, _sz, _p],
+    "vmamd_w8a8_block_fp8_matmul_noalloc": [_p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64,
+                                            _i32, _i32, _p],
     "vmamd_fused_moe_fp8_workspace_size": [_i64, _i32, _i32, _i64, _i64, _i32],
     "vmamd_fused_moe_fp8": [_p, _i32, _i64, _i64, _p, _p, _p, _p, _i32, _i64, _p, _p, _i32, _p,
                             _i64, _f32, _i32, _i32, _p, _p, _sz, _p],
