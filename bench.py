@@ -10,14 +10,22 @@ activations ~N(0, 1), logits ~N(0, 1), score bias ~N(0, 0.1).
 
 Printed (rank 0, one JSON line): value = algorithmic TFLOP/s of the layer at
 T=4096 (2*T*topk*3*H*I flops per call), ms_per_step from HIP events around the
-K timed steps; `sweep` gives us / TFLOP/s / GB/s and roofline fractions at
-T = 1, 16, 256, 4096 (cold weights: a 1 GiB buffer is read between
-iterations; `graph_us` is the same step replayed from a HIP graph, as a
-serving engine runs decode); `roofline` is the dominant kernel (W13 grouped
-GEMM at T=4096) timed on its own with HIP events on its launch stream, its
-`traffic` (HBM bytes per launch) read from the committed rocprofv3 counter
-summary; `cpu_baseline` times the CPU oracle on a bounded sample of the same
-layer.
+K timed steps; `roofline` is the dominant kernel (W13 grouped GEMM at T=4096)
+timed on its own with HIP events on its launch stream, its `traffic` (HBM
+bytes per launch) and `mfma_util` read from the committed rocprofv3 counter
+summaries; `cpu_baseline` times the torch CPU restatement of the layer on a
+bounded sample of the same layer.  The other configurations of the metric are
+extra keys, each point the median of --sweep-iters HIP-event timings after 10
+warm-ups with cold weights (a 1 GiB buffer is read before each call), with
+us / TFLOP/s / GB/s and the fraction of min(peak compute, AI x 8 TB/s):
+  sweep      fp8 DeepSeek-V3 layer (this workload) at T = 1, 16, 256, 4096,
+             also replayed from a HIP graph (`graph_us`, as a server runs decode)
+  dense      w8a8 block-fp8 linear, (N, K) in (24576, 1536), (7168, 18432),
+             (2112, 7168), (7168, 2048), M = 1, 4, 16, 64, 512, 4096: 1x128
+             activation quantiser + GEMM (`us`) and the GEMM alone (`gemm_us`)
+  bf16_moe   bf16 layer E=128, top-8 softmax renorm, H=2048, I=768 at
+             T = 1, 16, 128, 1024, 8192, uniform and skewed (+2.0 on 8 experts)
+  w4afp8_moe w4afp8 layer E=128, top-8, H=4096, I=1536 at T = 1, 32, 512, 4096
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-sweep] [--no-cpu]
   python bench.py --traffic-probe   # the launches profiled for FETCH_SIZE / WRITE_SIZE
@@ -40,9 +48,11 @@ for _p in (ROOT, os.path.join(ROOT, "vllm-musa_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
-# MI355X published peaks.
+# MI355X published peaks (dense).
 PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
+PEAK_BF16_TFLOPS = 2500.0
+WARMUP_SWEEP = 10
 
 E, H, I, TOPK, GROUPS, TOPK_GROUP, SCALE = 256, 7168, 2048, 8, 8, 4, 2.5
 T_HEADLINE = 4096
@@ -51,20 +61,26 @@ WEIGHT_SEED = 3000
 
 METRIC = "fp8-block MoE layer µs, TFLOPS & HBM GB/s (% roofline) at T=1..4096"
 
-# rocprofv3 counter summary of the W13 kernel at T=4096 (FETCH_SIZE and
-# WRITE_SIZE per dispatch, scaled by a 1 GiB copy); its
-# "traffic_bytes_per_launch:" line fills roofline.traffic.
+# rocprofv3 counter summaries of the W13 kernel at T=4096: FETCH_SIZE and
+# WRITE_SIZE per dispatch scaled by a 1 GiB copy ("traffic_bytes_per_launch:"
+# fills roofline.traffic), and the fp8 MFMA counters ("mfma_util_w13:" fills
+# roofline.mfma_util: MFMA flops per second over the dense fp8 peak).
 TRAFFIC_SUMMARY = os.path.join("profiles", "moe_w13_gemm_fp8_dsv3_T4096_traffic.md")
+MFMA_SUMMARY = os.path.join("profiles", "mfma_utilisation_large_t.md")
 
 
-def read_traffic() -> int | None:
-    path = os.path.join(ROOT, TRAFFIC_SUMMARY)
+def read_summary_value(rel: str, key: str, cast=int):
+    path = os.path.join(ROOT, rel)
     if not os.path.exists(path):
         return None
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":", 1)[1].strip())
+        if line.startswith(key + ":"):
+            return cast(line.split(":", 1)[1].strip())
     return None
+
+
+def read_traffic() -> int | None:
+    return read_summary_value(TRAFFIC_SUMMARY, "traffic_bytes_per_launch")
 
 
 def layer_flops(routes: int) -> float:
@@ -150,46 +166,56 @@ def graph_median(torch, fn, iters: int, flush) -> float:
     return ms
 
 
-def cpu_baseline(torch, layer: Layer, target_s: float = 15.0) -> dict:
-    """Time the CPU oracle on a bounded sample of the T=4096 layer: the routes
-    of a few experts (their tokens, their weights), same arithmetic as the
-    full layer.  Reported in the layer's unit (TFLOP/s)."""
+def cpu_baseline(torch, layer: Layer, max_experts: int = 16) -> dict:
+    """The torch CPU restatement of the layer (oracle/moe_torch.py: float32
+    contractions on dequantised operands, every host thread) on a bounded
+    sample of the T=4096 layer: the routes of its most loaded experts, with
+    their tokens and weights.  Median of 5 timed passes after 1 warm-up,
+    reported in the layer's unit (TFLOP/s)."""
+    import platform
+
     import numpy as np
 
-    from oracle import moe as omoe
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([d.get("num_threads", 1) for d in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = 1
+    from oracle import moe_torch
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
     w, ids = layer.route()
     ids_np = ids.cpu().numpy()
-    w_np = w.cpu().numpy()
-    x_np = layer.x.float().cpu().numpy()
     counts = np.bincount(ids_np.ravel(), minlength=E)
-    order = np.argsort(-counts, kind="stable")
-    done_routes, elapsed, n_exp = 0, 0.0, 0
-    for e in order:
-        if elapsed >= target_s or n_exp >= 16:
-            break
-        toks = np.nonzero((ids_np == e).any(axis=1))[0]
-        sub_ids = np.where(ids_np[toks] == e, 0, -1).astype(np.int32)
-        sel = torch.tensor([int(e)], device=layer.w13.device)
-        u8 = lambda t: t.view(torch.uint8).index_select(0, sel).cpu().numpy()
-        f32 = lambda t: t.index_select(0, sel).cpu().numpy()
-        args = (x_np[toks], u8(layer.w13), f32(layer.s13), u8(layer.w2), f32(layer.s2),
-                w_np[toks], sub_ids)
+    experts = np.argsort(-counts, kind="stable")[:max_experts]
+    toks = np.nonzero(np.isin(ids_np, experts).any(axis=1))[0]
+    # the sample's own expert stack: the chosen experts as 0..n-1, others dropped
+    remap = np.full(E, -1, np.int64)
+    remap[experts] = np.arange(experts.size)
+    sub_ids = torch.from_numpy(remap[ids_np[toks]].astype(np.int64))
+    sel = torch.from_numpy(experts.astype(np.int64)).to(layer.w13.device)
+    u8 = lambda t: t.view(torch.uint8).index_select(0, sel).cpu()
+    f32 = lambda t: t.index_select(0, sel).cpu()
+    args = (layer.x.float().cpu()[torch.from_numpy(toks)], u8(layer.w13), f32(layer.s13),
+            u8(layer.w2), f32(layer.s2), w.cpu()[torch.from_numpy(toks)], sub_ids)
+    routes = int((sub_ids >= 0).sum())
+    moe_torch.fused_experts_fp8(*args)
+    times = []
+    for _ in range(5):
         t0 = time.perf_counter()
-        omoe.fused_experts_fp8(*args)
-        elapsed += time.perf_counter() - t0
-        done_routes += int((sub_ids >= 0).sum())
-        n_exp += 1
-    tflops = layer_flops(done_routes) / elapsed / 1e12
-    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
-            "sample": f"numpy float64 oracle (oracle/moe.py fused_experts_fp8) on {n_exp} experts of "
-                      f"the T={layer.t} layer ({done_routes} routes, {elapsed:.1f} s); full-layer "
-                      f"CPU time extrapolates to "
-                      f"{layer_flops(layer.t * TOPK) / (tflops * 1e12):.0f} s"}
+        moe_torch.fused_experts_fp8(*args)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    tflops = layer_flops(routes) / med / 1e12
+    model = platform.processor() or "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": int(torch.get_num_threads()),
+            "kind": "port", "cpu": model,
+            "sample": f"torch float32 CPU restatement (oracle/moe_torch.py) of the T={layer.t} "
+                      f"layer on its {experts.size} most loaded experts ({routes} routes of "
+                      f"{toks.size} tokens), median of 5 after 1 warm-up = {med:.2f} s; the full "
+                      f"layer extrapolates to {layer_flops(layer.t * TOPK) / (tflops * 1e12):.0f} s"}
 
 
 # DeepSeek-V3 linear layers as [N, K] (fused q_a + kv_a, q_b, kv_b, o_proj,
@@ -346,6 +372,119 @@ def w4_sweep(torch, iters: int, log) -> int:
     return 0
 
 
+def point(us: float, flops: float, nbytes: float, peak_tflops: float) -> dict:
+    """us / TFLOP/s / GB/s and the fractions of the roofline of one timed call."""
+    ideal = max(flops / (peak_tflops * 1e12), nbytes / (PEAK_HBM_GBS * 1e9))
+    return {"us": round(us, 1), "tflops": round(flops / (us * 1e-6) / 1e12, 2),
+            "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "frac_peak": round(flops / (us * 1e-6) / 1e12 / peak_tflops, 4),
+            "frac_roofline": round(ideal / (us * 1e-6), 4)}
+
+
+def median_us(torch, fn, iters: int, flush) -> float:
+    """Median HIP-event time (us) of `fn` after WARMUP_SWEEP warm-ups, caches
+    flushed before each timed call."""
+    for _ in range(WARMUP_SWEEP):
+        fn()
+    torch.cuda.synchronize()
+    return statistics.median(time_events(torch, fn, iters, flush)) * 1e3
+
+
+C1_SHAPES = ((24576, 1536), (7168, 18432), (2112, 7168), (7168, 2048))
+C1_M = (1, 4, 16, 64, 512, 4096)
+
+
+def dense_configs(torch, iters: int, flush, log) -> list:
+    """Dense w8a8 block-fp8 linear at its benchmark shapes: the reference op
+    (1x128 quantisation of bf16 A, then the block GEMM) and the GEMM alone.
+    Bytes = N*K + 4*ceil(N/128)*(K/128) + 2*M*K + 2*M*N (A in bf16)."""
+    from vllm_musa_amd import per_token_group_quant_fp8, synthetic
+    from vllm_musa_amd.block_fp8 import apply_w8a8_block_fp8_linear, w8a8_block_fp8_matmul
+    out = []
+    for n, k in C1_SHAPES:
+        w, ws = synthetic.dense_fp8_weight(n, k, 7)
+        for m in C1_M:
+            x = synthetic.activations(m, k, 8)
+            q, s = per_token_group_quant_fp8(x, 128)
+            wsz = n * k + 4 * ((n + 127) // 128) * (k // 128)
+            fl = 2.0 * m * n * k
+            us = median_us(torch, lambda: apply_w8a8_block_fp8_linear(x, w, ws), iters, flush)
+            g_us = median_us(torch, lambda: w8a8_block_fp8_matmul(q, w, s, ws, [128, 128]), iters, flush)
+            row = {"N": n, "K": k, "M": m, **point(us, fl, wsz + 2 * m * k + 2 * m * n, PEAK_FP8_TFLOPS)}
+            g = point(g_us, fl, wsz + m * k + 4 * m * (k // 128) + 2 * m * n, PEAK_FP8_TFLOPS)
+            row.update({"gemm_us": g["us"], "gemm_frac_roofline": g["frac_roofline"]})
+            out.append(row)
+        log(f"bench: dense {n}x{k} done")
+        del w, ws
+    return out
+
+
+C2_E, C2_H, C2_I = 128, 2048, 768
+C2_T = (1, 16, 128, 1024, 8192)
+
+
+def bf16_configs(torch, iters: int, flush, log) -> list:
+    """bf16 fused MoE (Qwen3-30B-A3B-like): routing (top-8 softmax renorm on
+    ~N(0,1) logits, `skewed`: +2.0 on experts 0..7) + fused_experts_impl.
+    Bytes = touched experts' W13 + W2 (bf16) + x in + out + logits + routing."""
+    from vllm_musa_amd import fused_topk, synthetic
+    from vllm_musa_amd.fused_moe import fused_experts_impl
+    w13, w2 = synthetic.moe_bf16_weights(C2_E, C2_H, C2_I, 4000)
+    out = []
+    for skewed in (False, True):
+        for t in C2_T:
+            x = synthetic.activations(t, C2_H, 4001 + t)
+            logits = synthetic.router_logits(t, C2_E, 4002 + t, hot=8 if skewed else 0)
+
+            def step():
+                w, ids, _ = fused_topk(x, logits, TOPK, True)
+                return fused_experts_impl(x, w13, w2, w, ids)
+            _, ids, _ = fused_topk(x, logits, TOPK, True)
+            u = int(torch.unique(ids).numel())
+            fl = 2.0 * t * TOPK * 3 * C2_H * C2_I
+            by = u * 3 * C2_H * C2_I * 2 + 4.0 * t * C2_H + 4.0 * t * C2_E + 8.0 * t * TOPK
+            row = {"T": t, "skewed": skewed, "experts_touched": u,
+                   **point(median_us(torch, step, iters, flush), fl, by, PEAK_BF16_TFLOPS)}
+            row["graph_us"] = round(graph_median(torch, step, iters, flush) * 1e3, 1)
+            out.append(row)
+        log(f"bench: bf16 layer ({'skewed' if skewed else 'uniform'}) done")
+    del w13, w2
+    return out
+
+
+C4_E, C4_H, C4_I = 128, 4096, 1536
+C4_T = (1, 32, 512, 4096)
+
+
+def w4_configs(torch, iters: int, flush, log) -> list:
+    """w4afp8 fused MoE: routing (top-8 softmax renorm) + w4afp8_moe.  Bytes =
+    touched experts' int4 weights and bf16 group scales + x in + out + logits +
+    routing."""
+    from vllm_musa_amd import fused_topk, synthetic, w4afp8_moe
+    w13, w2, s13, s2 = synthetic.moe_w4a8_weights(C4_E, C4_H, C4_I, 5000)
+    per_expert = 3 * C4_I * C4_H // 2 + 2 * 3 * C4_I * (C4_H // 128)
+    out = []
+    for t in C4_T:
+        x = synthetic.activations(t, C4_H, 5001 + t)
+        logits = synthetic.router_logits(t, C4_E, 5002 + t)
+
+        def step():
+            w, ids, _ = fused_topk(x, logits, TOPK, True)
+            return w4afp8_moe(x, w13, w2, s13, s2, w, ids)
+        _, ids, _ = fused_topk(x, logits, TOPK, True)
+        u = int(torch.unique(ids).numel())
+        fl = 2.0 * t * TOPK * 3 * C4_H * C4_I
+        by = u * per_expert + 4.0 * t * C4_H + 4.0 * t * C4_E + 8.0 * t * TOPK
+        row = {"T": t, "experts_touched": u,
+               **point(median_us(torch, step, iters, flush), fl, by, PEAK_FP8_TFLOPS)}
+        row["graph_us"] = round(graph_median(torch, step, iters, flush) * 1e3, 1)
+        out.append(row)
+    log("bench: w4afp8 layer done")
+    del w13, w2, s13, s2
+    return out
+
+
 def scales_sweep(torch, iters: int, log) -> int:
     """HIP-event medians of vmamd_convert_scales on checkpoint-load workloads
     (caches flushed by a 1 GiB read before each call): the e8m0 -> f32 upcast of
@@ -423,12 +562,14 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--sweep-iters", type=int, default=20)
+    ap.add_argument("--sweep-iters", type=int, default=50)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
-                    help="only launch the W13 kernel at T=4096 three times, then three "
-                         "1 GiB device copies (the counter calibration), for rocprofv3 --pmc")
+                    help="only launch, three times each, the large-T kernels profiled with "
+                         "rocprofv3 --pmc (fp8 W13 and W2 grouped GEMMs at T=4096, the dense "
+                         "GEMM at M=4096 for 7168x18432 and 24576x1536, the w4afp8 layer at "
+                         "T=4096), then three 1 GiB device copies (the traffic calibration)")
     ap.add_argument("--profile-t", type=int, default=0,
                     help="only run --steps layer steps at this T (caches flushed by a 1 GiB "
                          "read before each), for rocprofv3 --kernel-trace; prints no JSON")
@@ -493,8 +634,27 @@ def main() -> int:
         st.align()
         for _ in range(3):
             st.w13_stage()
+        for _ in range(3):
+            st.w2_stage()
         torch.cuda.synchronize()
         del st, layer, weights
+        torch.cuda.empty_cache()
+        from vllm_musa_amd import fused_topk, per_token_group_quant_fp8, w4afp8_moe
+        from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+        for n, k in ((7168, 18432), (24576, 1536)):
+            wd, wsd = synthetic.dense_fp8_weight(n, k, 7)
+            q, s = per_token_group_quant_fp8(synthetic.activations(4096, k, 8), 128)
+            for _ in range(3):
+                w8a8_block_fp8_matmul(q, wd, s, wsd, [128, 128])
+            torch.cuda.synchronize()
+            del wd, wsd, q, s
+        w4 = synthetic.moe_w4a8_weights(C4_E, C4_H, C4_I, 5000)
+        x4 = synthetic.activations(4096, C4_H, 5001 + 4096)
+        w, ids, _ = fused_topk(x4, synthetic.router_logits(4096, C4_E, 5002 + 4096), TOPK, True)
+        for _ in range(3):
+            w4afp8_moe(x4, w4[0], w4[1], w4[2], w4[3], w, ids)
+        torch.cuda.synchronize()
+        del w4, x4
         torch.cuda.empty_cache()
         # Calibration: a plain 1 GiB device copy whose source was evicted from
         # the caches by reading another 1 GiB first.
@@ -505,7 +665,7 @@ def main() -> int:
             other.max()
             dst.copy_(src)
         torch.cuda.synchronize()
-        log("bench: traffic probe done (3 W13 launches, 3 x 1 GiB copies)")
+        log("bench: traffic probe done (3 launches of each kernel, 3 x 1 GiB copies)")
         return 0
 
     if args.profile_t > 0:
@@ -560,7 +720,9 @@ def main() -> int:
                 "kernel": "moe_gemm_dma_kernel<kFp8, W13>",
                 "kernel_us": round(k_ms * 1e3, 1),
                 "kernel_tflops": round(2.0 * T_HEADLINE * TOPK * 2 * I * H / (k_ms * 1e-3) / 1e12, 1),
-                "algorithmic_bytes": int(k_bytes)}
+                "algorithmic_bytes": int(k_bytes),
+                "mfma_util": read_summary_value(MFMA_SUMMARY, "mfma_util_w13", float),
+                "mfma_source": MFMA_SUMMARY}
     del st
 
     # ------------------------------------------------------------- sweep ---
@@ -575,11 +737,7 @@ def main() -> int:
         for t in SWEEP_T:
             lay = layer if t == T_HEADLINE else Layer(torch, t, weights)
             u = lay.used_experts()
-            for _ in range(3):
-                lay.step()
-            torch.cuda.synchronize()
-            times = time_events(torch, lay.step, args.sweep_iters, flush)
-            med = statistics.median(times)
+            med = median_us(torch, lay.step, args.sweep_iters, flush) * 1e-3
             gmed = graph_median(torch, lay.step, args.sweep_iters, flush)
             f = layer_flops(t * TOPK)
             b = layer_bytes(t, u)
@@ -593,6 +751,16 @@ def main() -> int:
                           "graph_us": round(gmed * 1e3, 1),
                           "graph_frac_roofline": round(ideal / (gmed * 1e-3), 4)})
             log(f"bench: sweep {sweep[-1]}")
+        del flush_buf
+
+    # ---------------------------------- the metric's other configurations --
+    extra = {}
+    if not args.no_sweep:
+        flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+        flush = lambda: flush_buf.max()
+        extra["dense"] = dense_configs(torch, args.sweep_iters, flush, log)
+        extra["bf16_moe"] = bf16_configs(torch, args.sweep_iters, flush, log)
+        extra["w4afp8_moe"] = w4_configs(torch, args.sweep_iters, flush, log)
         del flush_buf
 
     cpu = None
@@ -611,7 +779,7 @@ def main() -> int:
                    "weights": "e4m3fn, 128x128 block scales", "activations": "1x128 fp8 groups",
                    "experts_touched": u_head, "algorithmic_gbps":
                        round(head_bytes / (ms * 1e-3) / 1e9, 1)},
-        "roofline": roofline, "cpu_baseline": cpu, "sweep": sweep,
+        "roofline": roofline, "cpu_baseline": cpu, "sweep": sweep, **extra,
     }
     print(json.dumps(line), flush=True)
     return 0
