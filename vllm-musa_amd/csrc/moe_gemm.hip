@@ -1267,17 +1267,19 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma_bf16x2(f.w[nt], f.x[mt], acc[mt][nt]);
     }
   };
-  // Step kb: `nxt` is read (two LDS reads after each MFMA) while `cur` runs
-  // on MFMA; buffer kb % NS is refilled with step kb + NS after the MFMAs are
-  // issued, so a wave does not start its MFMAs late behind the DMA issue of
-  // the other waves.
+  // Step kb: buffer kb % NS (whose fragments every wave read during step
+  // kb - 1, as the barrier proves) is refilled with step kb + NS first, so
+  // the DMA has almost two steps to land; then `nxt` is read (two LDS reads
+  // after each MFMA) while `cur` runs on MFMA.  Issuing the refill ahead of
+  // the MFMAs rather than after them measured 5-7 % faster on the DeepSeek-V3
+  // layer at T=4096 (W13 2083 -> 1936 us, W2 1160 -> 1101 us).
   auto step = [&](int kb, const Frags& cur, Frags& nxt) {
     wait_lgkmcnt0();
     wait_vmcnt<(NS - 2) * P::kIPS>();
     barrier_lds();
+    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
     read(smem_dyn + ((kb + 1) % NS) * P::kStage, nxt);
     mma(cur);
-    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
   };
 #pragma unroll
   for (int s = 0; s < NS; ++s) p.issue(smem_dyn + s * P::kStage, min(s, KS - 1));
