@@ -65,7 +65,7 @@ METRIC = "fp8-block MoE layer µs, TFLOPS & HBM GB/s (% roofline) at T=1..4096"
 # WRITE_SIZE per dispatch scaled by a 1 GiB copy ("traffic_bytes_per_launch:"
 # fills roofline.traffic), and the fp8 MFMA counters ("mfma_util_w13:" fills
 # roofline.mfma_util: MFMA flops per second over the dense fp8 peak).
-TRAFFIC_SUMMARY = os.path.join("profiles", "moe_w13_gemm_fp8_dsv3_T4096_traffic.md")
+TRAFFIC_SUMMARY = os.path.join("profiles", "gemm_traffic_large_t.md")
 MFMA_SUMMARY = os.path.join("profiles", "mfma_utilisation_large_t.md")
 
 
