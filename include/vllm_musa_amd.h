@@ -370,8 +370,9 @@ int vmamd_moe_bf16_w2(const void* a2, int64_t T, int topk, const int32_t* sorted
  *   y  = bf16(sum_kb (q_row(a) . W2_int4[e]^T)_kb * s2[e, n, kb] * s_a)
  *   out[t] = bf16(sum_k y[t, k] * w[t, k])  (fp32 accumulator)
  * x [T, H] bf16; w13 [E, 2I, H/2] int8 with w13_s [E, 2I, H/128] bf16; w2
- * [E, H, I/2] int8 with w2_s [E, H, I/128] bf16; topk / expert_map / path /
- * workspace rules as vmamd_fused_moe_fp8.  H, I <= 16384.
+ * [E, H, I/2] int8 with w2_s [E, H, I/128] bf16 (both scale arrays 4-byte
+ * aligned); topk / expert_map / path / workspace rules as
+ * vmamd_fused_moe_fp8.  H, I <= 16384.
  * Replaces w4afp8_moe (vllm_musa/kernels/w4afp8_moe.py:164-362) and the MATE
  * S4FP8 grouped GEMMs it calls (283-318), reached from
  * MusaW4AFp8MoEMethod.apply (model_executor/layers/quantization/w4afp8.py:147-170). */

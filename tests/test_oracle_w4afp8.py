@@ -9,7 +9,11 @@
   int4 scales are constant on 128x128 blocks and every 128-group of a row has
   the row's absmax (then per-row and per-group quantisation coincide);
 - the W2 scales enter linearly: doubling them doubles the layer exactly;
-- one expert, top-1, weight 1: the output is the expert output y.
+- one expert, top-1, weight 1: the output is the expert output y;
+- the kernels' int4 operand encoding (mfma_fp8.h w4_frag): restated
+  bit-for-bit on the host, every code decodes (torch's float8_e4m3fn) to
+  (x + 8) / 512, the accumulator-input correction recovers the int4 dot
+  product exactly, and the byte planes follow the activations' w4 order.
 """
 from __future__ import annotations
 
@@ -135,52 +139,68 @@ def test_e4m3_of_int4_values():
     np.testing.assert_array_equal(e4m3_decode(e4m3_encode(v)), v)
 
 
-def _perm(s0: int, s1: int, sel: int) -> int:
-    """v_perm_b32: byte i of the result from selector byte sel_i over the 8
-    bytes of {s0:s1} (s1 low): 0..7 pick a byte; 8, 9, 10, 11 replicate bit 7
-    of byte 1, 3, 5, 7; 12 gives 0x00 and 13..255 give 0xFF."""
-    data = (s0 << 32) | s1
+def _bitop3(s0: int, s1: int, s2: int, table: int) -> int:
+    """v_bitop3_b32: bit i of the result is bit (s0_i << 2 | s1_i << 1 | s2_i)
+    of the 8-bit truth table (s0 -> 0xF0, s1 -> 0xCC, s2 -> 0xAA)."""
     out = 0
-    for i in range(4):
-        k = (sel >> (8 * i)) & 0xFF
-        if k < 8:
-            b = (data >> (8 * k)) & 0xFF
-        elif k < 12:
-            b = 0xFF * ((data >> (8 * (2 * (k - 8) + 1) + 7)) & 1)
-        else:
-            b = 0x00 if k == 12 else 0xFF
-        out |= b << (8 * i)
+    for i in range(32):
+        idx = (((s0 >> i) & 1) << 2) | (((s1 >> i) & 1) << 1) | ((s2 >> i) & 1)
+        out |= ((table >> idx) & 1) << i
     return out
 
 
-def _int4x8_to_fp8(x: int) -> int:
-    """Host restatement of the kernels' nibble -> e4m3 conversion (mfma_fp8.h):
-    8 packed int4 in a dword -> 8 e4m3 codes (64 bits, element order)."""
-    m32 = 0xFFFFFFFF
-    se, so = x & 0x07070707, (x >> 4) & 0x07070707
-    qe = (x << 4) & m32
-    me = _perm((qe << 8) & m32, qe, 0x090B080A)
-    mo = _perm((x << 8) & m32, x, 0x090B080A)
-    ce = (_perm(0xB8C0C4C8, 0xCACCCED0, se) & me) | (_perm(0x4E4C4A48, 0x44403800, se) & ~me & m32)
-    co = (_perm(0xB8C0C4C8, 0xCACCCED0, so) & mo) | (_perm(0x4E4C4A48, 0x44403800, so) & ~mo & m32)
-    return _perm(co, ce, 0x05010400) | (_perm(co, ce, 0x07030602) << 32)
+def _w4_frag_word(w: int) -> tuple[int, int]:
+    """Host restatement of one word of the kernels' w4_frag (mfma_fp8.h):
+    8 packed int4 -> (even-element plane, odd-element plane) of e4m3 codes."""
+    even = _bitop3(w, 0x88888888, 0x0F0F0F0F, 0x28)
+    odd = _bitop3(w >> 4, 0x88888888, 0x0F0F0F0F, 0x28)
+    return even, odd
 
 
-def test_perm_emulation_known_selectors():
-    """The emulated v_perm_b32 on selectors whose results the ISA fixes."""
-    assert _perm(0x07060504, 0x03020100, 0x07050301) == 0x07050301
-    assert _perm(0, 0x00008000, 0x08080808) == 0xFFFFFFFF  # bit 15 -> selector 8
-    assert _perm(0x80000000, 0, 0x0B0B0B0B) == 0xFFFFFFFF  # bit 63 -> selector 11
-    assert _perm(0xFFFFFFFF, 0xFFFFFFFF, 0x0D0C0D0C) == 0xFF00FF00
+def test_bitop3_table_0x28_is_xor_then_and():
+    g = np.random.Generator(np.random.PCG64(3))
+    for a, b, c in g.integers(0, 1 << 32, (200, 3), dtype=np.uint64).tolist():
+        assert _bitop3(a, b, c, 0x28) == (a ^ b) & c
 
 
-def test_kernel_nibble_table_is_e4m3_of_the_int4_value():
+W4_ORDER = [0, 2, 4, 6, 1, 3, 5, 7]  # element of each byte position within 8 K-elements
+
+
+def test_w4_codes_are_the_int4_value_plus_8_times_2_pow_minus_9():
+    """Every nibble in every position: the code w4_frag emits at the position
+    the w4 order gives decodes (torch's float8_e4m3fn) to (x + 8) / 512 exactly."""
     g = np.random.Generator(np.random.PCG64(5))
-    words = list(range(0, 1 << 16, 7)) + [int(w) for w in g.integers(0, 1 << 32, 4000, dtype=np.uint64)]
+    words = list(range(0, 1 << 16, 7)) + [int(w) for w in g.integers(0, 1 << 32, 2000, dtype=np.uint64)]
     words += [0x88888888, 0x77777777, 0xF0F0F0F0, 0x0F0F0F0F, 0x80808080, 0x08080808]
-    for t in words:  # every nibble value in every position, many combinations
-        out = _int4x8_to_fp8(t)
-        for i in range(8):
-            v = (t >> (4 * i)) & 0xF
-            v = v - 16 if v >= 8 else v
-            assert (out >> (8 * i)) & 0xFF == int(e4m3_encode(np.float32(v))), (hex(t), i)
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float()
+    for t in words:
+        even, odd = _w4_frag_word(t)
+        planes = (even | (odd << 32))
+        for p in range(8):
+            code = (planes >> (8 * p)) & 0xFF
+            x = (t >> (4 * W4_ORDER[p])) & 0xF
+            x = x - 16 if x >= 8 else x
+            assert float(codes[code]) == (x + 8) / 512.0, (hex(t), p)
+
+
+def test_offset_correction_recovers_the_int4_dot_product(rng):
+    """sum_k a_k * code_k + c with c = -(sum_k a_k) / 64 equals 2^-9 sum_k a_k x_k
+    exactly (float64 over e4m3-valued activations), for any K-permutation that
+    both operands share -- the identity the kernels' MFMA accumulator input uses."""
+    for _ in range(50):
+        a = e4m3_decode(e4m3_encode(rng.standard_normal(128).astype(np.float32) * 100)).astype(np.float64)
+        x = rng.integers(-8, 8, 128)
+        perm = rng.permutation(128)
+        lhs = np.sum(a[perm] * ((x[perm] + 8) / 512.0)) - np.sum(a) / 64.0
+        assert lhs == np.sum(a * x) / 512.0
+
+
+def test_w4_order_matches_the_fragment_planes():
+    """A word of 8 consecutive elements expands to [e0, e2, e4, e6 | e1, e3, e5, e7]:
+    the order the activation quantisers store each 8-element chunk in."""
+    t = 0
+    for i in range(8):
+        t |= ((i - 4) & 0xF) << (4 * i)  # element i holds value i - 4
+    even, odd = _w4_frag_word(t)
+    got = [((even | (odd << 32)) >> (8 * p)) & 0xFF for p in range(8)]
+    assert [c - 8 + 4 for c in got] == W4_ORDER

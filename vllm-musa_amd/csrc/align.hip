@@ -209,15 +209,16 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_quant_kernel(
                            -448.f, 448.f, xq, cols, xs, groups_per_row, 1);
 }
 
-// As moe_align_quant_kernel, with the w4afp8 per-row quantiser: each quant
-// workgroup quantises kAlignThreads / kRowThreads rows, one per 256-thread part.
+// As moe_align_quant_kernel, with the w4afp8 per-row quantiser (w4 order and
+// block corrections): each quant workgroup quantises kAlignThreads /
+// kRowThreads rows, one per 256-thread part.
 __global__ __launch_bounds__(kAlignThreads) void moe_align_rowquant_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int align_groups, int E, int bs,
     const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ active_out, int32_t* __restrict__ num_active_out,
     const uint16_t* __restrict__ x, int64_t rows, int cols, uint8_t* __restrict__ xq,
-    float* __restrict__ xs) {
+    float* __restrict__ xs, float* __restrict__ xcorr) {
   if (static_cast<int>(blockIdx.x) < align_groups) {
     align_body(blockIdx.x, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids,
                ntpp, offsets_out, nullptr, active_out, num_active_out);
@@ -227,8 +228,8 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_rowquant_kernel(
   __shared__ float red[kAlignThreads / kWave];
   const int part = threadIdx.x / kRowThreads;
   const int64_t row = static_cast<int64_t>(blockIdx.x - align_groups) * kParts + part;
-  row_quant_part(x, cols, cols, 1e-4f, -448.f, 448.f, xq, xs, row, row < rows,
-                 threadIdx.x % kRowThreads, red + part * (kRowThreads / kWave));
+  row_quant_part<true>(x, cols, cols, 1e-4f, -448.f, 448.f, xq, xs, row, row < rows,
+                       threadIdx.x % kRowThreads, red + part * (kRowThreads / kWave), xcorr);
 }
 
 }  // namespace vmamd
@@ -278,7 +279,8 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
                             int block_size, const int32_t* expert_map, int64_t expert_map_len,
                             int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
                             int32_t* offsets, int32_t* active, int32_t* num_active, const void* x,
-                            int64_t rows, int64_t cols, uint8_t* xq, float* xs, hipStream_t st) {
+                            int64_t rows, int64_t cols, uint8_t* xq, float* xs, float* xcorr,
+                            hipStream_t st) {
   const char* who = "moe align + row quant";
   VMAMD_REQUIRE(num_experts > 0 && num_experts <= kMaxAlignExperts && block_size > 0, "%s: bad sizes",
                 who);
@@ -286,9 +288,10 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
                     capacity >= numel + static_cast<int64_t>(num_experts) * (block_size - 1),
                 "%s: bad route count or capacity", who);
   VMAMD_REQUIRE(!expert_map || expert_map_len > 0, "%s: empty expert_map", who);
-  VMAMD_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= kRowThreads * 8 * kRowChunks,
-                "%s: cols must be a multiple of 8 and at most %d", who, kRowThreads * 8 * kRowChunks);
-  VMAMD_REQUIRE((topk_ids || numel == 0) && sorted && expert_ids && ntpp && (x || rows == 0) &&
+  VMAMD_REQUIRE(rows >= 0 && cols > 0 && cols % 128 == 0 && cols <= kRowThreads * 8 * kRowChunks,
+                "%s: cols must be a multiple of 128 and at most %d", who, kRowThreads * 8 * kRowChunks);
+  VMAMD_REQUIRE((topk_ids || numel == 0) && sorted && expert_ids && ntpp &&
+                    ((x && xq && xs && xcorr) || rows == 0) &&
                     reinterpret_cast<uintptr_t>(x) % 16 == 0 && (reinterpret_cast<uintptr_t>(xq) & 7) == 0,
                 "%s: null or misaligned pointer", who);
   int64_t chunk;
@@ -300,7 +303,7 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
   moe_align_rowquant_kernel<<<static_cast<int>(groups + qblocks), kAlignThreads, 0, st>>>(
       topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted,
       capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x), rows,
-      static_cast<int>(cols), xq, xs);
+      static_cast<int>(cols), xq, xs, xcorr);
   return check_launch(who);
 }
 }  // namespace vmamd

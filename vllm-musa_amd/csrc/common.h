@@ -34,12 +34,15 @@ int align_and_group_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_ex
                               int32_t* offsets, int32_t* active, int32_t* num_active,
                               const void* x, int64_t rows, int64_t cols, uint8_t* xq, float* xs,
                               hipStream_t st);
-// The same with the w4afp8 per-row quantiser (eps 1e-4): xs [rows].
+// The same with the w4afp8 per-row quantiser (eps 1e-4): xs [rows]; xq in
+// w4 order with the block corrections xcorr [rows, cols / 128] (cols a
+// multiple of 128).
 int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_experts,
                             int block_size, const int32_t* expert_map, int64_t expert_map_len,
                             int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
                             int32_t* offsets, int32_t* active, int32_t* num_active, const void* x,
-                            int64_t rows, int64_t cols, uint8_t* xq, float* xs, hipStream_t st);
+                            int64_t rows, int64_t cols, uint8_t* xq, float* xs, float* xcorr,
+                            hipStream_t st);
 
 // Top-k combine (moe_sum.hip): out[t] = round(sum_k x[t, k] (* wts[t, k])) over
 // the live slots; num_experts > 0 also drops slots whose local id is >= it.

@@ -44,35 +44,43 @@ __device__ __forceinline__ v4f mfma_bf16x2(const v8i& a, const v8i& b, v4f c) {
   return c;
 }
 
-// 8 signed int4 values (element 2j in the low nibble of byte j of `x`, 2j+1
-// in the high nibble) -> their 8 e4m3 codes, in element order.  Every integer
-// in [-8, 7] is exact in e4m3.  The even and the odd elements are taken as
-// two byte planes; in each, a byte-permute lookup on the nibble's low three
-// bits reads the codes of 0..7 and another those of -8..-1, and the nibble's
-// sign (bit 3) selects between them through a per-byte mask that v_perm_b32
-// itself builds (selectors 8..11 replicate bit 7 of bytes 1 and 3 of either
-// source dword: the mask of x needs the sign bits at bit 7 of every byte,
-// which x has for the odd plane and x << 4 for the even one, and x << 8 moves
-// bytes 0 and 2 into the positions the selectors read).  Two more permutes
-// re-interleave the planes.  16 VALU operations per 8 elements.
-__device__ __forceinline__ uint2 int4x8_to_fp8(uint32_t x) {
-  constexpr uint32_t kPosLo = 0x44403800u, kPosHi = 0x4E4C4A48u;  // e4m3 of 0..7
-  constexpr uint32_t kNegLo = 0xCACCCED0u, kNegHi = 0xB8C0C4C8u;  // e4m3 of -8..-1
-  constexpr uint32_t kSignSel = 0x090B080Au;  // byte i <- bit 7 of byte i of q, from {q << 8, q}
-  const uint32_t se = x & 0x07070707u, so = (x >> 4) & 0x07070707u;
-  const uint32_t qe = x << 4;  // bit 7 of byte i: sign of the even element i
-  const uint32_t me = __builtin_amdgcn_perm(qe << 8, qe, kSignSel);
-  const uint32_t mo = __builtin_amdgcn_perm(x << 8, x, kSignSel);
-  const uint32_t ce = (__builtin_amdgcn_perm(kNegHi, kNegLo, se) & me) |
-                      (__builtin_amdgcn_perm(kPosHi, kPosLo, se) & ~me);
-  const uint32_t co = (__builtin_amdgcn_perm(kNegHi, kNegLo, so) & mo) |
-                      (__builtin_amdgcn_perm(kPosHi, kPosLo, so) & ~mo);
-  return uint2{__builtin_amdgcn_perm(co, ce, 0x05010400u), __builtin_amdgcn_perm(co, ce, 0x07030602u)};
+// w4afp8 weight operands.  A signed int4 weight x (two per byte, element 2j
+// in the low nibble of byte j) enters the MFMA as the e4m3 code u = x + 8,
+// which is the nibble with its top bit flipped.  Codes 0..15 are the e4m3
+// subnormals and the first normal binade, which are evenly spaced: code u has
+// the value u * 2^-9 exactly, and the fp8 MFMA takes subnormal inputs at their
+// value.  So a weight costs one XOR and one mask (the odd elements one shift
+// more) instead of a table lookup.  The offset leaves the accumulator input:
+// with c = -(sum_k a_k) / 64 for the activation row and K block (8 * 2^-9 =
+// 2^-6),
+//     mfma(u, a, c) = 2^-9 * sum_k a_k * x_k,
+// so every block product carries a factor 2^-9, which the epilogues undo
+// (times kW4Unit = 512, exact).
+//
+// The even elements of a 32-bit word of packed weights become one byte plane
+// and the odd elements another, so within every 8 K-elements the weight bytes
+// run [0, 2, 4, 6, 1, 3, 5, 7].  The activations are stored in that order by
+// their quantisers ("w4 order"), and lane group g of a fragment takes the 32
+// contiguous elements [32g, 32g + 32) of the K block: packed weight bytes
+// [16g, 16g + 16), activation bytes [32g, 32g + 32).
+constexpr float kW4Unit = 512.0f;
+
+// 16 packed bytes (32 int4 in K order) -> the 32 e4m3 codes x + 8, w4 order.
+// v_bitop3_b32 with table 0x28 computes (s0 ^ s1) & s2.
+__device__ __forceinline__ v8i w4_frag(const v4i& raw) {
+  v8i f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = static_cast<uint32_t>(raw[j]);
+    f[2 * j] = static_cast<int>(__builtin_amdgcn_bitop3_b32(w, 0x88888888u, 0x0F0F0F0Fu, 0x28));
+    f[2 * j + 1] = static_cast<int>(__builtin_amdgcn_bitop3_b32(w >> 4, 0x88888888u, 0x0F0F0F0Fu, 0x28));
+  }
+  return f;
 }
-__device__ __forceinline__ v4i int4x16_to_fp8(uint2 p) {
-  const uint2 a = int4x8_to_fp8(p.x), b = int4x8_to_fp8(p.y);
-  return v4i{static_cast<int>(a.x), static_cast<int>(a.y), static_cast<int>(b.x), static_cast<int>(b.y)};
-}
+
+// The accumulator input {c, c, c, c} of one MFMA (c: the activation row's
+// offset correction for the K block).
+__device__ __forceinline__ v4f splat4(float c) { return v4f{c, c, c, c}; }
 
 // Loads from LDS through address-space-3 pointers, so the compiler knows
 // they touch LDS (a read through a generic pointer makes it wait for every
@@ -108,27 +116,6 @@ __device__ __forceinline__ v8i global_frag(const uint8_t* p, int g) {
 // for the HIP uint4 struct).
 __device__ __forceinline__ v4i ld16(const uint8_t* p) { return *reinterpret_cast<const v4i*>(p); }
 __device__ __forceinline__ void st16(uint8_t* p, const v4i& v) { *reinterpret_cast<v4i*>(p) = v; }
-
-// Operand fragment of one 128-element K-block of a packed int4 row (64 bytes
-// at p), converted to e4m3 in the same K order as global_frag: lane group g
-// takes elements [16g, 16g+16) and [64+16g, 64+16g+16).
-// The packed bytes of such a fragment (16 bytes per lane, kept packed until
-// the MFMA needs them), and their conversion.
-__device__ __forceinline__ uint4 global_frag_int4_raw(const uint8_t* p, int g) {
-  const uint2 lo = *reinterpret_cast<const uint2*>(p + 8 * g);
-  const uint2 hi = *reinterpret_cast<const uint2*>(p + 32 + 8 * g);
-  return uint4{lo.x, lo.y, hi.x, hi.y};
-}
-__device__ __forceinline__ v8i int4_frag_to_fp8(const uint4& raw) {
-  const v4i a = int4x16_to_fp8(uint2{raw.x, raw.y}), b = int4x16_to_fp8(uint2{raw.z, raw.w});
-  v8i f;
-  f[0] = a[0]; f[1] = a[1]; f[2] = a[2]; f[3] = a[3];
-  f[4] = b[0]; f[5] = b[1]; f[6] = b[2]; f[7] = b[3];
-  return f;
-}
-__device__ __forceinline__ v8i global_frag_int4(const uint8_t* p, int g) {
-  return int4_frag_to_fp8(global_frag_int4_raw(p, g));
-}
 
 // acc += p * s, element-wise (the per-K-block scale promotion).
 __device__ __forceinline__ void fma4(v4f& acc, const v4f& p, float s) {

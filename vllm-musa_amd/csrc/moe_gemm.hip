@@ -86,7 +86,7 @@ __device__ __forceinline__ float swiglu_w4(float g, float u, float limit) {
 
 template <int KIND>
 __device__ __forceinline__ v8i weight_frag(const uint8_t* p, int g) {
-  if constexpr (KIND == kW4) return global_frag_int4(p, g);
+  if constexpr (KIND == kW4) return w4_frag(ld16(p + 16 * g));
   else return global_frag(p, g);
 }
 
@@ -110,16 +110,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 __device__ __forceinline__ v4i buffer_ld16(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
   return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, 0));
 }
-// Activation fragment at byte offset off (row + K-block start) of a buffer.
+// Activation fragment at byte offset off (row + K-block start) of a buffer
+// (kW4: the 32 contiguous bytes of lane group g, matching w4_frag).
+template <int KIND>
 __device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
-  const v4i lo = buffer_ld16(rs, off + 16u * g);
-  const v4i hi = buffer_ld16(rs, off + 64u + 16u * g);
+  const uint32_t o0 = KIND == kW4 ? 32u * g : 16u * g;
+  const uint32_t o1 = KIND == kW4 ? 32u * g + 16u : 64u + 16u * g;
+  const v4i lo = buffer_ld16(rs, off + o0);
+  const v4i hi = buffer_ld16(rs, off + o1);
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// act: [rows, K] activation bytes (rows = numel / act_div), act_bytes its
-// size (< 2^31); act_s: kFp8 [rows, K/128] group scales; kW4 / kBf16 unused.
-// ws: kFp8 f32 block scales; kW4 bf16 row scales.
+// act: [rows, K] activation bytes (rows = numel / act_div, kW4 in w4 order),
+// act_bytes its size (< 2^31); act_s: kFp8 [rows, K/128] group scales, kW4
+// [rows, K/128] offset corrections, kBf16 unused.  ws: kFp8 f32 block scales;
+// kW4 bf16 row scales.  kW4 results are scaled by kW4Unit before they are
+// stored.
 //
 // Start-up order: the expert id is the only load the weight stream depends
 // on, so the first K group of weights is requested before the route list is
@@ -134,7 +140,8 @@ __device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t o
 // VS (K/128 a multiple of U and aligned scale rows): kFp8 reads the U block
 // scales of a group, and each route's U activation scales, with one 16-byte
 // load each instead of U scattered ones; kW4 reads each of the lane's four
-// rows' U bf16 scales with one 8-byte load instead of U 2-byte ones.  Splits
+// rows' U bf16 scales with one 8-byte load instead of U 2-byte ones, and each
+// route's U corrections with one 16-byte load.  Splits
 // start on group boundaries, so with VS every group lies entirely inside its
 // split.
 template <int MAXB, int KIND, bool VS = false>
@@ -182,7 +189,7 @@ moe_gemv_kernel(
   // making the weight stream wait for scalar loads.
   const __amdgpu_buffer_rsrc_t wsrs = buffer_rsrc(wsr, KIND == kFp8 ? KS * 4 : 0);
   const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(act, act_bytes);
-  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(act_s, KIND == kFp8 ? act_bytes / 32 : 0);
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(act_s, KIND != kBf16 ? act_bytes / 32 : 0);
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
 
   // One K group of weights (U steps from kb, clamped to the split's range).
@@ -191,7 +198,7 @@ moe_gemv_kernel(
   // its MFMA; with several blocks a fragment is converted once per group.
   constexpr bool kRawW4 = KIND == kW4 && MAXB == 1;
   v8i wf[kRawW4 ? 1 : U];
-  uint4 wraw[kRawW4 ? U : 1];
+  v4i wraw[kRawW4 ? U : 1];
   uint2 swr[4];  // kW4 + VS: packed bf16 scales, U per row
   float sb[U];
   v4f sw[U];
@@ -205,7 +212,7 @@ moe_gemv_kernel(
     for (int u = 0; u < U; ++u) {
       const int k = min(kb + u, kb1 - 1);
       if constexpr (kRawW4)
-        wraw[u] = global_frag_int4_raw(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
+        wraw[u] = ld16(wrow + static_cast<int64_t>(k) * KB_::kW + 16 * lg);
       else
         wf[u] = weight_frag<KIND>(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
       if constexpr (!VS) sb[u] = 0.f;
@@ -255,9 +262,9 @@ moe_gemv_kernel(
         for (int u = 0; u < U; ++u) {
           const bool live = aoff[b] != kBufferOff && kb + u < kb1;
           const uint32_t off = live ? aoff[b] + static_cast<uint32_t>((kb + u) * KB_::kAct) : kBufferOff;
-          xf[u] = buffer_frag(ars, off, lg);
+          xf[u] = buffer_frag<KIND>(ars, off, lg);
           if constexpr (!VS) as[u] = 0.f;
-          if constexpr (KIND == kFp8 && !VS)  // scale byte offset = activation byte offset / 32
+          if constexpr (KIND != kBf16 && !VS)  // scale byte offset = activation byte offset / 32
             as[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                   srs, static_cast<int>(live ? off / 32 : kBufferOff), 0, 0));
         }
@@ -267,9 +274,9 @@ moe_gemv_kernel(
             fma4(acc[b], mfma_fp8(wf[u], xf[u], zero), as[u] * sb[u]);
           } else if constexpr (KIND == kW4) {
             if constexpr (kRawW4)
-              fma4v(acc[b], mfma_fp8(int4_frag_to_fp8(wraw[u]), xf[u], zero), w4_scales(u));
+              fma4v(acc[b], mfma_fp8(w4_frag(wraw[u]), xf[u], splat4(as[u])), w4_scales(u));
             else
-              fma4v(acc[b], mfma_fp8(wf[u], xf[u], zero), w4_scales(u));
+              fma4v(acc[b], mfma_fp8(wf[u], xf[u], splat4(as[u])), w4_scales(u));
           } else {
             acc[b] = mfma_bf16x2(wf[u], xf[u], acc[b]);
           }
@@ -311,7 +318,7 @@ moe_gemv_kernel(
     for (int b = 0; b < MAXB; ++b) {
       if (b >= nb || rr[b] < 0) continue;
       const int r = rr[b];
-      const v4f a = acc[b];
+      const v4f a = KIND == kW4 ? acc[b] * kW4Unit : acc[b];
       if (y) {
         const float rw = route_w ? route_w[r] : 1.0f;
         *reinterpret_cast<uint2*>(y + static_cast<int64_t>(r) * N + n) =
@@ -450,10 +457,12 @@ __global__ __launch_bounds__(256) void moe_act_bf16_kernel(const float* __restri
 // pass, one kRowThreads block per route row: the bf16-rounded activations stay
 // in registers for the row maximum and the quantiser (the values the separate
 // quantiser would read back), so neither the bf16 activation nor a second
-// launch is needed.  I <= kRowThreads * 8 * kRowChunks.
+// launch is needed.  a2q is written in w4 order with its block corrections
+// a2corr [numel, I/128].  I <= kRowThreads * 8 * kRowChunks.
 __global__ __launch_bounds__(kRowThreads) void moe_act_rowquant_w4_kernel(
     const float* __restrict__ partial, int splits, int numel, int I, float limit,
-    const float* __restrict__ xs, int topk, uint8_t* __restrict__ a2q, float* __restrict__ a2s) {
+    const float* __restrict__ xs, int topk, uint8_t* __restrict__ a2q, float* __restrict__ a2s,
+    float* __restrict__ a2corr) {
   __shared__ float red[kRowThreads / kWave];
   const int r = blockIdx.x;
   const int nchunk = I / 8;
@@ -485,9 +494,21 @@ __global__ __launch_bounds__(kRowThreads) void moe_act_rowquant_w4_kernel(
   for (int c = 0; c < kRowChunks; ++c) {
     const int ch = threadIdx.x + c * kRowThreads;
     if (ch < nchunk)
-      *reinterpret_cast<uint2*>(a2q + static_cast<int64_t>(r) * I + ch * 8) =
-          quant8(v[c], s, -448.0f, 448.0f);
+      w4_store_chunk(a2q + static_cast<int64_t>(r) * I, a2corr + static_cast<int64_t>(r) * (I / 128), ch,
+                     v[c], s, -448.0f, 448.0f);
   }
+}
+
+// kW4 prefill: the per-row a2 quantiser of the bf16 activation (one
+// kRowThreads block per padded route row below ntpp[0]), in w4 order with the
+// block corrections a2corr [rows, I/128].
+__global__ __launch_bounds__(kRowThreads) void moe_rowquant_w4_kernel(
+    const uint16_t* __restrict__ a, int I, const int32_t* __restrict__ ntpp, uint8_t* __restrict__ a2q,
+    float* __restrict__ a2s, float* __restrict__ a2corr) {
+  if (static_cast<int>(blockIdx.x) >= ntpp[0]) return;  // uniform: past the last block
+  __shared__ float red[kRowThreads / kWave];
+  row_quant_part<true>(a, I, I, 1e-4f, -448.f, 448.f, a2q, a2s, blockIdx.x, true, threadIdx.x, red,
+                       a2corr);
 }
 
 // A route's slot is live when its expert id is >= 0 and its local id
@@ -686,436 +707,6 @@ __device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* _
   tn_out = local / nb;
   mb_out = b0 + local % nb;
   return true;
-}
-
-// Weight-tile loader of the prefill GEMMs.  One pass moves THREADS/CPR rows;
-// kFp8 / kBf16 copy 16-byte chunks (CPR = 8 per 128-byte row step), kW4 reads
-// 16 packed bytes (32 elements) per thread (CPR = 4) and writes the two
-// 16-byte e4m3 chunks they expand to.
-template <int KIND, int THREADS, int BN>
-struct WLoader {
-  static constexpr int CPR = KIND == kW4 ? 4 : 8;
-  static constexpr int RSTEP = THREADS / CPR;
-  static constexpr int BCH = BN / RSTEP;
-  using Raw = typename std::conditional<KIND == kW4, uint4, v4i>::type;
-  int64_t goff[BCH];
-  int l0, l1;  // LDS byte offsets (row 0 of the pass) of the chunks written
-  Raw raw[BCH];
-
-  __device__ __forceinline__ void load(const uint8_t* __restrict__ w, int step) {
-#pragma unroll
-    for (int c = 0; c < BCH; ++c) {
-      const uint8_t* p = w + goff[c] + static_cast<int64_t>(step) * KindBytes<KIND>::kW;
-      if constexpr (KIND == kW4) raw[c] = *reinterpret_cast<const uint4*>(p);
-      else raw[c] = ld16(p);
-    }
-  }
-  __device__ __forceinline__ void store(uint8_t* tile) const {
-#pragma unroll
-    for (int c = 0; c < BCH; ++c) {
-      if constexpr (KIND == kW4) {
-        st16(tile + l0 + c * RSTEP * 128, int4x16_to_fp8(uint2{raw[c].x, raw[c].y}));
-        st16(tile + l1 + c * RSTEP * 128, int4x16_to_fp8(uint2{raw[c].z, raw[c].w}));
-      } else {
-        st16(tile + l0 + c * RSTEP * 128, raw[c]);
-      }
-    }
-  }
-};
-
-// W13: tile = 128 routes x (128 gate + 128 up rows); 8 waves as 2 (m) x 4 (n);
-// local weight row j: pair p = j / 32, q = j % 32 -> gate row n0 + 16p + q
-// (q < 16) or up row I + n0 + 16p + q - 16.  Dynamic LDS per stage: the two
-// tiles, plus (kW4) the fp32 scales of the 256 weight rows.
-constexpr int kW13Threads = 512;
-constexpr int kW13BN = 256;
-template <int KIND>
-constexpr int w13_stage_bytes() { return (kMoeBM + kW13BN) * 128 + (KIND == kW4 ? kW13BN * 4 : 0); }
-
-// xs: kFp8 [T, H/128] group scales, kW4 [T] row scales.  w13s: kFp8 f32
-// block scales, kW4 bf16 row scales.  a2: kFp8 e4m3 [rows, I] (+ a2s), kBf16 /
-// kW4 bf16 [rows, I].
-template <int KIND>
-__global__ __launch_bounds__(kW13Threads, 1) void moe_w13_gemm_kernel(
-    const uint8_t* __restrict__ xa, const float* __restrict__ xs, int topk, int H,
-    const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles,
-    const uint8_t* __restrict__ w13, const void* __restrict__ w13s, int I, float limit,
-    uint8_t* __restrict__ a2, float* __restrict__ a2s) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
-  using KB_ = KindBytes<KIND>;
-  constexpr int BM = kMoeBM, BN = kW13BN, THREADS = kW13Threads;
-  constexpr int WN = 4, WTM = 64, WTN = 64, MT = 4, NT = 4;
-  constexpr int RSTEP = THREADS / 8;   // activation rows per copy pass
-  constexpr int ACH = BM / RSTEP;      // 2
-  constexpr int STAGE = w13_stage_bytes<KIND>();
-
-  const int TN = I / 128;
-  int e, mb, tn;
-  if (!moe_tile(blockIdx.x, max_tiles, offsets, ntpp, E, TN, e, mb, tn)) return;
-  const int n0 = tn * 128;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int wm = wave / WN, wn = wave % WN;
-  const int li = lane % 16, lg = lane / 16;
-  const int KS = H / KB_::kElems;
-  const int64_t arowb = static_cast<int64_t>(KS) * KB_::kAct;
-  const int64_t wrowb = static_cast<int64_t>(KS) * KB_::kW;
-  const int NB2 = (2 * I + 127) / 128;
-
-  const int crow = tid / 8, cch = tid % 8;
-  const int la0 = lds_off(crow, cch);
-  // Padding rows of the block load row 0 and are zeroed in registers.
-  int64_t goff_a[ACH];
-  bool aval[ACH];
-#pragma unroll
-  for (int c = 0; c < ACH; ++c) {
-    const int r = sorted[mb * BM + crow + c * RSTEP];
-    aval[c] = r < numel;
-    goff_a[c] = (aval[c] ? static_cast<int64_t>(r / topk) * arowb : 0) + cch * 16;
-  }
-  auto w13_row = [&](int j) {  // local weight row -> row of w13[e]
-    const int p = j / 32, q = j % 32;
-    return q < 16 ? n0 + 16 * p + q : I + n0 + 16 * p + (q - 16);
-  };
-  WLoader<KIND, THREADS, BN> wl;
-  {
-    using WL = WLoader<KIND, THREADS, BN>;
-    const int wr = tid / WL::CPR, wc = tid % WL::CPR;
-#pragma unroll
-    for (int c = 0; c < WL::BCH; ++c)
-      wl.goff[c] = (static_cast<int64_t>(e) * 2 * I + w13_row(wr + c * WL::RSTEP)) * wrowb + wc * 16;
-    wl.l0 = BM * 128 + lds_off(wr, KIND == kW4 ? 2 * wc : wc);
-    wl.l1 = BM * 128 + lds_off(wr, 2 * wc + 1);
-  }
-  // kW4: thread j < BN stages the scale of local weight row j.
-  const uint16_t* wsc_row = nullptr;
-  if constexpr (KIND == kW4)
-    wsc_row = tid < BN ? static_cast<const uint16_t*>(w13s) +
-                             (static_cast<int64_t>(e) * 2 * I + w13_row(tid)) * KS
-                       : nullptr;
-  const float* xs_row[MT];
-  bool tval[MT];
-  float srow[MT];  // kW4: activation row scales
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = sorted[mb * BM + wm * WTM + mt * 16 + li];
-    tval[mt] = r < numel;
-    const int64_t tok = tval[mt] ? r / topk : 0;
-    xs_row[mt] = KIND == kFp8 ? xs + tok * KS : nullptr;
-    srow[mt] = KIND == kW4 ? (tval[mt] ? xs[tok] : 0.f) : 0.f;
-  }
-  const float* sg = nullptr;
-  const float* su = nullptr;
-  if constexpr (KIND == kFp8) {
-    sg = static_cast<const float*>(w13s) + (static_cast<int64_t>(e) * NB2 + n0 / 128) * KS;
-    su = static_cast<const float*>(w13s) + (static_cast<int64_t>(e) * NB2 + (I + n0) / 128) * KS;
-  }
-
-  v4f acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  const v4i z4 = {0, 0, 0, 0};
-  v4i ra[ACH];
-#pragma unroll
-  for (int c = 0; c < ACH; ++c) {
-    const v4i v = ld16(xa + goff_a[c]);
-    ra[c] = aval[c] ? v : z4;
-  }
-  wl.load(w13, 0);
-  float wsc = 0.f;
-  if constexpr (KIND == kW4)
-    if (wsc_row) wsc = bf16_to_f32(wsc_row[0]);
-#pragma unroll
-  for (int c = 0; c < ACH; ++c) st16(&smem_dyn[la0 + c * RSTEP * 128], ra[c]);
-  wl.store(smem_dyn);
-  if constexpr (KIND == kW4)
-    if (wsc_row) reinterpret_cast<float*>(smem_dyn + (BM + BN) * 128)[tid] = wsc;
-  float sa[MT], sbg = 0.f, sbu = 0.f;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) sa[mt] = 0.f;
-  if constexpr (KIND == kFp8) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) sa[mt] = tval[mt] ? xs_row[mt][0] : 0.f;
-    sbg = sg[0];
-    sbu = su[0];
-  }
-  __syncthreads();
-
-  const v4f zero = {0.f, 0.f, 0.f, 0.f};
-  for (int kb = 0; kb < KS; ++kb) {
-    const int cur = kb & 1;
-    // Prefetch step kb+1 (the last iteration re-reads step KS-1 into the idle
-    // buffer; that copy is never used).
-    const int kn = min(kb + 1, KS - 1);
-#pragma unroll
-    for (int c = 0; c < ACH; ++c) {
-      const v4i v = ld16(xa + goff_a[c] + static_cast<int64_t>(kn) * KB_::kAct);
-      ra[c] = aval[c] ? v : z4;
-    }
-    wl.load(w13, kn);
-    float san[MT], sbgn = 0.f, sbun = 0.f, wscn = 0.f;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) san[mt] = 0.f;
-    if constexpr (KIND == kFp8) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const float v = xs_row[mt][kn];
-        san[mt] = tval[mt] ? v : 0.f;
-      }
-      sbgn = sg[kn];
-      sbun = su[kn];
-    }
-    if constexpr (KIND == kW4)
-      if (wsc_row) wscn = bf16_to_f32(wsc_row[kn]);
-
-    const uint8_t* tile = smem_dyn + cur * STAGE;
-    v8i xf[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xf[mt] = lds_frag(tile, wm * WTM + mt * 16 + li, lg);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int wrow_l = wn * WTN + nt * 16;
-      const v8i wf = lds_frag(tile + BM * 128, wrow_l + li, lg);
-      if constexpr (KIND == kFp8) {
-        const float sb = (nt & 1) ? sbu : sbg;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) fma4(acc[mt][nt], mfma_fp8(wf, xf[mt], zero), sa[mt] * sb);
-      } else if constexpr (KIND == kW4) {
-        const v4f swv = *reinterpret_cast<const v4f*>(tile + (BM + BN) * 128 + (wrow_l + 4 * lg) * 4);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) fma4v(acc[mt][nt], mfma_fp8(wf, xf[mt], zero), swv);
-      } else {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma_bf16x2(wf, xf[mt], acc[mt][nt]);
-      }
-    }
-    uint8_t* nxt = smem_dyn + (cur ^ 1) * STAGE;
-#pragma unroll
-    for (int c = 0; c < ACH; ++c) st16(&nxt[la0 + c * RSTEP * 128], ra[c]);
-    wl.store(nxt);
-    if constexpr (KIND == kW4)
-      if (wsc_row) reinterpret_cast<float*>(nxt + (BM + BN) * 128)[tid] = wscn;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) sa[mt] = san[mt];
-    sbg = sbgn;
-    sbu = sbun;
-    __syncthreads();
-  }
-
-  if constexpr (KIND == kFp8) {
-    // Epilogue: activation, row amax across the 4 n-waves through LDS, quantise.
-    float* red = reinterpret_cast<float*>(smem_dyn);  // [WN][BM]
-    float v[MT][2][4];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float amax = 0.f;
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float x = swiglu_bf16(bf16r(acc[mt][2 * q][r]), bf16r(acc[mt][2 * q + 1][r]), limit);
-          v[mt][q][r] = x;
-          amax = fmaxf(amax, fabsf(x));
-        }
-      amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
-      amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
-      if (lg == 0) red[wn * BM + wm * WTM + mt * 16 + li] = amax;
-    }
-    __syncthreads();
-    const int gpr = I / 128;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int ml = wm * WTM + mt * 16 + li;
-      float amax = 1e-10f;
-#pragma unroll
-      for (int w = 0; w < WN; ++w) amax = fmaxf(amax, red[w * BM + ml]);
-      const float scale = amax / 448.0f;
-      const int64_t row = static_cast<int64_t>(mb) * BM + ml;
-      if (wn == 0 && lg == 0) a2s[row * gpr + tn] = scale;
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        float o[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float x = v[mt][q][r];
-          o[r] = x != x ? -448.0f : fminf(fmaxf(x / scale, -448.0f), 448.0f);
-        }
-        const int col = n0 + (wn * 2 + q) * 16 + 4 * lg;
-        *reinterpret_cast<uint32_t*>(a2 + row * I + col) = f32x4_to_fp8x4(o[0], o[1], o[2], o[3]);
-      }
-    }
-  } else {
-    uint16_t* a2b = reinterpret_cast<uint16_t*>(a2);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int64_t row = static_cast<int64_t>(mb) * BM + wm * WTM + mt * 16 + li;
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        float o[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if constexpr (KIND == kW4)
-            o[r] = swiglu_w4(bf16r(acc[mt][2 * q][r] * srow[mt]),
-                             bf16r(acc[mt][2 * q + 1][r] * srow[mt]), limit);
-          else
-            o[r] = swiglu_bf16(bf16r(acc[mt][2 * q][r]), bf16r(acc[mt][2 * q + 1][r]), limit);
-        }
-        const int col = n0 + (wn * 2 + q) * 16 + 4 * lg;
-        *reinterpret_cast<uint2*>(a2b + row * I + col) = pack_bf16x4(o[0], o[1], o[2], o[3]);
-      }
-    }
-  }
-}
-
-// W2: tile = 128 routes x 128 hidden rows, 4 waves as 2 x 2, K = I.
-// a2s: kFp8 [rows, I/128] group scales, kW4 [rows] row scales.
-// y[r] = bf16(acc * route_w[r]) (kFp8 / kBf16) or bf16(acc * a2s[row]) (kW4).
-template <int KIND>
-__global__ __launch_bounds__(256, 2) void moe_w2_gemm_kernel(
-    const uint8_t* __restrict__ a2, const float* __restrict__ a2s, int I,
-    const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles,
-    const uint8_t* __restrict__ w2, const void* __restrict__ w2s, int H,
-    const float* __restrict__ route_w, uint16_t* __restrict__ y) {
-  using KB_ = KindBytes<KIND>;
-  constexpr int BM = kMoeBM, BN = 128, THREADS = 256, WN = 2, WTM = 64, WTN = 64, MT = 4, NT = 4;
-  constexpr int RSTEP = THREADS / 8, ACH = BM / RSTEP;
-  constexpr int STAGE = (BM + BN) * 128 + (KIND == kW4 ? BN * 4 : 0);
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][STAGE];
-
-  const int TN = (H + BN - 1) / BN;
-  int e, mb, tn;
-  if (!moe_tile(blockIdx.x, max_tiles, offsets, ntpp, E, TN, e, mb, tn)) return;
-  const int n0 = tn * BN;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int wm = wave / WN, wn = wave % WN;
-  const int li = lane % 16, lg = lane / 16;
-  const int KS = I / KB_::kElems;
-  const int64_t arowb = static_cast<int64_t>(KS) * KB_::kAct;
-  const int64_t wrowb = static_cast<int64_t>(KS) * KB_::kW;
-  const int NBH = (H + 127) / 128;
-
-  const int crow = tid / 8, cch = tid % 8;
-  const int la0 = lds_off(crow, cch);
-  int64_t goff_a[ACH];
-#pragma unroll
-  for (int c = 0; c < ACH; ++c)
-    goff_a[c] = (static_cast<int64_t>(mb) * BM + crow + c * RSTEP) * arowb + cch * 16;
-  WLoader<KIND, THREADS, BN> wl;
-  {
-    using WL = WLoader<KIND, THREADS, BN>;
-    const int wr = tid / WL::CPR, wc = tid % WL::CPR;
-#pragma unroll
-    for (int c = 0; c < WL::BCH; ++c)
-      wl.goff[c] = (static_cast<int64_t>(e) * H + min(n0 + wr + c * WL::RSTEP, H - 1)) * wrowb + wc * 16;
-    wl.l0 = BM * 128 + lds_off(wr, KIND == kW4 ? 2 * wc : wc);
-    wl.l1 = BM * 128 + lds_off(wr, 2 * wc + 1);
-  }
-  const uint16_t* wsc_row = nullptr;
-  if constexpr (KIND == kW4)
-    wsc_row = tid < BN ? static_cast<const uint16_t*>(w2s) +
-                             (static_cast<int64_t>(e) * H + min(n0 + tid, H - 1)) * KS
-                       : nullptr;
-  const float* sb_p = nullptr;
-  if constexpr (KIND == kFp8)
-    sb_p = static_cast<const float*>(w2s) + (static_cast<int64_t>(e) * NBH + n0 / 128) * KS;
-  const int64_t arow0 = static_cast<int64_t>(mb) * BM + wm * WTM + li;
-
-  v4f acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  v4i ra[ACH];
-#pragma unroll
-  for (int c = 0; c < ACH; ++c) ra[c] = ld16(a2 + goff_a[c]);
-  wl.load(w2, 0);
-  float wsc = 0.f;
-  if constexpr (KIND == kW4)
-    if (wsc_row) wsc = bf16_to_f32(wsc_row[0]);
-#pragma unroll
-  for (int c = 0; c < ACH; ++c) st16(&smem[0][la0 + c * RSTEP * 128], ra[c]);
-  wl.store(smem[0]);
-  if constexpr (KIND == kW4)
-    if (wsc_row) reinterpret_cast<float*>(smem[0] + (BM + BN) * 128)[tid] = wsc;
-  float sa[MT], sb = 0.f;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) sa[mt] = 0.f;
-  if constexpr (KIND == kFp8) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) sa[mt] = a2s[(arow0 + mt * 16) * KS];
-    sb = sb_p[0];
-  }
-  __syncthreads();
-
-  const v4f zero = {0.f, 0.f, 0.f, 0.f};
-  for (int kb = 0; kb < KS; ++kb) {
-    const int cur = kb & 1;
-    const int kn = min(kb + 1, KS - 1);
-#pragma unroll
-    for (int c = 0; c < ACH; ++c) ra[c] = ld16(a2 + goff_a[c] + static_cast<int64_t>(kn) * KB_::kAct);
-    wl.load(w2, kn);
-    float san[MT], sbn = 0.f, wscn = 0.f;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) san[mt] = 0.f;
-    if constexpr (KIND == kFp8) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) san[mt] = a2s[(arow0 + mt * 16) * KS + kn];
-      sbn = sb_p[kn];
-    }
-    if constexpr (KIND == kW4)
-      if (wsc_row) wscn = bf16_to_f32(wsc_row[kn]);
-    const uint8_t* tile = smem[cur];
-    v8i xf[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xf[mt] = lds_frag(tile, wm * WTM + mt * 16 + li, lg);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int wrow_l = wn * WTN + nt * 16;
-      const v8i wf = lds_frag(tile + BM * 128, wrow_l + li, lg);
-      if constexpr (KIND == kFp8) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) fma4(acc[mt][nt], mfma_fp8(wf, xf[mt], zero), sa[mt] * sb);
-      } else if constexpr (KIND == kW4) {
-        const v4f swv = *reinterpret_cast<const v4f*>(tile + (BM + BN) * 128 + (wrow_l + 4 * lg) * 4);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) fma4v(acc[mt][nt], mfma_fp8(wf, xf[mt], zero), swv);
-      } else {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma_bf16x2(wf, xf[mt], acc[mt][nt]);
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < ACH; ++c) st16(&smem[cur ^ 1][la0 + c * RSTEP * 128], ra[c]);
-    wl.store(smem[cur ^ 1]);
-    if constexpr (KIND == kW4)
-      if (wsc_row) reinterpret_cast<float*>(smem[cur ^ 1] + (BM + BN) * 128)[tid] = wscn;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) sa[mt] = san[mt];
-    sb = sbn;
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = sorted[arow0 + mt * 16];
-    if (r >= numel) continue;
-    float rw = 1.0f;
-    if constexpr (KIND == kW4) rw = a2s[arow0 + mt * 16];
-    else rw = route_w ? route_w[r] : 1.0f;
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int n = n0 + wn * WTN + nt * 16 + 4 * lg;
-      if (n >= H) continue;
-      const v4f a = acc[mt][nt];
-      *reinterpret_cast<uint2*>(y + static_cast<int64_t>(r) * H + n) =
-          pack_bf16x4(a[0] * rw, a[1] * rw, a[2] * rw, a[3] * rw);
-    }
-  }
 }
 
 // ------------------------------------- prefill GEMMs on the DMA ring -------
@@ -1385,6 +976,263 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
   }
 }
 
+// ------------------------------------------- w4afp8 prefill GEMMs ---------
+// Tile: 128 routes x 256 weight rows, 8 waves as 2 (m) x 4 (n) with 64 x 64
+// per wave, on a W4Pipe::NS-deep LDS ring fed by direct global->LDS loads
+// (the discipline of tile_pipe.h).  A stage holds one K step (128 elements):
+//   [activations 128 x 128 B, w4 order, row r chunk c at lds_off(r, c)]
+//   [packed weights 256 x 64 B, row r chunk c at slot c ^ ((r >> 2) & 3): the
+//    16 rows one lane group reads hit 16 distinct 16-byte bank groups]
+//   [activation corrections 128 x 16 B, each row's value four times, which is
+//    an MFMA accumulator input as read]
+//   [weight-scale words 256 x 4 B: the aligned 4 bytes holding row r's bf16
+//    scale of the step, next to that of the step before or after it]
+//   [256 x 4 B that waves 4-7 fill with a copy of the scale words, so every
+//    wave issues the same number of loads per stage (the waits count per wave)]
+// The weights cross LDS packed; each wave expands its fragments after the LDS
+// read (w4_frag), with the offset correction as the MFMA accumulator input
+// and the bf16 weight scale applied per step (acc += p * s, 4 FMAs per MFMA).
+// W13: the 256 weight rows are 128 gate + 128 up rows interleaved by 16, the
+// epilogue writes the bf16 SwiGLU activation of every padded route row;
+// W2: 256 hidden rows, epilogue y[r] = bf16(acc * a2 row scale).
+// EVEN: K / 128 is even (a row's scale words never straddle two rows).
+// Buffer-descriptor forms of dma16 / dma4: a lane whose byte offset lies
+// past the buffer's end fetches nothing.
+__device__ __forceinline__ void buffer_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint8_t* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)((lds_u8*)lds), 16, static_cast<int>(off), 0, 0, 0);
+}
+__device__ __forceinline__ void buffer_dma4(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint8_t* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)((lds_u8*)lds), 4, static_cast<int>(off), 0, 0, 0);
+}
+
+struct W4Pipe {
+  static constexpr int BM = 128, BN = 256, NS = 4, MT = 4, NT = 4;
+  static_assert(NS >= 2, "the ring keeps NS - 1 steps in flight");
+  static constexpr int kOffB = BM * 128;
+  static constexpr int kOffC = kOffB + BN * 64;
+  static constexpr int kOffS = kOffC + BM * 16;
+  static constexpr int kOffD = kOffS + BN * 4;
+  static constexpr int kStage = kOffD + BN * 4;
+  static constexpr int kLds = NS * kStage;
+  static constexpr int kIPS = 6;  // loads per stage per wave: 2 activation, 2 weight, 1 correction, 1 scale
+};
+static_assert(W4Pipe::kLds <= 160 * 1024, "LDS ring exceeds the CU's LDS");
+
+// Packed weight chunk c of LDS tile row r.
+__device__ __forceinline__ int w4_lds_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+
+// act: W13 the quantised x [T, K] (rows = tokens), W2 a2 [rows, K] in padded
+// route order, act_bytes its size (< 2^31); act_scale: W13 the token row
+// scales, W2 the a2 row scales; act_corr: [rows, K/128] offset corrections;
+// ws: bf16 [E, N, K/128].
+// out: W13 bf16 activation [padded rows, I]; W2 y [numel, N].
+template <bool W13, bool EVEN>
+__global__ __launch_bounds__(512, 1) void moe_w4_gemm_kernel(
+    const uint8_t* __restrict__ act, const float* __restrict__ act_scale,
+    const float* __restrict__ act_corr, int act_bytes, int topk, int K,
+    const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles, const uint8_t* __restrict__ w,
+    const uint16_t* __restrict__ ws, int N, int I, float limit, uint16_t* __restrict__ out) {
+  using P = W4Pipe;
+  constexpr int BM = P::BM, BN = P::BN, NS = P::NS, MT = P::MT, NT = P::NT, WN = 4, WTM = 64, WTN = 64;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
+  const int TN = W13 ? I / 128 : (N + BN - 1) / BN;
+  int e, mb, tn;
+  if (!moe_tile(blockIdx.x, max_tiles, offsets, ntpp, E, TN, e, mb, tn)) return;
+  const int n0 = W13 ? tn * 128 : tn * BN;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wm = wave / WN, wn = wave % WN, li = lane % 16, lg = lane / 16;
+  const int KS = K / 128;
+
+  auto wrow = [&](int j) -> int {  // weight row of local tile row j
+    if constexpr (W13) {
+      const int p = j / 32, q = j % 32;
+      return q < 16 ? n0 + 16 * p + q : I + n0 + 16 * p + (q - 16);
+    } else {
+      return min(n0 + j, N - 1);
+    }
+  };
+  auto arow = [&](int r) -> int64_t {  // activation row of tile row r (-1: padding)
+    const int rr = mb * BM + r;
+    const int s = sorted[rr];
+    if (s >= numel) return -1;
+    return W13 ? static_cast<int64_t>(s / topk) : rr;
+  };
+
+  // Per-lane load sources at K step 0 and wave-uniform LDS offsets in a
+  // stage.  Activation rows and corrections are read through buffer
+  // descriptors: a padding row's lanes get an offset past the end and fetch
+  // nothing (their LDS bytes are left undefined; only padding outputs, which
+  // are never stored or used, depend on them).
+  const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(act, act_bytes);
+  const __amdgpu_buffer_rsrc_t crs = buffer_rsrc(act_corr, act_bytes / 32);
+  uint32_t offA[2];
+  const uint8_t* srcB[2];
+  int ldsA[2], ldsB[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int ga = wave + 8 * j;  // 8-row activation group
+    const int64_t ra = arow(ga * 8 + lane / 8);
+    offA[j] = ra >= 0 ? static_cast<uint32_t>(ra * KS * 128 + ((lane % 8) ^ (lane / 8)) * 16) : kBufferOff;
+    ldsA[j] = ga * 1024;
+    const int rb = ga * 16 + lane / 4;  // 16-row weight group ga
+    srcB[j] = w + (static_cast<int64_t>(e) * N + wrow(rb)) * KS * 64 + (((lane % 4) ^ (lane / 16)) << 4);
+    ldsB[j] = P::kOffB + ga * 1024;
+  }
+  const int64_t rc = arow(wave * 16 + lane / 4);
+  const uint32_t offC = rc >= 0 ? static_cast<uint32_t>(rc * KS * 4) : kBufferOff;
+  const int ldsC = P::kOffC + wave * 256;
+  const int64_t rowKS = (static_cast<int64_t>(e) * N + wrow((wave % 4) * 64 + lane)) * KS;
+  const uint8_t* wsb = reinterpret_cast<const uint8_t*>(ws);
+  const int ldsS = (wave < 4 ? P::kOffS : P::kOffD) + (wave % 4) * 256;
+  auto issue = [&](uint8_t* st, int step) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) buffer_dma16(ars, offA[j] + static_cast<uint32_t>(step) * 128, st + ldsA[j]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(srcB[j] + static_cast<int64_t>(step) * 64, st + ldsB[j]);
+    buffer_dma4(crs, offC + static_cast<uint32_t>(step) * 4, st + ldsC);
+    dma4(wsb + ((rowKS + step) & ~static_cast<int64_t>(1)) * 2, st + ldsS);
+  };
+  // Padding routes close a block, so a wave whose first route is padding
+  // holds none.
+  const bool wave_live = sorted[mb * BM + wm * WTM] < numel;
+
+  v4f acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // Operand fragments (double-buffered across steps) and the step's
+  // corrections and scale words (read in the step that uses them).
+  struct Frags {
+    v8i x[MT];
+    v4i w[NT];
+  };
+  struct Small {
+    v4f c[MT];
+    v4i s[NT];
+  };
+  auto read = [&](const uint8_t* st, Frags& f) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = wm * WTM + mt * 16 + li;
+      const v4i lo = lds_load<v4i>(st, lds_off(r, 2 * lg));
+      const v4i hi = lds_load<v4i>(st, lds_off(r, 2 * lg + 1));
+      f.x[mt] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) f.w[nt] = lds_load<v4i>(st, P::kOffB + w4_lds_off(wn * WTN + nt * 16 + li, lg));
+  };
+  auto read_small = [&](const uint8_t* st, Small& q) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) q.c[mt] = lds_load<v4f>(st, P::kOffC + (wm * WTM + mt * 16 + li) * 16);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) q.s[nt] = lds_load<v4i>(st, P::kOffS + (wn * WTN + nt * 16 + 4 * lg) * 4);
+  };
+  // MFMAs n-tile by n-tile: the expansion of a weight fragment serves its
+  // four MFMAs; the promotion of MFMA i - 1 runs while MFMA i executes.  PAR:
+  // parity of the K step, which picks each scale word's half.
+  auto mma = [&](const Frags& f, const Small& q, auto par_tag) {
+    constexpr int PAR = decltype(par_tag)::value;
+    if (!wave_live) return;
+    auto scales = [&](int nt) {
+      v4f sc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t wd = static_cast<uint32_t>(q.s[nt][r]);
+        const bool hi = EVEN ? PAR != 0 : ((r ^ PAR) & 1) != 0;
+        sc[r] = __uint_as_float(hi ? (wd & 0xFFFF0000u) : (wd << 16));
+      }
+      return sc;
+    };
+    constexpr int NI = MT * NT;
+    v8i wx[2];
+    v4f t[2];
+#pragma unroll
+    for (int i = 0; i <= NI; ++i) {
+      if (i < NI) {
+        const int nt = i / MT, mt = i % MT;
+        if (mt == 0) wx[nt & 1] = w4_frag(f.w[nt]);
+        t[i & 1] = mfma_fp8(wx[nt & 1], f.x[mt], q.c[mt]);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      if (i > 0) {
+        const int j = i - 1, nt = j / MT, mt = j % MT;
+        fma4v(acc[mt][nt], t[j & 1], scales(nt));
+        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+      }
+    }
+  };
+  using Even = std::integral_constant<int, 0>;
+  using Odd = std::integral_constant<int, 1>;
+  // Step kb: buffer kb % NS -- step kb, whose fragments and small values
+  // every wave read during step kb - 1, as the barrier proves -- is refilled
+  // with step kb + NS (NS - 1 steps in flight); step kb + 1's fragments are
+  // read while step kb's MFMAs run, and its small values after them.
+  auto step = [&](int kb, const Frags& cur, Frags& nxt, Small& q, auto par_tag) {
+    wait_lgkmcnt0();
+    wait_vmcnt<(NS - 2) * P::kIPS>();
+    barrier_lds();
+    issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
+    read(smem_dyn + ((kb + 1) % NS) * P::kStage, nxt);
+    mma(cur, q, par_tag);
+    read_small(smem_dyn + ((kb + 1) % NS) * P::kStage, q);
+  };
+#pragma unroll
+  for (int st = 0; st < NS; ++st) issue(smem_dyn + st * P::kStage, min(st, KS - 1));
+  wait_vmcnt<(NS - 1) * P::kIPS>();
+  barrier_lds();
+  Frags f0, f1;
+  Small q;
+  read(smem_dyn, f0);
+  read_small(smem_dyn, q);
+  for (int kb = 0; kb < KS; kb += 2) {
+    step(kb, f0, f1, q, Even{});
+    if (kb + 1 < KS) step(kb + 1, f1, f0, q, Odd{});
+  }
+  wait_lgkmcnt0();
+  wait_vmcnt<0>();  // the ring's trailing loads land before LDS is released
+  barrier_lds();
+
+  if constexpr (W13) {
+    uint16_t* a = out;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int64_t row = static_cast<int64_t>(mb) * BM + wm * WTM + mt * 16 + li;
+      const int r = sorted[row];
+      const float srow = r < numel ? act_scale[r / topk] * kW4Unit : 0.f;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[j] = swiglu_w4(bf16r(acc[mt][2 * q][j] * srow), bf16r(acc[mt][2 * q + 1][j] * srow), limit);
+        const int col = n0 + (wn * 2 + q) * 16 + 4 * lg;
+        *reinterpret_cast<uint2*>(a + row * I + col) = pack_bf16x4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int64_t row = static_cast<int64_t>(mb) * BM + wm * WTM + mt * 16 + li;
+      const int r = sorted[row];
+      if (r >= numel) continue;
+      const float rs = act_scale[row] * kW4Unit;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int n = n0 + wn * WTN + nt * 16 + 4 * lg;
+        if (n >= N) continue;
+        const v4f v = acc[mt][nt];
+        *reinterpret_cast<uint2*>(out + static_cast<int64_t>(r) * N + n) =
+            pack_bf16x4(v[0] * rs, v[1] * rs, v[2] * rs, v[3] * rs);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------ host side ---
 // Split-K factor of the decode GEMVs: enough waves to cover the chip
 // (kGemvTargetWaves over the active experts' n-tiles), at least 4 K steps
@@ -1443,18 +1291,47 @@ static size_t stage_scratch(int64_t numel, int E, int64_t H, int64_t I, int bloc
                   w2_scratch(numel, E, H, I, block_m, kind));
 }
 
-template <int KIND>
-static int raise_w13_lds() {
+template <bool W13, bool EVEN>
+static int raise_w4_lds() {
   static bool done = false;
   if (done) return VMAMD_OK;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_w13_gemm_kernel<KIND>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                          2 * w13_stage_bytes<KIND>()) != hipSuccess) {
-    set_error("moe w13: cannot raise the LDS limit of the W13 kernel");
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_w4_gemm_kernel<W13, EVEN>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, W4Pipe::kLds) != hipSuccess) {
+    set_error("w4afp8 moe: cannot raise the LDS limit of the grouped GEMM kernel");
     return VMAMD_ERR_HIP;
   }
   done = true;
   return VMAMD_OK;
+}
+
+// kW4 grouped GEMM launch (W13: N = 2I, out = bf16 activation; W2: N = H,
+// out = y).  The scale words are read 4 bytes at a time, so the scale array
+// must be 4-byte aligned.
+template <bool W13>
+static int launch_w4_gemm(const uint8_t* act, int64_t act_rows, const float* act_scale,
+                          const float* act_corr, int topk, int K, const int32_t* sorted,
+                          const int32_t* offs, const int32_t* ntpp, int E, int numel, int tiles,
+                          const uint8_t* w, const void* ws, int N, int I, float limit, uint16_t* out,
+                          hipStream_t st) {
+  VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(ws) % 4 == 0,
+                "w4afp8 moe: weight scales must be 4-byte aligned for the grouped GEMMs");
+  VMAMD_REQUIRE(act_rows * K < (1ll << 31), "w4afp8 moe: the grouped GEMMs take activations below 2 GiB");
+  const int act_bytes = static_cast<int>(act_rows * K);
+  const uint16_t* wsh = static_cast<const uint16_t*>(ws);
+  if ((K / 128) % 2 == 0) {
+    int rc = raise_w4_lds<W13, true>();
+    if (rc) return rc;
+    moe_w4_gemm_kernel<W13, true><<<xcd_grid(tiles), 512, W4Pipe::kLds, st>>>(
+        act, act_scale, act_corr, act_bytes, topk, K, sorted, offs, ntpp, E, numel, tiles, w, wsh, N, I,
+        limit, out);
+  } else {
+    int rc = raise_w4_lds<W13, false>();
+    if (rc) return rc;
+    moe_w4_gemm_kernel<W13, false><<<xcd_grid(tiles), 512, W4Pipe::kLds, st>>>(
+        act, act_scale, act_corr, act_bytes, topk, K, sorted, offs, ntpp, E, numel, tiles, w, wsh, N, I,
+        limit, out);
+  }
+  return check_launch(W13 ? "w4afp8 moe w13 (gemm)" : "w4afp8 moe w2 (gemm)");
 }
 
 template <int KIND, bool W13>
@@ -1501,32 +1378,39 @@ static void launch_gemv(dim3 grid, hipStream_t st, int T, bool vs, Args... args)
 
 // True when a GEMV over K may read its scales U at a time: K/128 a multiple
 // of U and the scale arrays aligned so that every row is (kFp8: 16 bytes for
-// both scale sets; kW4: 8 bytes for the bf16 weight scales).
+// both scale sets; kW4: 8 bytes for the bf16 weight scales, 16 for the
+// activation corrections).
 template <int KIND>
 static bool gemv_vector_scales(int64_t K, const void* act_s, const void* w_s) {
   if constexpr (KIND == kFp8)
     return (K / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(act_s) % 16 == 0 &&
            reinterpret_cast<uintptr_t>(w_s) % 16 == 0;
-  if constexpr (KIND == kW4) return (K / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(w_s) % 8 == 0;
+  if constexpr (KIND == kW4)
+    return (K / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(w_s) % 8 == 0 &&
+           reinterpret_cast<uintptr_t>(act_s) % 16 == 0;
   return false;
 }
 
 // Launches of the two stages; arguments are validated by the callers.  kBf16:
-// xa is x itself, xs / w13_s / a2s unused.  kW4: xs are the token row scales,
-// a2 receives the bf16 activation (quantised per row by the caller).
+// xa is x itself, xs / w13_s / a2s unused.  kW4: xa in w4 order with the
+// block corrections xcorr, xs the token row scales; the decode path writes
+// a2 (w4 order) with a2s and a2corr, the prefill path the bf16 activation to
+// a2 (quantised per row by the caller).
 template <int KIND>
-static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk,
+static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, int T, int H, int topk,
                       const int32_t* sorted, int64_t cap, int block_m, const int32_t* offs,
                       const int32_t* ntpp, const int32_t* active, const int32_t* nact,
                       const uint8_t* w13, const void* w13_s, int E, int I, float limit,
-                      const float* route_w, uint8_t* a2, float* a2s, float* scratch, hipStream_t st) {
+                      const float* route_w, uint8_t* a2, float* a2s, float* a2corr, float* scratch,
+                      hipStream_t st) {
   const int numel = T * topk;
+  const float* act_s = KIND == kW4 ? xcorr : xs;  // per-step activation values the GEMV reads
   if (block_m == kGemvBlock) {
     const int s13 = w13_splits(numel, E, H, I, KIND);
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s13);
-    launch_gemv<KIND>(g13, st, T, gemv_vector_scales<KIND>(H, xs, w13_s), xa, gemv_act_bytes<KIND>(T, H),
-                      xs, topk, H, sorted, offs, active,
+    launch_gemv<KIND>(g13, st, T, gemv_vector_scales<KIND>(H, act_s, w13_s), xa, gemv_act_bytes<KIND>(T, H),
+                      act_s, topk, H, sorted, offs, active,
                       nact, w13, w13_s, 2 * I, numel, s13, scratch,
                       static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr));
     int rc = check_launch("moe w13 (gemv)");
@@ -1546,7 +1430,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
 #undef VMAMD_ACTQ
     } else if constexpr (KIND == kW4) {  // a2: fp8 [numel, I], a2s: row scales
       moe_act_rowquant_w4_kernel<<<numel, kRowThreads, 0, st>>>(scratch, s13, numel, I, limit, xs,
-                                                                topk, a2, a2s);
+                                                                topk, a2, a2s, a2corr);
     } else {
       const int64_t chunks = static_cast<int64_t>(numel) * (I / 8);
       moe_act_bf16_kernel<KIND><<<static_cast<int>((chunks + 255) / 256), 256, 0, st>>>(
@@ -1557,10 +1441,8 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
   const int tiles = max_blocks * (I / 128);
   if constexpr (KIND == kW4) {
-    int rc = raise_w13_lds<KIND>();
-    if (rc) return rc;
-    moe_w13_gemm_kernel<KIND><<<xcd_grid(tiles), kW13Threads, 2 * w13_stage_bytes<KIND>(), st>>>(
-        xa, xs, topk, H, sorted, offs, ntpp, E, numel, tiles, w13, w13_s, I, limit, a2, a2s);
+    return launch_w4_gemm<true>(xa, T, xs, xcorr, topk, H, sorted, offs, ntpp, E, numel, tiles, w13,
+                                w13_s, 2 * I, I, limit, reinterpret_cast<uint16_t*>(a2), st);
   } else {
     int rc = raise_dma_lds<KIND, true>();
     if (rc) return rc;
@@ -1571,12 +1453,14 @@ static int launch_w13(const uint8_t* xa, const float* xs, int T, int H, int topk
   return check_launch("moe w13 (gemm)");
 }
 
-// kW4: a2s are the a2 row scales and take the routed weight's place in y.
+// kW4: a2s are the a2 row scales and take the routed weight's place in y;
+// a2corr the block corrections of a2 (w4 order).
 // combined_out: when given and the decode path splits K, the reduce and the
 // top-k combine run as one kernel writing the layer output there (y is not
 // written) and *combined is set; otherwise y is written as usual.
 template <int KIND>
-static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const int32_t* sorted,
+static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, int T, int topk,
+                     const int32_t* sorted,
                      int64_t cap, int block_m, const int32_t* offs, const int32_t* ntpp,
                      const int32_t* active, const int32_t* nact, const uint8_t* w2, const void* w2_s,
                      int E, int H, int I, const float* topk_weights, const float* route_w,
@@ -1585,13 +1469,14 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
                      bool* combined = nullptr) {
   const int numel = T * topk;
   const float* yscale = KIND == kW4 ? a2s : route_w;
+  const float* act_s = KIND == kW4 ? a2corr : a2s;  // per-step activation values the GEMV reads
   if (combined) *combined = false;
   if (block_m == kGemvBlock) {
     const int s2 = w2_splits(numel, E, H, I, KIND);
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g2((H / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s2);
     if (s2 > 1 && combined_out && combined && H % 8 == 0) {
-      launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, a2s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs, active,
+      launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, act_s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), act_s, 1, I, sorted, offs, active,
                         nact, w2, w2_s, H, numel, s2, scratch, static_cast<const float*>(nullptr),
                         static_cast<uint16_t*>(nullptr));
       int rc = check_launch("moe w2 (gemv)");
@@ -1606,11 +1491,11 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
       return check_launch("moe w2 (combine)");
     }
     if (s2 == 1) {
-      launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, a2s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs,
+      launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, act_s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), act_s, 1, I, sorted, offs,
                         active, nact, w2, w2_s, H, numel, 1, static_cast<float*>(nullptr), yscale, y);
       return check_launch("moe w2 (gemv)");
     }
-    launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, a2s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), a2s, 1, I, sorted, offs, active,
+    launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, act_s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), act_s, 1, I, sorted, offs, active,
                       nact, w2, w2_s, H, numel, s2, scratch, static_cast<const float*>(nullptr),
                       static_cast<uint16_t*>(nullptr));
     int rc = check_launch("moe w2 (gemv)");
@@ -1622,10 +1507,9 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
   }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
   if constexpr (KIND == kW4) {
-    const int tiles = max_blocks * ((H + 127) / 128);
-    moe_w2_gemm_kernel<KIND><<<xcd_grid(tiles), 256, 0, st>>>(a2, a2s, I, sorted, offs, ntpp, E,
-                                                              numel, tiles, w2, w2_s, H,
-                                                              topk_weights, y);
+    const int tiles = max_blocks * ((H + W4Pipe::BN - 1) / W4Pipe::BN);
+    return launch_w4_gemm<false>(a2, cap, a2s, a2corr, 1, I, sorted, offs, ntpp, E, numel, tiles, w2,
+                                 w2_s, H, I, 0.f, y, st);
   } else {
     const int tiles = max_blocks * ((H + 255) / 256);
     int rc = raise_dma_lds<KIND, false>();
@@ -1642,7 +1526,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, int T, int topk, const
 // scratch shares one region.  kFp8 / kW4 add the quantised x and scales; kW4
 // also keeps the bf16 activation before its row quantiser.
 struct MoeWs {
-  size_t xq, xs, sorted, eids, ntpp, offs, active, nact, abf, a2, a2s, y, scratch, total;
+  size_t xq, xs, xcorr, sorted, eids, ntpp, offs, active, nact, abf, a2, a2s, a2corr, y, scratch, total;
 };
 
 static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm, int kind) {
@@ -1655,6 +1539,7 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
     w.xq = take(T * H);
     w.xs = take(kind == kFp8 ? T * (H / 128) * 4 : T * 4);
   }
+  if (kind == kW4) w.xcorr = take(T * (H / 128) * 4);
   w.sorted = take(cap * 4);
   w.eids = take(((cap + bm - 1) / bm) * 4);
   w.ntpp = take(4);
@@ -1665,7 +1550,10 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   if (kind == kW4) w.abf = take(arows * I * 2);
   w.a2 = take(arows * I * (kind == kBf16 ? 2 : 1));
   if (kind == kFp8) w.a2s = take(arows * (I / 128) * 4);
-  if (kind == kW4) w.a2s = take(arows * 4);
+  if (kind == kW4) {
+    w.a2s = take(arows * 4);
+    w.a2corr = take(arows * (I / 128) * 4);
+  }
   w.y = take(numel * H * 2);
   w.scratch = take(stage_scratch(numel, E, H, I, bm, kind));
   w.total = o;
@@ -1720,6 +1608,9 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   if (rc) return rc;
   VMAMD_REQUIRE(KIND != kW4 || (H <= 16384 && I <= 16384),
                 "%s: per-row quantisation supports rows of up to 16384", who);
+  VMAMD_REQUIRE(KIND != kW4 || (reinterpret_cast<uintptr_t>(w13_s) % 4 == 0 &&
+                                reinterpret_cast<uintptr_t>(w2_s) % 4 == 0),
+                "%s: weight scales must be 4-byte aligned", who);
   if (T == 0) return VMAMD_OK;
   VMAMD_REQUIRE(x && w13 && w2 && topk_weights && topk_ids && out &&
                     (KIND == kBf16 || (w13_s && w2_s)),
@@ -1747,6 +1638,8 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
 
   const uint8_t* xa = static_cast<const uint8_t*>(x);
   const float* xs = nullptr;
+  float* xcorr = KIND == kW4 ? reinterpret_cast<float*>(ws + L.xcorr) : nullptr;
+  float* a2corr = KIND == kW4 ? reinterpret_cast<float*>(ws + L.a2corr) : nullptr;
   if constexpr (KIND == kFp8) {  // quantiser and alignment in one launch
     uint8_t* xq = ws + L.xq;
     float* xsw = reinterpret_cast<float*>(ws + L.xs);
@@ -1759,7 +1652,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     uint8_t* xq = ws + L.xq;
     float* xsw = reinterpret_cast<float*>(ws + L.xs);
     rc = align_and_row_quant_fp8(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
-                                 eids, ntpp, offs, active, nact, x, T, H, xq, xsw, st);
+                                 eids, ntpp, offs, active, nact, x, T, H, xq, xsw, xcorr, st);
     if (rc) return rc;
     xa = xq;
     xs = xsw;
@@ -1775,18 +1668,20 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   // activation (apply_router_weight_on_input), otherwise in the W2 epilogue.
   const float* w13_rw = weight_on_input ? topk_weights : nullptr;
   const float* w2_rw = weight_on_input ? nullptr : topk_weights;
-  rc = launch_w13<KIND>(xa, xs, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
+  rc = launch_w13<KIND>(xa, xs, xcorr, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
                         static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, w13_rw, act_out,
-                        a2s, scratch, st);
+                        a2s, a2corr, scratch, st);
   if (rc) return rc;
   if constexpr (KIND == kW4) {
-    if (bm != kGemvBlock) {
-      rc = vmamd_per_token_quant_fp8(act_out, cap, I, I, 1e-4f, -448.f, 448.f, a2, a2s, stream);
+    if (bm != kGemvBlock) {  // rows past the last block are skipped on the device
+      moe_rowquant_w4_kernel<<<static_cast<unsigned>(cap), kRowThreads, 0, st>>>(
+          reinterpret_cast<const uint16_t*>(act_out), i, ntpp, a2, a2s, a2corr);
+      rc = check_launch("w4afp8_moe (a2 quantiser)");
       if (rc) return rc;
     }
   }
   bool combined = false;
-  rc = launch_w2<KIND>(a2, a2s, t, topk, sorted, cap, bm, offs, ntpp, active, nact,
+  rc = launch_w2<KIND>(a2, a2s, a2corr, t, topk, sorted, cap, bm, offs, ntpp, active, nact,
                        static_cast<const uint8_t*>(w2), w2_s, E, h, i, topk_weights, w2_rw, topk_ids,
                        expert_map, expert_map_len, y, scratch, st, static_cast<uint16_t*>(out),
                        &combined);
@@ -1818,10 +1713,10 @@ static int stage_w13(const char* who, const void* xa, const float* xs, int64_t T
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(xa) % 16 == 0 && reinterpret_cast<uintptr_t>(a2) % 16 == 0,
                 "%s: activations, a2 and workspace must be 16-byte aligned", who);
-  return launch_w13<KIND>(static_cast<const uint8_t*>(xa), xs, static_cast<int>(T), static_cast<int>(H),
+  return launch_w13<KIND>(static_cast<const uint8_t*>(xa), xs, nullptr, static_cast<int>(T), static_cast<int>(H),
                           topk, sorted, capacity, block_m, offs, ntpp, active, nact,
                           static_cast<const uint8_t*>(w13), w13_s, E, static_cast<int>(I), limit,
-                          nullptr, static_cast<uint8_t*>(a2), a2s, static_cast<float*>(workspace),
+                          nullptr, static_cast<uint8_t*>(a2), a2s, nullptr, static_cast<float*>(workspace),
                           reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -1846,7 +1741,7 @@ static int stage_w2(const char* who, const void* a2, const float* a2s, int64_t T
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(a2) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0,
                 "%s: a2 and workspace must be 16-byte and y 8-byte aligned", who);
-  return launch_w2<KIND>(static_cast<const uint8_t*>(a2), a2s, static_cast<int>(T), topk, sorted,
+  return launch_w2<KIND>(static_cast<const uint8_t*>(a2), a2s, nullptr, static_cast<int>(T), topk, sorted,
                          capacity, block_m, offs, ntpp, active, nact, static_cast<const uint8_t*>(w2),
                          w2_s, E, static_cast<int>(H), static_cast<int>(I), topk_weights,
                          KIND == kW4 ? nullptr : topk_weights, topk_ids,

@@ -78,16 +78,43 @@ __device__ __forceinline__ void group_quant_group(
 constexpr int kRowThreads = 256;
 constexpr int kRowChunks = 8;  // rows of up to 256 * 8 * 8 = 16384 columns
 
+// w4afp8 activation chunk (8 consecutive columns 8ch.., ch = a chunk index
+// of the row): quantised with `scale`, stored in w4 order ([0, 2, 4, 6, 1, 3,
+// 5, 7], the order the int4 weight fragments take), and the row's offset
+// correction of each 128-column block, corr[ch / 16] = -(sum of the block's
+// 128 e4m3 values) / 64, written by the chunk's first lane.  The 16 chunks of
+// a block must sit in 16 consecutive lanes (chunk index = lane + a multiple
+// of 16) that all call this; the block sum is taken in a fixed order (8
+// values in sequence, then an xor butterfly over the 16 lanes).
+__device__ __forceinline__ void w4_store_chunk(uint8_t* __restrict__ qrow, float* __restrict__ corr_row,
+                                               int ch, const float (&v)[8], float scale, float qmin,
+                                               float qmax) {
+  const float o[8] = {v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]};
+  const uint2 b = quant8(o, scale, qmin, qmax);
+  *reinterpret_cast<uint2*>(qrow + ch * 8) = b;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s += fp8_to_f32((b.x >> (8 * j)) & 0xFFu);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s += fp8_to_f32((b.y >> (8 * j)) & 0xFFu);
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m, kWave);
+  if ((ch & 15) == 0) corr_row[ch / 16] = s * (-1.0f / 64.0f);
+}
+
 // Per-row quantiser (w4afp8 activations): s = max(eps, amax of the row) /
 // qmax, q = e4m3fn(clamp(x / s, qmin, qmax)).  A part of kRowThreads threads
 // (t = 0 .. kRowThreads - 1 within it) handles one bf16 row; red holds the
 // part's kRowThreads / 64 wave maxima.  Every thread of the block must call
 // it (it synchronises the block); live = false parts only take part in the
-// barrier.
+// barrier.  W4: q in w4 order plus the block corrections corr [rows,
+// cols / 128] (w4_store_chunk; cols a multiple of 128).
+template <bool W4 = false>
 __device__ __forceinline__ void row_quant_part(const uint16_t* __restrict__ x, int64_t x_row_stride,
                                                int cols, float eps, float qmin, float qmax,
                                                uint8_t* __restrict__ q, float* __restrict__ s,
-                                               int64_t row, bool live, int t, float* red) {
+                                               int64_t row, bool live, int t, float* red,
+                                               float* __restrict__ corr = nullptr) {
   const uint16_t* xr = x + row * x_row_stride;
   const int nchunk = live ? cols / 8 : 0;
   float v[kRowChunks][8];
@@ -112,8 +139,12 @@ __device__ __forceinline__ void row_quant_part(const uint16_t* __restrict__ x, i
 #pragma unroll
   for (int c = 0; c < kRowChunks; ++c) {
     const int ch = t + c * kRowThreads;
-    if (ch < nchunk)
-      *reinterpret_cast<uint2*>(q + row * cols + ch * 8) = quant8(v[c], scale, qmin, qmax);
+    if (ch < nchunk) {
+      if constexpr (W4)
+        w4_store_chunk(q + row * cols, corr + row * (cols / 128), ch, v[c], scale, qmin, qmax);
+      else
+        *reinterpret_cast<uint2*>(q + row * cols + ch * 8) = quant8(v[c], scale, qmin, qmax);
+    }
   }
 }
 

@@ -62,6 +62,9 @@ def w4afp8_moe(hidden_states: torch.Tensor, gateup_weight: torch.Tensor,
     emap = None if expert_map is None else expert_map.to(torch.int32).contiguous()
     w13, w2 = gateup_weight.contiguous(), down_weight.contiguous()
     s13, s2 = gateup_scale.contiguous(), down_scale.contiguous()
+    # The grouped GEMMs read the bf16 scales in aligned 4-byte words.
+    s13 = s13 if s13.data_ptr() % 4 == 0 else s13.clone()
+    s2 = s2 if s2.data_ptr() % 4 == 0 else s2.clone()
     _lib.check_cuda(x, w13, w2, s13, s2, wts, ids, emap)
     topk = ids.shape[1]
     code = PATHS[path]
