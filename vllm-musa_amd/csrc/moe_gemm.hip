@@ -980,9 +980,8 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
 // Tile: 128 routes x 256 weight rows, 8 waves as 2 (m) x 4 (n) with 64 x 64
 // per wave, on a W4Pipe::NS-deep LDS ring fed by direct global->LDS loads
 // (the discipline of tile_pipe.h).  A stage holds one K step (128 elements):
-//   [activations 128 x 128 B, w4 order, row r chunk c at lds_off(r, c)]
-//   [packed weights 256 x 64 B, row r chunk c at slot c ^ ((r >> 2) & 3): the
-//    16 rows one lane group reads hit 16 distinct 16-byte bank groups]
+//   [activations 128 x 128 B, w4 order, row r chunk c at w4_act_off(r, c)]
+//   [packed weights 256 x 64 B, row r chunk c at w4_lds_off(r, c)]
 //   [activation corrections 128 x 16 B, each row's value four times, which is
 //    an MFMA accumulator input as read]
 //   [weight-scale words 256 x 4 B: the aligned 4 bytes holding row r's bf16
@@ -1018,8 +1017,17 @@ struct W4Pipe {
 };
 static_assert(W4Pipe::kLds <= 160 * 1024, "LDS ring exceeds the CU's LDS");
 
-// Packed weight chunk c of LDS tile row r.
-__device__ __forceinline__ int w4_lds_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+// LDS slots of the W4 tiles.  A lane group reads one 16-byte chunk of 16
+// consecutive rows; the swizzles spread those 16 reads over 16 distinct
+// 16-byte bank groups of a 256-byte bank line, and any 8 consecutive rows of
+// them over 8 distinct groups of a 128-byte line.
+// Activation chunk c (of 8) of row r: slot c ^ (r & 7) ^ ((r >> 3) & 1).
+__device__ __forceinline__ int w4_act_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int w4_act_off(int r, int c) { return r * 128 + ((c ^ w4_act_swz(r)) << 4); }
+// Packed weight chunk c (of 4) of row r: slot c ^ f(r), f a bijection of row
+// bits 1-2 (8-row lines) and of bits 2-3 (16-row lines).
+__device__ __forceinline__ int w4_wt_swz(int r) { return (((r >> 1) ^ (r >> 3)) & 1) | (((r >> 2) & 1) << 1); }
+__device__ __forceinline__ int w4_lds_off(int r, int c) { return r * 64 + ((c ^ w4_wt_swz(r)) << 4); }
 
 // act: W13 the quantised x [T, K] (rows = tokens), W2 a2 [rows, K] in padded
 // route order, act_bytes its size (< 2^31); act_scale: W13 the token row
@@ -1074,10 +1082,12 @@ __global__ __launch_bounds__(512, 1) void moe_w4_gemm_kernel(
   for (int j = 0; j < 2; ++j) {
     const int ga = wave + 8 * j;  // 8-row activation group
     const int64_t ra = arow(ga * 8 + lane / 8);
-    offA[j] = ra >= 0 ? static_cast<uint32_t>(ra * KS * 128 + ((lane % 8) ^ (lane / 8)) * 16) : kBufferOff;
+    const int slot_a = lane % 8;  // lane writes slot lane % 8 of row 8 * ga + lane / 8
+    offA[j] = ra >= 0 ? static_cast<uint32_t>(ra * KS * 128 + ((slot_a ^ w4_act_swz(ga * 8 + lane / 8)) << 4))
+                      : kBufferOff;
     ldsA[j] = ga * 1024;
     const int rb = ga * 16 + lane / 4;  // 16-row weight group ga
-    srcB[j] = w + (static_cast<int64_t>(e) * N + wrow(rb)) * KS * 64 + (((lane % 4) ^ (lane / 16)) << 4);
+    srcB[j] = w + (static_cast<int64_t>(e) * N + wrow(rb)) * KS * 64 + (((lane % 4) ^ w4_wt_swz(rb)) << 4);
     ldsB[j] = P::kOffB + ga * 1024;
   }
   const int64_t rc = arow(wave * 16 + lane / 4);
@@ -1118,52 +1128,67 @@ __global__ __launch_bounds__(512, 1) void moe_w4_gemm_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int r = wm * WTM + mt * 16 + li;
-      const v4i lo = lds_load<v4i>(st, lds_off(r, 2 * lg));
-      const v4i hi = lds_load<v4i>(st, lds_off(r, 2 * lg + 1));
+      const v4i lo = lds_load<v4i>(st, w4_act_off(r, 2 * lg));
+      const v4i hi = lds_load<v4i>(st, w4_act_off(r, 2 * lg + 1));
       f.x[mt] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) f.w[nt] = lds_load<v4i>(st, P::kOffB + w4_lds_off(wn * WTN + nt * 16 + li, lg));
   };
-  auto read_small = [&](const uint8_t* st, Small& q) {
+  // with_s: also the scale words (EVEN: an odd step reuses its even
+  // predecessor's words, which hold both steps' scales).
+  auto read_small = [&](const uint8_t* st, Small& q, bool with_s) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) q.c[mt] = lds_load<v4f>(st, P::kOffC + (wm * WTM + mt * 16 + li) * 16);
+    if (with_s) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) q.s[nt] = lds_load<v4i>(st, P::kOffS + (wn * WTN + nt * 16 + 4 * lg) * 4);
+      for (int nt = 0; nt < NT; ++nt) q.s[nt] = lds_load<v4i>(st, P::kOffS + (wn * WTN + nt * 16 + 4 * lg) * 4);
+    }
   };
   // MFMAs n-tile by n-tile: the expansion of a weight fragment serves its
-  // four MFMAs; the promotion of MFMA i - 1 runs while MFMA i executes.  PAR:
-  // parity of the K step, which picks each scale word's half.
+  // four MFMAs.  The sequence is software-pipelined in blocks separated by
+  // scheduling barriers, so the compiler cannot regroup it: block i issues
+  // MFMA i, then the promotion of MFMA i - 1 (acc += p * s, whose result is
+  // ready by then) and a quarter of the next fragment's expansion and scale
+  // words -- about as many VALU cycles as the MFMA takes, and no VALU
+  // instruction waits on the MFMA in flight.  PAR: parity of the K step,
+  // which picks each scale word's half.
   auto mma = [&](const Frags& f, const Small& q, auto par_tag) {
     constexpr int PAR = decltype(par_tag)::value;
     if (!wave_live) return;
-    auto scales = [&](int nt) {
-      v4f sc;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t wd = static_cast<uint32_t>(q.s[nt][r]);
-        const bool hi = EVEN ? PAR != 0 : ((r ^ PAR) & 1) != 0;
-        sc[r] = __uint_as_float(hi ? (wd & 0xFFFF0000u) : (wd << 16));
-      }
-      return sc;
+    auto scale = [&](int nt, int r) {
+      const uint32_t wd = static_cast<uint32_t>(q.s[nt][r]);
+      const bool hi = EVEN ? PAR != 0 : ((r ^ PAR) & 1) != 0;
+      return __uint_as_float(hi ? (wd & 0xFFFF0000u) : (wd << 16));
+    };
+    auto expand_word = [&](int nt, int j, v8i& dst) {
+      const uint32_t wd = static_cast<uint32_t>(f.w[nt][j]);
+      dst[2 * j] = static_cast<int>(__builtin_amdgcn_bitop3_b32(wd, 0x88888888u, 0x0F0F0F0Fu, 0x28));
+      dst[2 * j + 1] = static_cast<int>(__builtin_amdgcn_bitop3_b32(wd >> 4, 0x88888888u, 0x0F0F0F0Fu, 0x28));
     };
     constexpr int NI = MT * NT;
     v8i wx[2];
+    v4f sc[2];
     v4f t[2];
 #pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      expand_word(0, j, wx[0]);
+      sc[0][j] = scale(0, j);
+    }
+#pragma unroll
     for (int i = 0; i <= NI; ++i) {
-      if (i < NI) {
-        const int nt = i / MT, mt = i % MT;
-        if (mt == 0) wx[nt & 1] = w4_frag(f.w[nt]);
-        t[i & 1] = mfma_fp8(wx[nt & 1], f.x[mt], q.c[mt]);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
+      const int nt = i / MT, mt = i % MT;
+      if (i < NI) t[i & 1] = mfma_fp8(wx[nt & 1], f.x[mt], q.c[mt]);
+      __builtin_amdgcn_sched_barrier(0);
       if (i > 0) {
-        const int j = i - 1, nt = j / MT, mt = j % MT;
-        fma4v(acc[mt][nt], t[j & 1], scales(nt));
-        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+        const int jp = i - 1;
+        fma4v(acc[jp % MT][jp / MT], t[jp & 1], sc[(jp / MT) & 1]);
       }
+      if (i < NI && nt + 1 < NT) {
+        expand_word(nt + 1, mt, wx[(nt + 1) & 1]);
+        sc[(nt + 1) & 1][mt] = scale(nt + 1, mt);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   using Even = std::integral_constant<int, 0>;
@@ -1179,7 +1204,7 @@ __global__ __launch_bounds__(512, 1) void moe_w4_gemm_kernel(
     issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
     read(smem_dyn + ((kb + 1) % NS) * P::kStage, nxt);
     mma(cur, q, par_tag);
-    read_small(smem_dyn + ((kb + 1) % NS) * P::kStage, q);
+    read_small(smem_dyn + ((kb + 1) % NS) * P::kStage, q, !EVEN || decltype(par_tag)::value == 1);
   };
 #pragma unroll
   for (int st = 0; st < NS; ++st) issue(smem_dyn + st * P::kStage, min(st, KS - 1));
@@ -1188,7 +1213,7 @@ __global__ __launch_bounds__(512, 1) void moe_w4_gemm_kernel(
   Frags f0, f1;
   Small q;
   read(smem_dyn, f0);
-  read_small(smem_dyn, q);
+  read_small(smem_dyn, q, true);
   for (int kb = 0; kb < KS; kb += 2) {
     step(kb, f0, f1, q, Even{});
     if (kb + 1 < KS) step(kb + 1, f1, f0, q, Odd{});
