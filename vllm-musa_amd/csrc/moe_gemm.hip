@@ -285,6 +285,101 @@ moe_gemv_kernel(
     }
   };
 
+  // One route block of int4 weights with vector-loaded scales (the other
+  // forms need more registers than their occupancy leaves): the K loop is
+  // software-pipelined.  Slot u
+  // holds step kb + u's weights, activations and scales; right after its MFMA
+  // the slot is refilled with step kb + U + u, and a group's vector-loaded
+  // scales are copied out and their successors requested before its first
+  // MFMA, so U steps stay in flight instead of draining at every group.
+  // The weights of group kb0 were requested by the caller.
+  auto stream1 = [&](int kbs) {
+    v8i xf[U];
+    float as[U];
+    auto load_act = [&](int kb, int u) {
+      const bool live = aoff[0] != kBufferOff && kb + u < kb1;
+      const uint32_t off = live ? aoff[0] + static_cast<uint32_t>((kb + u) * KB_::kAct) : kBufferOff;
+      xf[u] = buffer_frag<KIND>(ars, off, lg);
+      if constexpr (KIND != kBf16 && !VS)
+        as[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              srs, static_cast<int>(live ? off / 32 : kBufferOff), 0, 0));
+    };
+    auto load_as_vs = [&](int kb) {  // the group's U activation scales
+      const uint32_t off = aoff[0] != kBufferOff ? aoff[0] / 32 + static_cast<uint32_t>(kb * 4) : kBufferOff;
+      return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(srs, static_cast<int>(off), 0, 0));
+    };
+    auto load_w_slot = [&](int kb, int u) {
+      const int k = min(kb + u, kb1 - 1);
+      if constexpr (kRawW4)
+        wraw[u] = ld16(wrow + static_cast<int64_t>(k) * KB_::kW + 16 * lg);
+      else
+        wf[u] = weight_frag<KIND>(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
+      if constexpr (KIND == kFp8 && !VS)
+        sb[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsrs, k * 4, 0, 0));
+      if constexpr (KIND == kW4 && !VS)
+        sw[u] = v4f{bf16_to_f32(wsw[0][k]), bf16_to_f32(wsw[1][k]), bf16_to_f32(wsw[2][k]),
+                    bf16_to_f32(wsw[3][k])};
+    };
+    v4f asn = zero;
+    if constexpr (VS && KIND != kBf16) asn = load_as_vs(kbs);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if constexpr (!VS) as[u] = 0.f;
+      load_act(kbs, u);
+    }
+    for (int kb = kbs; kb < kb1; kb += U) {
+      const bool more = kb + U < kb1;  // uniform
+      // This group's vector-loaded scales, then the next group's requests.
+      float sbc[U];
+      uint2 swc[4];
+#pragma unroll
+      for (int u = 0; u < U; ++u) sbc[u] = sb[u];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) swc[r] = swr[r];
+      if constexpr (VS) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) as[u] = asn[u];
+        if (more) {
+          if constexpr (KIND != kBf16) asn = load_as_vs(kb + U);
+          if constexpr (KIND == kFp8) {
+            const v4f s4 = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(wsrs, (kb + U) * 4, 0, 0));
+#pragma unroll
+            for (int u = 0; u < U; ++u) sb[u] = s4[u];
+          }
+          if constexpr (KIND == kW4) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) swr[r] = *reinterpret_cast<const uint2*>(wsw[r] + kb + U);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if constexpr (KIND == kFp8) {
+          fma4(acc[0], mfma_fp8(wf[u], xf[u], zero), as[u] * (VS ? sbc[u] : sb[u]));
+        } else if constexpr (KIND == kW4) {
+          v4f sc;
+          if constexpr (VS) {
+            const uint32_t lo = u < 2 ? 0 : 1;
+            auto pick = [&](const uint2& v) {
+              const uint32_t w = lo ? v.y : v.x;
+              return __uint_as_float((u & 1) ? (w & 0xFFFF0000u) : (w << 16));
+            };
+            sc = v4f{pick(swc[0]), pick(swc[1]), pick(swc[2]), pick(swc[3])};
+          } else {
+            sc = sw[u];
+          }
+          fma4v(acc[0], mfma_fp8(w4_frag(wraw[u]), xf[u], splat4(as[u])), sc);
+        } else {
+          acc[0] = mfma_bf16x2(wf[u], xf[u], acc[0]);
+        }
+        if (more) {
+          load_w_slot(kb + U, u);
+          load_act(kb + U, u);
+        }
+      }
+    }
+  };
+
   const int seg0 = offsets[e];
   const int nblk = (offsets[e + 1] - seg0) / kGemvBlock;  // >= 1 for an active expert
   int b0 = 0;
@@ -309,10 +404,14 @@ moe_gemv_kernel(
       aoff[b] = valid ? static_cast<uint32_t>((r / act_div) * arowb) : kBufferOff;
       acc[b] = zero;
     }
-    group(kb0, nb);
-    for (int kb = kb0 + U; kb < kb1; kb += U) {
-      load_w(kb);
-      group(kb, nb);
+    if constexpr (MAXB == 1 && KIND == kW4 && VS) {
+      stream1(kb0);
+    } else {
+      group(kb0, nb);
+      for (int kb = kb0 + U; kb < kb1; kb += U) {
+        load_w(kb);
+        group(kb, nb);
+      }
     }
 #pragma unroll
     for (int b = 0; b < MAXB; ++b) {
