@@ -95,9 +95,11 @@ constexpr int kMoeGemvWaves = 4;
 constexpr int kGemvBlock = 16;  // routes per block (one MFMA column tile)
 // K steps each wave keeps in flight (8 KiB of weights per wave; 4 and 8
 // measured alike, 4 needs fewer registers), and the number of waves the
-// split-K factor aims to launch (16 per CU).
+// split-K factor aims to launch (12 per CU: the single-block fp8 GEMV runs
+// three waves per SIMD; 3072 measured 1-3 % faster than 4096 on the
+// DeepSeek-V3 layer at T = 1, 4, 16).
 constexpr int kGemvU = 4;
-constexpr int kGemvTargetWaves = 4096;
+constexpr int kGemvTargetWaves = 3072;
 
 // Raw buffer loads (gfx9 descriptor: base, no stride, num_records bytes):
 // a lane whose byte offset is past num_records reads zeros and fetches
@@ -134,8 +136,8 @@ __device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t o
 // leave HBM idle.  The route ids are read with uniform (scalar) loads, which
 // are counted apart from the vector loads, so waiting for them does not wait
 // for the weights.  Columns of padding routes fetch no activation bytes.
-// Four waves per SIMD hold the whole T = 1 grid of a DeepSeek-V3-sized layer
-// at once; the int4 variant fits three and the 4-block variant two.
+// The single-block fp8 and int4 forms run three waves per SIMD (bf16 four,
+// the 4-block variant two).
 //
 // VS (K/128 a multiple of U and aligned scale rows): kFp8 reads the U block
 // scales of a group, and each route's U activation scales, with one 16-byte
@@ -144,8 +146,14 @@ __device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t o
 // route's U corrections with one 16-byte load.  Splits
 // start on group boundaries, so with VS every group lies entirely inside its
 // split.
+// The software-pipelined single-block form (stream1) of kFp8 and of kW4 with
+// vector scales keeps a group's loads in flight while the previous group
+// computes; it fits three waves per SIMD.
+template <int MAXB, int KIND, bool VS>
+constexpr bool gemv_stream1() { return MAXB == 1 && (KIND == kFp8 || (KIND == kW4 && VS)); }
+
 template <int MAXB, int KIND, bool VS = false>
-__global__ __launch_bounds__(kMoeGemvWaves * kWave, MAXB == 1 ? (KIND == kW4 ? 3 : 4) : 2) void
+__global__ __launch_bounds__(kMoeGemvWaves * kWave, MAXB == 1 ? (KIND == kBf16 ? 4 : 3) : 2) void
 moe_gemv_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_div,
     int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
@@ -154,6 +162,7 @@ moe_gemv_kernel(
     float* __restrict__ partial, const float* __restrict__ route_w, uint16_t* __restrict__ y) {
   using KB_ = KindBytes<KIND>;
   constexpr int U = kGemvU;
+  constexpr bool kStream1 = gemv_stream1<MAXB, KIND, VS>();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const int li = lane % 16, lg = lane / 16;
   const int ntile = blockIdx.x * kMoeGemvWaves + wave;
@@ -285,8 +294,8 @@ moe_gemv_kernel(
     }
   };
 
-  // One route block of int4 weights with vector-loaded scales (the other
-  // forms need more registers than their occupancy leaves): the K loop is
+  // One route block (fp8, or int4 with vector-loaded scales; the other forms
+  // need more registers than their occupancy leaves): the K loop is
   // software-pipelined.  Slot u
   // holds step kb + u's weights, activations and scales; right after its MFMA
   // the slot is refilled with step kb + U + u, and a group's vector-loaded
@@ -404,7 +413,7 @@ moe_gemv_kernel(
       aoff[b] = valid ? static_cast<uint32_t>((r / act_div) * arowb) : kBufferOff;
       acc[b] = zero;
     }
-    if constexpr (MAXB == 1 && KIND == kW4 && VS) {
+    if constexpr (kStream1) {
       stream1(kb0);
     } else {
       group(kb0, nb);
