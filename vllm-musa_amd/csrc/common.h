@@ -168,32 +168,48 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Merge (v, idx) with a partner's under the order (value desc, index asc).
-__device__ __forceinline__ void argmax_merge(float& v, int& idx, float ov, int oi) {
-  if (ov > v || (ov == v && oi < idx)) {
-    v = ov;
-    idx = oi;
-  }
+// (value, index) as one unsigned key under the order (value desc, index
+// asc): the high word is the float's bits made monotonic as an unsigned
+// integer (-0 taken as +0, NaN below every number), the low word the inverted
+// index (0 <= index < 2^31).  Key 0 lies below every entry.
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+  const uint32_t b = __float_as_uint(v + 0.0f);
+  uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  if (v != v) o = 1u;
+  return (static_cast<uint64_t>(o) << 32) | static_cast<uint32_t>(~idx);
+}
+__device__ __forceinline__ float argmax_key_value(uint64_t k) {
+  const uint32_t o = static_cast<uint32_t>(k >> 32);
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+__device__ __forceinline__ int argmax_key_index(uint64_t k) { return static_cast<int>(~static_cast<uint32_t>(k)); }
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+constexpr int kDppBcast15 = 0x142;  // lane 15 of each row to the next row
+constexpr int kDppBcast31 = 0x143;  // lane 31 to rows 2 and 3
+// DPP move of a 64-bit value; rows outside ROWS keep their own value.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const int lo = static_cast<int>(static_cast<uint32_t>(v)), hi = static_cast<int>(v >> 32);
+  const uint32_t l = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWS, 0xF, false));
+  const uint32_t h = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWS, 0xF, false));
+  return (static_cast<uint64_t>(h) << 32) | l;
 }
 
-// Argmax over the wave with ties broken towards the lower index; every lane
-// ends with the result (every lane of the wave must be active).  The merge is
-// a maximum under a total order, so any pairing that joins disjoint lane sets
-// works: quad swaps and the 8- and 16-lane mirrors run as DPP moves inside
-// each 16-lane row, then the four rows' results are read with v_readlane and
-// merged as wave-uniform values.
-__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
-  argmax_merge(v, idx, dpp_f<kDppXor1>(v), dpp_i<kDppXor1>(idx));
-  argmax_merge(v, idx, dpp_f<kDppXor2>(v), dpp_i<kDppXor2>(idx));
-  argmax_merge(v, idx, dpp_f<kDppHalfMirror>(v), dpp_i<kDppHalfMirror>(idx));
-  argmax_merge(v, idx, dpp_f<kDppMirror>(v), dpp_i<kDppMirror>(idx));
-  float v0 = lane_value(v, 0), v1 = lane_value(v, 16), v2 = lane_value(v, 32), v3 = lane_value(v, 48);
-  int i0 = lane_value(idx, 0), i1 = lane_value(idx, 16), i2 = lane_value(idx, 32), i3 = lane_value(idx, 48);
-  argmax_merge(v0, i0, v1, i1);
-  argmax_merge(v2, i2, v3, i3);
-  argmax_merge(v0, i0, v2, i2);
-  v = v0;
-  idx = i0;
+// Maximum key over the wave, in every lane (every lane must be active):
+// quad swaps and the 8- and 16-lane mirrors leave each 16-lane row's maximum
+// in all its lanes, the row broadcasts carry rows 0-2 into row 3, and lane
+// 63 is read out.  Branch-free: one 64-bit compare and two selects a level.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+  k = max_u64(k, dpp_u64<kDppXor1>(k));
+  k = max_u64(k, dpp_u64<kDppXor2>(k));
+  k = max_u64(k, dpp_u64<kDppHalfMirror>(k));
+  k = max_u64(k, dpp_u64<kDppMirror>(k));
+  k = max_u64(k, dpp_u64<kDppBcast15, 0xA>(k));
+  k = max_u64(k, dpp_u64<kDppBcast31, 0xC>(k));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(k)), 63));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(k >> 32), 63));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
 // Top-2 (t1 >= t2) of the union of two disjoint value sets.

@@ -28,24 +28,24 @@ __device__ __forceinline__ float sigmoid_cr(float x) {
 }
 
 // One selection round over the live entries of a wave: returns the winning
-// (value, expert id) to every lane and retires the winner in its owner lane.
+// (value, expert id) to every lane and retires the winner in its owner lane
+// (id 0x7fffffff and -inf when no entry is live).  Ties go to the lower id:
+// each entry is one 64-bit key (argmax_key) and the round is a wave maximum.
 template <int VPT>
 __device__ __forceinline__ int select_round(const float (&v)[VPT], uint32_t& alive, float& best) {
   const int lane = lane_id();
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
+  uint64_t k = 0;
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const bool live = (alive >> i) & 1u;
-    // Lower slot index means lower expert id, so strict '>' keeps ties low.
-    if (live && (v[i] > bv || bi == 0x7fffffff)) {
-      bv = v[i];
-      bi = lane + kWave * i;
-    }
+  for (int i = 0; i < VPT; ++i)
+    if ((alive >> i) & 1u) k = max_u64(k, argmax_key(v[i], lane + kWave * i));
+  k = wave_max_key(k);
+  if (k == 0) {
+    best = -INFINITY;
+    return 0x7fffffff;
   }
-  wave_argmax(bv, bi);
-  if (bi != 0x7fffffff && (bi % kWave) == lane) alive &= ~(1u << (bi / kWave));
-  best = bv;
+  const int bi = argmax_key_index(k);
+  if ((bi % kWave) == lane) alive &= ~(1u << (bi / kWave));
+  best = argmax_key_value(k);
   return bi;
 }
 
