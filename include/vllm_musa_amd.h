@@ -96,19 +96,22 @@ int vmamd_per_token_quant_fp8(const void* x, int64_t rows, int64_t cols, int64_t
  * of l' in descending order, ties to the lower expert id; weights =
  * softmax(l')[ids], renormalised over the selection when renormalize != 0.
  * gating: [tokens, experts] f32/f16/bf16; weights f32 and ids i32 [tokens, topk].
- * experts <= 1024.  Replaces topk_softmax
+ * experts <= 1024.  token_expert_indices (NULL: not written): i32 [tokens,
+ * topk] with [t, k] = k * tokens + t, the third output of upstream fused_topk
+ * that its topk_softmax op writes in the same kernel.  Replaces topk_softmax
  * (vllm_musa/jit_kernel/csrc/topk.py:211-242; kernels
  * jit_kernel/csrc/topk/topk_gating.mu:63-147, 458-529, 612-702). */
 int vmamd_topk_softmax(const void* gating, int dtype, int64_t tokens, int experts, int topk,
                        int renormalize, float softcap, const float* bias, float* topk_weights,
-                       int32_t* topk_ids, vmamd_stream_t stream);
+                       int32_t* topk_ids, int32_t* token_expert_indices, vmamd_stream_t stream);
 
 /* Sigmoid top-k.  s = sigmoid(gating); ids = top-k of s (+ bias), ties to the
- * lower id; weights = s[ids], renormalised when renormalize != 0.  Replaces
- * topk_sigmoid (vllm_musa/jit_kernel/csrc/topk.py:245-275). */
+ * lower id; weights = s[ids], renormalised when renormalize != 0;
+ * token_expert_indices as vmamd_topk_softmax.  Replaces topk_sigmoid
+ * (vllm_musa/jit_kernel/csrc/topk.py:245-275). */
 int vmamd_topk_sigmoid(const void* gating, int dtype, int64_t tokens, int experts, int topk,
                        int renormalize, const float* bias, float* topk_weights,
-                       int32_t* topk_ids, vmamd_stream_t stream);
+                       int32_t* topk_ids, int32_t* token_expert_indices, vmamd_stream_t stream);
 
 /* Folded shared expert: out = [topk_weights | w_s], [topk_ids | shared_expert_id]
  * ([tokens, topk + 1]) with w_s = sigmoid(shared_logits[t]) computed in fp32

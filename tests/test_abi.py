@@ -40,7 +40,7 @@ def test_abi_version():
 def test_argument_errors_are_reported_without_a_gpu():
     from vllm_musa_amd import _lib
     with pytest.raises(ValueError, match="experts must be in"):
-        _lib.call("vmamd_topk_softmax", None, 2, 4, 0, 1, 0, 0.0, None, None, None, None)
+        _lib.call("vmamd_topk_softmax", None, 2, 4, 0, 1, 0, 0.0, None, None, None, None, None)
     with pytest.raises(ValueError, match="group_size must be 128"):
         _lib.call("vmamd_per_token_group_quant_fp8", None, 2, 1, 128, 128, 64, 1e-10, -448.0,
                   448.0, None, None, 1, 1, None)

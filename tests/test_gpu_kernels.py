@@ -110,10 +110,14 @@ def test_topk_softmax(T, E, K, renorm):
     logits = g.standard_normal((T, E)).astype(np.float32)
     logits[:, :4] = np.round(logits[:, :4])  # exact ties
     lt = torch.from_numpy(logits).to(DEV)
-    w, ids, _ = fused_topk(lt, lt, K, renorm)
+    w, ids, tei = fused_topk(lt, lt, K, renorm)
     w_ref, ids_ref = oroute.topk_softmax(logits, K, renorm)
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
     np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=1e-5, atol=1e-7)
+    # upstream fused_topk's third output: [t, k] = k * T + t
+    np.testing.assert_array_equal(tei.cpu().numpy(), np.arange(K)[None, :] * T + np.arange(T)[:, None])
+    _, _, tei_s = fused_topk(lt, lt, K, renorm, scoring_func="sigmoid")
+    np.testing.assert_array_equal(tei_s.cpu().numpy(), tei.cpu().numpy())
 
 
 def test_topk_softmax_bias_bf16():

@@ -136,8 +136,7 @@ __device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t o
 // leave HBM idle.  The route ids are read with uniform (scalar) loads, which
 // are counted apart from the vector loads, so waiting for them does not wait
 // for the weights.  Columns of padding routes fetch no activation bytes.
-// The single-block fp8 and int4 forms run three waves per SIMD (bf16 four,
-// the 4-block variant two).
+// The single-block forms run three waves per SIMD (the 4-block variant two).
 //
 // VS (K/128 a multiple of U and aligned scale rows): kFp8 reads the U block
 // scales of a group, and each route's U activation scales, with one 16-byte
@@ -146,14 +145,14 @@ __device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t o
 // route's U corrections with one 16-byte load.  Splits
 // start on group boundaries, so with VS every group lies entirely inside its
 // split.
-// The software-pipelined single-block form (stream1) of kFp8 and of kW4 with
-// vector scales keeps a group's loads in flight while the previous group
-// computes; it fits three waves per SIMD.
+// The software-pipelined single-block form (stream1; kW4 only with vector
+// scales) keeps a group's loads in flight while the previous group computes;
+// it fits three waves per SIMD.
 template <int MAXB, int KIND, bool VS>
-constexpr bool gemv_stream1() { return MAXB == 1 && (KIND == kFp8 || (KIND == kW4 && VS)); }
+constexpr bool gemv_stream1() { return MAXB == 1 && (KIND != kW4 || VS); }
 
 template <int MAXB, int KIND, bool VS = false>
-__global__ __launch_bounds__(kMoeGemvWaves * kWave, MAXB == 1 ? (KIND == kBf16 ? 4 : 3) : 2) void
+__global__ __launch_bounds__(kMoeGemvWaves * kWave, MAXB == 1 ? 3 : 2) void
 moe_gemv_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_div,
     int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
@@ -294,8 +293,8 @@ moe_gemv_kernel(
     }
   };
 
-  // One route block (fp8, or int4 with vector-loaded scales; the other forms
-  // need more registers than their occupancy leaves): the K loop is
+  // One route block (int4 only with vector-loaded scales: the other int4
+  // form needs more registers than its occupancy leaves): the K loop is
   // software-pipelined.  Slot u
   // holds step kb + u's weights, activations and scales; right after its MFMA
   // the slot is refilled with step kb + U + u, and a group's vector-loaded

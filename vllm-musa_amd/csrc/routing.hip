@@ -53,10 +53,13 @@ __device__ __forceinline__ int select_round(const float (&v)[VPT], uint32_t& ali
 // the token's shared gate logit computed in fp32 and rounded to the logit
 // dtype, id = the shared expert's id (topk_gating.mu:369-456 writes it in the
 // same kernel as the routed top-k).  logits == nullptr: no shared column.
+// tei (when not null, no shared column): token_expert_indices [tokens, topk],
+// tei[t, k] = k * tokens + t, upstream fused_topk's third output.
 struct SharedCol {
   const void* logits;
   int dtype;
   int32_t id;
+  int32_t* tei;
 };
 
 template <int DT>
@@ -76,7 +79,8 @@ __device__ __forceinline__ float shared_weight_rt(const SharedCol& sh, int64_t t
 // Output row r holds the routed top-k in columns [0, topk) and, with a shared
 // column, that expert in column topk (row stride topk + 1).
 __device__ __forceinline__ void write_shared(const SharedCol& sh, int lane, int topk, int64_t row,
-                                             float* w_out, int32_t* id_out) {
+                                             int64_t tokens, float* w_out, int32_t* id_out) {
+  if (sh.tei && lane < topk) sh.tei[row * topk + lane] = static_cast<int32_t>(lane * tokens + row);
   if (sh.logits && lane == topk) {
     w_out[row * (topk + 1) + topk] = shared_weight_rt(sh, row);
     id_out[row * (topk + 1) + topk] = sh.id;
@@ -135,7 +139,7 @@ __global__ __launch_bounds__(kRouteWaves * kWave) void topk_softmax_kernel(
     w_out[row * ostride + lane] = my_w / denom;
     id_out[row * ostride + lane] = my_id;
   }
-  write_shared(sh, lane, topk, row, w_out, id_out);
+  write_shared(sh, lane, topk, row, tokens, w_out, id_out);
 }
 
 // ------------------------------------------------------- sigmoid top-k ----
@@ -183,7 +187,7 @@ __global__ __launch_bounds__(kRouteWaves * kWave) void topk_sigmoid_kernel(
     w_out[row * ostride + lane] = renorm ? my_w / sum : my_w;
     id_out[row * ostride + lane] = my_id;
   }
-  write_shared(sh, lane, topk, row, w_out, id_out);
+  write_shared(sh, lane, topk, row, tokens, w_out, id_out);
 }
 
 // ------------------------------------------------------- grouped top-k ----
@@ -436,7 +440,8 @@ extern "C" int vmamd_extend_topk_with_shared(const float* topk_weights, const in
 
 extern "C" int vmamd_topk_softmax(const void* gating, int dtype, int64_t tokens, int experts,
                                   int topk, int renormalize, float softcap, const float* bias,
-                                  float* topk_weights, int32_t* topk_ids, vmamd_stream_t stream) {
+                                  float* topk_weights, int32_t* topk_ids,
+                                  int32_t* token_expert_indices, vmamd_stream_t stream) {
   VMAMD_REQUIRE(experts > 0 && experts <= 1024, "topk_softmax: experts must be in [1, 1024] (got %d)",
                 experts);
   VMAMD_REQUIRE(topk > 0 && topk <= experts && topk <= 64,
@@ -444,8 +449,9 @@ extern "C" int vmamd_topk_softmax(const void* gating, int dtype, int64_t tokens,
   VMAMD_REQUIRE(tokens >= 0, "topk_softmax: negative token count");
   if (tokens == 0) return VMAMD_OK;
   VMAMD_REQUIRE(gating && topk_weights && topk_ids, "topk_softmax: null pointer");
+  VMAMD_REQUIRE(tokens * topk < (1ll << 31), "topk_softmax: too many routes");
   VMAMD_ROUTE_DISPATCH(topk_softmax_kernel, gating, tokens, experts, topk, renormalize != 0, softcap,
-                       bias, topk_weights, topk_ids, SharedCol{nullptr, 0, 0});
+                       bias, topk_weights, topk_ids, SharedCol{nullptr, 0, 0, token_expert_indices});
   return check_launch("topk_softmax");
 }
 
@@ -467,13 +473,14 @@ extern "C" int vmamd_topk_softmax_shared(const void* gating, int dtype, int64_t 
                 "topk_softmax_shared: null pointer");
   VMAMD_ROUTE_DISPATCH(topk_softmax_kernel, gating, tokens, experts, topk, renormalize != 0, softcap,
                        bias, topk_weights, topk_ids,
-                       SharedCol{shared_logits, shared_dtype, shared_expert_id});
+                       SharedCol{shared_logits, shared_dtype, shared_expert_id, nullptr});
   return check_launch("topk_softmax_shared");
 }
 
 extern "C" int vmamd_topk_sigmoid(const void* gating, int dtype, int64_t tokens, int experts,
                                   int topk, int renormalize, const float* bias, float* topk_weights,
-                                  int32_t* topk_ids, vmamd_stream_t stream) {
+                                  int32_t* topk_ids, int32_t* token_expert_indices,
+                                  vmamd_stream_t stream) {
   VMAMD_REQUIRE(experts > 0 && experts <= 1024, "topk_sigmoid: experts must be in [1, 1024] (got %d)",
                 experts);
   VMAMD_REQUIRE(topk > 0 && topk <= experts && topk <= 64,
@@ -481,8 +488,9 @@ extern "C" int vmamd_topk_sigmoid(const void* gating, int dtype, int64_t tokens,
   VMAMD_REQUIRE(tokens >= 0, "topk_sigmoid: negative token count");
   if (tokens == 0) return VMAMD_OK;
   VMAMD_REQUIRE(gating && topk_weights && topk_ids, "topk_sigmoid: null pointer");
+  VMAMD_REQUIRE(tokens * topk < (1ll << 31), "topk_sigmoid: too many routes");
   VMAMD_ROUTE_DISPATCH(topk_sigmoid_kernel, gating, tokens, experts, topk, renormalize != 0, bias,
-                       topk_weights, topk_ids, SharedCol{nullptr, 0, 0});
+                       topk_weights, topk_ids, SharedCol{nullptr, 0, 0, token_expert_indices});
   return check_launch("topk_sigmoid");
 }
 
@@ -503,7 +511,7 @@ extern "C" int vmamd_topk_sigmoid_shared(const void* gating, int dtype, int64_t 
                 "topk_sigmoid_shared: null pointer");
   VMAMD_ROUTE_DISPATCH(topk_sigmoid_kernel, gating, tokens, experts, topk, renormalize != 0, bias,
                        topk_weights, topk_ids,
-                       SharedCol{shared_logits, shared_dtype, shared_expert_id});
+                       SharedCol{shared_logits, shared_dtype, shared_expert_id, nullptr});
   return check_launch("topk_sigmoid_shared");
 }
 

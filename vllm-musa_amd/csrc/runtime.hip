@@ -28,4 +28,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* vmamd_last_error(void) { return vmamd::g_last_error; }
 
-extern "C" int vmamd_abi_version(void) { return 2; }
+extern "C" int vmamd_abi_version(void) { return 3; }

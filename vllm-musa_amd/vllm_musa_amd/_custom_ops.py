@@ -161,16 +161,25 @@ def _shared_columns(topk_weights, shared_expert_gate_output, num_fused_shared_ex
     return topk_weights.shape[1] - 1, True
 
 
+def _check_tei(tei: torch.Tensor | None, topk_ids: torch.Tensor) -> None:
+    if tei is not None and (tei.shape != topk_ids.shape or tei.dtype != torch.int32
+                            or not tei.is_contiguous() or tei.device != topk_ids.device):
+        raise ValueError("token_expert_indices must be a contiguous int32 tensor shaped like topk_ids")
+
+
 def topk_softmax(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_output: torch.Tensor,
                  renormalize: bool = False, moe_softcapping: float = 0.0,
                  correction_bias: torch.Tensor | None = None,
                  shared_expert_gate_output: torch.Tensor | None = None,
-                 num_fused_shared_experts: int = 0) -> None:
+                 num_fused_shared_experts: int = 0,
+                 token_expert_indices: torch.Tensor | None = None) -> None:
     """Reference: topk_softmax (vllm_musa/jit_kernel/csrc/topk.py:211-242).  With a
     shared gate output and one fused shared expert, the last of the
     topk_weights.shape[1] columns is that expert (id = number of routed experts,
     weight = sigmoid of its gate, outside the renormalisation), as the fused-shared
-    kernel writes it (csrc/topk/topk_gating.mu:369-456)."""
+    kernel writes it (csrc/topk/topk_gating.mu:369-456).  token_expert_indices
+    (routed columns only) receives [t, k] = k * T + t from the same kernel, as
+    upstream fused_topk's op fills it."""
     _check_routing_out(topk_weights, topk_ids, gating_output)
     if correction_bias is not None:
         check_cuda(correction_bias)
@@ -178,6 +187,9 @@ def topk_softmax(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_outp
             raise ValueError("correction_bias must be float32 [num_experts]")
     t, e = gating_output.shape
     k, shared = _shared_columns(topk_weights, shared_expert_gate_output, num_fused_shared_experts)
+    if token_expert_indices is not None and shared:
+        raise NotImplementedError("token_expert_indices with a fused shared expert")
+    _check_tei(token_expert_indices, topk_ids)
     if shared:
         logits = _shared_logits(shared_expert_gate_output, t)
         call("vmamd_topk_softmax_shared", ptr(gating_output), dtype_code(gating_output.dtype), t,
@@ -187,15 +199,17 @@ def topk_softmax(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_outp
         return
     call("vmamd_topk_softmax", ptr(gating_output), dtype_code(gating_output.dtype), t, e,
          k, int(bool(renormalize)), float(moe_softcapping),
-         ptr(correction_bias), ptr(topk_weights), ptr(topk_ids), stream_of(gating_output))
+         ptr(correction_bias), ptr(topk_weights), ptr(topk_ids), ptr(token_expert_indices),
+         stream_of(gating_output))
 
 
 def topk_sigmoid(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_output: torch.Tensor,
                  renormalize: bool = False, correction_bias: torch.Tensor | None = None,
                  shared_expert_gate_output: torch.Tensor | None = None,
-                 num_fused_shared_experts: int = 0) -> None:
+                 num_fused_shared_experts: int = 0,
+                 token_expert_indices: torch.Tensor | None = None) -> None:
     """Reference: topk_sigmoid (vllm_musa/jit_kernel/csrc/topk.py:245-275); the fused
-    shared expert as for topk_softmax."""
+    shared expert and token_expert_indices as for topk_softmax."""
     _check_routing_out(topk_weights, topk_ids, gating_output)
     if correction_bias is not None:
         check_cuda(correction_bias)
@@ -203,6 +217,9 @@ def topk_sigmoid(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_outp
             raise ValueError("correction_bias must be float32 [num_experts]")
     t, e = gating_output.shape
     k, shared = _shared_columns(topk_weights, shared_expert_gate_output, num_fused_shared_experts)
+    if token_expert_indices is not None and shared:
+        raise NotImplementedError("token_expert_indices with a fused shared expert")
+    _check_tei(token_expert_indices, topk_ids)
     if shared:
         logits = _shared_logits(shared_expert_gate_output, t)
         call("vmamd_topk_sigmoid_shared", ptr(gating_output), dtype_code(gating_output.dtype), t,
@@ -212,7 +229,7 @@ def topk_sigmoid(topk_weights: torch.Tensor, topk_ids: torch.Tensor, gating_outp
         return
     call("vmamd_topk_sigmoid", ptr(gating_output), dtype_code(gating_output.dtype), t, e, k,
          int(bool(renormalize)), ptr(correction_bias), ptr(topk_weights), ptr(topk_ids),
-         stream_of(gating_output))
+         ptr(token_expert_indices), stream_of(gating_output))
 
 
 def grouped_topk_into(topk_weights: torch.Tensor, topk_ids: torch.Tensor,

@@ -42,8 +42,8 @@ SIGNATURES: dict[str, list] = {
     "vmamd_topk_softmax_shared": [_p, _i32, _i64, _i32, _i32, _i32, _f32, _p, _p, _i32, _i32, _p, _p,
                                   _p],
     "vmamd_topk_sigmoid_shared": [_p, _i32, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _p, _p, _p],
-    "vmamd_topk_softmax": [_p, _i32, _i64, _i32, _i32, _i32, _f32, _p, _p, _p, _p],
-    "vmamd_topk_sigmoid": [_p, _i32, _i64, _i32, _i32, _i32, _p, _p, _p, _p],
+    "vmamd_topk_softmax": [_p, _i32, _i64, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p],
+    "vmamd_topk_sigmoid": [_p, _i32, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p],
     "vmamd_grouped_topk": [_p, _i32, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _p,
                            _p],
     "vmamd_moe_align_block_size": [_p, _i64, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _p, _p, _p,

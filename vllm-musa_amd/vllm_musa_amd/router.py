@@ -35,15 +35,16 @@ def fused_topk(hidden_states: torch.Tensor, gating_output: torch.Tensor, topk: i
     dev = gating_output.device
     w = torch.empty(t, topk, dtype=torch.float32, device=dev)
     ids = torch.empty(t, topk, dtype=torch.int32, device=dev)
+    token_expert_indices = torch.empty(t, topk, dtype=torch.int32, device=dev)
     g = gating_output.contiguous()
     if scoring_func == "softmax":
-        ops.topk_softmax(w, ids, g, renormalize, correction_bias=correction_bias)
+        ops.topk_softmax(w, ids, g, renormalize, correction_bias=correction_bias,
+                         token_expert_indices=token_expert_indices)
     elif scoring_func == "sigmoid":
-        ops.topk_sigmoid(w, ids, g, renormalize, correction_bias=correction_bias)
+        ops.topk_sigmoid(w, ids, g, renormalize, correction_bias=correction_bias,
+                         token_expert_indices=token_expert_indices)
     else:
         raise ValueError(f"Unsupported scoring function: {scoring_func}")
-    token_expert_indices = (torch.arange(topk, device=dev, dtype=torch.int32)[None, :] * t +
-                            torch.arange(t, device=dev, dtype=torch.int32)[:, None])
     if indices_type is not None and indices_type != torch.int32:
         ids = ids.to(indices_type)
     return w, ids, token_expert_indices
