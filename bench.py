@@ -30,7 +30,7 @@ us / TFLOP/s / GB/s and the fraction of min(peak compute, AI x 8 TB/s):
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-sweep] [--no-cpu]
   python bench.py --traffic-probe   # the launches profiled for FETCH_SIZE / WRITE_SIZE
   python bench.py --dense           # dense block-fp8 linear shapes, M = 1 .. 4096 (JSON lines)
-  python bench.py --w4              # w4afp8 MoE layer, T = 1 .. 1024 (JSON lines)
+  python bench.py --w4              # w4afp8 MoE layer, T = 1, 32, 512, 4096 (JSON lines)
   python bench.py --swiglu          # clamped SwiGLU + block-fp8 down projection (JSON lines)
   python bench.py --fold            # shared expert folded into the MoE vs run as dense GEMMs
 """
@@ -344,31 +344,12 @@ W4_E, W4_H, W4_I = 128, 4096, 1536
 
 
 def w4_sweep(torch, iters: int, log) -> int:
-    """HIP-event medians of routing + w4afp8_moe (caches flushed by a 1 GiB read
-    before each call); bytes = touched experts' int4 weights and bf16 scales +
-    activations + output."""
-    from vllm_musa_amd import fused_topk, synthetic, w4afp8_moe
-    w13, w2, s13, s2 = synthetic.moe_w4a8_weights(W4_E, W4_H, W4_I, 12)
+    """The w4afp8 layer at T = 1, 32, 512, 4096 (w4_configs: routing +
+    w4afp8_moe, HIP-event medians with caches flushed, graph replay), one JSON
+    line per T."""
     flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
-    per_expert = 3 * W4_I * W4_H // 2 + 2 * 3 * W4_I * (W4_H // 128)
-    for t in (1, 16, 256, 1024):
-        x = synthetic.activations(t, W4_H, 100 + t)
-        logits = synthetic.router_logits(t, W4_E, 200 + t)
-        def f():
-            w, ids, _ = fused_topk(x, logits, TOPK, True)
-            return w4afp8_moe(x, w13, w2, s13, s2, w, ids)
-        for _ in range(3):
-            f()
-        torch.cuda.synchronize()
-        _, ids, _ = fused_topk(x, logits, TOPK, True)
-        used = int(torch.unique(ids).numel())
-        us = statistics.median(time_events(torch, f, iters, lambda: flush_buf.max())) * 1e3
-        by = used * per_expert + 2 * t * W4_H * 2
-        fl = 2.0 * t * TOPK * 3 * W4_H * W4_I
-        print(json.dumps({"T": t, "experts_touched": used, "us": round(us, 1),
-                          "frac_hbm": round(by / (us * 1e-6) / (PEAK_HBM_GBS * 1e9), 3),
-                          "tflops": round(fl / (us * 1e-6) / 1e12, 2)}), flush=True)
-    log("bench: w4afp8 sweep done")
+    for row in w4_configs(torch, iters, lambda: flush_buf.max(), log):
+        print(json.dumps(row), flush=True)
     return 0
 
 
@@ -578,7 +559,7 @@ def main() -> int:
                          "linear shapes (one JSON line per shape)")
     ap.add_argument("--w4", action="store_true",
                     help="only time the w4afp8 MoE layer (E=128, top-8, H=4096, I=1536) at "
-                         "T = 1, 16, 256, 1024 (one JSON line per T)")
+                         "T = 1, 32, 512, 4096 (one JSON line per T)")
     ap.add_argument("--swiglu", action="store_true",
                     help="only time the clamp-aware SwiGLU + block-fp8 down projection at the "
                          "DeepSeek-V3 dense-MLP and shared-expert shapes (one JSON line per shape)")
