@@ -1488,23 +1488,27 @@ static int gemv_act_bytes(int64_t rows, int64_t K) {
   return static_cast<int>(rows * (K / KindBytes<KIND>::kElems) * KindBytes<KIND>::kAct);
 }
 
-// Decode GEMV launch: an expert holds at most T routes when each token's
-// top-k ids are distinct, so T <= 16 needs one 16-route block per pass
-// (MAXB = 1, fewer registers); more blocks are still handled, by re-streaming
-// the expert's weights once per block.
+// Decode GEMV launch.  one_block: the single-block form (MAXB = 1: fewer
+// registers, the pipelined K loop), which still handles an expert with more
+// than 16 routes by re-streaming its weights once per block; chosen while
+// experts average at most 8 routes (gemv_one_block), where it measured as
+// fast or faster than the 4-block form (w4afp8 E=128 at T=32: 366 -> 285 us,
+// T=64: 422 -> 338 us; bf16 E=128 T=128 and fp8 E=256 T=64 1-3 % faster).
 // vs: the kFp8 scale layout allows one 16-byte load per group of scales.
+static bool gemv_one_block(int64_t numel, int E) { return numel <= 8 * static_cast<int64_t>(E); }
+
 template <int KIND, typename... Args>
-static void launch_gemv(dim3 grid, hipStream_t st, int T, bool vs, Args... args) {
+static void launch_gemv(dim3 grid, hipStream_t st, bool one_block, bool vs, Args... args) {
   if constexpr (KIND != kBf16) {
     if (vs) {
-      if (T <= kGemvBlock)
+      if (one_block)
         moe_gemv_kernel<1, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
       else
         moe_gemv_kernel<4, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
       return;
     }
   }
-  if (T <= kGemvBlock)
+  if (one_block)
     moe_gemv_kernel<1, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
   else
     moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
@@ -1543,7 +1547,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
     const int s13 = w13_splits(numel, E, H, I, KIND);
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s13);
-    launch_gemv<KIND>(g13, st, T, gemv_vector_scales<KIND>(H, act_s, w13_s), xa, gemv_act_bytes<KIND>(T, H),
+    launch_gemv<KIND>(g13, st, gemv_one_block(numel, E), gemv_vector_scales<KIND>(H, act_s, w13_s), xa, gemv_act_bytes<KIND>(T, H),
                       act_s, topk, H, sorted, offs, active,
                       nact, w13, w13_s, 2 * I, numel, s13, scratch,
                       static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr));
@@ -1610,7 +1614,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g2((H / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s2);
     if (s2 > 1 && combined_out && combined && H % 8 == 0) {
-      launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, act_s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), act_s, 1, I, sorted, offs, active,
+      launch_gemv<KIND>(g2, st, gemv_one_block(numel, E), gemv_vector_scales<KIND>(I, act_s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), act_s, 1, I, sorted, offs, active,
                         nact, w2, w2_s, H, numel, s2, scratch, static_cast<const float*>(nullptr),
                         static_cast<uint16_t*>(nullptr));
       int rc = check_launch("moe w2 (gemv)");
@@ -1625,11 +1629,11 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
       return check_launch("moe w2 (combine)");
     }
     if (s2 == 1) {
-      launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, act_s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), act_s, 1, I, sorted, offs,
+      launch_gemv<KIND>(g2, st, gemv_one_block(numel, E), gemv_vector_scales<KIND>(I, act_s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), act_s, 1, I, sorted, offs,
                         active, nact, w2, w2_s, H, numel, 1, static_cast<float*>(nullptr), yscale, y);
       return check_launch("moe w2 (gemv)");
     }
-    launch_gemv<KIND>(g2, st, T, gemv_vector_scales<KIND>(I, act_s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), act_s, 1, I, sorted, offs, active,
+    launch_gemv<KIND>(g2, st, gemv_one_block(numel, E), gemv_vector_scales<KIND>(I, act_s, w2_s), a2, gemv_act_bytes<KIND>(numel, I), act_s, 1, I, sorted, offs, active,
                       nact, w2, w2_s, H, numel, s2, scratch, static_cast<const float*>(nullptr),
                       static_cast<uint16_t*>(nullptr));
     int rc = check_launch("moe w2 (gemv)");
