@@ -210,8 +210,10 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_quant_kernel(
 }
 
 // As moe_align_quant_kernel, with the w4afp8 per-row quantiser (w4 order and
-// block corrections): each quant workgroup quantises kAlignThreads /
-// kRowThreads rows, one per 256-thread part.
+// block corrections).  CPL > 0: a quant workgroup quantises one row per wave
+// (cols <= 512 * CPL); CPL = 0: kAlignThreads / kRowThreads rows, one per
+// 256-thread part.
+template <int CPL>
 __global__ __launch_bounds__(kAlignThreads) void moe_align_rowquant_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int align_groups, int E, int bs,
     const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
@@ -224,12 +226,18 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_rowquant_kernel(
                ntpp, offsets_out, nullptr, active_out, num_active_out);
     return;
   }
-  constexpr int kParts = kAlignThreads / kRowThreads;
-  __shared__ float red[kAlignThreads / kWave];
-  const int part = threadIdx.x / kRowThreads;
-  const int64_t row = static_cast<int64_t>(blockIdx.x - align_groups) * kParts + part;
-  row_quant_part<true>(x, cols, cols, 1e-4f, -448.f, 448.f, xq, xs, row, row < rows,
-                       threadIdx.x % kRowThreads, red + part * (kRowThreads / kWave), xcorr);
+  if constexpr (CPL > 0) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x - align_groups) * (kAlignThreads / kWave) +
+                        threadIdx.x / kWave;
+    row_quant_wave<true, CPL>(x, cols, cols, 1e-4f, -448.f, 448.f, xq, xs, row, row < rows, xcorr);
+  } else {
+    constexpr int kParts = kAlignThreads / kRowThreads;
+    __shared__ float red[kAlignThreads / kWave];
+    const int part = threadIdx.x / kRowThreads;
+    const int64_t row = static_cast<int64_t>(blockIdx.x - align_groups) * kParts + part;
+    row_quant_part<true>(x, cols, cols, 1e-4f, -448.f, 448.f, xq, xs, row, row < rows,
+                         threadIdx.x % kRowThreads, red + part * (kRowThreads / kWave), xcorr);
+  }
 }
 
 }  // namespace vmamd
@@ -298,12 +306,28 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
   int groups;
   align_grid(numel, chunk, groups);
   groups = std::max(groups, 1);
-  constexpr int kParts = kAlignThreads / kRowThreads;
-  const int64_t qblocks = (rows + kParts - 1) / kParts;
-  moe_align_rowquant_kernel<<<static_cast<int>(groups + qblocks), kAlignThreads, 0, st>>>(
-      topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted,
-      capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x), rows,
-      static_cast<int>(cols), xq, xs, xcorr);
+  // One row per wave for rows of up to 2048 columns; longer rows keep four
+  // 256-thread rows per workgroup (at H = 4096, T = 4096 the wave form
+  // measured 31.4 against 25.8 us: 16 rows per workgroup leave too few
+  // workgroups in flight).
+  const int cpl0 = static_cast<int>((cols + 511) / 512);
+  const int cpl = cpl0 <= 4 ? cpl0 : 0;
+  const int rows_per_block = cpl > 0 ? kAlignThreads / kWave : kAlignThreads / kRowThreads;
+  const int64_t qblocks = (rows + rows_per_block - 1) / rows_per_block;
+  const dim3 grid(static_cast<unsigned>(groups + qblocks));
+#define VMAMD_ARQ(C)                                                                              \
+  moe_align_rowquant_kernel<C><<<grid, kAlignThreads, 0, st>>>(                                   \
+      topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted, \
+      capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),     \
+      rows, static_cast<int>(cols), xq, xs, xcorr)
+  switch (cpl) {
+    case 1: VMAMD_ARQ(1); break;
+    case 2: VMAMD_ARQ(2); break;
+    case 3: VMAMD_ARQ(3); break;
+    case 4: VMAMD_ARQ(4); break;
+    default: VMAMD_ARQ(0); break;
+  }
+#undef VMAMD_ARQ
   return check_launch(who);
 }
 }  // namespace vmamd

@@ -606,16 +606,44 @@ __global__ __launch_bounds__(kRowThreads) void moe_act_rowquant_w4_kernel(
   }
 }
 
-// kW4 prefill: the per-row a2 quantiser of the bf16 activation (one
-// kRowThreads block per padded route row below ntpp[0]), in w4 order with the
-// block corrections a2corr [rows, I/128].
+// kW4 prefill: the per-row a2 quantiser of the bf16 activation for the
+// padded route rows below ntpp[0], in w4 order with the block corrections
+// a2corr [rows, I/128].  CPL > 0: one wave per row (I <= 512 * CPL, four rows
+// per workgroup); CPL = 0: one kRowThreads workgroup per row.
+template <int CPL>
 __global__ __launch_bounds__(kRowThreads) void moe_rowquant_w4_kernel(
     const uint16_t* __restrict__ a, int I, const int32_t* __restrict__ ntpp, uint8_t* __restrict__ a2q,
     float* __restrict__ a2s, float* __restrict__ a2corr) {
-  if (static_cast<int>(blockIdx.x) >= ntpp[0]) return;  // uniform: past the last block
-  __shared__ float red[kRowThreads / kWave];
-  row_quant_part<true>(a, I, I, 1e-4f, -448.f, 448.f, a2q, a2s, blockIdx.x, true, threadIdx.x, red,
-                       a2corr);
+  if constexpr (CPL > 0) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kRowThreads / kWave) + threadIdx.x / kWave;
+    row_quant_wave<true, CPL>(a, I, I, 1e-4f, -448.f, 448.f, a2q, a2s, row, row < ntpp[0], a2corr);
+  } else {
+    if (static_cast<int>(blockIdx.x) >= ntpp[0]) return;  // uniform: past the last block
+    __shared__ float red[kRowThreads / kWave];
+    row_quant_part<true>(a, I, I, 1e-4f, -448.f, 448.f, a2q, a2s, blockIdx.x, true, threadIdx.x, red,
+                         a2corr);
+  }
+}
+
+// Launch of moe_rowquant_w4_kernel over `rows` padded route rows.
+static void launch_rowquant_w4(const uint16_t* a, int I, int64_t rows, const int32_t* ntpp,
+                               uint8_t* a2q, float* a2s, float* a2corr, hipStream_t st) {
+  const int cpl = (I + 511) / 512;
+  const unsigned waves_grid = static_cast<unsigned>((rows + kRowThreads / kWave - 1) / (kRowThreads / kWave));
+#define VMAMD_RQ(C) \
+  moe_rowquant_w4_kernel<C><<<waves_grid, kRowThreads, 0, st>>>(a, I, ntpp, a2q, a2s, a2corr)
+  switch (cpl) {
+    case 1: VMAMD_RQ(1); break;
+    case 2: VMAMD_RQ(2); break;
+    case 3: VMAMD_RQ(3); break;
+    case 4: VMAMD_RQ(4); break;
+    case 5: case 6: VMAMD_RQ(6); break;
+    case 7: case 8: VMAMD_RQ(8); break;
+    default:
+      moe_rowquant_w4_kernel<0><<<static_cast<unsigned>(rows), kRowThreads, 0, st>>>(a, I, ntpp, a2q, a2s,
+                                                                                    a2corr);
+  }
+#undef VMAMD_RQ
 }
 
 // A route's slot is live when its expert id is >= 0 and its local id
@@ -1812,8 +1840,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   if (rc) return rc;
   if constexpr (KIND == kW4) {
     if (bm != kGemvBlock) {  // rows past the last block are skipped on the device
-      moe_rowquant_w4_kernel<<<static_cast<unsigned>(cap), kRowThreads, 0, st>>>(
-          reinterpret_cast<const uint16_t*>(act_out), i, ntpp, a2, a2s, a2corr);
+      launch_rowquant_w4(reinterpret_cast<const uint16_t*>(act_out), i, cap, ntpp, a2, a2s, a2corr, st);
       rc = check_launch("w4afp8_moe (a2 quantiser)");
       if (rc) return rc;
     }

@@ -148,4 +148,44 @@ __device__ __forceinline__ void row_quant_part(const uint16_t* __restrict__ x, i
   }
 }
 
+// The per-row quantiser with one wave per row (no block barrier; several rows
+// per workgroup): lane l takes chunks l, l + 64, ... (CPL of them, cols <=
+// 512 * CPL), the same maximum (order-independent) and the same bytes as
+// row_quant_part.  Every lane of the wave must call it; rows past the end
+// (live = false) return before any cross-lane step, wave-uniformly.
+template <bool W4, int CPL>
+__device__ __forceinline__ void row_quant_wave(const uint16_t* __restrict__ x, int64_t x_row_stride,
+                                               int cols, float eps, float qmin, float qmax,
+                                               uint8_t* __restrict__ q, float* __restrict__ s,
+                                               int64_t row, bool live, float* __restrict__ corr) {
+  if (!live) return;
+  const int lane = lane_id();
+  const uint16_t* xr = x + row * x_row_stride;
+  const int nchunk = cols / 8;
+  float v[CPL][8];
+  float amax = eps;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = lane + c * kWave;
+    if (ch < nchunk) {
+      load8<kBF16>(xr + ch * 8, true, v[c]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
+    }
+  }
+  amax = wave_max(amax);
+  const float scale = amax / qmax;
+  if (lane == 0) s[row] = scale;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = lane + c * kWave;
+    if (ch < nchunk) {
+      if constexpr (W4)
+        w4_store_chunk(q + row * cols, corr + row * (cols / 128), ch, v[c], scale, qmin, qmax);
+      else
+        *reinterpret_cast<uint2*>(q + row * cols + ch * 8) = quant8(v[c], scale, qmin, qmax);
+    }
+  }
+}
+
 }  // namespace vmamd
