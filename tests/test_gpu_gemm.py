@@ -59,6 +59,31 @@ def test_block_fp8_gemm_m4096(N, K):
     _run(4096, N, K, seed=77, sample_rows=24, sample_cols=512)
 
 
+@pytest.mark.parametrize("M", [3600, 4000])
+def test_block_fp8_gemm_256_row_tiles_ragged(M):
+    """M and N where the 256 x 256 GEMM is chosen (two rounds of 128 x 256
+    tiles against one of 256 x 256), with the last row tile (M = 4000) and
+    the last column tile (N = 2112) only partly inside the output."""
+    _run(M, 2112, 1024, seed=31 + M, sample_rows=64, sample_cols=2112)
+
+
+def test_block_fp8_gemm_256_row_tiles_column_major_scales():
+    """The 256-row GEMM reads activation scales through their strides: the
+    column-major layout gives the same bits as the row-major one."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    M, N, K = 4000, 2112, 1024
+    w, ws = synthetic.dense_fp8_weight(N, K, 41)
+    x = synthetic.activations(M, K, 42)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    xq2, xs2 = per_token_group_quant_fp8(x, 128, column_major_scales=True)
+    assert xs2.stride(0) == 1
+    a = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    b = w8a8_block_fp8_matmul(xq2, w, xs2, ws, [128, 128])
+    assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("M", [3, 17, 33, 65, 100, 130])
 def test_block_fp8_gemm_ragged_m(M):
     _run(M, 2112, 1024, seed=5 + M, sample_rows=200, sample_cols=2112)

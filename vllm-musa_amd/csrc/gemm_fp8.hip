@@ -2,10 +2,12 @@
 //   A  [M, K] e4m3 (1x128 activation groups, scales As[m*as_sm + kb*as_sk])
 //   B  [N, K] e4m3 (128x128 weight blocks, scales Bs[ceil(N/128), K/128])
 //
-// Two kernels:
+// Three kernels:
 //  * gemm_fp8_dma_kernel -- 128 x 256 workgroup tile, 8 waves, K-block of 128
 //    per step, 3-stage LDS ring fed by direct global->LDS loads (one barrier
-//    per K-block), XCD-aware tile order.  For M > 64.
+//    per K-block), XCD-aware tile order, optional split K.  For M > 64.
+//  * gemm_fp8_big_kernel -- 256 x 256 tile, 2 LDS stages, for large M where
+//    it needs fewer rounds of workgroups (fewer bytes moved per flop).
 //  * gemv_fp8_bs_kernel  -- decode-sized M (<= 64): one workgroup per NT x 16
 //    weight rows, its waves split K and stream the rows straight from HBM
 //    into registers; each 16x128 weight fragment multiplies every 16-row
@@ -171,6 +173,204 @@ __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
   }
 }
 
+// Raw buffer loads (gfx9 descriptor: base, no stride, num_records bytes); a
+// lane whose byte offset is past num_records reads zeros and fetches nothing,
+// which masks rows past M and K-blocks past a split without branches.
+constexpr int kGemvBufferFlags = 0x00020000;
+constexpr uint32_t kGemvMasked = 0x80000000u;  // offset of a masked lane (buffers are < 2 GiB)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemv_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kGemvBufferFlags);
+}
+
+// ------------------------------------------- 256-row tiled GEMM ---------
+// For large M.  A CU's loads stream at the rate its vector cache keeps
+// requests in flight (measured: the 128 x 256 kernel's DMA ring alone, with
+// no MFMA, runs at the same speed as with them), so the bytes a workgroup
+// moves per flop set the pace: a 256 x 256 tile moves 64 KiB per K step for
+// 16.8 MFLOP, the 128 x 256 tile 48 KiB for 8.4 MFLOP.  8 waves as 4 (m) x
+// 2 (n), 64 x 128 per wave (128 accumulator registers a lane; the wave's 128
+// weight rows are one 128-row scale block).  Two LDS stages: the DMA of step
+// kb + 1 lands while step kb runs.  Each wave reads its step's 4 activation
+// fragments when the step starts and streams its 8 weight fragments, two
+// register sets deep, under the MFMAs.  Rows past M / N come from the buffer
+// descriptors' range check (no fetch) and are not stored.  (A 256 x 224 tile,
+// which gives 7168-row weights 32 column tiles -- two full rounds of 256 CUs
+// at M = 4096 instead of 1.75 -- measured 3 % slower there.)
+struct BigPipe {
+  static constexpr int BM = 256, NT = 8, BN = 32 * NT, WM = 4, WN = 2, MT = 4, kWaves = 8;
+  static_assert(BM / 8 == 4 * kWaves && BN / 8 == 4 * kWaves, "4 DMAs of 8 rows per wave and operand");
+  static constexpr int kThreads = kWaves * kWave;
+  static constexpr int kOffB = BM * 128;
+  static constexpr int kOffSA = (BM + BN) * 128;
+  static constexpr int kOffSB = kOffSA + BM * 4;
+  static constexpr int kStage = kOffSB + 256;  // the B-scale DMA writes 64 lanes x 4 bytes
+  static constexpr int kLds = 2 * kStage;
+  static_assert(kLds <= 160 * 1024, "LDS stages exceed the CU's LDS");
+};
+
+__device__ __forceinline__ void big_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint8_t* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)((lds_u8*)lds), 16, static_cast<int>(off), 0, 0, 0);
+}
+
+// as_bytes: the extent of As in bytes (< 2 GiB); the host keeps (M + 256) K
+// and (N + 256) K below 2^31.
+__global__ __launch_bounds__(BigPipe::kThreads, 1) void gemm_fp8_big_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t as_sm, int64_t as_sk,
+    int as_bytes, const uint8_t* __restrict__ B, const float* __restrict__ Bs, uint16_t* __restrict__ C,
+    int M, int N, int K, int TM, int TN) {
+  using P = BigPipe;
+  constexpr int NT = P::NT;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
+  int tm, tn;
+  if (!xcd_tile(blockIdx.x, TM, TN, tm, tn)) return;
+  const int m0 = tm * P::BM, n0 = tn * P::BN;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wm = wave / P::WN, wn = wave % P::WN;
+  const int li = lane % 16, lg = lane / 16;
+  const int KS = K / 128, NB = (N + 127) / 128;
+
+  // Lane L of DMA j fills LDS row (wave + 8 j) * 8 + L / 8, slot L % 8, from
+  // global chunk (L % 8) ^ (L / 8) (the tile's row swizzle).
+  const __amdgpu_buffer_rsrc_t ra = gemv_rsrc(A, M * K), rb = gemv_rsrc(B, N * K);
+  const uint32_t chunk = static_cast<uint32_t>(((lane % 8) ^ (lane / 8)) * 16);
+  const uint32_t offA = static_cast<uint32_t>(m0 + wave * 8 + lane / 8) * K + chunk;
+  const uint32_t offB = static_cast<uint32_t>(n0 + wave * 8 + lane / 8) * K + chunk;
+  const uint32_t rows64 = 64u * static_cast<uint32_t>(K);
+  // Scales through buffer descriptors too (a global->LDS load in the loop
+  // makes the compiler wait for every LDS read at once).  Waves 0-3: the
+  // activation scales of tile rows 64 * wave + lane; wave 4: the weight-block
+  // scales of the tile's two 128-row blocks.
+  uint32_t offS, stepS;
+  int ldsS;
+  __amdgpu_buffer_rsrc_t rs;
+  if (wave < P::BM / 64) {
+    const int m = min(m0 + 64 * wave + lane, M - 1);
+    rs = gemv_rsrc(As, as_bytes);
+    offS = static_cast<uint32_t>((m * as_sm) * 4);
+    stepS = static_cast<uint32_t>(as_sk * 4);
+    ldsS = P::kOffSA + 64 * wave * 4;
+  } else {
+    const int nb = min(n0 / 128 + min(lane, 1), NB - 1);
+    rs = gemv_rsrc(Bs, NB * KS * 4);
+    offS = static_cast<uint32_t>(nb * KS * 4);
+    stepS = 4;
+    ldsS = P::kOffSB;
+  }
+  auto issue = [&](uint8_t* stage, int step) {
+    const uint32_t ks = static_cast<uint32_t>(step) * 128;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) big_dma16(ra, offA + ks + j * rows64, stage + (wave + 8 * j) * 8 * 128);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) big_dma16(rb, offB + ks + j * rows64, stage + P::kOffB + (wave + 8 * j) * 8 * 128);
+    if (wave <= P::BM / 64)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)((lds_u8*)(stage + ldsS)), 4,
+                                               static_cast<int>(offS + step * stepS), 0, 0, 0);
+  };
+
+  v4f acc[P::MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < P::MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  const int nw = wn * 16 * NT;  // the wave's first weight row in the tile
+
+  // One K step from LDS stage `st`: the MFMAs in (n tile, m tile) order, the
+  // promotion of MFMA i - 1 (acc += p * sa * sb, 4 FMAs) issued after MFMA i,
+  // and weight fragment nt + 1 read under the MFMAs of nt.  The order is
+  // pinned (the scheduler otherwise moves each promotion next to its own
+  // MFMA and waits for it).
+  auto mma = [&](const uint8_t* st) {
+    const float sb = lds_load<float>(st, P::kOffSB + 4 * wn);
+    float sc[P::MT];
+#pragma unroll
+    for (int mt = 0; mt < P::MT; ++mt) sc[mt] = lds_load<float>(st, P::kOffSA + (wm * 64 + mt * 16 + li) * 4);
+    v8i w[2], x[P::MT];
+    w[0] = lds_frag(st + P::kOffB, nw + li, lg);
+#pragma unroll
+    for (int mt = 0; mt < P::MT; ++mt) x[mt] = lds_frag(st, wm * 64 + mt * 16 + li, lg);
+    __builtin_amdgcn_sched_barrier(0);
+    v4f t[2];
+    constexpr int NI = P::MT * NT;
+#pragma unroll
+    for (int i = 0; i <= NI; ++i) {
+      const int nt = i / P::MT, mt = i % P::MT;
+      if (i < NI) {
+        t[i & 1] = mfma_fp8(w[nt & 1], x[mt], zero);
+        __builtin_amdgcn_sched_barrier(0);
+        if (mt == 0 && nt + 1 < NT) w[(nt + 1) & 1] = lds_frag(st + P::kOffB, nw + (nt + 1) * 16 + li, lg);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (i > 0) {
+        const int j = i - 1;
+        if (j < P::MT) sc[j] *= sb;  // activation row scale x weight-block scale, at first use
+        fma4(acc[j % P::MT][j / P::MT], t[j & 1], sc[j % P::MT]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  issue(smem_dyn, 0);
+  wait_lgkmcnt0();
+  for (int kb = 0; kb < KS; ++kb) {
+    wait_vmcnt<0>();  // this wave's DMAs of step kb have landed
+    barrier_lds();    // ... every wave's, and step kb - 1's buffer is no longer read
+    if (kb + 1 < KS) issue(smem_dyn + ((kb + 1) & 1) * P::kStage, kb + 1);
+    mma(smem_dyn + (kb & 1) * P::kStage);
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < P::MT; ++mt) {
+    const int m = m0 + wm * 64 + mt * 16 + li;
+    if (m >= M) continue;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = n0 + nw + nt * 16 + 4 * lg;
+      if (n >= N) continue;
+      const v4f a = acc[mt][nt];
+      *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) = pack_bf16x4(a[0], a[1], a[2], a[3]);
+    }
+  }
+}
+
+static int device_cus();
+
+// Whether the 256 x 256 GEMM beats the 128 x 256 one for an M x N product.
+// Time is modelled as rounds of resident workgroups (one per CU) times the
+// bytes a workgroup moves per K step, (rows + cols) x 128: over the
+// DeepSeek-V3 dense shapes at M = 1024..4096 this picks the faster kernel in
+// every measured case where they differ by more than 3 %.  The 256-row
+// kernel also needs its buffer offsets below 2 GiB.
+static bool use_big_gemm(int M, int N, int K, int64_t as_extent) {
+  if (M < 512) return false;
+  const int64_t cus = device_cus();
+  auto cost = [&](int64_t bm, int64_t bn) {
+    const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    return (tiles + cus - 1) / cus * (bm + bn);
+  };
+  return cost(256, 256) < cost(128, 256) && static_cast<int64_t>(M + 256) * K < (1ll << 31) &&
+         static_cast<int64_t>(N + 256) * K < (1ll << 31) && as_extent < (1ll << 31);
+}
+
+static int launch_big(const uint8_t* a, const float* As, int64_t as_sm, int64_t as_sk, int as_bytes,
+                      const uint8_t* b, const float* Bs, uint16_t* c, int m, int n, int k, hipStream_t st) {
+  using P = BigPipe;
+  static bool raised = false;
+  if (!raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_fp8_big_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, P::kLds) != hipSuccess) {
+      set_error("w8a8_block_fp8_matmul: cannot raise the LDS limit of the GEMM kernel");
+      return VMAMD_ERR_HIP;
+    }
+    raised = true;
+  }
+  const int TM = (m + P::BM - 1) / P::BM, TN = (n + P::BN - 1) / P::BN;
+  gemm_fp8_big_kernel<<<xcd_grid(TM * TN), P::kThreads, P::kLds, st>>>(a, As, as_sm, as_sk, as_bytes, b, Bs, c, m,
+                                                                      n, k, TM, TN);
+  return check_launch("w8a8_block_fp8_matmul(gemm)");
+}
+
 // C = bf16(sum_s partial[s]) over the S split-K partials of an M x N output,
 // added in split order (deterministic), 4 elements per lane (M * N is a
 // multiple of 16).  All S loads of a lane are issued before its first add,
@@ -213,14 +413,6 @@ static void splitk_reduce(const float* partial, int splits, int64_t mn, uint16_t
 // ------------------------------------------------------------ split-K GEMV --
 constexpr int kGemvU = 4;  // K-blocks of weights per pass (8 KiB per wave)
 
-// Raw buffer loads (gfx9 descriptor: base, no stride, num_records bytes); a
-// lane whose byte offset is past num_records reads zeros and fetches nothing,
-// which masks rows past M and K-blocks past a split without branches.
-constexpr int kGemvBufferFlags = 0x00020000;
-constexpr uint32_t kGemvMasked = 0x80000000u;  // offset of a masked lane (buffers are < 2 GiB)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemv_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kGemvBufferFlags);
-}
 __device__ __forceinline__ v8i gemv_buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
   const v4i lo = __builtin_bit_cast(
       v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off + 16u * g), 0, 0));
@@ -638,6 +830,11 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
     VMAMD_REQUIRE(false, "w8a8_block_fp8_matmul: no GEMV instance for %d x %d x %d", g.mt, g.nt, g.u);
 #undef VMAMD_GEMV
     return check_launch("w8a8_block_fp8_matmul(gemv)");
+  }
+  if (plan.splits == 1 && as_stride_m >= 0 && as_stride_k >= 0) {
+    const int64_t as_extent = ((m - 1) * as_stride_m + (k / 128 - 1) * as_stride_k + 1) * 4;
+    if (use_big_gemm(m, n, k, as_extent))
+      return launch_big(a, As, as_stride_m, as_stride_k, static_cast<int>(as_extent), b, Bs, c, m, n, k, st);
   }
   static bool lds_raised = false;
   if (!lds_raised) {
