@@ -698,7 +698,7 @@ def main() -> int:
     roofline = {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": read_traffic(),
                 "traffic_source": TRAFFIC_SUMMARY,
-                "kernel": "moe_gemm_dma_kernel<kFp8, W13>",
+                "kernel": "moe_big_kernel<W13>" if st.block_m == 256 else "moe_gemm_dma_kernel<kFp8, W13>",
                 "kernel_us": round(k_ms * 1e3, 1),
                 "kernel_tflops": round(2.0 * T_HEADLINE * TOPK * 2 * I * H / (k_ms * 1e-3) / 1e12, 1),
                 "algorithmic_bytes": int(k_bytes),

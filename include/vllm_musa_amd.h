@@ -295,12 +295,14 @@ int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H, const 
  * expert_offsets, num_tokens_post_pad, and for block_m 16 active_experts /
  * num_active).  block_m selects the kernels and must equal the align call's
  * block_size: 16 = decode (expert-major GEMV, each weight row streamed once
- * per call), 128 = prefill (grouped MFMA GEMM over 128-route blocks).
+ * per call), 128 = prefill (grouped MFMA GEMM over 128-route blocks), 256 =
+ * long prefill (256-route blocks; same results as 128).  The fused call
+ * takes 256 from 128 routes per expert.
  *
  * W13:  a = bf16(silu(h_gate) * h_up), h = bf16(W13[e] . q(x[t])), then a is
  *       quantised per 1x128 group into a2q (fp8) / a2s (f32, [rows, I/128]).
  *       Rows of a2q/a2s are routes (r = t*topk + k, [T*topk, I]) for
- *       block_m 16, positions of sorted_token_ids ([capacity, I]) for 128.
+ *       block_m 16, positions of sorted_token_ids ([capacity, I]) for 128 / 256.
  * W2:   y[r] = bf16(W2[e] . dequant(a2q[row(r)]) * topk_weights[r]),
  *       y [T*topk, H] bf16; rows of dropped routes are left unwritten.
  * Scratch: vmamd_moe_fp8_stage_workspace_size() bytes, 16-byte aligned

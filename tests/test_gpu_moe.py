@@ -87,6 +87,45 @@ def test_fp8_moe_hot_expert_multi_block(path):
     _check(out, _oracle(*case))
 
 
+def test_fp8_moe_256_route_blocks_vs_oracle():
+    """From 128 routes per expert the grouped GEMMs take 256-route blocks
+    (here 1200 routes on 8 experts); H = 640 leaves the last 256-row W2 tile
+    half outside the output and I = 384 gives three 128-column W13 tiles."""
+    case = _case(600, 8, 640, 384, 2, seed=71)
+    out = _run(*case, path="gemm")
+    _check(out, _oracle(*case))
+
+
+@pytest.mark.parametrize("variant", ["hot", "expert_map", "limit"])
+def test_fp8_moe_256_route_blocks_match_128(variant):
+    """256- and 128-route blocks give the same bits: every route's row sees the
+    same K order and roundings whatever tile it lands in.  A hot expert (1000
+    routes: four 256-route blocks), an expert map with dropped routes, and the
+    clamped SwiGLU."""
+    from vllm_musa_amd.fused_moe import Fp8MoeStages
+    emap, limit = None, None
+    if variant == "hot":
+        x, w13, s13, w2, s2, w, ids = _case(1000, 8, 512, 256, 2, seed=81, hot=5)
+    else:
+        x, w13, s13, w2, s2, w, ids = _case(700, 8, 768, 256, 2, seed=82)
+    if variant == "expert_map":
+        g = torch.Generator().manual_seed(83)
+        ids = torch.stack([torch.randperm(12, generator=g)[:2] for _ in range(700)]).to(torch.int32).to(DEV)
+        emap = torch.full((12,), -1, dtype=torch.int32)
+        emap[4:] = torch.arange(8, dtype=torch.int32)
+        emap = emap.to(DEV)
+    if variant == "limit":
+        limit = 7.0
+    big = Fp8MoeStages(x, w13, s13, w2, s2, w, ids, path="gemm", expert_map=emap, swiglu_limit=limit)
+    assert big.block_m == 256
+    small = Fp8MoeStages(x, w13, s13, w2, s2, w, ids, path="gemm", expert_map=emap, swiglu_limit=limit,
+                         block_m=128)
+    a = big.run().clone()
+    b = small.run()
+    assert torch.equal(a, b)
+    assert torch.equal(_run(x, w13, s13, w2, s2, w, ids, "gemm", emap=emap, limit=limit), a)
+
+
 @pytest.mark.parametrize("path", ["gemv", "gemm"])
 def test_fp8_moe_expert_map(path):
     x, w13, s13, w2, s2, w, ids = _case(40, 8, 512, 256, 4, seed=11)

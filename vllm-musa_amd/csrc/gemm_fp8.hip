@@ -196,21 +196,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemv_rsrc(const void* base, in
 // descriptors' range check (no fetch) and are not stored.  (A 256 x 224 tile,
 // which gives 7168-row weights 32 column tiles -- two full rounds of 256 CUs
 // at M = 4096 instead of 1.75 -- measured 3 % slower there.)
-struct BigPipe {
-  static constexpr int BM = 256, NT = 8, BN = 32 * NT, WM = 4, WN = 2, MT = 4, kWaves = 8;
-  static_assert(BM / 8 == 4 * kWaves && BN / 8 == 4 * kWaves, "4 DMAs of 8 rows per wave and operand");
-  static constexpr int kThreads = kWaves * kWave;
-  static constexpr int kOffB = BM * 128;
-  static constexpr int kOffSA = (BM + BN) * 128;
-  static constexpr int kOffSB = kOffSA + BM * 4;
-  static constexpr int kStage = kOffSB + 256;  // the B-scale DMA writes 64 lanes x 4 bytes
-  static constexpr int kLds = 2 * kStage;
-  static_assert(kLds <= 160 * 1024, "LDS stages exceed the CU's LDS");
-};
-
-__device__ __forceinline__ void big_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint8_t* lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)((lds_u8*)lds), 16, static_cast<int>(off), 0, 0, 0);
-}
+using BigPipe = BigTile;
 
 // as_bytes: the extent of As in bytes (< 2 GiB); the host keeps (M + 256) K
 // and (N + 256) K below 2^31.
@@ -260,12 +246,10 @@ __global__ __launch_bounds__(BigPipe::kThreads, 1) void gemm_fp8_big_kernel(
   auto issue = [&](uint8_t* stage, int step) {
     const uint32_t ks = static_cast<uint32_t>(step) * 128;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) big_dma16(ra, offA + ks + j * rows64, stage + (wave + 8 * j) * 8 * 128);
+    for (int j = 0; j < 4; ++j) buffer_dma16(ra, offA + ks + j * rows64, stage + (wave + 8 * j) * 8 * 128);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) big_dma16(rb, offB + ks + j * rows64, stage + P::kOffB + (wave + 8 * j) * 8 * 128);
-    if (wave <= P::BM / 64)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)((lds_u8*)(stage + ldsS)), 4,
-                                               static_cast<int>(offS + step * stepS), 0, 0, 0);
+    for (int j = 0; j < 4; ++j) buffer_dma16(rb, offB + ks + j * rows64, stage + P::kOffB + (wave + 8 * j) * 8 * 128);
+    if (wave <= P::BM / 64) buffer_dma4(rs, offS + step * stepS, stage + ldsS);
   };
 
   v4f acc[P::MT][NT];

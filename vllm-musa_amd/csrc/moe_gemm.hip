@@ -819,11 +819,13 @@ constexpr int kMoeBM = 128;
 // kXcds after xcd_grid); the tiles actually used are split into kXcds
 // contiguous ranges, one per XCD (workgroup wg runs on XCD wg % kXcds), so
 // every XCD gets an equal share whatever the routing.  Returns false for
-// workgroups past the used tiles.
+// workgroups past the used tiles.  BM: routes per block (the alignment's
+// block size).
+template <int BM = kMoeBM>
 __device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* __restrict__ offsets,
                                          const int32_t* __restrict__ ntpp, int E, int TN,
                                          int& e_out, int& mb_out, int& tn_out) {
-  const int used = min(ntpp[0] / kMoeBM * TN, max_tiles);
+  const int used = min(ntpp[0] / BM * TN, max_tiles);
   const int per = (used + kXcds - 1) / kXcds;
   const int q = wg / kXcds;
   if (q >= per) return false;
@@ -833,10 +835,10 @@ __device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* _
   int lo = 0, hi = E - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (offsets[mid] / kMoeBM * TN <= L) lo = mid; else hi = mid - 1;
+    if (offsets[mid] / BM * TN <= L) lo = mid; else hi = mid - 1;
   }
-  const int b0 = offsets[lo] / kMoeBM;
-  const int nb = offsets[lo + 1] / kMoeBM - b0;
+  const int b0 = offsets[lo] / BM;
+  const int nb = offsets[lo + 1] / BM - b0;
   const int local = L - b0 * TN;
   e_out = lo;
   tn_out = local / nb;
@@ -1111,6 +1113,220 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
   }
 }
 
+// ------------------------------- fp8 prefill GEMMs on 256-route tiles ----
+// For long prefills (block size 256): a CU's loads stream at the rate its
+// vector cache keeps requests in flight, so the bytes a workgroup moves per
+// flop set the pace, and a 256-route x 256-row tile moves 64 KiB per K step
+// for twice the flops of the 128-route tile's 48 KiB.  A wave of 64 padding
+// routes skips its MFMAs, so the larger block costs little where an
+// expert's last block is mostly padding: an 8-row group of padding
+// routes loads nothing (its LDS rows keep stale bytes, which reach only the
+// padding routes' outputs, never stored).  8 waves as 4 (m: 64
+// routes) x 2 (n: 128 weight rows), two LDS stages, all loads through buffer
+// descriptors (activations, scales; the weights per expert), MFMA order and
+// promotion as gemm_fp8_big_kernel.  W13: the 256 weight rows are 128 gate +
+// 128 up rows interleaved by 16 (n tile 2q gate, 2q + 1 up); epilogue
+// SiLU-and-mul and the 1x128 a2 quantiser; W2: 256 hidden rows, epilogue the
+// routed weight.
+constexpr int kMoeBigBM = 256;
+
+template <bool W13>
+__global__ __launch_bounds__(512, 1) void moe_big_kernel(
+    const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_s_bytes,
+    int topk, int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles, const uint8_t* __restrict__ w,
+    const float* __restrict__ ws, int N, int I, float limit, const float* __restrict__ route_w,
+    uint8_t* __restrict__ a2, float* __restrict__ a2s, uint16_t* __restrict__ y) {
+  using P = BigTile;
+  constexpr int BM = P::BM, NT = P::NT, MT = P::MT;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
+  const int TN = W13 ? I / 128 : (N + P::BN - 1) / P::BN;
+  int e, mb, tn;
+  if (!moe_tile<BM>(blockIdx.x, max_tiles, offsets, ntpp, E, TN, e, mb, tn)) return;
+  const int n0 = W13 ? tn * 128 : tn * P::BN;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wm = wave / P::WN, wn = wave % P::WN;
+  const int li = lane % 16, lg = lane / 16;
+  const int KS = K / 128, NB = (N + 127) / 128;
+  const int64_t base = static_cast<int64_t>(mb) * BM;
+
+  auto wrow = [&](int j) -> int {  // weight row of local tile row j
+    if constexpr (W13) {
+      const int p = j / 32, q = j % 32;
+      return q < 16 ? n0 + 16 * p + q : I + n0 + 16 * p + (q - 16);
+    } else {
+      return n0 + j;  // rows past N: past the descriptor's range
+    }
+  };
+  auto arow = [&](int r) -> int {  // activation row of tile row r
+    if constexpr (W13) {
+      const int s = sorted[base + r];
+      return s < numel ? s / topk : 0;
+    } else {
+      return static_cast<int>(base) + r;
+    }
+  };
+
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(act, act_bytes);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(w + static_cast<int64_t>(e) * N * K, N * K);
+  const uint32_t chunk = static_cast<uint32_t>(((lane % 8) ^ (lane / 8)) * 16);
+  uint32_t offA[4], offB[4];
+  uint64_t liveA[4];  // activation row groups holding a route (padding groups load nothing)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = (wave + 8 * j) * 8 + lane / 8;
+    offA[j] = static_cast<uint32_t>(arow(r)) * K + chunk;
+    offB[j] = static_cast<uint32_t>(wrow(r)) * K + chunk;
+    liveA[j] = __builtin_amdgcn_ballot_w64(sorted[base + r] < numel);
+  }
+  uint32_t offS, stepS = 4;
+  int ldsS;
+  __amdgpu_buffer_rsrc_t rs;
+  if (wave < BM / 64) {  // activation scales of tile rows 64 * wave + lane
+    rs = buffer_rsrc(act_s, act_s_bytes);
+    offS = static_cast<uint32_t>(arow(64 * wave + lane)) * KS * 4;
+    ldsS = P::kOffSA + 64 * wave * 4;
+  } else {  // weight-block scales: W13 gate / up block, W2 the tile's two 128-row blocks
+    const int slot = min(lane, 1);
+    const int brow = W13 ? (slot ? (I + n0) / 128 : n0 / 128) : min(n0 / 128 + slot, NB - 1);
+    rs = buffer_rsrc(ws, E * NB * KS * 4);
+    offS = static_cast<uint32_t>((e * NB + brow) * KS) * 4;
+    ldsS = P::kOffSB;
+  }
+  auto issue = [&](uint8_t* stage, int step) {
+    const uint32_t ks = static_cast<uint32_t>(step) * 128;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (liveA[j]) buffer_dma16(ra, offA[j] + ks, stage + (wave + 8 * j) * 8 * 128);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) buffer_dma16(rb, offB[j] + ks, stage + P::kOffB + (wave + 8 * j) * 8 * 128);
+    if (wave <= BM / 64) buffer_dma4(rs, offS + step * stepS, stage + ldsS);
+  };
+  // Padding routes close a block, so a wave whose first route is padding
+  // holds none.
+  const bool wave_live = sorted[base + wm * 64] < numel;
+
+  v4f acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  const int nw = wn * 16 * NT;  // the wave's first local weight row
+
+  // One K step from LDS stage `st` (see gemm_fp8_big_kernel).  W13: n tile
+  // nt takes the gate (even) or up (odd) block scale.
+  auto mma = [&](const uint8_t* st) {
+    const float sb0 = lds_load<float>(st, P::kOffSB + (W13 ? 0 : 4 * wn));
+    const float sb1 = W13 ? lds_load<float>(st, P::kOffSB + 4) : sb0;
+    float sa[MT], sc[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) sa[mt] = lds_load<float>(st, P::kOffSA + (wm * 64 + mt * 16 + li) * 4);
+    v8i wf[2], x[MT];
+    wf[0] = lds_frag(st + P::kOffB, nw + li, lg);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) x[mt] = lds_frag(st, wm * 64 + mt * 16 + li, lg);
+    __builtin_amdgcn_sched_barrier(0);
+    v4f t[2];
+    constexpr int NI = MT * NT;
+#pragma unroll
+    for (int i = 0; i <= NI; ++i) {
+      const int nt = i / MT, mt = i % MT;
+      if (i < NI) {
+        t[i & 1] = mfma_fp8(wf[nt & 1], x[mt], zero);
+        __builtin_amdgcn_sched_barrier(0);
+        if (mt == 0 && nt + 1 < NT) wf[(nt + 1) & 1] = lds_frag(st + P::kOffB, nw + (nt + 1) * 16 + li, lg);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (i > 0) {
+        const int j = i - 1, jm = j % MT, jn = j / MT;
+        if (jn < 2) sc[jm][jn] = sa[jm] * (jn ? sb1 : sb0);  // at first use
+        fma4(acc[jm][jn], t[j & 1], sc[jm][W13 ? (jn & 1) : 0]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  issue(smem_dyn, 0);
+  wait_lgkmcnt0();
+  for (int kb = 0; kb < KS; ++kb) {
+    wait_vmcnt<0>();  // this wave's DMAs of step kb have landed
+    barrier_lds();    // ... every wave's, and step kb - 1's buffer is no longer read
+    if (kb + 1 < KS) issue(smem_dyn + ((kb + 1) & 1) * P::kStage, kb + 1);
+    if (wave_live) mma(smem_dyn + (kb & 1) * P::kStage);
+  }
+  barrier_lds();  // every wave is done with the stages before LDS is reused
+
+  if constexpr (W13) {
+    // route_w (apply_router_weight_on_input): gate/up times the route's weight
+    // before their bf16 rounding; without it the factor is 1 (exact).
+    float rw[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      rw[mt] = 1.0f;
+      if (route_w) {
+        const int r = sorted[base + wm * 64 + mt * 16 + li];
+        rw[mt] = r < numel ? route_w[r] : 0.0f;
+      }
+    }
+    // SiLU-and-mul, row amax across the 2 n-waves through LDS, 1x128 quantiser.
+    float* red = reinterpret_cast<float*>(smem_dyn);  // [WN][BM]
+    float v[MT][NT / 2][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float amax = 0.f;
+#pragma unroll
+      for (int q = 0; q < NT / 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float xv = swiglu_bf16(bf16r(acc[mt][2 * q][r] * rw[mt]), bf16r(acc[mt][2 * q + 1][r] * rw[mt]), limit);
+          v[mt][q][r] = xv;
+          amax = fmaxf(amax, fabsf(xv));
+        }
+      amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
+      amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+      if (lg == 0) red[wn * BM + wm * 64 + mt * 16 + li] = amax;
+    }
+    __syncthreads();
+    const int gpr = I / 128;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int ml = wm * 64 + mt * 16 + li;
+      const float amax = fmaxf(1e-10f, fmaxf(red[ml], red[BM + ml]));
+      const float scale = amax / 448.0f;
+      const int64_t row = base + ml;
+      if (wn == 0 && lg == 0) a2s[row * gpr + tn] = scale;
+#pragma unroll
+      for (int q = 0; q < NT / 2; ++q) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float xv = v[mt][q][r];
+          o[r] = xv != xv ? -448.0f : fminf(fmaxf(xv / scale, -448.0f), 448.0f);
+        }
+        const int col = n0 + (4 * wn + q) * 16 + 4 * lg;
+        *reinterpret_cast<uint32_t*>(a2 + row * I + col) = f32x4_to_fp8x4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = sorted[base + wm * 64 + mt * 16 + li];
+      if (r >= numel) continue;
+      const float rw = route_w ? route_w[r] : 1.0f;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int n = n0 + nw + nt * 16 + 4 * lg;
+        if (n >= N) continue;
+        const v4f a = acc[mt][nt];
+        *reinterpret_cast<uint2*>(y + static_cast<int64_t>(r) * N + n) =
+            pack_bf16x4(a[0] * rw, a[1] * rw, a[2] * rw, a[3] * rw);
+      }
+    }
+  }
+}
+
 // ------------------------------------------- w4afp8 prefill GEMMs ---------
 // Tile: 128 routes x 256 weight rows, 8 waves as 2 (m) x 4 (n) with 64 x 64
 // per wave, on a W4Pipe::NS-deep LDS ring fed by direct global->LDS loads
@@ -1130,14 +1346,6 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
 // epilogue writes the bf16 SwiGLU activation of every padded route row;
 // W2: 256 hidden rows, epilogue y[r] = bf16(acc * a2 row scale).
 // EVEN: K / 128 is even (a row's scale words never straddle two rows).
-// Buffer-descriptor forms of dma16 / dma4: a lane whose byte offset lies
-// past the buffer's end fetches nothing.
-__device__ __forceinline__ void buffer_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint8_t* lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)((lds_u8*)lds), 16, static_cast<int>(off), 0, 0, 0);
-}
-__device__ __forceinline__ void buffer_dma4(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint8_t* lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)((lds_u8*)lds), 4, static_cast<int>(off), 0, 0, 0);
-}
 
 struct W4Pipe {
   static constexpr int BM = 128, BN = 256, NS = 4, MT = 4, NT = 4;
@@ -1509,6 +1717,26 @@ static int raise_dma_lds() {
   return VMAMD_OK;
 }
 
+template <bool W13>
+static int raise_big_lds() {
+  static bool done = false;
+  if (done) return VMAMD_OK;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_big_kernel<W13>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, BigTile::kLds) != hipSuccess) {
+    set_error("moe gemm: cannot raise the LDS limit of the grouped GEMM kernel");
+    return VMAMD_ERR_HIP;
+  }
+  done = true;
+  return VMAMD_OK;
+}
+
+// The 256-route kernels read activations, scales and each expert's weights
+// through buffer descriptors: all below 2 GiB.
+static bool big_fits(int64_t act_rows, int64_t K, int64_t N, int E) {
+  return act_rows * K < (1ll << 31) && act_rows * (K / 128) * 4 < (1ll << 31) && N * K < (1ll << 31) &&
+         static_cast<int64_t>(E) * ((N + 127) / 128) * (K / 128) * 4 < (1ll << 31);
+}
+
 // Bytes of a decode GEMV's activation operand ([rows, K]); the GEMV reads it
 // through a buffer descriptor, which the callers keep below 2 GiB.
 template <int KIND>
@@ -1604,6 +1832,19 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
     }
     return check_launch("moe w13 (activation)");
   }
+  if constexpr (KIND == kFp8) {
+    if (block_m == kMoeBigBM) {
+      VMAMD_REQUIRE(big_fits(T, H, 2ll * I, E), "moe w13: operands past 2 GiB for the 256-route GEMM");
+      const int tiles = static_cast<int>((cap + kMoeBigBM - 1) / kMoeBigBM) * (I / 128);
+      int rc = raise_big_lds<true>();
+      if (rc) return rc;
+      moe_big_kernel<true><<<xcd_grid(tiles), BigTile::kThreads, BigTile::kLds, st>>>(
+          xa, static_cast<int>(static_cast<int64_t>(T) * H), xs, static_cast<int>(static_cast<int64_t>(T) * (H / 128) * 4),
+          topk, H, sorted, offs, ntpp, E, numel, tiles, w13, static_cast<const float*>(w13_s), 2 * I, I, limit,
+          route_w, a2, a2s, nullptr);
+      return check_launch("moe w13 (gemm)");
+    }
+  }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
   const int tiles = max_blocks * (I / 128);
   if constexpr (KIND == kW4) {
@@ -1671,6 +1912,18 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
         scratch, s2, numel, H, topk_ids, emap, emap_len, E, yscale, y);
     return check_launch("moe w2 (reduce)");
   }
+  if constexpr (KIND == kFp8) {
+    if (block_m == kMoeBigBM) {
+      VMAMD_REQUIRE(big_fits(cap, I, H, E), "moe w2: operands past 2 GiB for the 256-route GEMM");
+      const int tiles = static_cast<int>((cap + kMoeBigBM - 1) / kMoeBigBM) * ((H + 255) / 256);
+      int rc = raise_big_lds<false>();
+      if (rc) return rc;
+      moe_big_kernel<false><<<xcd_grid(tiles), BigTile::kThreads, BigTile::kLds, st>>>(
+          a2, static_cast<int>(cap * I), a2s, static_cast<int>(cap * (I / 128) * 4), 1, I, sorted, offs, ntpp, E,
+          numel, tiles, w2, static_cast<const float*>(w2_s), H, I, 0.f, route_w, nullptr, nullptr, y);
+      return check_launch("moe w2 (gemm)");
+    }
+  }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
   if constexpr (KIND == kW4) {
     const int tiles = max_blocks * ((H + W4Pipe::BN - 1) / W4Pipe::BN);
@@ -1728,16 +1981,21 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
 
 // Path choice of `auto`: the decode kernels (GEMV over 16-route blocks) up to
 // a number of routes per expert measured on MI355X, the grouped GEMMs over
-// 128-route blocks above.  Measured crossovers (graph replay, caches
+// 128- or 256-route blocks above.  Measured crossovers (graph replay, caches
 // flushed): fp8 DeepSeek-V3 (E=256, H=7168, I=2048, top-8) between 2 and 3
 // routes per expert (T=64 / 96); bf16 (E=128, H=2048, I=768) and w4afp8
 // (E=128, H=4096, I=1536) between 8 and 16 (T=128 / 256).
+// fp8 layers with at least 128 routes per expert take 256-route blocks
+// (moe_big_kernel): measured on DeepSeek-V3 (E=256, H=7168, I=2048, top-8),
+// W13 / W2: T=3072 +3 % / -3 %, T=4096 -1 % / -6 %, T=6144 -8 % / -10 %,
+// T=8192 -2 % / -10 % against 128-route blocks.
 static int moe_block_m(int64_t T, int topk, int E, int path, int kind) {
   if (path == VMAMD_MOE_PATH_GEMV) return kGemvBlock;
-  if (path == VMAMD_MOE_PATH_GEMM) return kMoeBM;
   const int64_t routes = T * topk;
+  const int grouped = kind == kFp8 && routes >= 128 * static_cast<int64_t>(E) ? kMoeBigBM : kMoeBM;
+  if (path == VMAMD_MOE_PATH_GEMM) return grouped;
   const int64_t limit = kind == kFp8 ? (5 * static_cast<int64_t>(E)) / 2 : 12 * static_cast<int64_t>(E);
-  return routes <= limit ? kGemvBlock : kMoeBM;
+  return routes <= limit ? kGemvBlock : grouped;
 }
 
 static int check_stage_common(const char* who, int64_t T, int topk, int E, int64_t H, int64_t I,
@@ -1747,8 +2005,8 @@ static int check_stage_common(const char* who, int64_t T, int topk, int E, int64
   VMAMD_REQUIRE(H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0,
                 "%s: hidden (%lld) and intermediate (%lld) sizes must be multiples of 128", who,
                 (long long)H, (long long)I);
-  VMAMD_REQUIRE(block_m == kGemvBlock || block_m == kMoeBM, "%s: block_m must be %d or %d (got %d)",
-                who, kGemvBlock, kMoeBM, block_m);
+  VMAMD_REQUIRE(block_m == kGemvBlock || block_m == kMoeBM || block_m == kMoeBigBM,
+                "%s: block_m must be %d, %d or %d (got %d)", who, kGemvBlock, kMoeBM, kMoeBigBM, block_m);
   VMAMD_REQUIRE(T * topk < (1ll << 30) && T * H < (1ll << 40), "%s: problem too large", who);
   VMAMD_REQUIRE(block_m != kGemvBlock || (T * H * 2 < (1ll << 31) && T * topk * I * 2 < (1ll << 31)),
                 "%s: the decode path (block_m 16) takes activations below 2 GiB", who);
@@ -1870,7 +2128,7 @@ static int stage_w13(const char* who, const void* xa, const float* xs, int64_t T
   VMAMD_REQUIRE(xa && sorted && offs && ntpp && w13 && a2 &&
                     (KIND == kBf16 || (xs && w13_s)) && (KIND != kFp8 || a2s),
                 "%s: null pointer", who);
-  VMAMD_REQUIRE(block_m == kMoeBM || (active && nact),
+  VMAMD_REQUIRE(block_m != kGemvBlock || (active && nact),
                 "%s: the decode path (block_m 16) needs active_experts / num_active", who);
   const size_t need = w13_scratch(T * topk, E, H, I, block_m, KIND);
   VMAMD_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
@@ -1898,7 +2156,7 @@ static int stage_w2(const char* who, const void* a2, const float* a2s, int64_t T
   VMAMD_REQUIRE(a2 && sorted && offs && ntpp && w2 && topk_ids && y &&
                     (KIND == kBf16 || (a2s && w2_s)) && (KIND == kW4 || topk_weights),
                 "%s: null pointer", who);
-  VMAMD_REQUIRE(block_m == kMoeBM || (active && nact),
+  VMAMD_REQUIRE(block_m != kGemvBlock || (active && nact),
                 "%s: the decode path (block_m 16) needs active_experts / num_active", who);
   const size_t need = w2_scratch(T * topk, E, H, I, block_m, KIND);
   VMAMD_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),

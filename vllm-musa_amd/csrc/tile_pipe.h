@@ -35,6 +35,16 @@ __device__ __forceinline__ void dma4(const uint8_t* g, uint8_t* lds) {
   __builtin_amdgcn_global_load_lds(g, (lds_void_ptr)((lds_u8*)lds), 4, 0, 0);
 }
 
+// Buffer-descriptor forms of dma16 / dma4: a lane whose byte offset lies
+// past the buffer's end fetches nothing.  (Unlike the global forms, these
+// also leave the compiler free to wait for LDS reads one at a time.)
+__device__ __forceinline__ void buffer_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint8_t* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)((lds_u8*)lds), 16, static_cast<int>(off), 0, 0, 0);
+}
+__device__ __forceinline__ void buffer_dma4(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint8_t* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)((lds_u8*)lds), 4, static_cast<int>(off), 0, 0, 0);
+}
+
 // Wait until at most N of this wave's vector-memory loads are outstanding
 // (gfx9 s_waitcnt encoding: vmcnt in [3:0] and [15:14], expcnt and lgkmcnt
 // left at their no-wait maxima).
@@ -52,6 +62,24 @@ __device__ __forceinline__ void barrier_lds() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
+
+// The 256 x 256 tile of the large-M GEMMs (dense and grouped): 8 waves as
+// 4 (m) x 2 (n), 64 x 128 per wave, two LDS stages of
+//   [A 256 x 128 B][B 256 x 128 B][A scales 256 x f32][B scales 64 x f32]
+// filled by 4 + 4 row-group DMAs per wave (rows (wave + 8 j) * 8 + L / 8)
+// and one scale DMA from waves 0-4.
+struct BigTile {
+  static constexpr int BM = 256, BN = 256, WM = 4, WN = 2, MT = 4, NT = 8, kWaves = 8;
+  static constexpr int kThreads = kWaves * kWave;
+  static constexpr int kOffB = BM * 128;
+  static constexpr int kOffSA = (BM + BN) * 128;
+  static constexpr int kOffSB = kOffSA + BM * 4;
+  static constexpr int kStage = kOffSB + 256;  // the B-scale DMA writes 64 lanes x 4 bytes
+  static constexpr int kLds = 2 * kStage;
+  static_assert(BM / 8 == 4 * kWaves && BN / 8 == 4 * kWaves, "4 DMAs of 8 rows per wave and operand");
+  static_assert(BN == 2 * 16 * NT && BM == 4 * 16 * MT, "wave tiles");
+  static_assert(kLds <= 160 * 1024, "LDS stages exceed the CU's LDS");
+};
 
 template <bool SCALED, int BM, int BN, int WM, int WN, int NS>
 struct TilePipe {
