@@ -822,15 +822,8 @@ constexpr int kMoeBM = 128;
 // workgroups past the used tiles.  BM: routes per block (the alignment's
 // block size).
 template <int BM = kMoeBM>
-__device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* __restrict__ offsets,
-                                         const int32_t* __restrict__ ntpp, int E, int TN,
-                                         int& e_out, int& mb_out, int& tn_out) {
-  const int used = min(ntpp[0] / BM * TN, max_tiles);
-  const int per = (used + kXcds - 1) / kXcds;
-  const int q = wg / kXcds;
-  if (q >= per) return false;
-  const int L = (wg % kXcds) * per + q;
-  if (L >= used) return false;
+__device__ __forceinline__ void moe_tile_decode(int L, const int32_t* __restrict__ offsets, int E, int TN,
+                                                int& e_out, int& mb_out, int& tn_out) {
   // largest e with offsets[e] / BM * TN <= L (empty experts collapse onto the next)
   int lo = 0, hi = E - 1;
   while (lo < hi) {
@@ -843,6 +836,19 @@ __device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* _
   e_out = lo;
   tn_out = local / nb;
   mb_out = b0 + local % nb;
+}
+
+template <int BM = kMoeBM>
+__device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* __restrict__ offsets,
+                                         const int32_t* __restrict__ ntpp, int E, int TN,
+                                         int& e_out, int& mb_out, int& tn_out) {
+  const int used = min(ntpp[0] / BM * TN, max_tiles);
+  const int per = (used + kXcds - 1) / kXcds;
+  const int q = wg / kXcds;
+  if (q >= per) return false;
+  const int L = (wg % kXcds) * per + q;
+  if (L >= used) return false;
+  moe_tile_decode<BM>(L, offsets, E, TN, e_out, mb_out, tn_out);
   return true;
 }
 
