@@ -869,7 +869,7 @@ using MoePipe = typename std::conditional<KIND == kFp8, MoePipeFp8, MoePipeBf16>
 
 template <int KIND, bool W13>
 __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
-    const uint8_t* __restrict__ act, const float* __restrict__ act_s, int topk, int K,
+    const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int topk, int K,
     const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles,
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int N, int I, float limit,
@@ -898,20 +898,28 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
       return min(n0 + j, N - 1);
     }
   };
-  auto arow = [&](int r) -> int64_t {  // activation row of tile row r
+  auto arow = [&](int r) -> int64_t {  // activation row of tile row r (-1: padding)
     const int rr = mb * BM + r;
-    if constexpr (W13) {
-      const int s = sorted[rr];
-      return s < numel ? static_cast<int64_t>(s / topk) : 0;
-    } else {
-      return rr;
-    }
+    const int s = sorted[rr];
+    if (s >= numel) return -1;
+    return W13 ? static_cast<int64_t>(s / topk) : rr;
   };
 
+  // W2 reads its activation rows through a buffer descriptor, where a padding
+  // row's lanes get an offset past the end and fetch nothing (only padding
+  // outputs, never stored, read those LDS bytes): its padding rows are rows
+  // of their own.  W13's padding rows all read token 0's row, already in L2
+  // (the buffer form measured up to 3 % slower there).
   P p;
+  const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(act, act_bytes);
+  uint32_t offA[P::kDmaA];
 #pragma unroll
   for (int j = 0; j < P::kDmaA; ++j) {
-    p.srcA[j] = act + arow(P::rowA(wave, lane, j)) * rowb + P::chunk(lane);
+    const int64_t ar = arow(P::rowA(wave, lane, j));
+    if constexpr (W13)
+      p.srcA[j] = act + max(ar, int64_t{0}) * rowb + P::chunk(lane);
+    else
+      offA[j] = ar >= 0 ? static_cast<uint32_t>(ar * rowb + P::chunk(lane)) : kBufferOff;
     p.ldsA[j] = (wave + j * P::kWaves) * 8 * 128;
   }
 #pragma unroll
@@ -921,7 +929,7 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
   }
   if constexpr (KIND == kFp8) {
     if (wave < BM / 64) {  // activation group scales of tile rows 64*wave + lane
-      p.srcS = reinterpret_cast<const uint8_t*>(act_s + arow(64 * wave + lane) * KS);
+      p.srcS = reinterpret_cast<const uint8_t*>(act_s + max(arow(64 * wave + lane), int64_t{0}) * KS);
       p.ldsS = P::kOffSA + 64 * wave * 4;
     } else {  // weight-block scales: W13 gate / up block, W2 the tile's two 128-row blocks
       const int slot = min(lane, 1);
@@ -1007,16 +1015,29 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
   // after each MFMA) while `cur` runs on MFMA.  Issuing the refill ahead of
   // the MFMAs rather than after them measured 5-7 % faster on the DeepSeek-V3
   // layer at T=4096 (W13 2083 -> 1936 us, W2 1160 -> 1101 us).
+  auto issue = [&](uint8_t* stage, int step) {
+    const uint32_t ks = static_cast<uint32_t>(step) * 128;
+#pragma unroll
+    for (int j = 0; j < P::kDmaA; ++j) {
+      if constexpr (W13)
+        dma16(p.srcA[j] + static_cast<int64_t>(step) * 128, stage + p.ldsA[j]);
+      else
+        buffer_dma16(ars, offA[j] + ks, stage + p.ldsA[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < P::kDmaB; ++j) dma16(p.srcB[j] + static_cast<int64_t>(step) * 128, stage + p.ldsB[j]);
+    if constexpr (KIND == kFp8) dma4(p.srcS + static_cast<int64_t>(step) * p.stepS, stage + p.ldsS);
+  };
   auto step = [&](int kb, const Frags& cur, Frags& nxt) {
     wait_lgkmcnt0();
     wait_vmcnt<(NS - 2) * P::kIPS>();
     barrier_lds();
-    p.issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
+    issue(smem_dyn + (kb % NS) * P::kStage, min(kb + NS, KS - 1));
     read(smem_dyn + ((kb + 1) % NS) * P::kStage, nxt);
     mma(cur);
   };
 #pragma unroll
-  for (int s = 0; s < NS; ++s) p.issue(smem_dyn + s * P::kStage, min(s, KS - 1));
+  for (int s = 0; s < NS; ++s) issue(smem_dyn + s * P::kStage, min(s, KS - 1));
   wait_vmcnt<(NS - 1) * P::kIPS>();
   barrier_lds();
   Frags f0, f1;
@@ -1859,8 +1880,10 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
   } else {
     int rc = raise_dma_lds<KIND, true>();
     if (rc) return rc;
+    const int64_t abytes = static_cast<int64_t>(T) * H * KindBytes<KIND>::kAct / KindBytes<KIND>::kElems;
+    VMAMD_REQUIRE(abytes < (1ll << 31), "moe w13: activations past 2 GiB for the grouped GEMM");
     moe_gemm_dma_kernel<KIND, true><<<xcd_grid(tiles), 512, MoePipe<KIND>::kLds, st>>>(
-        xa, xs, topk, H, sorted, offs, ntpp, E, numel, tiles, w13,
+        xa, static_cast<int>(abytes), xs, topk, H, sorted, offs, ntpp, E, numel, tiles, w13,
         static_cast<const float*>(w13_s), 2 * I, I, limit, route_w, a2, a2s, nullptr);
   }
   return check_launch("moe w13 (gemm)");
@@ -1939,8 +1962,10 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
     const int tiles = max_blocks * ((H + 255) / 256);
     int rc = raise_dma_lds<KIND, false>();
     if (rc) return rc;
+    const int64_t abytes = cap * I * KindBytes<KIND>::kAct / KindBytes<KIND>::kElems;
+    VMAMD_REQUIRE(abytes < (1ll << 31), "moe w2: activations past 2 GiB for the grouped GEMM");
     moe_gemm_dma_kernel<KIND, false><<<xcd_grid(tiles), 512, MoePipe<KIND>::kLds, st>>>(
-        a2, a2s, 1, I, sorted, offs, ntpp, E, numel, tiles, w2, static_cast<const float*>(w2_s), H,
+        a2, static_cast<int>(abytes), a2s, 1, I, sorted, offs, ntpp, E, numel, tiles, w2, static_cast<const float*>(w2_s), H,
         I, 0.f, route_w, nullptr, nullptr, y);
   }
   return check_launch("moe w2 (gemm)");
