@@ -297,7 +297,7 @@ int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H, const 
  * block_size: 16 = decode (expert-major GEMV, each weight row streamed once
  * per call), 128 = prefill (grouped MFMA GEMM over 128-route blocks), 256 =
  * long prefill (256-route blocks; same results as 128).  The fused call
- * takes 256 from 128 routes per expert.
+ * takes 256 from 128 routes per expert (fp8 and bf16).
  *
  * W13:  a = bf16(silu(h_gate) * h_up), h = bf16(W13[e] . q(x[t])), then a is
  *       quantised per 1x128 group into a2q (fp8) / a2s (f32, [rows, I/128]).

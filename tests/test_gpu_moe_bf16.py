@@ -97,6 +97,44 @@ def test_bf16_moe_expert_map(path):
     _check(_run(x, w13, w2, w, gids, path, emap=emap), _oracle(x, w13, w2, w, gids, emap=emap))
 
 
+def test_bf16_moe_256_route_blocks_vs_oracle():
+    """From 128 routes per expert the grouped GEMMs take 256-route blocks (1200
+    routes on 8 experts); H = 640 leaves the last 256-row W2 tile half outside
+    the output, I = 384 gives three 128-column W13 tiles."""
+    from vllm_musa_amd import synthetic
+    w13, w2 = _weights(8, 640, 384, 51)
+    x = synthetic.activations(600, 640, 52)
+    w, ids = _routing(600, 8, 2, 53)
+    _check(_run(x, w13, w2, w, ids, "gemm"), _oracle(x, w13, w2, w, ids))
+
+
+@pytest.mark.parametrize("variant", ["plain", "expert_map", "limit"])
+def test_bf16_moe_256_route_blocks_match_128(variant):
+    """256- and 128-route blocks give the same bits (each route's row sees the
+    same K order and roundings in either tile)."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.fused_moe import MoeStages
+    w13, w2 = _weights(8, 512, 256, 61)
+    x = synthetic.activations(700, 512, 62)
+    w, ids = _routing(700, 8, 2, 63)
+    emap, limit = None, None
+    if variant == "expert_map":
+        g = torch.Generator().manual_seed(64)
+        ids = torch.stack([torch.randperm(12, generator=g)[:2] for _ in range(700)]).to(torch.int32).to(DEV)
+        emap = torch.full((12,), -1, dtype=torch.int32)
+        emap[4:] = torch.arange(8, dtype=torch.int32)
+        emap = emap.to(DEV)
+    if variant == "limit":
+        limit = 7.0
+    big = MoeStages(x, w13, None, w2, None, w, ids, path="gemm", expert_map=emap, swiglu_limit=limit)
+    assert big.block_m == 256
+    small = MoeStages(x, w13, None, w2, None, w, ids, path="gemm", expert_map=emap, swiglu_limit=limit,
+                      block_m=128)
+    a = big.run().clone()
+    assert torch.equal(a, small.run())
+    assert torch.equal(_run(x, w13, w2, w, ids, "gemm", emap=emap, limit=limit), a)
+
+
 def test_bf16_moe_paths_agree_and_deterministic():
     from vllm_musa_amd import synthetic
     w13, w2 = _weights(32, 2048, 768, 21)

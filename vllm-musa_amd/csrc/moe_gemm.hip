@@ -1157,7 +1157,7 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
 // routed weight.
 constexpr int kMoeBigBM = 256;
 
-template <bool W13>
+template <int KIND, bool W13>
 __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_s_bytes,
     int topk, int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
@@ -1175,7 +1175,9 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int wm = wave / P::WN, wn = wave % P::WN;
   const int li = lane % 16, lg = lane / 16;
-  const int KS = K / 128, NB = (N + 127) / 128;
+  constexpr bool kScaled = KIND == kFp8;
+  const int KS = K / KindBytes<KIND>::kElems, NB = (N + 127) / 128;
+  const int rowb = KS * 128;  // bytes per activation / weight row
   const int64_t base = static_cast<int64_t>(mb) * BM;
 
   auto wrow = [&](int j) -> int {  // weight row of local tile row j
@@ -1196,21 +1198,22 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   };
 
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(act, act_bytes);
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(w + static_cast<int64_t>(e) * N * K, N * K);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(w + static_cast<int64_t>(e) * N * rowb, N * rowb);
   const uint32_t chunk = static_cast<uint32_t>(((lane % 8) ^ (lane / 8)) * 16);
   uint32_t offA[4], offB[4];
   uint64_t liveA[4];  // activation row groups holding a route (padding groups load nothing)
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = (wave + 8 * j) * 8 + lane / 8;
-    offA[j] = static_cast<uint32_t>(arow(r)) * K + chunk;
-    offB[j] = static_cast<uint32_t>(wrow(r)) * K + chunk;
+    offA[j] = static_cast<uint32_t>(arow(r)) * rowb + chunk;
+    offB[j] = static_cast<uint32_t>(wrow(r)) * rowb + chunk;
     liveA[j] = __builtin_amdgcn_ballot_w64(sorted[base + r] < numel);
   }
-  uint32_t offS, stepS = 4;
-  int ldsS;
-  __amdgpu_buffer_rsrc_t rs;
-  if (wave < BM / 64) {  // activation scales of tile rows 64 * wave + lane
+  uint32_t offS = 0, stepS = 4;
+  int ldsS = 0;
+  __amdgpu_buffer_rsrc_t rs = buffer_rsrc(act_s, 0);
+  if (!kScaled) {
+  } else if (wave < BM / 64) {  // activation scales of tile rows 64 * wave + lane
     rs = buffer_rsrc(act_s, act_s_bytes);
     offS = static_cast<uint32_t>(arow(64 * wave + lane)) * KS * 4;
     ldsS = P::kOffSA + 64 * wave * 4;
@@ -1228,7 +1231,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
       if (liveA[j]) buffer_dma16(ra, offA[j] + ks, stage + (wave + 8 * j) * 8 * 128);
 #pragma unroll
     for (int j = 0; j < 4; ++j) buffer_dma16(rb, offB[j] + ks, stage + P::kOffB + (wave + 8 * j) * 8 * 128);
-    if (wave <= BM / 64) buffer_dma4(rs, offS + step * stepS, stage + ldsS);
+    if (kScaled && wave <= BM / 64) buffer_dma4(rs, offS + step * stepS, stage + ldsS);
   };
   // Padding routes close a block, so a wave whose first route is padding
   // holds none.
@@ -1243,13 +1246,16 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   const int nw = wn * 16 * NT;  // the wave's first local weight row
 
   // One K step from LDS stage `st` (see gemm_fp8_big_kernel).  W13: n tile
-  // nt takes the gate (even) or up (odd) block scale.
+  // nt takes the gate (even) or up (odd) block scale.  bf16: two chained
+  // MFMAs per fragment pair into the accumulators, no scales.
   auto mma = [&](const uint8_t* st) {
-    const float sb0 = lds_load<float>(st, P::kOffSB + (W13 ? 0 : 4 * wn));
-    const float sb1 = W13 ? lds_load<float>(st, P::kOffSB + 4) : sb0;
-    float sa[MT], sc[MT][2];
+    float sb0 = 0.f, sb1 = 0.f, sa[MT], sc[MT][2];
+    if constexpr (kScaled) {
+      sb0 = lds_load<float>(st, P::kOffSB + (W13 ? 0 : 4 * wn));
+      sb1 = W13 ? lds_load<float>(st, P::kOffSB + 4) : sb0;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) sa[mt] = lds_load<float>(st, P::kOffSA + (wm * 64 + mt * 16 + li) * 4);
+      for (int mt = 0; mt < MT; ++mt) sa[mt] = lds_load<float>(st, P::kOffSA + (wm * 64 + mt * 16 + li) * 4);
+    }
     v8i wf[2], x[MT];
     wf[0] = lds_frag(st + P::kOffB, nw + li, lg);
 #pragma unroll
@@ -1261,12 +1267,15 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     for (int i = 0; i <= NI; ++i) {
       const int nt = i / MT, mt = i % MT;
       if (i < NI) {
-        t[i & 1] = mfma_fp8(wf[nt & 1], x[mt], zero);
+        if constexpr (kScaled)
+          t[i & 1] = mfma_fp8(wf[nt & 1], x[mt], zero);
+        else
+          acc[mt][nt] = mfma_bf16x2(wf[nt & 1], x[mt], acc[mt][nt]);
         __builtin_amdgcn_sched_barrier(0);
         if (mt == 0 && nt + 1 < NT) wf[(nt + 1) & 1] = lds_frag(st + P::kOffB, nw + (nt + 1) * 16 + li, lg);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (i > 0) {
+      if (kScaled && i > 0) {
         const int j = i - 1, jm = j % MT, jn = j / MT;
         if (jn < 2) sc[jm][jn] = sa[jm] * (jn ? sb1 : sb0);  // at first use
         fma4(acc[jm][jn], t[j & 1], sc[jm][W13 ? (jn & 1) : 0]);
@@ -1296,6 +1305,23 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
         const int r = sorted[base + wm * 64 + mt * 16 + li];
         rw[mt] = r < numel ? route_w[r] : 0.0f;
       }
+    }
+    if constexpr (!kScaled) {  // bf16 activation
+      uint16_t* a2b = reinterpret_cast<uint16_t*>(a2);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int64_t row = base + wm * 64 + mt * 16 + li;
+#pragma unroll
+        for (int q = 0; q < NT / 2; ++q) {
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            o[r] = swiglu_bf16(bf16r(acc[mt][2 * q][r] * rw[mt]), bf16r(acc[mt][2 * q + 1][r] * rw[mt]), limit);
+          const int col = n0 + (4 * wn + q) * 16 + 4 * lg;
+          *reinterpret_cast<uint2*>(a2b + row * I + col) = pack_bf16x4(o[0], o[1], o[2], o[3]);
+        }
+      }
+      return;
     }
     // SiLU-and-mul, row amax across the 2 n-waves through LDS, 1x128 quantiser.
     float* red = reinterpret_cast<float*>(smem_dyn);  // [WN][BM]
@@ -1744,11 +1770,11 @@ static int raise_dma_lds() {
   return VMAMD_OK;
 }
 
-template <bool W13>
+template <int KIND, bool W13>
 static int raise_big_lds() {
   static bool done = false;
   if (done) return VMAMD_OK;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_big_kernel<W13>),
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_big_kernel<KIND, W13>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, BigTile::kLds) != hipSuccess) {
     set_error("moe gemm: cannot raise the LDS limit of the grouped GEMM kernel");
     return VMAMD_ERR_HIP;
@@ -1859,14 +1885,15 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
     }
     return check_launch("moe w13 (activation)");
   }
-  if constexpr (KIND == kFp8) {
+  if constexpr (KIND != kW4) {
     if (block_m == kMoeBigBM) {
-      VMAMD_REQUIRE(big_fits(T, H, 2ll * I, E), "moe w13: operands past 2 GiB for the 256-route GEMM");
+      constexpr int eb = KIND == kBf16 ? 2 : 1;  // bytes per element
+      VMAMD_REQUIRE(big_fits(T, H * eb, 2ll * I, E), "moe w13: operands past 2 GiB for the 256-route GEMM");
       const int tiles = static_cast<int>((cap + kMoeBigBM - 1) / kMoeBigBM) * (I / 128);
-      int rc = raise_big_lds<true>();
+      int rc = raise_big_lds<KIND, true>();
       if (rc) return rc;
-      moe_big_kernel<true><<<xcd_grid(tiles), BigTile::kThreads, BigTile::kLds, st>>>(
-          xa, static_cast<int>(static_cast<int64_t>(T) * H), xs, static_cast<int>(static_cast<int64_t>(T) * (H / 128) * 4),
+      moe_big_kernel<KIND, true><<<xcd_grid(tiles), BigTile::kThreads, BigTile::kLds, st>>>(
+          xa, static_cast<int>(static_cast<int64_t>(T) * H * eb), xs, static_cast<int>(static_cast<int64_t>(T) * (H / 128) * 4),
           topk, H, sorted, offs, ntpp, E, numel, tiles, w13, static_cast<const float*>(w13_s), 2 * I, I, limit,
           route_w, a2, a2s, nullptr);
       return check_launch("moe w13 (gemm)");
@@ -1941,14 +1968,15 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
         scratch, s2, numel, H, topk_ids, emap, emap_len, E, yscale, y);
     return check_launch("moe w2 (reduce)");
   }
-  if constexpr (KIND == kFp8) {
+  if constexpr (KIND != kW4) {
     if (block_m == kMoeBigBM) {
-      VMAMD_REQUIRE(big_fits(cap, I, H, E), "moe w2: operands past 2 GiB for the 256-route GEMM");
+      constexpr int eb = KIND == kBf16 ? 2 : 1;  // bytes per element
+      VMAMD_REQUIRE(big_fits(cap, I * eb, H, E), "moe w2: operands past 2 GiB for the 256-route GEMM");
       const int tiles = static_cast<int>((cap + kMoeBigBM - 1) / kMoeBigBM) * ((H + 255) / 256);
-      int rc = raise_big_lds<false>();
+      int rc = raise_big_lds<KIND, false>();
       if (rc) return rc;
-      moe_big_kernel<false><<<xcd_grid(tiles), BigTile::kThreads, BigTile::kLds, st>>>(
-          a2, static_cast<int>(cap * I), a2s, static_cast<int>(cap * (I / 128) * 4), 1, I, sorted, offs, ntpp, E,
+      moe_big_kernel<KIND, false><<<xcd_grid(tiles), BigTile::kThreads, BigTile::kLds, st>>>(
+          a2, static_cast<int>(cap * I * eb), a2s, static_cast<int>(cap * (I / 128) * 4), 1, I, sorted, offs, ntpp, E,
           numel, tiles, w2, static_cast<const float*>(w2_s), H, I, 0.f, route_w, nullptr, nullptr, y);
       return check_launch("moe w2 (gemm)");
     }
@@ -2016,14 +2044,16 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
 // flushed): fp8 DeepSeek-V3 (E=256, H=7168, I=2048, top-8) between 2 and 3
 // routes per expert (T=64 / 96); bf16 (E=128, H=2048, I=768) and w4afp8
 // (E=128, H=4096, I=1536) between 8 and 16 (T=128 / 256).
-// fp8 layers with at least 128 routes per expert take 256-route blocks
-// (moe_big_kernel): measured on DeepSeek-V3 (E=256, H=7168, I=2048, top-8),
-// W13 / W2: T=3072 +3 % / -3 %, T=4096 -1 % / -6 %, T=6144 -8 % / -10 %,
-// T=8192 -2 % / -10 % against 128-route blocks.
+// fp8 and bf16 layers with at least 128 routes per expert take 256-route
+// blocks (moe_big_kernel), against 128-route blocks, W13 / W2: fp8
+// DeepSeek-V3 (E=256, H=7168, I=2048, top-8) T=3072 +3 % / -3 %, T=4096
+// -1 % / -6 %, T=6144 -8 % / -10 %, T=8192 -2 % / -10 %; bf16 (E=128,
+// H=2048, I=768, top-8) T=2048 -7 % / -10 %, T=4096 -12 % / 0, T=8192
+// -10 % / -17 %.
 static int moe_block_m(int64_t T, int topk, int E, int path, int kind) {
   if (path == VMAMD_MOE_PATH_GEMV) return kGemvBlock;
   const int64_t routes = T * topk;
-  const int grouped = kind == kFp8 && routes >= 128 * static_cast<int64_t>(E) ? kMoeBigBM : kMoeBM;
+  const int grouped = kind != kW4 && routes >= 128 * static_cast<int64_t>(E) ? kMoeBigBM : kMoeBM;
   if (path == VMAMD_MOE_PATH_GEMM) return grouped;
   const int64_t limit = kind == kFp8 ? (5 * static_cast<int64_t>(E)) / 2 : 12 * static_cast<int64_t>(E);
   return routes <= limit ? kGemvBlock : grouped;

@@ -237,11 +237,11 @@ class MoeStages:
         # 2.5 routes per expert for fp8, 12 for bf16 (measured crossovers).
         limit = (5 * self.e) // 2 if self.fp8 else 12 * self.e
         gemv = path == "gemv" or (path == "auto" and numel <= limit)
-        # grouped GEMMs: 256-route blocks for fp8 from 128 routes per expert
-        self.block_m = 16 if gemv else 256 if self.fp8 and numel >= 128 * self.e else 128
-        if block_m is not None:  # the grouped GEMMs' route tile: 128, or 256 (fp8)
-            if gemv or block_m not in (128, 256) or (block_m == 256 and not self.fp8):
-                raise ValueError(f"block_m {block_m} needs the grouped GEMMs (128, or 256 for fp8)")
+        # grouped GEMMs: 256-route blocks from 128 routes per expert
+        self.block_m = 16 if gemv else 256 if numel >= 128 * self.e else 128
+        if block_m is not None:  # the grouped GEMMs' route tile: 128 or 256
+            if gemv or block_m not in (128, 256):
+                raise ValueError(f"block_m {block_m} needs the grouped GEMMs (128 or 256)")
             self.block_m = block_m
         self.w13, self.w2 = w13.contiguous(), w2.contiguous()
         if self.fp8:
