@@ -139,6 +139,53 @@ def test_fp8_moe_expert_map(path):
     _check(out, _oracle(x, w13, s13, w2, s2, w, gids, emap=emap))
 
 
+@pytest.mark.parametrize("T,K,variant", [(1, 4, "plain"), (2, 8, "plain"), (1, 8, "expert_map"),
+                                         (2, 4, "limit"), (1, 8, "duplicate")])
+def test_fp8_moe_direct_decode_matches_grouped(T, K, variant):
+    """Up to 16 routes the fused decode call gives every route its own GEMV
+    slot (no alignment) and sums the top-k inside the W2 launch; its output
+    equals the stage-by-stage grouped decode path (alignment, GEMVs over the
+    active experts, moe_sum) bit for bit, and the oracle.  Variants: an expert
+    map that drops routes, the clamped SwiGLU, and a token that names one
+    expert twice."""
+    from vllm_musa_amd.fused_moe import Fp8MoeStages
+    E = 16
+    x, w13, s13, w2, s2, w, ids = _case(T, E, 1024, 512, K, seed=131 + 10 * T + K)
+    emap, limit = None, None
+    if variant == "expert_map":  # global ids 0..23, local experts = global 8..23
+        g = torch.Generator().manual_seed(137)
+        ids = torch.stack([torch.randperm(24, generator=g)[:K] for _ in range(T)]).to(torch.int32).to(DEV)
+        emap = torch.full((24,), -1, dtype=torch.int32)
+        emap[8:] = torch.arange(16, dtype=torch.int32)
+        emap = emap.to(DEV)
+    if variant == "limit":
+        limit = 7.0
+    if variant == "duplicate":
+        ids[0, 1] = ids[0, 0]
+    st = Fp8MoeStages(x, w13, s13, w2, s2, w, ids, path="gemv", expert_map=emap, swiglu_limit=limit)
+    assert st.block_m == 16
+    grouped = st.run().clone()
+    direct = _run(x, w13, s13, w2, s2, w, ids, "gemv", emap=emap, limit=limit)
+    assert torch.equal(direct, grouped)
+    if limit is None:
+        _check(direct, _oracle(x, w13, s13, w2, s2, w, ids, emap=emap))
+
+
+def test_fp8_moe_direct_decode_dsv3_t1():
+    """The DeepSeek-V3 layer at T=1 (8 routes, grouped sigmoid routing): the
+    direct decode call equals the grouped decode stages bit for bit."""
+    from vllm_musa_amd import grouped_topk, synthetic
+    from vllm_musa_amd.fused_moe import Fp8MoeStages
+    E, H, I = 256, 7168, 2048
+    w13, s13, w2, s2 = synthetic.moe_fp8_weights(E, H, I, seed=3000)
+    x = synthetic.activations(1, H, 3101)
+    logits = synthetic.router_logits(1, E, 3102)
+    bias = synthetic.score_bias(E, 3003)
+    w, ids = grouped_topk(x, logits, 8, True, 8, 4, "sigmoid", 2.5, bias)
+    grouped = Fp8MoeStages(x, w13, s13, w2, s2, w, ids, path="gemv").run().clone()
+    assert torch.equal(_run(x, w13, s13, w2, s2, w, ids, "auto"), grouped)
+
+
 def test_fp8_moe_paths_agree():
     case = _case(48, 32, 2048, 768, 8, seed=21)
     a = _run(*case, path="gemv").float()

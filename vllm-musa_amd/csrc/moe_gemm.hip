@@ -151,28 +151,64 @@ __device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t o
 template <int MAXB, int KIND, bool VS>
 constexpr bool gemv_stream1() { return MAXB == 1 && (KIND != kW4 || VS); }
 
-template <int MAXB, int KIND, bool VS = false>
-__global__ __launch_bounds__(kMoeGemvWaves * kWave, MAXB == 1 ? 3 : 2) void
+// Route slots of the decode GEMVs.  kGemvGrouped: blockIdx.y walks the
+// active experts of the alignment, each wave one 16-row tile of that expert
+// for all its routes.  kGemvDirect (one token): blockIdx.y is the route, its
+// expert read from topk_ids, no alignment.  kGemvCombine (W2, one token per
+// blockIdx.y): the workgroup is one 16-row tile, wave k computes route k and
+// the top-k sum is taken in LDS (slot order, as moe_sum), so the layer output
+// is written directly.
+constexpr int kGemvGrouped = 0, kGemvDirect = 1, kGemvCombine = 2;
+constexpr int kMaxCombineSlots = 8;
+
+// Local expert of a route, -1 when it is dropped (negative id, not mapped,
+// or past the local experts) -- the rule of the alignment and of moe_sum.
+__device__ __forceinline__ int route_expert(const int32_t* __restrict__ ids, int64_t route,
+                                            const int32_t* __restrict__ emap, int64_t emap_len, int E) {
+  int e = ids[route];
+  if (e >= 0 && emap) e = e < emap_len ? emap[e] : -1;
+  return e >= 0 && e < E ? e : -1;
+}
+
+template <int MAXB, int KIND, bool VS = false, int MODE = kGemvGrouped>
+__global__ __launch_bounds__((MODE == kGemvCombine ? kMaxCombineSlots : kMoeGemvWaves) * kWave, MAXB == 1 ? 3 : 2) void
 moe_gemv_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_div,
     int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ active, const int32_t* __restrict__ num_active,
     const uint8_t* __restrict__ w, const void* __restrict__ ws, int N, int numel, int splits,
-    float* __restrict__ partial, const float* __restrict__ route_w, uint16_t* __restrict__ y) {
+    float* __restrict__ partial, const float* __restrict__ route_w, uint16_t* __restrict__ y,
+    const int32_t* __restrict__ ids, const int32_t* __restrict__ emap, int64_t emap_len, int E_,
+    uint16_t* __restrict__ comb) {
   using KB_ = KindBytes<KIND>;
   constexpr int U = kGemvU;
   constexpr bool kStream1 = gemv_stream1<MAXB, KIND, VS>();
+  static_assert(MODE == kGemvGrouped || MAXB == 1, "direct route slots take one route per block");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const int li = lane % 16, lg = lane / 16;
-  const int ntile = blockIdx.x * kMoeGemvWaves + wave;
-  if (ntile * 16 >= N) return;  // wave-uniform, no barriers in this kernel
-  const int slot = blockIdx.y;
-  // The exit test reads both values, so both loads are in flight together;
-  // active[] has one entry per expert and gridDim.y never exceeds the expert
-  // count, so the read is in bounds.
-  const int e = active[slot];
-  const int na = num_active[0];
-  if (slot >= na || e < 0) return;
+  const int ntile = MODE == kGemvCombine ? static_cast<int>(blockIdx.x) : blockIdx.x * kMoeGemvWaves + wave;
+  // Wave-uniform (workgroup-uniform for kGemvCombine, whose only barrier
+  // comes after it).
+  if (ntile * 16 >= N) return;
+  const int slot = MODE == kGemvCombine ? static_cast<int>(blockIdx.y * (blockDim.x / kWave)) + wave
+                                        : static_cast<int>(blockIdx.y);
+  int e;
+  bool dead = false;  // kGemvCombine: a dropped route still takes part in the sum's barrier
+  if constexpr (MODE == kGemvGrouped) {
+    // The exit test reads both values, so both loads are in flight together;
+    // active[] has one entry per expert and gridDim.y never exceeds the
+    // expert count, so the read is in bounds.
+    e = active[slot];
+    const int na = num_active[0];
+    if (slot >= na || e < 0) return;
+  } else if constexpr (MODE == kGemvDirect) {
+    e = route_expert(ids, slot, emap, emap_len, E_);
+    if (e < 0) return;
+  } else {
+    e = route_expert(ids, slot, emap, emap_len, E_);
+    dead = e < 0;
+    e = dead ? 0 : e;
+  }
   const int split = blockIdx.z;
   const int KS = K / KB_::kElems;                    // K steps
   const int arowb = KS * KB_::kAct;
@@ -388,21 +424,26 @@ moe_gemv_kernel(
     }
   };
 
-  const int seg0 = offsets[e];
-  const int nblk = (offsets[e + 1] - seg0) / kGemvBlock;  // >= 1 for an active expert
+  int seg0 = 0, nblk = 1;
+  if constexpr (MODE == kGemvGrouped) {
+    seg0 = offsets[e];
+    nblk = (offsets[e + 1] - seg0) / kGemvBlock;  // >= 1 for an active expert
+  }
   int b0 = 0;
-  do {
+  if (!dead) do {
     load_w(kb0);  // first group: in flight while the routes are resolved
     const int nb = min(MAXB, nblk - b0);
     int rr[MAXB];
 #pragma unroll
     for (int b = 0; b < MAXB; ++b) {
       int r = numel;
-      if (b < nb) {
-        const int32_t* ids = sorted + seg0 + (b0 + b) * kGemvBlock;
+      if constexpr (MODE != kGemvGrouped) {
+        r = li == 0 ? slot : numel;  // column 0 of the block holds the route
+      } else if (b < nb) {
+        const int32_t* bids = sorted + seg0 + (b0 + b) * kGemvBlock;
         int sid[kGemvBlock];
 #pragma unroll
-        for (int j = 0; j < kGemvBlock; ++j) sid[j] = ids[j];
+        for (int j = 0; j < kGemvBlock; ++j) sid[j] = bids[j];
         r = sid[0];
 #pragma unroll
         for (int j = 1; j < kGemvBlock; ++j) r = li == j ? sid[j] : r;
@@ -426,7 +467,9 @@ moe_gemv_kernel(
       if (b >= nb || rr[b] < 0) continue;
       const int r = rr[b];
       const v4f a = KIND == kW4 ? acc[b] * kW4Unit : acc[b];
-      if (y) {
+      if constexpr (MODE == kGemvCombine) {
+        break;  // the sum below
+      } else if (y) {
         const float rw = route_w ? route_w[r] : 1.0f;
         *reinterpret_cast<uint2*>(y + static_cast<int64_t>(r) * N + n) =
             pack_bf16x4(a[0] * rw, a[1] * rw, a[2] * rw, a[3] * rw);
@@ -437,6 +480,26 @@ moe_gemv_kernel(
     }
     b0 += MAXB;
   } while (b0 < nblk);
+  if constexpr (MODE == kGemvCombine) {
+    // y_k = bf16(acc * w_k) for the 16 rows (lanes of column 0), then the
+    // layer output = bf16(sum over k in slot order of y_k), dropped routes
+    // contributing nothing (+0.0 leaves the fp32 sum unchanged: it starts at
+    // +0.0 and an exact cancellation gives +0.0).
+    __shared__ float part[kMaxCombineSlots * 16];
+    if (li == 0) {
+      const v4f a = dead ? zero : KIND == kW4 ? acc[0] * kW4Unit : acc[0];
+      const float rw = route_w && !dead ? route_w[slot] : 1.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) part[wave * 16 + 4 * lg + q] = dead ? 0.0f : bf16r(a[q] * rw);
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+      const int nslots = blockDim.x / kWave;
+      float s = 0.0f;
+      for (int k = 0; k < nslots; ++k) s += part[k * 16 + lane];
+      comb[static_cast<int64_t>(blockIdx.y) * N + ntile * 16 + lane] = f32_to_bf16(s);
+    }
+  }
 }
 
 // Gate/up sums of 8 consecutive columns c0.. of route r: split partials in a
@@ -1808,19 +1871,32 @@ static bool gemv_one_block(int64_t numel, int E) { return numel <= 8 * static_ca
 
 template <int KIND, typename... Args>
 static void launch_gemv(dim3 grid, hipStream_t st, bool one_block, bool vs, Args... args) {
+  const int32_t* none = nullptr;
   if constexpr (KIND != kBf16) {
     if (vs) {
       if (one_block)
-        moe_gemv_kernel<1, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
+        moe_gemv_kernel<1, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr);
       else
-        moe_gemv_kernel<4, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
+        moe_gemv_kernel<4, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr);
       return;
     }
   }
   if (one_block)
-    moe_gemv_kernel<1, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
+    moe_gemv_kernel<1, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr);
   else
-    moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args...);
+    moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr);
+}
+
+// The decode GEMV with direct route slots (kGemvDirect / kGemvCombine).
+template <int KIND, int MODE, typename... Args>
+static void launch_gemv_direct(dim3 grid, int threads, hipStream_t st, bool vs, Args... args) {
+  if constexpr (KIND != kBf16) {
+    if (vs) {
+      moe_gemv_kernel<1, KIND, true, MODE><<<grid, threads, 0, st>>>(args...);
+      return;
+    }
+  }
+  moe_gemv_kernel<1, KIND, false, MODE><<<grid, threads, 0, st>>>(args...);
 }
 
 // True when a GEMV over K may read its scales U at a time: K/128 a multiple
@@ -1843,6 +1919,37 @@ static bool gemv_vector_scales(int64_t K, const void* act_s, const void* w_s) {
 // block corrections xcorr, xs the token row scales; the decode path writes
 // a2 (w4 order) with a2s and a2corr, the prefill path the bf16 activation to
 // a2 (quantised per row by the caller).
+// The decode path's activation: split-K sum of the W13 partials, SwiGLU and
+// a2 (kFp8: 1x128 quantiser; kW4: per-row quantiser in w4 order; kBf16: the
+// bf16 activation).
+template <int KIND>
+static int launch_act_decode(const float* scratch, int s13, int numel, int I, float limit,
+                             const float* route_w, const float* xs, int topk, uint8_t* a2,
+                             float* a2s, float* a2corr, hipStream_t st) {
+  if constexpr (KIND == kFp8) {
+    const int64_t groups = static_cast<int64_t>(numel) * (I / 128);
+    const int blocks = static_cast<int>((groups + 15) / 16);
+#define VMAMD_ACTQ(S) \
+  moe_act_quant_kernel<S><<<blocks, 256, 0, st>>>(scratch, s13, numel, I, limit, route_w, a2, a2s)
+    switch (s13) {
+      case 1: VMAMD_ACTQ(1); break;
+      case 2: VMAMD_ACTQ(2); break;
+      case 3: VMAMD_ACTQ(3); break;
+      case 4: VMAMD_ACTQ(4); break;
+      default: VMAMD_ACTQ(0); break;
+    }
+#undef VMAMD_ACTQ
+  } else if constexpr (KIND == kW4) {  // a2: fp8 [numel, I], a2s: row scales
+    moe_act_rowquant_w4_kernel<<<numel, kRowThreads, 0, st>>>(scratch, s13, numel, I, limit, xs,
+                                                              topk, a2, a2s, a2corr);
+  } else {
+    const int64_t chunks = static_cast<int64_t>(numel) * (I / 8);
+    moe_act_bf16_kernel<KIND><<<static_cast<int>((chunks + 255) / 256), 256, 0, st>>>(
+        scratch, s13, numel, I, limit, xs, topk, route_w, reinterpret_cast<uint16_t*>(a2));
+  }
+  return check_launch("moe w13 (activation)");
+}
+
 template <int KIND>
 static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, int T, int H, int topk,
                       const int32_t* sorted, int64_t cap, int block_m, const int32_t* offs,
@@ -1862,28 +1969,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
                       static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr));
     int rc = check_launch("moe w13 (gemv)");
     if (rc) return rc;
-    if constexpr (KIND == kFp8) {
-      const int64_t groups = static_cast<int64_t>(numel) * (I / 128);
-      const int blocks = static_cast<int>((groups + 15) / 16);
-#define VMAMD_ACTQ(S) \
-  moe_act_quant_kernel<S><<<blocks, 256, 0, st>>>(scratch, s13, numel, I, limit, route_w, a2, a2s)
-      switch (s13) {
-        case 1: VMAMD_ACTQ(1); break;
-        case 2: VMAMD_ACTQ(2); break;
-        case 3: VMAMD_ACTQ(3); break;
-        case 4: VMAMD_ACTQ(4); break;
-        default: VMAMD_ACTQ(0); break;
-      }
-#undef VMAMD_ACTQ
-    } else if constexpr (KIND == kW4) {  // a2: fp8 [numel, I], a2s: row scales
-      moe_act_rowquant_w4_kernel<<<numel, kRowThreads, 0, st>>>(scratch, s13, numel, I, limit, xs,
-                                                                topk, a2, a2s, a2corr);
-    } else {
-      const int64_t chunks = static_cast<int64_t>(numel) * (I / 8);
-      moe_act_bf16_kernel<KIND><<<static_cast<int>((chunks + 255) / 256), 256, 0, st>>>(
-          scratch, s13, numel, I, limit, xs, topk, route_w, reinterpret_cast<uint16_t*>(a2));
-    }
-    return check_launch("moe w13 (activation)");
+    return launch_act_decode<KIND>(scratch, s13, numel, I, limit, route_w, xs, topk, a2, a2s, a2corr, st);
   }
   if constexpr (KIND != kW4) {
     if (block_m == kMoeBigBM) {
@@ -2038,6 +2124,44 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   return w;
 }
 
+// One or two tokens on the fp8 decode path (at most kDirectMaxRoutes routes,
+// top-k <= kMaxCombineSlots): every route is its own GEMV slot, so the
+// alignment is skipped (the 1x128 quantiser of x runs alone), and the W2
+// GEMV sums the top-k in the same launch.  Each route reads its expert's
+// weights; with more tokens, routes that share an expert would read them
+// again, which the grouped slots avoid.
+constexpr int kDirectMaxRoutes = 16;
+static int fused_direct_fp8(const uint16_t* x, int T, int H, const uint8_t* w13, const float* w13_s,
+                            const uint8_t* w2, const float* w2_s, int E, int I, int topk,
+                            const int32_t* topk_ids, const int32_t* emap, int64_t emap_len,
+                            float limit, const float* w13_rw, const float* w2_rw, uint8_t* xq,
+                            float* xs, float* scratch, uint8_t* a2, float* a2s, uint16_t* out,
+                            hipStream_t st) {
+  const int numel = T * topk;
+  const int32_t* none = nullptr;
+  int rc = vmamd_per_token_group_quant_fp8(x, kBF16, T, H, H, 128, 1e-10f, -448.f, 448.f, xq, xs,
+                                           H / 128, 1, st);
+  if (rc) return rc;
+  const int s13 = w13_splits(numel, E, H, I, kFp8);
+  const dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, numel, s13);
+  launch_gemv_direct<kFp8, kGemvDirect>(
+      g13, kMoeGemvWaves * kWave, st, gemv_vector_scales<kFp8>(H, xs, w13_s), static_cast<const uint8_t*>(xq),
+      gemv_act_bytes<kFp8>(T, H), static_cast<const float*>(xs), topk, H, none, none, none, none, w13,
+      static_cast<const void*>(w13_s), 2 * I, numel, s13, scratch, static_cast<const float*>(nullptr),
+      static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E, static_cast<uint16_t*>(nullptr));
+  rc = check_launch("moe w13 (gemv)");
+  if (rc) return rc;
+  rc = launch_act_decode<kFp8>(scratch, s13, numel, I, limit, w13_rw, xs, topk, a2, a2s, nullptr, st);
+  if (rc) return rc;
+  const dim3 g2(H / 16, T, 1);
+  launch_gemv_direct<kFp8, kGemvCombine>(
+      g2, topk * kWave, st, gemv_vector_scales<kFp8>(I, a2s, w2_s), static_cast<const uint8_t*>(a2),
+      gemv_act_bytes<kFp8>(numel, I), static_cast<const float*>(a2s), 1, I, none, none, none, none, w2,
+      static_cast<const void*>(w2_s), H, numel, 1, static_cast<float*>(nullptr), w2_rw,
+      static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E, out);
+  return check_launch("moe w2 (gemv + top-k sum)");
+}
+
 // Path choice of `auto`: the decode kernels (GEMV over 16-route blocks) up to
 // a number of routes per expert measured on MI355X, the grouped GEMMs over
 // 128- or 256-route blocks above.  Measured crossovers (graph replay, caches
@@ -2121,6 +2245,19 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   const int numel = static_cast<int>(T * topk);
   const int h = static_cast<int>(H), i = static_cast<int>(I), t = static_cast<int>(T);
 
+  // The routed weight is applied once: on the W13 output before the
+  // activation (apply_router_weight_on_input), otherwise in the W2 epilogue.
+  const float* w13_rw = weight_on_input ? topk_weights : nullptr;
+  const float* w2_rw = weight_on_input ? nullptr : topk_weights;
+  if constexpr (KIND == kFp8) {
+    if (bm == kGemvBlock && numel <= kDirectMaxRoutes && topk <= kMaxCombineSlots)
+      return fused_direct_fp8(static_cast<const uint16_t*>(x), t, h, static_cast<const uint8_t*>(w13),
+                              static_cast<const float*>(w13_s), static_cast<const uint8_t*>(w2),
+                              static_cast<const float*>(w2_s), E, i, topk, topk_ids, expert_map,
+                              expert_map_len, swiglu_limit, w13_rw, w2_rw, ws + L.xq,
+                              reinterpret_cast<float*>(ws + L.xs), scratch, a2, a2s,
+                              static_cast<uint16_t*>(out), st);
+  }
   const uint8_t* xa = static_cast<const uint8_t*>(x);
   const float* xs = nullptr;
   float* xcorr = KIND == kW4 ? reinterpret_cast<float*>(ws + L.xcorr) : nullptr;
@@ -2149,10 +2286,6 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   // kW4 prefill: bf16 activation, quantised per row below (the decode path
   // writes the quantised a2 directly).
   uint8_t* act_out = KIND == kW4 && bm != kGemvBlock ? ws + L.abf : a2;
-  // The routed weight is applied once: on the W13 output before the
-  // activation (apply_router_weight_on_input), otherwise in the W2 epilogue.
-  const float* w13_rw = weight_on_input ? topk_weights : nullptr;
-  const float* w2_rw = weight_on_input ? nullptr : topk_weights;
   rc = launch_w13<KIND>(xa, xs, xcorr, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
                         static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, w13_rw, act_out,
                         a2s, a2corr, scratch, st);
