@@ -160,6 +160,33 @@ def test_bf16_moe_stages_match_fused(path):
     assert torch.equal(st.run(), ref)
 
 
+@pytest.mark.parametrize("T,K,variant", [(1, 8, "plain"), (2, 4, "expert_map"), (1, 4, "limit")])
+def test_bf16_moe_direct_decode_matches_grouped(T, K, variant):
+    """Up to 16 routes the fused decode call gives every route its own GEMV
+    slot and sums the top-k inside the W2 launch; bit for bit the grouped
+    decode stages (alignment, GEMVs over the active experts, moe_sum)."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.fused_moe import MoeStages
+    w13, w2 = _weights(16, 1024, 512, 41 + T)
+    x = synthetic.activations(T, 1024, 42 + T)
+    w, ids = _routing(T, 16, K, 43 + T)
+    emap, limit = None, None
+    if variant == "expert_map":  # global ids 0..23, local experts = global 8..23
+        g = torch.Generator().manual_seed(44)
+        ids = torch.stack([torch.randperm(24, generator=g)[:K] for _ in range(T)]).to(torch.int32).to(DEV)
+        emap = torch.full((24,), -1, dtype=torch.int32)
+        emap[8:] = torch.arange(16, dtype=torch.int32)
+        emap = emap.to(DEV)
+    if variant == "limit":
+        limit = 7.0
+    st = MoeStages(x, w13, None, w2, None, w, ids, path="gemv", expert_map=emap, swiglu_limit=limit)
+    grouped = st.run().clone()
+    direct = _run(x, w13, w2, w, ids, "gemv", emap=emap, limit=limit)
+    assert torch.equal(direct, grouped)
+    if limit is None:
+        _check(direct, _oracle(x, w13, w2, w, ids, emap=emap))
+
+
 def test_bf16_moe_rejects_scales():
     from vllm_musa_amd import synthetic
     from vllm_musa_amd.fused_moe import fused_experts_impl

@@ -179,7 +179,7 @@ moe_gemv_kernel(
     const uint8_t* __restrict__ w, const void* __restrict__ ws, int N, int numel, int splits,
     float* __restrict__ partial, const float* __restrict__ route_w, uint16_t* __restrict__ y,
     const int32_t* __restrict__ ids, const int32_t* __restrict__ emap, int64_t emap_len, int E_,
-    uint16_t* __restrict__ comb) {
+    uint16_t* __restrict__ comb, const float* __restrict__ comb_w) {
   using KB_ = KindBytes<KIND>;
   constexpr int U = kGemvU;
   constexpr bool kStream1 = gemv_stream1<MAXB, KIND, VS>();
@@ -481,22 +481,29 @@ moe_gemv_kernel(
     b0 += MAXB;
   } while (b0 < nblk);
   if constexpr (MODE == kGemvCombine) {
-    // y_k = bf16(acc * w_k) for the 16 rows (lanes of column 0), then the
-    // layer output = bf16(sum over k in slot order of y_k), dropped routes
-    // contributing nothing (+0.0 leaves the fp32 sum unchanged: it starts at
-    // +0.0 and an exact cancellation gives +0.0).
+    // y_k = bf16(acc * route_w[k]) for the 16 rows (lanes of column 0), as
+    // the per-route epilogue above; then the layer output = bf16 of the fp32
+    // sum over the live slots in slot order, y_k times comb_w[k] by one fma
+    // when given -- the rule of moe_sum.
     __shared__ float part[kMaxCombineSlots * 16];
-    if (li == 0) {
-      const v4f a = dead ? zero : KIND == kW4 ? acc[0] * kW4Unit : acc[0];
-      const float rw = route_w && !dead ? route_w[slot] : 1.0f;
+    __shared__ int live[kMaxCombineSlots];
+    if (li == 0 && !dead) {
+      const v4f a = KIND == kW4 ? acc[0] * kW4Unit : acc[0];
+      const float rw = route_w ? route_w[slot] : 1.0f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) part[wave * 16 + 4 * lg + q] = dead ? 0.0f : bf16r(a[q] * rw);
+      for (int q = 0; q < 4; ++q) part[wave * 16 + 4 * lg + q] = bf16r(a[q] * rw);
     }
+    if (lane == 0) live[wave] = dead ? 0 : 1;
     __syncthreads();
     if (wave == 0 && lane < 16) {
       const int nslots = blockDim.x / kWave;
+      const int64_t first = static_cast<int64_t>(blockIdx.y) * nslots;
       float s = 0.0f;
-      for (int k = 0; k < nslots; ++k) s += part[k * 16 + lane];
+      for (int k = 0; k < nslots; ++k) {
+        if (!live[k]) continue;
+        const float v = part[k * 16 + lane];
+        s = comb_w ? __builtin_fmaf(v, comb_w[first + k], s) : s + v;
+      }
       comb[static_cast<int64_t>(blockIdx.y) * N + ntile * 16 + lane] = f32_to_bf16(s);
     }
   }
@@ -1875,16 +1882,16 @@ static void launch_gemv(dim3 grid, hipStream_t st, bool one_block, bool vs, Args
   if constexpr (KIND != kBf16) {
     if (vs) {
       if (one_block)
-        moe_gemv_kernel<1, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr);
+        moe_gemv_kernel<1, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr);
       else
-        moe_gemv_kernel<4, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr);
+        moe_gemv_kernel<4, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr);
       return;
     }
   }
   if (one_block)
-    moe_gemv_kernel<1, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr);
+    moe_gemv_kernel<1, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr);
   else
-    moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr);
+    moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr);
 }
 
 // The decode GEMV with direct route slots (kGemvDirect / kGemvCombine).
@@ -2124,41 +2131,45 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   return w;
 }
 
-// One or two tokens on the fp8 decode path (at most kDirectMaxRoutes routes,
+// One or two tokens on the decode path (at most kDirectMaxRoutes routes,
 // top-k <= kMaxCombineSlots): every route is its own GEMV slot, so the
-// alignment is skipped (the 1x128 quantiser of x runs alone), and the W2
-// GEMV sums the top-k in the same launch.  Each route reads its expert's
-// weights; with more tokens, routes that share an expert would read them
-// again, which the grouped slots avoid.
+// alignment is skipped (kFp8 / kW4: x is quantised alone), and the W2 GEMV
+// sums the top-k in the same launch.  Each route reads its expert's weights;
+// with more tokens, routes that share an expert would read them again, which
+// the grouped slots avoid.  kW4: a2s are the a2 row scales (the W2 output
+// scale) and the routed weights enter the sum, as in the grouped form.
 constexpr int kDirectMaxRoutes = 16;
-static int fused_direct_fp8(const uint16_t* x, int T, int H, const uint8_t* w13, const float* w13_s,
-                            const uint8_t* w2, const float* w2_s, int E, int I, int topk,
-                            const int32_t* topk_ids, const int32_t* emap, int64_t emap_len,
-                            float limit, const float* w13_rw, const float* w2_rw, uint8_t* xq,
-                            float* xs, float* scratch, uint8_t* a2, float* a2s, uint16_t* out,
-                            hipStream_t st) {
+// xa: x as the W13 GEMV reads it (kFp8 / kW4: quantised by the caller, with
+// xs the 1x128 scales / the row scales and xcorr the kW4 block corrections).
+template <int KIND>
+static int fused_direct(const uint8_t* xa, const float* xs, const float* xcorr, int T, int H,
+                        const uint8_t* w13, const void* w13_s, const uint8_t* w2, const void* w2_s,
+                        int E, int I, int topk, const float* topk_weights, const int32_t* topk_ids,
+                        const int32_t* emap, int64_t emap_len, float limit, const float* w13_rw,
+                        const float* w2_rw, float* scratch, uint8_t* a2, float* a2s, float* a2corr,
+                        uint16_t* out, hipStream_t st) {
   const int numel = T * topk;
   const int32_t* none = nullptr;
-  int rc = vmamd_per_token_group_quant_fp8(x, kBF16, T, H, H, 128, 1e-10f, -448.f, 448.f, xq, xs,
-                                           H / 128, 1, st);
-  if (rc) return rc;
-  const int s13 = w13_splits(numel, E, H, I, kFp8);
+  const float* act_s = KIND == kW4 ? xcorr : xs;
+  const int s13 = w13_splits(numel, E, H, I, KIND);
   const dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, numel, s13);
-  launch_gemv_direct<kFp8, kGemvDirect>(
-      g13, kMoeGemvWaves * kWave, st, gemv_vector_scales<kFp8>(H, xs, w13_s), static_cast<const uint8_t*>(xq),
-      gemv_act_bytes<kFp8>(T, H), static_cast<const float*>(xs), topk, H, none, none, none, none, w13,
-      static_cast<const void*>(w13_s), 2 * I, numel, s13, scratch, static_cast<const float*>(nullptr),
-      static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E, static_cast<uint16_t*>(nullptr));
-  rc = check_launch("moe w13 (gemv)");
+  launch_gemv_direct<KIND, kGemvDirect>(
+      g13, kMoeGemvWaves * kWave, st, gemv_vector_scales<KIND>(H, act_s, w13_s), xa, gemv_act_bytes<KIND>(T, H),
+      act_s, topk, H, none, none, none, none, w13, w13_s, 2 * I, numel, s13, scratch,
+      static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E,
+      static_cast<uint16_t*>(nullptr), static_cast<const float*>(nullptr));
+  int rc = check_launch("moe w13 (gemv)");
   if (rc) return rc;
-  rc = launch_act_decode<kFp8>(scratch, s13, numel, I, limit, w13_rw, xs, topk, a2, a2s, nullptr, st);
+  rc = launch_act_decode<KIND>(scratch, s13, numel, I, limit, w13_rw, xs, topk, a2, a2s, a2corr, st);
   if (rc) return rc;
+  const float* a2_act_s = KIND == kW4 ? a2corr : a2s;
+  const float* yscale = KIND == kW4 ? a2s : w2_rw;
   const dim3 g2(H / 16, T, 1);
-  launch_gemv_direct<kFp8, kGemvCombine>(
-      g2, topk * kWave, st, gemv_vector_scales<kFp8>(I, a2s, w2_s), static_cast<const uint8_t*>(a2),
-      gemv_act_bytes<kFp8>(numel, I), static_cast<const float*>(a2s), 1, I, none, none, none, none, w2,
-      static_cast<const void*>(w2_s), H, numel, 1, static_cast<float*>(nullptr), w2_rw,
-      static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E, out);
+  launch_gemv_direct<KIND, kGemvCombine>(
+      g2, topk * kWave, st, gemv_vector_scales<KIND>(I, a2_act_s, w2_s), static_cast<const uint8_t*>(a2),
+      gemv_act_bytes<KIND>(numel, I), a2_act_s, 1, I, none, none, none, none, w2, w2_s, H, numel, 1,
+      static_cast<float*>(nullptr), yscale, static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E,
+      out, KIND == kW4 ? topk_weights : static_cast<const float*>(nullptr));
   return check_launch("moe w2 (gemv + top-k sum)");
 }
 
@@ -2249,13 +2260,27 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   // activation (apply_router_weight_on_input), otherwise in the W2 epilogue.
   const float* w13_rw = weight_on_input ? topk_weights : nullptr;
   const float* w2_rw = weight_on_input ? nullptr : topk_weights;
-  if constexpr (KIND == kFp8) {
-    if (bm == kGemvBlock && numel <= kDirectMaxRoutes && topk <= kMaxCombineSlots)
-      return fused_direct_fp8(static_cast<const uint16_t*>(x), t, h, static_cast<const uint8_t*>(w13),
-                              static_cast<const float*>(w13_s), static_cast<const uint8_t*>(w2),
-                              static_cast<const float*>(w2_s), E, i, topk, topk_ids, expert_map,
-                              expert_map_len, swiglu_limit, w13_rw, w2_rw, ws + L.xq,
-                              reinterpret_cast<float*>(ws + L.xs), scratch, a2, a2s,
+  if (bm == kGemvBlock && numel <= kDirectMaxRoutes && topk <= kMaxCombineSlots) {
+    const uint8_t* xd = static_cast<const uint8_t*>(x);
+    float* xsd = nullptr;
+    float* xcd = nullptr;
+    if constexpr (KIND == kFp8) {
+      xsd = reinterpret_cast<float*>(ws + L.xs);
+      rc = vmamd_per_token_group_quant_fp8(x, kBF16, T, H, H, 128, 1e-10f, -448.f, 448.f, ws + L.xq, xsd,
+                                           H / 128, 1, st);
+      xd = ws + L.xq;
+    } else if constexpr (KIND == kW4) {  // the alignment part of this launch sees no routes
+      xsd = reinterpret_cast<float*>(ws + L.xs);
+      xcd = reinterpret_cast<float*>(ws + L.xcorr);
+      rc = align_and_row_quant_fp8(topk_ids, 0, E, bm, expert_map, expert_map_len, sorted, cap, eids,
+                                   ntpp, offs, active, nact, x, T, H, ws + L.xq, xsd, xcd, st);
+      xd = ws + L.xq;
+    }
+    if (rc) return rc;
+    return fused_direct<KIND>(xd, xsd, xcd, t, h, static_cast<const uint8_t*>(w13), w13_s,
+                              static_cast<const uint8_t*>(w2), w2_s, E, i, topk, topk_weights, topk_ids,
+                              expert_map, expert_map_len, swiglu_limit, w13_rw, w2_rw, scratch, a2, a2s,
+                              KIND == kW4 ? reinterpret_cast<float*>(ws + L.a2corr) : nullptr,
                               static_cast<uint16_t*>(out), st);
   }
   const uint8_t* xa = static_cast<const uint8_t*>(x);
