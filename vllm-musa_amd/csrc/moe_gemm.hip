@@ -158,7 +158,11 @@ constexpr bool gemv_stream1() { return MAXB == 1 && (KIND != kW4 || VS); }
 // blockIdx.y): the workgroup is one 16-row tile, wave k computes route k and
 // the top-k sum is taken in LDS (slot order, as moe_sum), so the layer output
 // is written directly.
-constexpr int kGemvGrouped = 0, kGemvDirect = 1, kGemvCombine = 2;
+// kGemvDirectQ (kFp8 with vector-loaded scales): kGemvDirect with act the
+// bf16 x itself, each workgroup quantising its token's row per 1x128 group
+// into LDS (the quantiser's own per-group code, so the same bytes and scales)
+// instead of a separate quantiser launch.
+constexpr int kGemvGrouped = 0, kGemvDirect = 1, kGemvCombine = 2, kGemvDirectQ = 3;
 constexpr int kMaxCombineSlots = 8;
 
 // Local expert of a route, -1 when it is dropped (negative id, not mapped,
@@ -184,12 +188,14 @@ moe_gemv_kernel(
   constexpr int U = kGemvU;
   constexpr bool kStream1 = gemv_stream1<MAXB, KIND, VS>();
   static_assert(MODE == kGemvGrouped || MAXB == 1, "direct route slots take one route per block");
+  constexpr bool kQx = MODE == kGemvDirectQ;
+  static_assert(!kQx || (KIND == kFp8 && VS && kStream1), "in-workgroup x quantiser: fp8, vector scales");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const int li = lane % 16, lg = lane / 16;
   const int ntile = MODE == kGemvCombine ? static_cast<int>(blockIdx.x) : blockIdx.x * kMoeGemvWaves + wave;
   // Wave-uniform (workgroup-uniform for kGemvCombine, whose only barrier
-  // comes after it).
-  if (ntile * 16 >= N) return;
+  // comes after it); kGemvDirectQ leaves after its barrier.
+  if (!kQx && ntile * 16 >= N) return;
   const int slot = MODE == kGemvCombine ? static_cast<int>(blockIdx.y * (blockDim.x / kWave)) + wave
                                         : static_cast<int>(blockIdx.y);
   int e;
@@ -201,13 +207,27 @@ moe_gemv_kernel(
     e = active[slot];
     const int na = num_active[0];
     if (slot >= na || e < 0) return;
-  } else if constexpr (MODE == kGemvDirect) {
-    e = route_expert(ids, slot, emap, emap_len, E_);
+  } else if constexpr (MODE == kGemvDirect || MODE == kGemvDirectQ) {
+    e = route_expert(ids, slot, emap, emap_len, E_);  // workgroup-uniform
     if (e < 0) return;
   } else {
     e = route_expert(ids, slot, emap, emap_len, E_);
     dead = e < 0;
     e = dead ? 0 : e;
+  }
+  extern __shared__ __attribute__((aligned(16))) uint8_t qx_lds[];  // kQx: [K] fp8, then [K/128] f32
+  if constexpr (kQx) {
+    const int gpr = K / 128;
+    const uint16_t* xrow = reinterpret_cast<const uint16_t*>(act) + static_cast<int64_t>(slot / act_div) * K;
+    float* qs = reinterpret_cast<float*>(qx_lds + K);
+    for (int g0 = 0; g0 < gpr; g0 += static_cast<int>(blockDim.x) / kLanesPerGroup) {
+      const int g = g0 + static_cast<int>(threadIdx.x) / kLanesPerGroup;  // uniform over a group's lanes
+      if (g < gpr)
+        group_quant_group<kBF16>(xrow, K, gpr, g, threadIdx.x % kLanesPerGroup, true, 1e-10f, -448.f, 448.f,
+                                 qx_lds, K, qs, 0, 1);
+    }
+    __syncthreads();
+    if (ntile * 16 >= N) return;
   }
   const int split = blockIdx.z;
   const int KS = K / KB_::kElems;                    // K steps
@@ -342,6 +362,16 @@ moe_gemv_kernel(
     float as[U];
     auto load_act = [&](int kb, int u) {
       const bool live = aoff[0] != kBufferOff && kb + u < kb1;
+      if constexpr (kQx) {  // the route's column (li == 0) from LDS, zeros elsewhere
+        const int k = (kb + u) * 128;
+        xf[u] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+        if (live) {
+          const v4i lo = lds_load<v4i>(qx_lds, k + 16 * lg);
+          const v4i hi = lds_load<v4i>(qx_lds, k + 64 + 16 * lg);
+          xf[u] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        return;
+      }
       const uint32_t off = live ? aoff[0] + static_cast<uint32_t>((kb + u) * KB_::kAct) : kBufferOff;
       xf[u] = buffer_frag<KIND>(ars, off, lg);
       if constexpr (KIND != kBf16 && !VS)
@@ -349,6 +379,7 @@ moe_gemv_kernel(
                                               srs, static_cast<int>(live ? off / 32 : kBufferOff), 0, 0));
     };
     auto load_as_vs = [&](int kb) {  // the group's U activation scales
+      if constexpr (kQx) return lds_load<v4f>(qx_lds, K + 4 * kb);
       const uint32_t off = aoff[0] != kBufferOff ? aoff[0] / 32 + static_cast<uint32_t>(kb * 4) : kBufferOff;
       return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(srs, static_cast<int>(off), 0, 0));
     };
@@ -1896,14 +1927,18 @@ static void launch_gemv(dim3 grid, hipStream_t st, bool one_block, bool vs, Args
 
 // The decode GEMV with direct route slots (kGemvDirect / kGemvCombine).
 template <int KIND, int MODE, typename... Args>
-static void launch_gemv_direct(dim3 grid, int threads, hipStream_t st, bool vs, Args... args) {
-  if constexpr (KIND != kBf16) {
+static void launch_gemv_direct(dim3 grid, int threads, size_t lds, hipStream_t st, bool vs, Args... args) {
+  if constexpr (MODE == kGemvDirectQ) {  // fp8 with vector scales only
+    moe_gemv_kernel<1, kFp8, true, MODE><<<grid, threads, lds, st>>>(args...);
+    return;
+  }
+  if constexpr (KIND != kBf16 && MODE != kGemvDirectQ) {
     if (vs) {
-      moe_gemv_kernel<1, KIND, true, MODE><<<grid, threads, 0, st>>>(args...);
+      moe_gemv_kernel<1, KIND, true, MODE><<<grid, threads, lds, st>>>(args...);
       return;
     }
   }
-  moe_gemv_kernel<1, KIND, false, MODE><<<grid, threads, 0, st>>>(args...);
+  if constexpr (MODE != kGemvDirectQ) moe_gemv_kernel<1, KIND, false, MODE><<<grid, threads, lds, st>>>(args...);
 }
 
 // True when a GEMV over K may read its scales U at a time: K/128 a multiple
@@ -2140,9 +2175,10 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
 // scale) and the routed weights enter the sum, as in the grouped form.
 constexpr int kDirectMaxRoutes = 16;
 // xa: x as the W13 GEMV reads it (kFp8 / kW4: quantised by the caller, with
-// xs the 1x128 scales / the row scales and xcorr the kW4 block corrections).
+// xs the 1x128 scales / the row scales and xcorr the kW4 block corrections);
+// qx (kFp8): xa is the bf16 x, quantised by each W13 workgroup in LDS.
 template <int KIND>
-static int fused_direct(const uint8_t* xa, const float* xs, const float* xcorr, int T, int H,
+static int fused_direct(bool qx, const uint8_t* xa, const float* xs, const float* xcorr, int T, int H,
                         const uint8_t* w13, const void* w13_s, const uint8_t* w2, const void* w2_s,
                         int E, int I, int topk, const float* topk_weights, const int32_t* topk_ids,
                         const int32_t* emap, int64_t emap_len, float limit, const float* w13_rw,
@@ -2153,11 +2189,20 @@ static int fused_direct(const uint8_t* xa, const float* xs, const float* xcorr, 
   const float* act_s = KIND == kW4 ? xcorr : xs;
   const int s13 = w13_splits(numel, E, H, I, KIND);
   const dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, numel, s13);
-  launch_gemv_direct<KIND, kGemvDirect>(
-      g13, kMoeGemvWaves * kWave, st, gemv_vector_scales<KIND>(H, act_s, w13_s), xa, gemv_act_bytes<KIND>(T, H),
-      act_s, topk, H, none, none, none, none, w13, w13_s, 2 * I, numel, s13, scratch,
-      static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E,
-      static_cast<uint16_t*>(nullptr), static_cast<const float*>(nullptr));
+  if (qx) {
+    launch_gemv_direct<KIND, kGemvDirectQ>(
+        g13, kMoeGemvWaves * kWave, static_cast<size_t>(H) + (H / 128) * 4, st, true, xa,
+        static_cast<int>(static_cast<int64_t>(T) * H * 2), static_cast<const float*>(nullptr), topk, H, none, none,
+        none, none, w13, w13_s, 2 * I, numel, s13, scratch, static_cast<const float*>(nullptr),
+        static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E, static_cast<uint16_t*>(nullptr),
+        static_cast<const float*>(nullptr));
+  } else {
+    launch_gemv_direct<KIND, kGemvDirect>(
+        g13, kMoeGemvWaves * kWave, 0, st, gemv_vector_scales<KIND>(H, act_s, w13_s), xa,
+        gemv_act_bytes<KIND>(T, H), act_s, topk, H, none, none, none, none, w13, w13_s, 2 * I, numel, s13,
+        scratch, static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len,
+        E, static_cast<uint16_t*>(nullptr), static_cast<const float*>(nullptr));
+  }
   int rc = check_launch("moe w13 (gemv)");
   if (rc) return rc;
   rc = launch_act_decode<KIND>(scratch, s13, numel, I, limit, w13_rw, xs, topk, a2, a2s, a2corr, st);
@@ -2166,7 +2211,7 @@ static int fused_direct(const uint8_t* xa, const float* xs, const float* xcorr, 
   const float* yscale = KIND == kW4 ? a2s : w2_rw;
   const dim3 g2(H / 16, T, 1);
   launch_gemv_direct<KIND, kGemvCombine>(
-      g2, topk * kWave, st, gemv_vector_scales<KIND>(I, a2_act_s, w2_s), static_cast<const uint8_t*>(a2),
+      g2, topk * kWave, 0, st, gemv_vector_scales<KIND>(I, a2_act_s, w2_s), static_cast<const uint8_t*>(a2),
       gemv_act_bytes<KIND>(numel, I), a2_act_s, 1, I, none, none, none, none, w2, w2_s, H, numel, 1,
       static_cast<float*>(nullptr), yscale, static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E,
       out, KIND == kW4 ? topk_weights : static_cast<const float*>(nullptr));
@@ -2264,11 +2309,18 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     const uint8_t* xd = static_cast<const uint8_t*>(x);
     float* xsd = nullptr;
     float* xcd = nullptr;
+    // kFp8: each W13 workgroup quantises its token's x row (vector-loaded
+    // scales, whole workgroups of 16-row tiles); otherwise the quantiser
+    // runs first.
+    const bool qx = KIND == kFp8 && (H / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(w13_s) % 16 == 0 &&
+                    (2 * I) % (16 * kMoeGemvWaves) == 0 && H <= 32768;
     if constexpr (KIND == kFp8) {
-      xsd = reinterpret_cast<float*>(ws + L.xs);
-      rc = vmamd_per_token_group_quant_fp8(x, kBF16, T, H, H, 128, 1e-10f, -448.f, 448.f, ws + L.xq, xsd,
-                                           H / 128, 1, st);
-      xd = ws + L.xq;
+      if (!qx) {
+        xsd = reinterpret_cast<float*>(ws + L.xs);
+        rc = vmamd_per_token_group_quant_fp8(x, kBF16, T, H, H, 128, 1e-10f, -448.f, 448.f, ws + L.xq, xsd,
+                                             H / 128, 1, st);
+        xd = ws + L.xq;
+      }
     } else if constexpr (KIND == kW4) {  // the alignment part of this launch sees no routes
       xsd = reinterpret_cast<float*>(ws + L.xs);
       xcd = reinterpret_cast<float*>(ws + L.xcorr);
@@ -2277,7 +2329,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
       xd = ws + L.xq;
     }
     if (rc) return rc;
-    return fused_direct<KIND>(xd, xsd, xcd, t, h, static_cast<const uint8_t*>(w13), w13_s,
+    return fused_direct<KIND>(qx, xd, xsd, xcd, t, h, static_cast<const uint8_t*>(w13), w13_s,
                               static_cast<const uint8_t*>(w2), w2_s, E, i, topk, topk_weights, topk_ids,
                               expert_map, expert_map_len, swiglu_limit, w13_rw, w2_rw, scratch, a2, a2s,
                               KIND == kW4 ? reinterpret_cast<float*>(ws + L.a2corr) : nullptr,
