@@ -233,11 +233,21 @@ def test_fp8_moe_empty_and_inplace():
     assert got.data_ptr() == xi.data_ptr() and torch.equal(got, ref)
 
 
-def test_fp8_moe_poisoned_workspace(monkeypatch):
+@pytest.mark.parametrize("T", [33, 2])
+def test_fp8_moe_poisoned_workspace(monkeypatch, T):
     """Workspace and outputs start as NaN bytes: every value the layer reads
-    must have been written by it."""
-    case = _case(33, 16, 1024, 512, 4, seed=51)
-    ref = _oracle(*case)
+    must have been written by it (T=2: the direct decode route slots, with an
+    expert map that drops some routes, whose partials are never written)."""
+    case = _case(T, 16, 1024, 512, 4, seed=51)
+    emap = None
+    if T == 2:  # global ids 0..23, local experts = global 8..23
+        g = torch.Generator().manual_seed(52)
+        ids = torch.stack([torch.randperm(24, generator=g)[:4] for _ in range(T)]).to(torch.int32).to(DEV)
+        emap = torch.full((24,), -1, dtype=torch.int32)
+        emap[8:] = torch.arange(16, dtype=torch.int32)
+        emap = emap.to(DEV)
+        case = case[:6] + (ids,)
+    ref = _oracle(*case, emap=emap)
     real_empty = torch.empty
 
     def poisoned(*args, **kwargs):
@@ -250,7 +260,7 @@ def test_fp8_moe_poisoned_workspace(monkeypatch):
     monkeypatch.setattr(torch, "empty_like", lambda t, **kw: poisoned(t.shape, dtype=t.dtype,
                                                                       device=t.device))
     for path in ("gemv", "gemm"):
-        _check(_run(*case, path=path), ref)
+        _check(_run(*case, path=path, emap=emap), ref)
 
 
 @pytest.mark.parametrize("path", ["gemv", "gemm"])
