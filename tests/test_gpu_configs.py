@@ -231,17 +231,18 @@ def _fp8_case(T, E, H, I, K, seed):
 
 
 @pytest.mark.parametrize("path", ["gemv", "gemm"])
-@pytest.mark.parametrize("topk", [1, 4])
-def test_fp8_router_weight_on_input(path, topk):
+@pytest.mark.parametrize("T,topk", [(40, 1), (40, 4), (2, 4)])
+def test_fp8_router_weight_on_input(path, T, topk):
     """apply_router_weight_on_input: the routed weight multiplies the W13
     output before the SiLU, y is unweighted (oracle restates the reference's
-    mul_routed_weight on the first GEMV)."""
+    mul_routed_weight on the first GEMV).  T=2 on the decode kernels takes
+    the direct route slots."""
     from vllm_musa_amd.fused_moe import fused_experts_impl
-    x, w13, s13, w2, s2, w, ids = _fp8_case(40, 16, 1024, 512, topk, seed=700 + topk)
+    x, w13, s13, w2, s2, w, ids = _fp8_case(T, 16, 1024, 512, topk, seed=700 + topk + T)
     out = fused_experts_impl(x, w13, w2, w, ids, apply_router_weight_on_input=True,
                              use_fp8_w8a8=True, w1_scale=s13, w2_scale=s2, block_shape=[128, 128],
                              path=path)
-    rows = np.arange(40)
+    rows = np.arange(T)
     cids, sel = _compact(ids.cpu().numpy(), 16)
     u8 = lambda t: t.view(torch.uint8).index_select(0, sel).cpu().numpy()
     f32 = lambda t: t.index_select(0, sel).cpu().numpy()
@@ -254,10 +255,11 @@ def test_fp8_router_weight_on_input(path, topk):
 
 
 @pytest.mark.parametrize("path", ["gemv", "gemm"])
-def test_bf16_router_weight_on_input(path):
+@pytest.mark.parametrize("T", [33, 2])
+def test_bf16_router_weight_on_input(path, T):
     from vllm_musa_amd import synthetic
     from vllm_musa_amd.fused_moe import fused_experts_impl
-    T, E, H, I, K = 33, 8, 512, 256, 2
+    E, H, I, K = 8, 512, 256, 2
     w13, w2 = synthetic.moe_bf16_weights(E, H, I, 710)
     x = synthetic.activations(T, H, 711)
     gen = torch.Generator().manual_seed(712)
