@@ -306,7 +306,8 @@ int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H, const 
  *       Rows of a2q/a2s are routes (r = t*topk + k, [T*topk, I]) for
  *       block_m 16, positions of sorted_token_ids ([capacity, I]) for 128 / 256.
  * W2:   y[r] = bf16(W2[e] . dequant(a2q[row(r)]) * topk_weights[r]),
- *       y [T*topk, H] bf16; rows of dropped routes are left unwritten.
+ *       y [T*topk, H] bf16 (8-byte aligned; 16-byte for block_m 256); rows of
+ *       dropped routes are left unwritten.
  * Scratch: vmamd_moe_fp8_stage_workspace_size() bytes, 16-byte aligned
  * (enough for either stage).
  * Replace the two invoke_fused_moe_kernel launches of the upstream

@@ -1257,6 +1257,10 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
 // SiLU-and-mul and the 1x128 a2 quantiser; W2: 256 hidden rows, epilogue the
 // routed weight.
 constexpr int kMoeBigBM = 256;
+#ifndef VMAMD_W2_LDS_STORE
+#define VMAMD_W2_LDS_STORE 1
+#endif
+static_assert(kMoeBigBM * 512 <= BigTile::kLds, "the W2 output tile is staged in the stages' LDS");
 
 template <int KIND, bool W13>
 __global__ __launch_bounds__(512, 1) void moe_big_kernel(
@@ -1464,6 +1468,37 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
       }
     }
   } else {
+#if VMAMD_W2_LDS_STORE
+    // y = bf16(acc * w) staged through LDS so that each store writes 16 bytes
+    // per lane and whole 512-byte tile rows (the 8-byte fragment stores
+    // scatter 32-byte pieces over 16 rows per instruction).  Row r of the
+    // tile takes 512 bytes, its 16-byte chunk c at slot c ^ (r & 31).
+    uint8_t* yt = smem_dyn;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int row = wm * 64 + mt * 16 + li;
+      const int r = sorted[base + row];
+      const float rw = r < numel && route_w ? route_w[r] : 1.0f;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int col = nw + nt * 16 + 4 * lg;
+        const v4f a = acc[mt][nt];
+        const int off = row * 512 + (((col >> 3) ^ (row & 31)) << 4) + ((col >> 2) & 1) * 8;
+        *reinterpret_cast<uint2*>(yt + off) = pack_bf16x4(a[0] * rw, a[1] * rw, a[2] * rw, a[3] * rw);
+      }
+    }
+    __syncthreads();
+    const int c = lane % 32;
+    const int n = n0 + c * 8;
+#pragma unroll 4
+    for (int it = 0; it < BM / 16; ++it) {
+      const int row = it * 16 + wave * 2 + lane / 32;
+      const int r = sorted[base + row];
+      if (r >= numel || n >= N) continue;
+      const uint4 v = *reinterpret_cast<const uint4*>(yt + row * 512 + ((c ^ (row & 31)) << 4));
+      *reinterpret_cast<uint4*>(y + static_cast<int64_t>(r) * N + n) = v;
+    }
+#else
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int r = sorted[base + wm * 64 + mt * 16 + li];
@@ -1478,6 +1513,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
             pack_bf16x4(a[0] * rw, a[1] * rw, a[2] * rw, a[3] * rw);
       }
     }
+#endif
   }
 }
 
@@ -2433,8 +2469,10 @@ static int stage_w2(const char* who, const void* a2, const float* a2s, int64_t T
   VMAMD_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
                 "%s: workspace of %zu bytes required (got %zu)", who, need, workspace_bytes);
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
-                    reinterpret_cast<uintptr_t>(a2) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0,
-                "%s: a2 and workspace must be 16-byte and y 8-byte aligned", who);
+                    reinterpret_cast<uintptr_t>(a2) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(y) % (block_m == kMoeBigBM ? 16 : 8) == 0,
+                "%s: a2 and workspace must be 16-byte aligned, y 8-byte (16-byte for block_m %d)", who,
+                kMoeBigBM);
   return launch_w2<KIND>(static_cast<const uint8_t*>(a2), a2s, nullptr, static_cast<int>(T), topk, sorted,
                          capacity, block_m, offs, ntpp, active, nact, static_cast<const uint8_t*>(w2),
                          w2_s, E, static_cast<int>(H), static_cast<int>(I), topk_weights,
