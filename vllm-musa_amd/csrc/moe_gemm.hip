@@ -158,10 +158,12 @@ constexpr bool gemv_stream1() { return MAXB == 1 && (KIND != kW4 || VS); }
 // blockIdx.y): the workgroup is one 16-row tile, wave k computes route k and
 // the top-k sum is taken in LDS (slot order, as moe_sum), so the layer output
 // is written directly.
-// kGemvDirectQ (kFp8 with vector-loaded scales): kGemvDirect with act the
-// bf16 x itself, each workgroup quantising its token's row per 1x128 group
-// into LDS (the quantiser's own per-group code, so the same bytes and scales)
-// instead of a separate quantiser launch.
+// kGemvDirectQ (kFp8 / kW4 with vector-loaded scales): kGemvDirect with act
+// the bf16 x itself, each workgroup quantising its token's row into LDS with
+// the quantiser's own code (kFp8: 1x128 groups; kW4: the per-row quantiser in
+// w4 order with its block corrections, the token's row scale also written to
+// xs_out by the workgroup of the token's first route slot) instead of a
+// separate quantiser launch.
 constexpr int kGemvGrouped = 0, kGemvDirect = 1, kGemvCombine = 2, kGemvDirectQ = 3;
 constexpr int kMaxCombineSlots = 8;
 
@@ -183,13 +185,13 @@ moe_gemv_kernel(
     const uint8_t* __restrict__ w, const void* __restrict__ ws, int N, int numel, int splits,
     float* __restrict__ partial, const float* __restrict__ route_w, uint16_t* __restrict__ y,
     const int32_t* __restrict__ ids, const int32_t* __restrict__ emap, int64_t emap_len, int E_,
-    uint16_t* __restrict__ comb, const float* __restrict__ comb_w) {
+    uint16_t* __restrict__ comb, const float* __restrict__ comb_w, float* __restrict__ xs_out) {
   using KB_ = KindBytes<KIND>;
   constexpr int U = kGemvU;
   constexpr bool kStream1 = gemv_stream1<MAXB, KIND, VS>();
   static_assert(MODE == kGemvGrouped || MAXB == 1, "direct route slots take one route per block");
   constexpr bool kQx = MODE == kGemvDirectQ;
-  static_assert(!kQx || (KIND == kFp8 && VS && kStream1), "in-workgroup x quantiser: fp8, vector scales");
+  static_assert(!kQx || (KIND != kBf16 && VS && kStream1), "in-workgroup x quantiser: fp8 / w4, vector scales");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const int li = lane % 16, lg = lane / 16;
   const int ntile = MODE == kGemvCombine ? static_cast<int>(blockIdx.x) : blockIdx.x * kMoeGemvWaves + wave;
@@ -209,24 +211,38 @@ moe_gemv_kernel(
     if (slot >= na || e < 0) return;
   } else if constexpr (MODE == kGemvDirect || MODE == kGemvDirectQ) {
     e = route_expert(ids, slot, emap, emap_len, E_);  // workgroup-uniform
-    if (e < 0) return;
+    // kW4: the workgroup that writes the token's row scale runs the quantiser
+    // even when its route is dropped.
+    const bool writes_xs = KIND == kW4 && kQx && blockIdx.x == 0 && blockIdx.z == 0 && slot % act_div == 0;
+    if (e < 0 && !writes_xs) return;
   } else {
     e = route_expert(ids, slot, emap, emap_len, E_);
     dead = e < 0;
     e = dead ? 0 : e;
   }
-  extern __shared__ __attribute__((aligned(16))) uint8_t qx_lds[];  // kQx: [K] fp8, then [K/128] f32
+  // kQx LDS: [K] fp8 (kW4: w4 order), [K/128] f32 (kFp8: group scales,
+  // kW4: block corrections), kW4 then the row scale and 4 wave maxima.
+  extern __shared__ __attribute__((aligned(16))) uint8_t qx_lds[];
   if constexpr (kQx) {
     const int gpr = K / 128;
     const uint16_t* xrow = reinterpret_cast<const uint16_t*>(act) + static_cast<int64_t>(slot / act_div) * K;
     float* qs = reinterpret_cast<float*>(qx_lds + K);
-    for (int g0 = 0; g0 < gpr; g0 += static_cast<int>(blockDim.x) / kLanesPerGroup) {
-      const int g = g0 + static_cast<int>(threadIdx.x) / kLanesPerGroup;  // uniform over a group's lanes
-      if (g < gpr)
-        group_quant_group<kBF16>(xrow, K, gpr, g, threadIdx.x % kLanesPerGroup, true, 1e-10f, -448.f, 448.f,
-                                 qx_lds, K, qs, 0, 1);
+    if constexpr (KIND == kFp8) {
+      for (int g0 = 0; g0 < gpr; g0 += static_cast<int>(blockDim.x) / kLanesPerGroup) {
+        const int g = g0 + static_cast<int>(threadIdx.x) / kLanesPerGroup;  // uniform over a group's lanes
+        if (g < gpr)
+          group_quant_group<kBF16>(xrow, K, gpr, g, threadIdx.x % kLanesPerGroup, true, 1e-10f, -448.f, 448.f,
+                                   qx_lds, K, qs, 0, 1);
+      }
+      __syncthreads();
+    } else {  // one kRowThreads part: the whole workgroup (it synchronises the block)
+      float* rs = qs + gpr;
+      row_quant_part<true>(xrow, K, K, 1e-4f, -448.f, 448.f, qx_lds, rs, 0, true, threadIdx.x, rs + 1, qs);
+      __syncthreads();
+      if (blockIdx.x == 0 && blockIdx.z == 0 && slot % act_div == 0 && threadIdx.x == 0)
+        xs_out[slot / act_div] = rs[0];
+      if (e < 0) return;  // the row scale's writer of a dropped route
     }
-    __syncthreads();
     if (ntile * 16 >= N) return;
   }
   const int split = blockIdx.z;
@@ -363,11 +379,12 @@ moe_gemv_kernel(
     auto load_act = [&](int kb, int u) {
       const bool live = aoff[0] != kBufferOff && kb + u < kb1;
       if constexpr (kQx) {  // the route's column (li == 0) from LDS, zeros elsewhere
-        const int k = (kb + u) * 128;
+        const int k = (kb + u) * 128;  // layouts of buffer_frag
+        const int o0 = KIND == kW4 ? 32 * lg : 16 * lg, o1 = KIND == kW4 ? 32 * lg + 16 : 64 + 16 * lg;
         xf[u] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
         if (live) {
-          const v4i lo = lds_load<v4i>(qx_lds, k + 16 * lg);
-          const v4i hi = lds_load<v4i>(qx_lds, k + 64 + 16 * lg);
+          const v4i lo = lds_load<v4i>(qx_lds, k + o0);
+          const v4i hi = lds_load<v4i>(qx_lds, k + o1);
           xf[u] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
         return;
@@ -1949,23 +1966,23 @@ static void launch_gemv(dim3 grid, hipStream_t st, bool one_block, bool vs, Args
   if constexpr (KIND != kBf16) {
     if (vs) {
       if (one_block)
-        moe_gemv_kernel<1, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr);
+        moe_gemv_kernel<1, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
       else
-        moe_gemv_kernel<4, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr);
+        moe_gemv_kernel<4, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
       return;
     }
   }
   if (one_block)
-    moe_gemv_kernel<1, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr);
+    moe_gemv_kernel<1, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
   else
-    moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr);
+    moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
 }
 
 // The decode GEMV with direct route slots (kGemvDirect / kGemvCombine).
 template <int KIND, int MODE, typename... Args>
 static void launch_gemv_direct(dim3 grid, int threads, size_t lds, hipStream_t st, bool vs, Args... args) {
-  if constexpr (MODE == kGemvDirectQ) {  // fp8 with vector scales only
-    moe_gemv_kernel<1, kFp8, true, MODE><<<grid, threads, lds, st>>>(args...);
+  if constexpr (MODE == kGemvDirectQ) {  // kFp8 / kW4 with vector scales only
+    if constexpr (KIND != kBf16) moe_gemv_kernel<1, KIND, true, MODE><<<grid, threads, lds, st>>>(args...);
     return;
   }
   if constexpr (KIND != kBf16 && MODE != kGemvDirectQ) {
@@ -2212,7 +2229,8 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
 constexpr int kDirectMaxRoutes = 16;
 // xa: x as the W13 GEMV reads it (kFp8 / kW4: quantised by the caller, with
 // xs the 1x128 scales / the row scales and xcorr the kW4 block corrections);
-// qx (kFp8): xa is the bf16 x, quantised by each W13 workgroup in LDS.
+// qx (kFp8 / kW4): xa is the bf16 x, quantised by each W13 workgroup in LDS
+// (kW4: xs receives the row scales from the W13 launch).
 template <int KIND>
 static int fused_direct(bool qx, const uint8_t* xa, const float* xs, const float* xcorr, int T, int H,
                         const uint8_t* w13, const void* w13_s, const uint8_t* w2, const void* w2_s,
@@ -2227,17 +2245,17 @@ static int fused_direct(bool qx, const uint8_t* xa, const float* xs, const float
   const dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, numel, s13);
   if (qx) {
     launch_gemv_direct<KIND, kGemvDirectQ>(
-        g13, kMoeGemvWaves * kWave, static_cast<size_t>(H) + (H / 128) * 4, st, true, xa,
-        static_cast<int>(static_cast<int64_t>(T) * H * 2), static_cast<const float*>(nullptr), topk, H, none, none,
-        none, none, w13, w13_s, 2 * I, numel, s13, scratch, static_cast<const float*>(nullptr),
+        g13, kMoeGemvWaves * kWave, static_cast<size_t>(H) + (H / 128) * 4 + (KIND == kW4 ? 32 : 0), st, true,
+        xa, static_cast<int>(static_cast<int64_t>(T) * H * 2), static_cast<const float*>(nullptr), topk, H, none,
+        none, none, none, w13, w13_s, 2 * I, numel, s13, scratch, static_cast<const float*>(nullptr),
         static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E, static_cast<uint16_t*>(nullptr),
-        static_cast<const float*>(nullptr));
+        static_cast<const float*>(nullptr), KIND == kW4 ? const_cast<float*>(xs) : static_cast<float*>(nullptr));
   } else {
     launch_gemv_direct<KIND, kGemvDirect>(
         g13, kMoeGemvWaves * kWave, 0, st, gemv_vector_scales<KIND>(H, act_s, w13_s), xa,
         gemv_act_bytes<KIND>(T, H), act_s, topk, H, none, none, none, none, w13, w13_s, 2 * I, numel, s13,
         scratch, static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len,
-        E, static_cast<uint16_t*>(nullptr), static_cast<const float*>(nullptr));
+        E, static_cast<uint16_t*>(nullptr), static_cast<const float*>(nullptr), static_cast<float*>(nullptr));
   }
   int rc = check_launch("moe w13 (gemv)");
   if (rc) return rc;
@@ -2250,7 +2268,7 @@ static int fused_direct(bool qx, const uint8_t* xa, const float* xs, const float
       g2, topk * kWave, 0, st, gemv_vector_scales<KIND>(I, a2_act_s, w2_s), static_cast<const uint8_t*>(a2),
       gemv_act_bytes<KIND>(numel, I), a2_act_s, 1, I, none, none, none, none, w2, w2_s, H, numel, 1,
       static_cast<float*>(nullptr), yscale, static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E,
-      out, KIND == kW4 ? topk_weights : static_cast<const float*>(nullptr));
+      out, KIND == kW4 ? topk_weights : static_cast<const float*>(nullptr), static_cast<float*>(nullptr));
   return check_launch("moe w2 (gemv + top-k sum)");
 }
 
@@ -2345,11 +2363,12 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     const uint8_t* xd = static_cast<const uint8_t*>(x);
     float* xsd = nullptr;
     float* xcd = nullptr;
-    // kFp8: each W13 workgroup quantises its token's x row (vector-loaded
-    // scales, whole workgroups of 16-row tiles); otherwise the quantiser
-    // runs first.
-    const bool qx = KIND == kFp8 && (H / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(w13_s) % 16 == 0 &&
-                    (2 * I) % (16 * kMoeGemvWaves) == 0 && H <= 32768;
+    // kFp8 / kW4: each W13 workgroup quantises its token's x row (vector-
+    // loaded scales, whole workgroups of 16-row tiles); otherwise the
+    // quantiser runs first.
+    const bool qx = KIND != kBf16 && (H / 128) % kGemvU == 0 &&
+                    reinterpret_cast<uintptr_t>(w13_s) % (KIND == kFp8 ? 16 : 8) == 0 &&
+                    (2 * I) % (16 * kMoeGemvWaves) == 0 && H <= (KIND == kFp8 ? 32768 : 16384);
     if constexpr (KIND == kFp8) {
       if (!qx) {
         xsd = reinterpret_cast<float*>(ws + L.xs);
@@ -2359,10 +2378,12 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
       }
     } else if constexpr (KIND == kW4) {  // the alignment part of this launch sees no routes
       xsd = reinterpret_cast<float*>(ws + L.xs);
-      xcd = reinterpret_cast<float*>(ws + L.xcorr);
-      rc = align_and_row_quant_fp8(topk_ids, 0, E, bm, expert_map, expert_map_len, sorted, cap, eids,
-                                   ntpp, offs, active, nact, x, T, H, ws + L.xq, xsd, xcd, st);
-      xd = ws + L.xq;
+      if (!qx) {
+        xcd = reinterpret_cast<float*>(ws + L.xcorr);
+        rc = align_and_row_quant_fp8(topk_ids, 0, E, bm, expert_map, expert_map_len, sorted, cap, eids,
+                                     ntpp, offs, active, nact, x, T, H, ws + L.xq, xsd, xcd, st);
+        xd = ws + L.xq;
+      }
     }
     if (rc) return rc;
     return fused_direct<KIND>(qx, xd, xsd, xcd, t, h, static_cast<const uint8_t*>(w13), w13_s,
