@@ -160,16 +160,18 @@ def test_bf16_moe_stages_match_fused(path):
     assert torch.equal(st.run(), ref)
 
 
-@pytest.mark.parametrize("T,K,variant", [(1, 8, "plain"), (2, 4, "expert_map"), (1, 4, "limit")])
-def test_bf16_moe_direct_decode_matches_grouped(T, K, variant):
-    """Up to 16 routes the fused decode call gives every route its own GEMV
-    slot and sums the top-k inside the W2 launch; bit for bit the grouped
-    decode stages (alignment, GEMVs over the active experts, moe_sum)."""
+@pytest.mark.parametrize("T,K,E,variant", [(1, 8, 16, "plain"), (2, 4, 16, "expert_map"),
+                                           (1, 4, 16, "limit"), (4, 8, 64, "plain")])
+def test_bf16_moe_direct_decode_matches_grouped(T, K, E, variant):
+    """Up to E/2 routes the fused bf16 decode call gives every route its own
+    GEMV slot and sums the top-k inside the W2 launch; bit for bit the grouped
+    decode stages (alignment, GEMVs over the active experts, moe_sum).  T=4
+    over 64 experts: tokens share experts."""
     from vllm_musa_amd import synthetic
     from vllm_musa_amd.fused_moe import MoeStages
-    w13, w2 = _weights(16, 1024, 512, 41 + T)
+    w13, w2 = _weights(E, 1024, 512, 41 + T)
     x = synthetic.activations(T, 1024, 42 + T)
-    w, ids = _routing(T, 16, K, 43 + T)
+    w, ids = _routing(T, E, K, 43 + T)
     emap, limit = None, None
     if variant == "expert_map":  # global ids 0..23, local experts = global 8..23
         g = torch.Generator().manual_seed(44)
