@@ -140,17 +140,19 @@ def test_fp8_moe_expert_map(path):
 
 
 @pytest.mark.parametrize("T,K,variant", [(1, 4, "plain"), (2, 8, "plain"), (1, 8, "expert_map"),
-                                         (2, 4, "limit"), (1, 8, "duplicate")])
+                                         (2, 4, "limit"), (1, 8, "duplicate"), (2, 4, "h640")])
 def test_fp8_moe_direct_decode_matches_grouped(T, K, variant):
     """Up to 16 routes the fused decode call gives every route its own GEMV
     slot (no alignment) and sums the top-k inside the W2 launch; its output
     equals the stage-by-stage grouped decode path (alignment, GEMVs over the
     active experts, moe_sum) bit for bit, and the oracle.  Variants: an expert
     map that drops routes, the clamped SwiGLU, and a token that names one
-    expert twice."""
+    expert twice; H = 640 (five scale blocks per row: scales read one at a
+    time, x quantised by its own launch)."""
     from vllm_musa_amd.fused_moe import Fp8MoeStages
     E = 16
-    x, w13, s13, w2, s2, w, ids = _case(T, E, 1024, 512, K, seed=131 + 10 * T + K)
+    H = 640 if variant == "h640" else 1024
+    x, w13, s13, w2, s2, w, ids = _case(T, E, H, 512, K, seed=131 + 10 * T + K)
     emap, limit = None, None
     if variant == "expert_map":  # global ids 0..23, local experts = global 8..23
         g = torch.Generator().manual_seed(137)
