@@ -165,7 +165,7 @@ constexpr bool gemv_stream1() { return MAXB == 1 && (KIND != kW4 || VS); }
 // xs_out by the workgroup of the token's first route slot) instead of a
 // separate quantiser launch.
 constexpr int kGemvGrouped = 0, kGemvDirect = 1, kGemvCombine = 2, kGemvDirectQ = 3;
-constexpr int kMaxCombineSlots = 8;
+constexpr int kMaxCombineSlots = 16;
 
 // Local expert of a route, -1 when it is dropped (negative id, not mapped,
 // or past the local experts) -- the rule of the alignment and of moe_sum.
