@@ -269,10 +269,10 @@ int vmamd_w8a8_block_fp8_matmul_noalloc(const void* A, const float* As, int64_t 
  * fused_experts_impl does with MUL_ROUTED_WEIGHT on its first GEMM.  path: AUTO picks the
  * decode (expert-major GEMV, weights streamed once) kernels while T*topk <=
  * 2.5*E (12*E for the bf16 and w4afp8 layers) and the prefill (grouped MFMA
- * GEMM) kernels above; GEMV / GEMM force one.  On the decode kernels, up to
- * 16 routes (fp8; bf16: E/2, w4afp8: 3E/4; top-k <= 8) skip the alignment:
- * each route is its own GEMV slot, x is quantised inside the W13 launch and
- * the W2 launch sums the top-k (same bits as the aligned form).  Workspace:
+ * GEMM) kernels above; GEMV / GEMM force one.  On the decode kernels one
+ * token (top-k <= 16) skips the alignment: each route is its own GEMV slot,
+ * x is quantised inside the W13 launch and the W2 launch sums the top-k
+ * (same bits as the aligned form).  Workspace:
  * vmamd_fused_moe_fp8_workspace_size() bytes, 256-byte aligned.
  * Replaces fused_experts_impl / _musa_fused_experts_impl_dispatch
  * (vllm_musa/model_executor/layers/fused_moe/fused_moe.py:1935-2184,

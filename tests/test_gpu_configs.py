@@ -231,11 +231,11 @@ def _fp8_case(T, E, H, I, K, seed):
 
 
 @pytest.mark.parametrize("path", ["gemv", "gemm"])
-@pytest.mark.parametrize("T,topk", [(40, 1), (40, 4), (2, 4)])
+@pytest.mark.parametrize("T,topk", [(40, 1), (40, 4), (1, 4)])
 def test_fp8_router_weight_on_input(path, T, topk):
     """apply_router_weight_on_input: the routed weight multiplies the W13
     output before the SiLU, y is unweighted (oracle restates the reference's
-    mul_routed_weight on the first GEMV).  T=2 on the decode kernels takes
+    mul_routed_weight on the first GEMV).  T=1 on the decode kernels takes
     the direct route slots."""
     from vllm_musa_amd.fused_moe import fused_experts_impl
     x, w13, s13, w2, s2, w, ids = _fp8_case(T, 16, 1024, 512, topk, seed=700 + topk + T)
@@ -255,7 +255,7 @@ def test_fp8_router_weight_on_input(path, T, topk):
 
 
 @pytest.mark.parametrize("path", ["gemv", "gemm"])
-@pytest.mark.parametrize("T", [33, 2])
+@pytest.mark.parametrize("T", [33, 1])
 def test_bf16_router_weight_on_input(path, T):
     from vllm_musa_amd import synthetic
     from vllm_musa_amd.fused_moe import fused_experts_impl

@@ -139,16 +139,17 @@ def test_fp8_moe_expert_map(path):
     _check(out, _oracle(x, w13, s13, w2, s2, w, gids, emap=emap))
 
 
-@pytest.mark.parametrize("T,K,variant", [(1, 4, "plain"), (2, 8, "plain"), (1, 8, "expert_map"),
-                                         (2, 4, "limit"), (1, 8, "duplicate"), (2, 4, "h640")])
+@pytest.mark.parametrize("T,K,variant", [(1, 4, "plain"), (1, 8, "plain"), (1, 8, "expert_map"),
+                                         (1, 4, "limit"), (1, 8, "duplicate"), (1, 4, "h640"),
+                                         (2, 8, "plain")])
 def test_fp8_moe_direct_decode_matches_grouped(T, K, variant):
-    """Up to 16 routes the fused decode call gives every route its own GEMV
-    slot (no alignment) and sums the top-k inside the W2 launch; its output
-    equals the stage-by-stage grouped decode path (alignment, GEMVs over the
-    active experts, moe_sum) bit for bit, and the oracle.  Variants: an expert
-    map that drops routes, the clamped SwiGLU, and a token that names one
-    expert twice; H = 640 (five scale blocks per row: scales read one at a
-    time, x quantised by its own launch)."""
+    """One token: the fused decode call gives every route its own GEMV slot
+    (no alignment) and sums the top-k inside the W2 launch; its output equals
+    the stage-by-stage grouped decode path (alignment, GEMVs over the active
+    experts, moe_sum) bit for bit, and the oracle.  Variants: an expert map
+    that drops routes, the clamped SwiGLU, a token that names one expert
+    twice; H = 640 (five scale blocks per row: scales read one at a time, x
+    quantised by its own launch); T=2 takes the grouped slots in both."""
     from vllm_musa_amd.fused_moe import Fp8MoeStages
     E = 16
     H = 640 if variant == "h640" else 1024
@@ -235,14 +236,14 @@ def test_fp8_moe_empty_and_inplace():
     assert got.data_ptr() == xi.data_ptr() and torch.equal(got, ref)
 
 
-@pytest.mark.parametrize("T", [33, 2])
+@pytest.mark.parametrize("T", [33, 1])
 def test_fp8_moe_poisoned_workspace(monkeypatch, T):
     """Workspace and outputs start as NaN bytes: every value the layer reads
-    must have been written by it (T=2: the direct decode route slots, with an
+    must have been written by it (T=1: the direct decode route slots, with an
     expert map that drops some routes, whose partials are never written)."""
     case = _case(T, 16, 1024, 512, 4, seed=51)
     emap = None
-    if T == 2:  # global ids 0..23, local experts = global 8..23
+    if T == 1:  # global ids 0..23, local experts = global 8..23
         g = torch.Generator().manual_seed(52)
         ids = torch.stack([torch.randperm(24, generator=g)[:4] for _ in range(T)]).to(torch.int32).to(DEV)
         emap = torch.full((24,), -1, dtype=torch.int32)
@@ -278,11 +279,11 @@ def test_fp8_moe_stages_match_fused(path):
     assert torch.equal(st.run(), ref)  # buffers reused on a second pass
 
 
-@pytest.mark.parametrize("path,T", [("gemv", 24), ("gemm", 24), ("gemv", 2)])
+@pytest.mark.parametrize("path,T", [("gemv", 24), ("gemm", 24), ("gemv", 1)])
 def test_fp8_moe_graph_replay_matches_eager(path, T):
     """The layer captured in a HIP graph replays bit-identically to the eager
     call, across several replays with eager work and syncs in between and with
-    the routing changed in place between replays (T=2: the direct decode route
+    the routing changed in place between replays (T=1: the direct decode route
     slots, x quantised inside the W13 launch, top-k sum inside the W2 launch)."""
     x, w13, s13, w2, s2, w, ids = _case(T, 16, 1024, 512, 4, seed=71)
     eager = _run(x, w13, s13, w2, s2, w, ids, path)
@@ -300,7 +301,7 @@ def test_fp8_moe_graph_replay_matches_eager(path, T):
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
         _run(x, w13, s13, w2, s2, w, ids, path)  # eager work between replays
-    ids2 = ids.flip(0).contiguous()
+    ids2 = ids.flip(0).contiguous() if T > 1 else ids.flip(1).contiguous()
     ids.copy_(ids2)
     graph.replay()
     torch.cuda.synchronize()

@@ -160,13 +160,12 @@ def test_bf16_moe_stages_match_fused(path):
     assert torch.equal(st.run(), ref)
 
 
-@pytest.mark.parametrize("T,K,E,variant", [(1, 8, 16, "plain"), (2, 4, 16, "expert_map"),
-                                           (1, 4, 16, "limit"), (4, 8, 64, "plain")])
+@pytest.mark.parametrize("T,K,E,variant", [(1, 8, 16, "plain"), (1, 4, 16, "expert_map"),
+                                           (1, 4, 16, "limit"), (1, 8, 64, "plain")])
 def test_bf16_moe_direct_decode_matches_grouped(T, K, E, variant):
-    """Up to E/2 routes the fused bf16 decode call gives every route its own
-    GEMV slot and sums the top-k inside the W2 launch; bit for bit the grouped
-    decode stages (alignment, GEMVs over the active experts, moe_sum).  T=4
-    over 64 experts: tokens share experts."""
+    """One token: the fused bf16 decode call gives every route its own GEMV
+    slot and sums the top-k inside the W2 launch; bit for bit the grouped
+    decode stages (alignment, GEMVs over the active experts, moe_sum)."""
     from vllm_musa_amd import synthetic
     from vllm_musa_amd.fused_moe import MoeStages
     w13, w2 = _weights(E, 1024, 512, 41 + T)

@@ -2219,22 +2219,20 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   return w;
 }
 
-// Few tokens on the decode path (at most direct_max_routes routes, top-k <=
-// kMaxCombineSlots): every route is its own GEMV slot, so the alignment is
-// skipped (kFp8 / kW4: x is quantised inside the W13 launch), and the W2
-// GEMV sums the top-k in the same launch.  Each route reads its expert's
-// weights; with more tokens, routes that share an expert read them again,
-// which the grouped slots avoid, so the limit is where the two cross
-// (measured on MI355X, fused call, caches evicted): fp8 DeepSeek-V3 (E=256,
-// 44 MB experts, grouped routing) T=2 direct 135.5 / grouped 137.7 µs, T=3
-// 194.6 / 191.9, T=6 355 / 274: 16 routes; bf16 (E=128, H=2048, I=768,
-// top-8) T=8 106 / 117, T=12 146 / 145, T=16 188 / 176: E/2 routes;
-// w4afp8 (E=128, H=4096, I=1536, top-8) T=8 131 / 155, T=12 182 / 191,
-// T=16 231 / 210: 3E/4 routes.  kW4: a2s are the a2 row scales (the W2
-// output scale) and the routed weights enter the sum, as in the grouped form.
-static int64_t direct_max_routes(int kind, int E) {
-  return kind == kFp8 ? 16 : kind == kBf16 ? E / 2 : 3 * static_cast<int64_t>(E) / 4;
-}
+// One token on the decode path (top-k <= kMaxCombineSlots): every route is
+// its own GEMV slot, so the alignment is skipped (kFp8 / kW4: x is quantised
+// inside the W13 launch), and the W2 GEMV sums the top-k in the same launch.
+// Each route reads its expert's weights, so routes that share an expert read
+// them again: a token's top-k names distinct experts, but with more tokens a
+// batch whose tokens pick the same experts would read each expert's weights
+// once per token (measured: DeepSeek-V3 fp8 at T=2 with both tokens on the
+// same 8 experts, slower than the grouped GEMMs), which the grouped slots of
+// the alignment avoid.  With varied routing the direct slots measured faster
+// up to 16 routes (fp8 DeepSeek-V3) and 64 / 96 routes (bf16 / w4afp8 E=128
+// layers), but the dispatch has no sight of the routing before the launch.
+// kW4: a2s are the a2 row scales (the W2 output scale) and the routed weights
+// enter the sum, as in the grouped form.
+static bool use_direct_slots(int64_t T, int topk) { return T == 1 && topk <= kMaxCombineSlots; }
 // xa: x as the W13 GEMV reads it (kFp8 / kW4: quantised by the caller, with
 // xs the 1x128 scales / the row scales and xcorr the kW4 block corrections);
 // qx (kFp8 / kW4): xa is the bf16 x, quantised by each W13 workgroup in LDS
@@ -2367,7 +2365,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   // activation (apply_router_weight_on_input), otherwise in the W2 epilogue.
   const float* w13_rw = weight_on_input ? topk_weights : nullptr;
   const float* w2_rw = weight_on_input ? nullptr : topk_weights;
-  if (bm == kGemvBlock && numel <= direct_max_routes(KIND, E) && topk <= kMaxCombineSlots) {
+  if (bm == kGemvBlock && use_direct_slots(T, topk)) {
     const uint8_t* xd = static_cast<const uint8_t*>(x);
     float* xsd = nullptr;
     float* xcd = nullptr;
