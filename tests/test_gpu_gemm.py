@@ -84,6 +84,30 @@ def test_block_fp8_gemm_256_row_tiles_column_major_scales():
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("M", [512, 700])
+def test_block_fp8_gemm_256_row_tiles_split_k(M):
+    """Long rows at mid M (7168 x 16384): the 256 x 256 GEMM with K split over
+    workgroups (fp32 partials added by the reduce); M = 700 leaves the last
+    row tile mostly outside the output."""
+    _run(M, 7168, 16384, seed=57 + M, sample_rows=48, sample_cols=1024)
+
+
+def test_block_fp8_gemm_256_row_tiles_split_k_column_major_scales():
+    """The split 256-row GEMM reads column-major activation scales through
+    their strides: the same bits as row-major ones."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    M, N, K = 512, 7168, 16384
+    w, ws = synthetic.dense_fp8_weight(N, K, 43)
+    x = synthetic.activations(M, K, 44)
+    xq, xs = per_token_group_quant_fp8(x, 128)
+    xq2, xs2 = per_token_group_quant_fp8(x, 128, column_major_scales=True)
+    a = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    b = w8a8_block_fp8_matmul(xq2, w, xs2, ws, [128, 128])
+    assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("M", [3, 17, 33, 65, 100, 130])
 def test_block_fp8_gemm_ragged_m(M):
     _run(M, 2112, 1024, seed=5 + M, sample_rows=200, sample_cols=2112)

@@ -67,7 +67,7 @@ def test_no_alloc_matches_workspace_entry(first, second):
 
 def test_no_alloc_rejects_plans_beyond_the_scratch():
     from vllm_musa_amd import _lib
-    M, N, K = 1024, 3072, 32768  # a split plan whose partials (96 MiB) exceed 64 MiB
+    M, N, K = 384, 8192, 65536  # a split plan whose partials (96 MiB) exceed 64 MiB
     need = _lib.load().vmamd_w8a8_block_fp8_matmul_workspace_size(M, N, K)
     if need <= 64 << 20:
         pytest.skip(f"plan needs only {need} bytes here")

@@ -203,7 +203,7 @@ using BigPipe = BigTile;
 __global__ __launch_bounds__(BigPipe::kThreads, 1) void gemm_fp8_big_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t as_sm, int64_t as_sk,
     int as_bytes, const uint8_t* __restrict__ B, const float* __restrict__ Bs, uint16_t* __restrict__ C,
-    int M, int N, int K, int TM, int TN) {
+    int M, int N, int K, int TM, int TN, int kper, float* __restrict__ partial) {
   using P = BigPipe;
   constexpr int NT = P::NT;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
@@ -295,13 +295,16 @@ __global__ __launch_bounds__(BigPipe::kThreads, 1) void gemm_fp8_big_kernel(
     }
   };
 
-  issue(smem_dyn, 0);
+  // K steps [kb0, kb1) of split blockIdx.y (all of K without a split).
+  const int kb0 = blockIdx.y * kper, kb1 = min(KS, kb0 + kper);
+  issue(smem_dyn, kb0);
   wait_lgkmcnt0();
-  for (int kb = 0; kb < KS; ++kb) {
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int j = kb - kb0;
     wait_vmcnt<0>();  // this wave's DMAs of step kb have landed
     barrier_lds();    // ... every wave's, and step kb - 1's buffer is no longer read
-    if (kb + 1 < KS) issue(smem_dyn + ((kb + 1) & 1) * P::kStage, kb + 1);
-    mma(smem_dyn + (kb & 1) * P::kStage);
+    if (kb + 1 < kb1) issue(smem_dyn + ((j + 1) & 1) * P::kStage, kb + 1);
+    mma(smem_dyn + (j & 1) * P::kStage);
   }
 
 #pragma unroll
@@ -313,7 +316,11 @@ __global__ __launch_bounds__(BigPipe::kThreads, 1) void gemm_fp8_big_kernel(
       const int n = n0 + nw + nt * 16 + 4 * lg;
       if (n >= N) continue;
       const v4f a = acc[mt][nt];
-      *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) = pack_bf16x4(a[0], a[1], a[2], a[3]);
+      if (partial)  // split-K: this split's fp32 tile, partial[split][M][N]
+        *reinterpret_cast<float4*>(partial + (static_cast<int64_t>(blockIdx.y) * M + m) * N + n) =
+            float4{a[0], a[1], a[2], a[3]};
+      else
+        *reinterpret_cast<uint2*>(C + static_cast<int64_t>(m) * N + n) = pack_bf16x4(a[0], a[1], a[2], a[3]);
     }
   }
 }
@@ -337,8 +344,11 @@ static bool use_big_gemm(int M, int N, int K, int64_t as_extent) {
          static_cast<int64_t>(N + 256) * K < (1ll << 31) && as_extent < (1ll << 31);
 }
 
+static void splitk_reduce(const float* partial, int splits, int64_t mn, uint16_t* c, hipStream_t st);
+
 static int launch_big(const uint8_t* a, const float* As, int64_t as_sm, int64_t as_sk, int as_bytes,
-                      const uint8_t* b, const float* Bs, uint16_t* c, int m, int n, int k, hipStream_t st) {
+                      const uint8_t* b, const float* Bs, uint16_t* c, int m, int n, int k, hipStream_t st,
+                      int splits = 1, int kper = 0, float* partial = nullptr) {
   using P = BigPipe;
   static bool raised = false;
   if (!raised) {
@@ -350,9 +360,13 @@ static int launch_big(const uint8_t* a, const float* As, int64_t as_sm, int64_t 
     raised = true;
   }
   const int TM = (m + P::BM - 1) / P::BM, TN = (n + P::BN - 1) / P::BN;
-  gemm_fp8_big_kernel<<<xcd_grid(TM * TN), P::kThreads, P::kLds, st>>>(a, As, as_sm, as_sk, as_bytes, b, Bs, c, m,
-                                                                      n, k, TM, TN);
-  return check_launch("w8a8_block_fp8_matmul(gemm)");
+  if (splits <= 1) kper = k / 128;
+  gemm_fp8_big_kernel<<<dim3(xcd_grid(TM * TN), splits), P::kThreads, P::kLds, st>>>(
+      a, As, as_sm, as_sk, as_bytes, b, Bs, c, m, n, k, TM, TN, kper, splits > 1 ? partial : nullptr);
+  int rc = check_launch("w8a8_block_fp8_matmul(gemm)");
+  if (rc || splits <= 1) return rc;
+  splitk_reduce(partial, splits, static_cast<int64_t>(m) * n, c, st);
+  return check_launch("w8a8_block_fp8_matmul(reduce)");
 }
 
 // C = bf16(sum_s partial[s]) over the S split-K partials of an M x N output,
@@ -632,31 +646,50 @@ static int device_cus() {
 // was not measured), the best split of each case to 5573 us, no split to
 // 8091 us.  Returns the K steps per split.
 constexpr int64_t kSplitKMaxBytes = 256ll << 20;
-static int gemm_kper(int M, int N, int K) {
-  const int64_t T = static_cast<int64_t>((M + 127) / 128) * ((N + 255) / 256), KS = K / 128;
+// step: the modelled time of one K step of the tile relative to the 128 x 256
+// tile's (the 256 x 256 tile: kBigStep); min_per: K steps a split keeps at
+// least.  *cost_out: the model's time (us).
+static int gemm_kper(int M, int N, int K, int bm = 128, double step = 1.0, double* cost_out = nullptr,
+                     int min_per = 4) {
+  const int64_t T = static_cast<int64_t>((M + bm - 1) / bm) * ((N + 255) / 256), KS = K / 128;
   const int64_t cus = device_cus(), xcd_cus = max(1, static_cast<int>(cus / kXcds));
   const int64_t per_xcd = (T + kXcds - 1) / kXcds;
-  // Tiles that alone occupy more than half the CUs: splitting gained at most
-  // 5 % in the fit and lost up to 16 % where the model missed.
-  if (2 * T > cus) return static_cast<int>(KS);
   auto gemm_us = [&](int64_t se, int64_t per) {
     const double active = static_cast<double>(min(T * se, cus));
-    return static_cast<double>((per_xcd * se + xcd_cus - 1) / xcd_cus * per) * (1.0 + 0.004 * active);
+    return static_cast<double>((per_xcd * se + xcd_cus - 1) / xcd_cus * per) * step * (1.0 + 0.004 * active);
   };
   int best = static_cast<int>(KS);
   double cost = gemm_us(1, KS);
-  for (int64_t s = 2; s <= 16 && s * 4 <= KS; ++s) {
-    const int64_t per = (KS + s - 1) / s, se = (KS + per - 1) / per;
-    const int64_t bytes = se * static_cast<int64_t>(M) * N * 4;
-    if (bytes > kSplitKMaxBytes) break;
-    const double c = gemm_us(se, per) + (bytes + 2.0 * M * N) / 4e6 + 3.0;
-    if (c < cost) {
-      cost = c;
-      best = static_cast<int>(per);
+  // Tiles that alone occupy more than half the CUs: splitting gained at most
+  // 5 % in the fit and lost up to 16 % where the model missed.
+  if (2 * T <= cus) {
+    for (int64_t s = 2; s <= 16 && s * min_per <= KS; ++s) {
+      const int64_t per = (KS + s - 1) / s, se = (KS + per - 1) / per;
+      const int64_t bytes = se * static_cast<int64_t>(M) * N * 4;
+      if (bytes > kSplitKMaxBytes) break;
+      const double c = gemm_us(se, per) + (bytes + 2.0 * M * N) / 4e6 + 3.0;
+      if (c < cost) {
+        cost = c;
+        best = static_cast<int>(per);
+      }
     }
   }
+  if (cost_out) *cost_out = cost;
   return best;
 }
+
+#ifndef VMAMD_BIG_SPLIT
+#define VMAMD_BIG_SPLIT 1
+#endif
+// K step of the 256 x 256 tile against the 128 x 256 tile's: the bytes it
+// moves per step, (256 + 256) / (128 + 256).  Its splits keep at least
+// kBigMinSteps K steps: with fewer, each workgroup's fixed costs (first load,
+// a 256 KiB fp32 partial tile) outweigh the shorter loop (measured on MI355X
+// at M = 512: 7168 x 18432 102.9 -> 92.2 us and 7168 x 16384 97.4 -> 86.1 us
+// with 4 splits of 36 / 32 steps; 2112 x 7168 32.7 -> 37.0 us and 4096 x 7168
+// 37.1 -> 44.0 us with splits of 4-8 steps).
+constexpr double kBigStep = 512.0 / 384.0;
+constexpr int kBigMinSteps = 32;
 
 // The dense path for an M x N x K product: the GEMV up to M = 16, and up to
 // M = 32 / 64 unless the split GEMM is faster there -- weights of 96 MiB and
@@ -664,8 +697,12 @@ static int gemm_kper(int M, int N, int K) {
 // the DeepSeek-V3 linear shapes: e.g. 7168 x 18432 at M = 64, 61 us GEMV,
 // 39 us split GEMM).  `splits` > 1 needs splits * M * N * 4 bytes of
 // workspace.
+// big: the 256 x 256 kernel with K splits, where the 128 x 256 tiles would
+// split K too (too few tiles for the CUs) and the model prices the 256-row
+// tiles' splits lower (M >= 512).  Without a split the choice between the
+// two tile kernels is use_big_gemm's.
 struct DensePlan {
-  bool gemv;
+  bool gemv, big;
   int kper, splits;
 };
 static DensePlan dense_plan(int M, int N, int K) {
@@ -673,7 +710,17 @@ static DensePlan dense_plan(int M, int N, int K) {
   const int KS = K / 128;
   const bool heavy = static_cast<int64_t>(N) * K >= (96ll << 20);
   d.gemv = M <= 16 || (M <= 32 && !heavy) || (M <= kGemvMaxM && K < 4096 && !heavy);
-  d.kper = d.gemv ? KS : gemm_kper(M, N, K);
+  d.big = false;
+  double cost = 0.0;
+  d.kper = d.gemv ? KS : gemm_kper(M, N, K, 128, 1.0, &cost);
+  if (VMAMD_BIG_SPLIT && !d.gemv && d.kper < KS && M >= 512) {
+    double cost_big = 0.0;
+    const int kper_big = gemm_kper(M, N, K, 256, kBigStep, &cost_big, kBigMinSteps);
+    if (kper_big < KS && cost_big < cost) {
+      d.big = true;
+      d.kper = kper_big;
+    }
+  }
   d.splits = (KS + d.kper - 1) / d.kper;
   return d;
 }
@@ -815,10 +862,15 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
 #undef VMAMD_GEMV
     return check_launch("w8a8_block_fp8_matmul(gemv)");
   }
-  if (plan.splits == 1 && as_stride_m >= 0 && as_stride_k >= 0) {
+  if (as_stride_m >= 0 && as_stride_k >= 0) {
     const int64_t as_extent = ((m - 1) * as_stride_m + (k / 128 - 1) * as_stride_k + 1) * 4;
-    if (use_big_gemm(m, n, k, as_extent))
+    const bool big_ok = static_cast<int64_t>(m + 256) * k < (1ll << 31) &&
+                        static_cast<int64_t>(n + 256) * k < (1ll << 31) && as_extent < (1ll << 31);
+    if (plan.splits == 1 && use_big_gemm(m, n, k, as_extent))
       return launch_big(a, As, as_stride_m, as_stride_k, static_cast<int>(as_extent), b, Bs, c, m, n, k, st);
+    if (plan.splits > 1 && plan.big && big_ok)
+      return launch_big(a, As, as_stride_m, as_stride_k, static_cast<int>(as_extent), b, Bs, c, m, n, k, st,
+                        plan.splits, plan.kper, static_cast<float*>(workspace));
   }
   static bool lds_raised = false;
   if (!lds_raised) {
