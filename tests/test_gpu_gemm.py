@@ -84,6 +84,25 @@ def test_block_fp8_gemm_256_row_tiles_column_major_scales():
     assert torch.equal(a, b)
 
 
+def test_block_fp8_gemm_256_row_tiles_unaligned_out():
+    """The 256-row GEMM stages its bf16 tile through LDS and stores whole
+    16-byte chunks when C is 16-byte aligned; an output 8 bytes off that
+    alignment takes the per-fragment stores: the same bits."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    M, N, K = 4000, 2112, 1024
+    w, ws = synthetic.dense_fp8_weight(N, K, 45)
+    xq, xs = per_token_group_quant_fp8(synthetic.activations(M, K, 46), 128)
+    a = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    assert a.data_ptr() % 16 == 0
+    buf = torch.full((M * N + 4,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    out = buf[4:].view(M, N)
+    assert out.data_ptr() % 16 == 8
+    w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128], out=out)
+    assert torch.equal(a, out)
+
+
 @pytest.mark.parametrize("M", [512, 700])
 def test_block_fp8_gemm_256_row_tiles_split_k(M):
     """Long rows at mid M (7168 x 16384): the 256 x 256 GEMM with K split over

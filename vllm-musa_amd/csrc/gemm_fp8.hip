@@ -197,13 +197,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemv_rsrc(const void* base, in
 // which gives 7168-row weights 32 column tiles -- two full rounds of 256 CUs
 // at M = 4096 instead of 1.75 -- measured 3 % slower there.)
 using BigPipe = BigTile;
+static_assert(BigTile::BM * 512 <= BigTile::kLds, "the bf16 output tile is staged in the stages' LDS");
+#ifndef VMAMD_BIG_ROW_STORE
+#define VMAMD_BIG_ROW_STORE 1
+#endif
 
 // as_bytes: the extent of As in bytes (< 2 GiB); the host keeps (M + 256) K
 // and (N + 256) K below 2^31.
 __global__ __launch_bounds__(BigPipe::kThreads, 1) void gemm_fp8_big_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t as_sm, int64_t as_sk,
     int as_bytes, const uint8_t* __restrict__ B, const float* __restrict__ Bs, uint16_t* __restrict__ C,
-    int M, int N, int K, int TM, int TN, int kper, float* __restrict__ partial) {
+    int M, int N, int K, int TM, int TN, int kper, float* __restrict__ partial, int row_store) {
   using P = BigPipe;
   constexpr int NT = P::NT;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
@@ -307,6 +311,37 @@ __global__ __launch_bounds__(BigPipe::kThreads, 1) void gemm_fp8_big_kernel(
     mma(smem_dyn + (j & 1) * P::kStage);
   }
 
+  if (row_store) {
+    // bf16 C through LDS: tile row r takes 512 bytes, its 16-byte chunk c at
+    // slot c ^ (r & 31); then each half-wave stores one whole 512-byte tile
+    // row (the fragment stores below write 32-byte pieces of 16 rows per
+    // instruction).  The host sets row_store for N % 8 == 0, a 16-byte aligned
+    // C and no split.
+    uint8_t* ct = smem_dyn;
+    __syncthreads();  // every wave is done with the stages
+#pragma unroll
+    for (int mt = 0; mt < P::MT; ++mt) {
+      const int row = wm * 64 + mt * 16 + li;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int col = nw + nt * 16 + 4 * lg;
+        const v4f a = acc[mt][nt];
+        const int off = row * 512 + (((col >> 3) ^ (row & 31)) << 4) + ((col >> 2) & 1) * 8;
+        *reinterpret_cast<uint2*>(ct + off) = pack_bf16x4(a[0], a[1], a[2], a[3]);
+      }
+    }
+    __syncthreads();
+    const int c = lane % 32, n = n0 + c * 8;
+#pragma unroll 4
+    for (int it = 0; it < P::BM / 16; ++it) {
+      const int row = it * 16 + wave * 2 + lane / 32;
+      const int m = m0 + row;
+      if (m >= M || n >= N) continue;
+      const uint4 v = *reinterpret_cast<const uint4*>(ct + row * 512 + ((c ^ (row & 31)) << 4));
+      *reinterpret_cast<uint4*>(C + static_cast<int64_t>(m) * N + n) = v;
+    }
+    return;
+  }
 #pragma unroll
   for (int mt = 0; mt < P::MT; ++mt) {
     const int m = m0 + wm * 64 + mt * 16 + li;
@@ -361,8 +396,11 @@ static int launch_big(const uint8_t* a, const float* As, int64_t as_sm, int64_t 
   }
   const int TM = (m + P::BM - 1) / P::BM, TN = (n + P::BN - 1) / P::BN;
   if (splits <= 1) kper = k / 128;
+  const int row_store = VMAMD_BIG_ROW_STORE && splits <= 1 && n % 8 == 0 &&
+                        reinterpret_cast<uintptr_t>(c) % 16 == 0;
   gemm_fp8_big_kernel<<<dim3(xcd_grid(TM * TN), splits), P::kThreads, P::kLds, st>>>(
-      a, As, as_sm, as_sk, as_bytes, b, Bs, c, m, n, k, TM, TN, kper, splits > 1 ? partial : nullptr);
+      a, As, as_sm, as_sk, as_bytes, b, Bs, c, m, n, k, TM, TN, kper, splits > 1 ? partial : nullptr,
+      row_store);
   int rc = check_launch("w8a8_block_fp8_matmul(gemm)");
   if (rc || splits <= 1) return rc;
   splitk_reduce(partial, splits, static_cast<int64_t>(m) * n, c, st);
