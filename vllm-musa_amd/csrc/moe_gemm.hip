@@ -956,17 +956,33 @@ __device__ __forceinline__ void moe_tile_decode(int L, const int32_t* __restrict
   mb_out = b0 + local % nb;
 }
 
+#ifndef VMAMD_TILE_EIDS
+#define VMAMD_TILE_EIDS 1
+#endif
 template <int BM = kMoeBM>
 __device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* __restrict__ offsets,
-                                         const int32_t* __restrict__ ntpp, int E, int TN,
-                                         int& e_out, int& mb_out, int& tn_out) {
+                                         const int32_t* __restrict__ ntpp, const int32_t* __restrict__ eids,
+                                         int E, int TN, int& e_out, int& mb_out, int& tn_out) {
   const int used = min(ntpp[0] / BM * TN, max_tiles);
   const int per = (used + kXcds - 1) / kXcds;
   const int q = wg / kXcds;
   if (q >= per) return false;
   const int L = (wg % kXcds) * per + q;
   if (L >= used) return false;
-  moe_tile_decode<BM>(L, offsets, E, TN, e_out, mb_out, tn_out);
+  if (VMAMD_TILE_EIDS && eids) {
+    // Tile L lies in block L / TN, whose expert the alignment recorded (its
+    // block size is BM): one load, then the expert's two offsets together,
+    // instead of a dependent binary search over the offsets.
+    const int e = eids[L / TN];
+    const int b0 = offsets[e] / BM;
+    const int nb = offsets[e + 1] / BM - b0;
+    const int local = L - b0 * TN;
+    e_out = e;
+    tn_out = local / nb;
+    mb_out = b0 + local % nb;
+  } else {
+    moe_tile_decode<BM>(L, offsets, E, TN, e_out, mb_out, tn_out);
+  }
   return true;
 }
 
@@ -989,7 +1005,7 @@ template <int KIND, bool W13>
 __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int topk, int K,
     const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles,
+    const int32_t* __restrict__ ntpp, const int32_t* __restrict__ eids, int E, int numel, int max_tiles,
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int N, int I, float limit,
     const float* __restrict__ route_w, uint8_t* __restrict__ a2, float* __restrict__ a2s,
     uint16_t* __restrict__ y) {
@@ -999,7 +1015,7 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
   const int TN = W13 ? I / 128 : (N + BN - 1) / BN;
   int e, mb, tn;
-  if (!moe_tile(blockIdx.x, max_tiles, offsets, ntpp, E, TN, e, mb, tn)) return;
+  if (!moe_tile(blockIdx.x, max_tiles, offsets, ntpp, eids, E, TN, e, mb, tn)) return;
   const int n0 = W13 ? tn * 128 : tn * BN;
   const int tid = threadIdx.x, lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -1283,7 +1299,7 @@ template <int KIND, bool W13>
 __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_s_bytes,
     int topk, int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles, const uint8_t* __restrict__ w,
+    const int32_t* __restrict__ ntpp, const int32_t* __restrict__ eids, int E, int numel, int max_tiles, const uint8_t* __restrict__ w,
     const float* __restrict__ ws, int N, int I, float limit, const float* __restrict__ route_w,
     uint8_t* __restrict__ a2, float* __restrict__ a2s, uint16_t* __restrict__ y) {
   using P = BigTile;
@@ -1291,7 +1307,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
   const int TN = W13 ? I / 128 : (N + P::BN - 1) / P::BN;
   int e, mb, tn;
-  if (!moe_tile<BM>(blockIdx.x, max_tiles, offsets, ntpp, E, TN, e, mb, tn)) return;
+  if (!moe_tile<BM>(blockIdx.x, max_tiles, offsets, ntpp, eids, E, TN, e, mb, tn)) return;
   const int n0 = W13 ? tn * 128 : tn * P::BN;
   const int tid = threadIdx.x, lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -1591,14 +1607,14 @@ __global__ __launch_bounds__(512, 1) void moe_w4_gemm_kernel(
     const uint8_t* __restrict__ act, const float* __restrict__ act_scale,
     const float* __restrict__ act_corr, int act_bytes, int topk, int K,
     const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ ntpp, int E, int numel, int max_tiles, const uint8_t* __restrict__ w,
+    const int32_t* __restrict__ ntpp, const int32_t* __restrict__ eids, int E, int numel, int max_tiles, const uint8_t* __restrict__ w,
     const uint16_t* __restrict__ ws, int N, int I, float limit, uint16_t* __restrict__ out) {
   using P = W4Pipe;
   constexpr int BM = P::BM, BN = P::BN, NS = P::NS, MT = P::MT, NT = P::NT, WN = 4, WTM = 64, WTN = 64;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
   const int TN = W13 ? I / 128 : (N + BN - 1) / BN;
   int e, mb, tn;
-  if (!moe_tile(blockIdx.x, max_tiles, offsets, ntpp, E, TN, e, mb, tn)) return;
+  if (!moe_tile(blockIdx.x, max_tiles, offsets, ntpp, eids, E, TN, e, mb, tn)) return;
   const int n0 = W13 ? tn * 128 : tn * BN;
   const int tid = threadIdx.x, lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -1887,8 +1903,8 @@ static int raise_w4_lds() {
 template <bool W13>
 static int launch_w4_gemm(const uint8_t* act, int64_t act_rows, const float* act_scale,
                           const float* act_corr, int topk, int K, const int32_t* sorted,
-                          const int32_t* offs, const int32_t* ntpp, int E, int numel, int tiles,
-                          const uint8_t* w, const void* ws, int N, int I, float limit, uint16_t* out,
+                          const int32_t* offs, const int32_t* ntpp, const int32_t* eids, int E, int numel,
+                          int tiles, const uint8_t* w, const void* ws, int N, int I, float limit, uint16_t* out,
                           hipStream_t st) {
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(ws) % 4 == 0,
                 "w4afp8 moe: weight scales must be 4-byte aligned for the grouped GEMMs");
@@ -1899,13 +1915,13 @@ static int launch_w4_gemm(const uint8_t* act, int64_t act_rows, const float* act
     int rc = raise_w4_lds<W13, true>();
     if (rc) return rc;
     moe_w4_gemm_kernel<W13, true><<<xcd_grid(tiles), 512, W4Pipe::kLds, st>>>(
-        act, act_scale, act_corr, act_bytes, topk, K, sorted, offs, ntpp, E, numel, tiles, w, wsh, N, I,
+        act, act_scale, act_corr, act_bytes, topk, K, sorted, offs, ntpp, eids, E, numel, tiles, w, wsh, N, I,
         limit, out);
   } else {
     int rc = raise_w4_lds<W13, false>();
     if (rc) return rc;
     moe_w4_gemm_kernel<W13, false><<<xcd_grid(tiles), 512, W4Pipe::kLds, st>>>(
-        act, act_scale, act_corr, act_bytes, topk, K, sorted, offs, ntpp, E, numel, tiles, w, wsh, N, I,
+        act, act_scale, act_corr, act_bytes, topk, K, sorted, offs, ntpp, eids, E, numel, tiles, w, wsh, N, I,
         limit, out);
   }
   return check_launch(W13 ? "w4afp8 moe w13 (gemm)" : "w4afp8 moe w2 (gemm)");
@@ -2051,7 +2067,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
                       const int32_t* ntpp, const int32_t* active, const int32_t* nact,
                       const uint8_t* w13, const void* w13_s, int E, int I, float limit,
                       const float* route_w, uint8_t* a2, float* a2s, float* a2corr, float* scratch,
-                      hipStream_t st) {
+                      hipStream_t st, const int32_t* eids = nullptr) {
   const int numel = T * topk;
   const float* act_s = KIND == kW4 ? xcorr : xs;  // per-step activation values the GEMV reads
   if (block_m == kGemvBlock) {
@@ -2075,7 +2091,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
       if (rc) return rc;
       moe_big_kernel<KIND, true><<<xcd_grid(tiles), BigTile::kThreads, BigTile::kLds, st>>>(
           xa, static_cast<int>(static_cast<int64_t>(T) * H * eb), xs, static_cast<int>(static_cast<int64_t>(T) * (H / 128) * 4),
-          topk, H, sorted, offs, ntpp, E, numel, tiles, w13, static_cast<const float*>(w13_s), 2 * I, I, limit,
+          topk, H, sorted, offs, ntpp, eids, E, numel, tiles, w13, static_cast<const float*>(w13_s), 2 * I, I, limit,
           route_w, a2, a2s, nullptr);
       return check_launch("moe w13 (gemm)");
     }
@@ -2083,7 +2099,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
   const int tiles = max_blocks * (I / 128);
   if constexpr (KIND == kW4) {
-    return launch_w4_gemm<true>(xa, T, xs, xcorr, topk, H, sorted, offs, ntpp, E, numel, tiles, w13,
+    return launch_w4_gemm<true>(xa, T, xs, xcorr, topk, H, sorted, offs, ntpp, eids, E, numel, tiles, w13,
                                 w13_s, 2 * I, I, limit, reinterpret_cast<uint16_t*>(a2), st);
   } else {
     int rc = raise_dma_lds<KIND, true>();
@@ -2091,7 +2107,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
     const int64_t abytes = static_cast<int64_t>(T) * H * KindBytes<KIND>::kAct / KindBytes<KIND>::kElems;
     VMAMD_REQUIRE(abytes < (1ll << 31), "moe w13: activations past 2 GiB for the grouped GEMM");
     moe_gemm_dma_kernel<KIND, true><<<xcd_grid(tiles), 512, MoePipe<KIND>::kLds, st>>>(
-        xa, static_cast<int>(abytes), xs, topk, H, sorted, offs, ntpp, E, numel, tiles, w13,
+        xa, static_cast<int>(abytes), xs, topk, H, sorted, offs, ntpp, eids, E, numel, tiles, w13,
         static_cast<const float*>(w13_s), 2 * I, I, limit, route_w, a2, a2s, nullptr);
   }
   return check_launch("moe w13 (gemm)");
@@ -2110,7 +2126,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
                      int E, int H, int I, const float* topk_weights, const float* route_w,
                      const int32_t* topk_ids, const int32_t* emap, int64_t emap_len, uint16_t* y,
                      float* scratch, hipStream_t st, uint16_t* combined_out = nullptr,
-                     bool* combined = nullptr) {
+                     bool* combined = nullptr, const int32_t* eids = nullptr) {
   const int numel = T * topk;
   const float* yscale = KIND == kW4 ? a2s : route_w;
   const float* act_s = KIND == kW4 ? a2corr : a2s;  // per-step activation values the GEMV reads
@@ -2157,7 +2173,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
       int rc = raise_big_lds<KIND, false>();
       if (rc) return rc;
       moe_big_kernel<KIND, false><<<xcd_grid(tiles), BigTile::kThreads, BigTile::kLds, st>>>(
-          a2, static_cast<int>(cap * I * eb), a2s, static_cast<int>(cap * (I / 128) * 4), 1, I, sorted, offs, ntpp, E,
+          a2, static_cast<int>(cap * I * eb), a2s, static_cast<int>(cap * (I / 128) * 4), 1, I, sorted, offs, ntpp, eids, E,
           numel, tiles, w2, static_cast<const float*>(w2_s), H, I, 0.f, route_w, nullptr, nullptr, y);
       return check_launch("moe w2 (gemm)");
     }
@@ -2165,7 +2181,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
   if constexpr (KIND == kW4) {
     const int tiles = max_blocks * ((H + W4Pipe::BN - 1) / W4Pipe::BN);
-    return launch_w4_gemm<false>(a2, cap, a2s, a2corr, 1, I, sorted, offs, ntpp, E, numel, tiles, w2,
+    return launch_w4_gemm<false>(a2, cap, a2s, a2corr, 1, I, sorted, offs, ntpp, eids, E, numel, tiles, w2,
                                  w2_s, H, I, 0.f, y, st);
   } else {
     const int tiles = max_blocks * ((H + 255) / 256);
@@ -2174,7 +2190,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
     const int64_t abytes = cap * I * KindBytes<KIND>::kAct / KindBytes<KIND>::kElems;
     VMAMD_REQUIRE(abytes < (1ll << 31), "moe w2: activations past 2 GiB for the grouped GEMM");
     moe_gemm_dma_kernel<KIND, false><<<xcd_grid(tiles), 512, MoePipe<KIND>::kLds, st>>>(
-        a2, static_cast<int>(abytes), a2s, 1, I, sorted, offs, ntpp, E, numel, tiles, w2, static_cast<const float*>(w2_s), H,
+        a2, static_cast<int>(abytes), a2s, 1, I, sorted, offs, ntpp, eids, E, numel, tiles, w2, static_cast<const float*>(w2_s), H,
         I, 0.f, route_w, nullptr, nullptr, y);
   }
   return check_launch("moe w2 (gemm)");
@@ -2428,7 +2444,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   uint8_t* act_out = KIND == kW4 && bm != kGemvBlock ? ws + L.abf : a2;
   rc = launch_w13<KIND>(xa, xs, xcorr, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
                         static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, w13_rw, act_out,
-                        a2s, a2corr, scratch, st);
+                        a2s, a2corr, scratch, st, eids);
   if (rc) return rc;
   if constexpr (KIND == kW4) {
     if (bm != kGemvBlock) {  // rows past the last block are skipped on the device
@@ -2441,7 +2457,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   rc = launch_w2<KIND>(a2, a2s, a2corr, t, topk, sorted, cap, bm, offs, ntpp, active, nact,
                        static_cast<const uint8_t*>(w2), w2_s, E, h, i, topk_weights, w2_rw, topk_ids,
                        expert_map, expert_map_len, y, scratch, st, static_cast<uint16_t*>(out),
-                       &combined);
+                       &combined, eids);
   if (rc || combined) return rc;
   // Slots of dropped routes (negative ids, or non-local experts) hold no
   // expert output and are skipped by the combine.
