@@ -37,6 +37,7 @@ typedef struct ihipStream_t* vmamd_stream_t; /* == hipStream_t */
 #define VMAMD_DTYPE_F16 1
 #define VMAMD_DTYPE_BF16 2
 #define VMAMD_DTYPE_E8M0 3 /* unsigned power-of-two exponent byte (scales only) */
+#define VMAMD_DTYPE_E4M3 4 /* OCP float8 e4m3fn operand (the GEMV ops)            */
 
 /* Message of the last error on this thread ("" if none). */
 const char* vmamd_last_error(void);
@@ -225,9 +226,11 @@ int vmamd_moe_weighted_sum(const void* x, int dtype, int64_t tokens, int topk, i
  * and larger M the unsplit GEMM, whose fp32 sums run in another order.
  * Results are deterministic for a given shape and workspace.  Replaces
  * w8a8_triton_block_scaled_mm(A, B, As, Bs, block_size, output_dtype) as
- * called at vllm_musa/deepseek_v4_jit/fp8_einsum.py:399-406, fp8_gemm_nt in
- * _musa_deepgemm_fp8_op (model_executor/kernels/linear/scaled_mm/deep_gemm.py:233-262)
- * and the small-M GEMV musa_fused_gemv (csrc/musa/gemv.mu:723-925). */
+ * called at vllm_musa/deepseek_v4_jit/fp8_einsum.py:399-406 and fp8_gemm_nt in
+ * _musa_deepgemm_fp8_op (model_executor/kernels/linear/scaled_mm/deep_gemm.py:233-262),
+ * both W8A8: the activations arrive quantised.  The reference's small-M
+ * musa_fused_gemv, which reads bf16 activations unquantised, is
+ * vmamd_fused_gemv below. */
 size_t vmamd_w8a8_block_fp8_matmul_workspace_size(int64_t M, int64_t N, int64_t K);
 int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64_t as_stride_m,
                                 int64_t as_stride_k, const void* B, const float* Bs, void* C,
@@ -272,16 +275,26 @@ int vmamd_w8a8_block_fp8_matmul_noalloc(const void* A, const float* As, int64_t 
  * GEMM) kernels above; GEMV / GEMM force one.  On the decode kernels one
  * token (top-k <= 16) skips the alignment: each route is its own GEMV slot,
  * x is quantised inside the W13 launch and the W2 launch sums the top-k
- * (same bits as the aligned form).  Workspace:
- * vmamd_fused_moe_fp8_workspace_size() bytes, 256-byte aligned.
+ * (same bits as the aligned form).  NATIVE_GEMV computes the layer with the
+ * numerics of the reference's native GEMV-MoE instead (decode kernels only):
+ * x is not quantised (bf16 x dequantised fp8), gate and up stay fp32 through
+ * the SwiGLU (clamped with the limit rounded to bf16), and the routed weight
+ * multiplies gate and up before it (apply_router_weight_on_input) or the W2
+ * sum after it:
+ *   out[t] = bf16( sum_k bf16( (W2[e] . a) * w[t,k] ) ),
+ *   a = bf16(silu(g) * u), (g, u) = fp32 W13[e] . x[t]
+ * Workspace: vmamd_fused_moe_fp8_workspace_size() bytes (for the same path),
+ * 256-byte aligned.
  * Replaces fused_experts_impl / _musa_fused_experts_impl_dispatch
  * (vllm_musa/model_executor/layers/fused_moe/fused_moe.py:1935-2184,
- * 2214-2760) for use_fp8_w8a8 with block_shape [128, 128], including the
- * DeepGEMM prefill path (824-951) and the native GEMV-MoE
- * musa_fused_gemv_moe (csrc/musa/gemv.mu:927-1170). */
+ * 2214-2760) for use_fp8_w8a8 with block_shape [128, 128]: the W8A8
+ * upstream Triton and DeepGEMM prefill (824-951) paths (AUTO / GEMV / GEMM),
+ * and the driver loop over the native GEMV-MoE musa_fused_gemv_moe
+ * (fused_moe.py:2126-2184, csrc/musa/gemv.mu:249-514) as NATIVE_GEMV. */
 #define VMAMD_MOE_PATH_AUTO 0
 #define VMAMD_MOE_PATH_GEMV 1
 #define VMAMD_MOE_PATH_GEMM 2
+#define VMAMD_MOE_PATH_NATIVE_GEMV 3
 size_t vmamd_fused_moe_fp8_workspace_size(int64_t T, int topk, int num_experts, int64_t H,
                                           int64_t I, int path);
 int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H, const void* w13,
@@ -344,7 +357,10 @@ int vmamd_moe_fp8_w2(const void* a2q, const float* a2s, int64_t T, int topk,
  *   a = bf16(silu(h_g) * h_u),  h = bf16(W13[e] . x[t])   (fp32 accumulation)
  * x [T, H] bf16; w13 [E, 2I, H] bf16; w2 [E, H, I] bf16; a2 bf16 rows as for
  * fp8 ([T*topk, I] for block_m 16, [capacity, I] for 128).  Routing,
- * expert_map, swiglu_limit, path and workspace rules as for fp8. */
+ * expert_map, swiglu_limit, path and workspace rules as for fp8;
+ * NATIVE_GEMV keeps gate and up in fp32 through the SwiGLU, as the
+ * reference's native bf16 GEMV-MoE does (csrc/musa/gemv.mu:430-434, 477-487):
+ *   a = bf16(silu(g) * u), (g, u) = fp32 W13[e] . x[t]. */
 size_t vmamd_fused_moe_bf16_workspace_size(int64_t T, int topk, int num_experts, int64_t H,
                                            int64_t I, int path);
 int vmamd_fused_moe_bf16(const void* x, int64_t T, int64_t H, const void* w13, const void* w2,
@@ -393,6 +409,49 @@ int vmamd_w4afp8_moe(const void* x, int64_t T, int64_t H, const void* w13, const
                      const int32_t* expert_map, int64_t expert_map_len, float swiglu_limit,
                      int path, void* out, void* workspace, size_t workspace_bytes,
                      vmamd_stream_t stream);
+
+/* ------------------------------------------------- reference GEMV ops --
+ * The reference's native GEMVs with their numerics: the activations are read
+ * as they are (bf16 against fp8 weights dequantised per 128x128 block, no
+ * activation quantisation), sums in fp32, one bf16 rounding of the output.
+ *
+ * vmamd_fused_gemv_moe: A [rows, K]; B [E, N, K]; route r = row*topk + k
+ * (r < rows*topk) uses expert e = topk_ids[r] and writes row r of C:
+ *   acc = sum_kb B_scale[e, n/128, kb] * sum_{k in kb} A[row, k] * B[e, n, k]
+ *   acc *= topk_weights[r]                    (mul_routed_weight != 0)
+ *   use_swiglu: C [rows*topk, N/2] = bf16(g * sigmoid(g) * u), g = acc[n],
+ *               u = acc[N/2 + n], after g <= L, u in [-L, L] when
+ *               swiglu_limit L > 0 (L is rounded to bf16 for bf16 A)
+ *   otherwise   C [rows*topk, N] = bf16(acc)
+ * A: bf16 (B e4m3 with B_scale [E, ceil(N/128), K/128] f32, or B bf16 with
+ * no scales) or e4m3 with A_scale [rows, K/128] f32 (then B e4m3 and the
+ * products carry A_scale[row, kb] too).  topk_ids / topk_weights: i32 / f32
+ * with rows*topk entries.  A route whose id is outside [0, E) gets a zero
+ * row.  K % 128 == 0 (bf16 B: K % 64), N % 16 == 0 (use_swiglu: N % 32);
+ * A, B, C 16-byte aligned.  Up to 16 routes run one GEMV slot per route; more
+ * are grouped per expert (weights streamed once per 16 routes).  Workspace:
+ * vmamd_fused_gemv_moe_workspace_size() bytes, 256-byte aligned.
+ * Replaces musa_fused_gemv_moe (csrc/musa/gemv.mu:927-1170, kernel 249-514;
+ * schema csrc/musa/torch_bindings.cpp:11-15). */
+size_t vmamd_fused_gemv_moe_workspace_size(int64_t rows, int topk, int num_experts, int64_t N,
+                                           int64_t K, int a_dtype, int b_dtype);
+int vmamd_fused_gemv_moe(const void* A, int a_dtype, const float* A_scale, int64_t rows, int64_t K,
+                         const void* B, int b_dtype, const float* B_scale, int num_experts,
+                         int64_t N, const float* topk_weights, const int32_t* topk_ids, int topk,
+                         int mul_routed_weight, int use_swiglu, float swiglu_limit, void* C,
+                         void* workspace, size_t workspace_bytes, vmamd_stream_t stream);
+
+/* vmamd_fused_gemv: the dense GEMV, C [M, N or N/2] = the rows of A against
+ * one weight matrix B [N, K] (B_scale [ceil(N/128), K/128] for e4m3 B), with
+ * the vmamd_fused_gemv_moe rules for one expert, topk 1 and no routed weight.
+ * Workspace: vmamd_fused_gemv_workspace_size() bytes, 256-byte aligned.
+ * Replaces musa_fused_gemv (csrc/musa/gemv.mu:723-925; schema
+ * csrc/musa/torch_bindings.cpp:17-21) as _musa_fp8_small_m_gemv_op calls it
+ * (vllm_musa/model_executor/kernels/linear/scaled_mm/deep_gemm.py:512-536). */
+size_t vmamd_fused_gemv_workspace_size(int64_t M, int64_t N, int64_t K, int a_dtype, int b_dtype);
+int vmamd_fused_gemv(const void* A, int a_dtype, const float* A_scale, int64_t M, int64_t K,
+                     const void* B, int b_dtype, const float* B_scale, int64_t N, int use_swiglu,
+                     void* C, void* workspace, size_t workspace_bytes, vmamd_stream_t stream);
 
 /* ------------------------------------------------------ checkpoint scales --
  * Converts n weight scales from src_dtype (E8M0, F32 or BF16) to dst_dtype

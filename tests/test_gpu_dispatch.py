@@ -1,8 +1,10 @@
-"""fused_experts_impl(path="auto") follows the calibrated dispatch table on the
-GPU: on a calibrated fp8 shape (E=256, N=256, H=2048, top-8; decode path up
-to 64 tokens) the result is bitwise the forced decode path's up to the
-threshold and the forced grouped GEMMs' above it, the override applies, and
-a captured call follows the capture entry."""
+"""fused_experts_impl(path="auto") follows the dispatch on the GPU.  On the
+fp8 shape E=256, N=256, H=2048, top-8 the reference runs its native GEMV up
+to 13 tokens (its S5000 table), so auto computes those numerics there
+(path 3); above, MI355X's own table picks the W8A8 decode kernels up to 64
+tokens (path 1) and the grouped GEMMs beyond (path 2).  Each result is
+bitwise the forced path's, the overrides map to the reference's backends,
+and a captured call follows the capture entry."""
 from __future__ import annotations
 
 import pytest
@@ -22,8 +24,9 @@ def layer():
 
 @pytest.fixture
 def paths(monkeypatch):
-    """Records the path code (1 = decode kernels, 2 = grouped GEMMs) of every
-    fused fp8 layer launched through the C ABI."""
+    """Records the path code (1 = W8A8 decode kernels, 2 = grouped GEMMs,
+    3 = native GEMV numerics) of every fused fp8 layer launched through the
+    C ABI."""
     from vllm_musa_amd import fused_moe
     seen = []
     real = fused_moe.call
@@ -56,11 +59,12 @@ def test_auto_follows_the_calibrated_threshold(layer, paths):
     x = torch.zeros(1, H, dtype=torch.bfloat16, device="cuda")
     th = thresholds_for_shape(shape_of_layer(x, w13, w2, s13, s2, TOPK, [128, 128], None, "eager"))
     assert th.gemv_max_tokens == 64, th  # the device really is the calibrated MI355X
-    for t, code in ((1, 1), (64, 1), (65, 2), (300, 2)):
+    forced = {1: "gemv", 2: "gemm", 3: "native_gemv"}
+    for t, code in ((1, 3), (13, 3), (14, 1), (64, 1), (65, 2), (300, 2)):
         paths.clear()
         out = _run(layer, t)
         assert paths == [code], (t, paths)
-        assert torch.equal(out, _run(layer, t, "gemv" if code == 1 else "gemm"))
+        assert torch.equal(out, _run(layer, t, forced[code]))
     assert dp.resolve_path(x, w13, w2, s13, s2, TOPK, [128, 128], None) == "gemv"
 
 
@@ -72,7 +76,7 @@ def test_override_forces_a_backend(layer, monkeypatch, paths):
     _run(layer, 100)
     monkeypatch.setenv(dp.MUSA_FUSED_MOE_DISPATCH_ENV, "upstream")
     _run(layer, 4)
-    assert paths == [2, 1, 2]
+    assert paths == [2, 3, 1]
 
 
 def test_captured_call_uses_capture_entry(layer, paths):
@@ -85,7 +89,7 @@ def test_captured_call_uses_capture_entry(layer, paths):
     w = torch.full((t, TOPK), 1.0 / TOPK, device="cuda")
     call = lambda path: fused_experts_impl(x, w13, w2, w, ids, use_fp8_w8a8=True, w1_scale=s13,
                                            w2_scale=s2, block_shape=[128, 128], path=path)
-    eager = call("gemv")
+    eager = call("native_gemv")
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -95,7 +99,7 @@ def test_captured_call_uses_capture_entry(layer, paths):
     paths.clear()
     with torch.cuda.graph(graph):
         out = call("auto")
-    assert paths == [1]
+    assert paths == [3]
     for _ in range(3):
         graph.replay()
         torch.cuda.synchronize()

@@ -13,6 +13,7 @@ namespace vmamd {
 
 constexpr int kWave = 64;
 
+typedef int v16i __attribute__((ext_vector_type(16)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));

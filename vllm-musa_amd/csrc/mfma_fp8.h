@@ -44,6 +44,31 @@ __device__ __forceinline__ v4f mfma_bf16x2(const v8i& a, const v8i& b, v4f c) {
   return c;
 }
 
+// bf16 activations against fp8 weights (the W8A16 GEMVs).  The lane's fp8
+// weight fragment (32 bytes in the layout above: K = 16g + e for byte e < 16,
+// K = 64 + 16g + e - 16 above) becomes 32 bf16 values with
+// v_cvt_scalef32_pk_bf16_fp8 at scale 1.0, which is exact: every e4m3 value,
+// subnormals included, is a bf16 value.  The activation fragment holds the
+// 32 bf16 activations of the same K positions in the same order, and four
+// chained v_mfma_f32_16x16x32_bf16 take elements [8j, 8j + 8) of both, so the
+// products (a bf16 times an e4m3 value: at most 12 significant bits) are exact
+// and only the fp32 accumulation rounds.
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ v4f mfma_w8a16(const v8i& w, const v16i& x, v4f c) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w0 = static_cast<uint32_t>(w[2 * j]), w1 = static_cast<uint32_t>(w[2 * j + 1]);
+    const v4i a = {__builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+                   __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+                   __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+                   __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+    const v4i b = {x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]};
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c,
+                                                 0, 0, 0);
+  }
+  return c;
+}
+
 // w4afp8 weight operands.  A signed int4 weight x (two per byte, element 2j
 // in the low nibble of byte j) enters the MFMA as the e4m3 code u = x + 8,
 // which is the nibble with its top bit flipped.  Codes 0..15 are the e4m3

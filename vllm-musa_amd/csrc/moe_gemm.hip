@@ -8,15 +8,19 @@
 //         nibble of byte j), bf16 scale per (output row, 128-K group):
 //         w13 [E, 2I, H/2] + [E, 2I, H/128]; w2 [E, H, I/2] + [E, H, I/128];
 //         activations fp8 with one scale per row: xq [T, H] + xs [T]
+//   kW8A16 the kFp8 weights against bf16 activations that are not quantised
+//         (decode GEMVs only): x [T, H] bf16, a2 [T*topk, I] bf16
 //   w13 rows [0, I) gate, [I, 2I) up; routes r = t * topk + k; sorted /
 //   offsets / active come from moe_align_block_size.
 //
 // Every kind moves K in "steps": 128 K-elements for kFp8 / kW4 (one 16x16x128
 // fp8 MFMA; kW4 nibbles are converted to e4m3 codes on the way in, every
-// integer in [-8, 7] being exact in e4m3), 64 for kBf16 (two 16x16x32 bf16
-// MFMAs).  Per step kFp8 promotes acc += p * sa[m] * sb[n/128], kW4 promotes
-// acc += p * sw[n] with the row's own weight scale and applies the activation
-// row scale once at the end, kBf16 accumulates directly.
+// integer in [-8, 7] being exact in e4m3) and kW8A16 (four 16x16x32 bf16
+// MFMAs on the exactly converted weights), 64 for kBf16 (two 16x16x32 bf16
+// MFMAs).  Per step kFp8 promotes acc += p * sa[m] * sb[n/128], kW8A16
+// acc += p * sb[n/128], kW4 promotes acc += p * sw[n] with the row's own
+// weight scale and applies the activation row scale once at the end, kBf16
+// accumulates directly.
 //
 // Decode path (few routes per expert): moe_gemv_kernel.  A wave owns 16
 // weight rows of one active expert and a K range; it streams the rows from
@@ -35,6 +39,7 @@
 // per tile (interleaved by 16 so each lane holds matching gate/up values) and
 // fuses SiLU-and-mul (and the kFp8 1x128 a2 quantiser) into its epilogue.
 #include <algorithm>
+#include <cstring>
 #include <type_traits>
 
 #include "quant_dev.h"
@@ -43,13 +48,22 @@
 
 namespace vmamd {
 
-constexpr int kFp8 = 0, kBf16 = 1, kW4 = 2;
+constexpr int kFp8 = 0, kBf16 = 1, kW4 = 2, kW8A16 = 3;
 
 // Bytes of one K step: activation row, weight row.
 template <int KIND> struct KindBytes {
-  static constexpr int kAct = 128;
+  static constexpr int kAct = KIND == kW8A16 ? 256 : 128;
   static constexpr int kW = KIND == kW4 ? 64 : 128;
   static constexpr int kElems = KIND == kBf16 ? 64 : 128;  // K elements per step
+};
+
+// Operands of a kind: per-step activation values (kFp8 group scales, kW4
+// block corrections), f32 weight block scales [E, N/128, K/128] (kFp8,
+// kW8A16), and the activation fragment (kW8A16: 32 bf16 values).
+template <int KIND> struct KindOps {
+  static constexpr bool kActScale = KIND == kFp8 || KIND == kW4;
+  static constexpr bool kBlockScale = KIND == kFp8 || KIND == kW8A16;
+  using AFrag = std::conditional_t<KIND == kW8A16, v16i, v8i>;
 };
 
 // --------------------------------------------------------------- helpers --
@@ -113,20 +127,29 @@ __device__ __forceinline__ v4i buffer_ld16(__amdgpu_buffer_rsrc_t rs, uint32_t o
   return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, 0));
 }
 // Activation fragment at byte offset off (row + K-block start) of a buffer
-// (kW4: the 32 contiguous bytes of lane group g, matching w4_frag).
+// (kW4: the 32 contiguous bytes of lane group g, matching w4_frag; kW8A16:
+// the bf16 activations of the K positions of the fp8 weight fragment,
+// elements [16g, 16g + 16) and [64 + 16g, 80 + 16g) of the step).
 template <int KIND>
-__device__ __forceinline__ v8i buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t off, int g) {
-  const uint32_t o0 = KIND == kW4 ? 32u * g : 16u * g;
-  const uint32_t o1 = KIND == kW4 ? 32u * g + 16u : 64u + 16u * g;
-  const v4i lo = buffer_ld16(rs, off + o0);
-  const v4i hi = buffer_ld16(rs, off + o1);
-  return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+__device__ __forceinline__ typename KindOps<KIND>::AFrag buffer_frag(__amdgpu_buffer_rsrc_t rs, uint32_t off,
+                                                                     int g) {
+  if constexpr (KIND == kW8A16) {
+    const v4i a = buffer_ld16(rs, off + 32u * g), b = buffer_ld16(rs, off + 32u * g + 16u);
+    const v4i c = buffer_ld16(rs, off + 128u + 32u * g), d = buffer_ld16(rs, off + 144u + 32u * g);
+    return v16i{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3], c[0], c[1], c[2], c[3], d[0], d[1], d[2], d[3]};
+  } else {
+    const uint32_t o0 = KIND == kW4 ? 32u * g : 16u * g;
+    const uint32_t o1 = KIND == kW4 ? 32u * g + 16u : 64u + 16u * g;
+    const v4i lo = buffer_ld16(rs, off + o0);
+    const v4i hi = buffer_ld16(rs, off + o1);
+    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
 }
 
-// act: [rows, K] activation bytes (rows = numel / act_div, kW4 in w4 order),
-// act_bytes its size (< 2^31); act_s: kFp8 [rows, K/128] group scales, kW4
-// [rows, K/128] offset corrections, kBf16 unused.  ws: kFp8 f32 block scales;
-// kW4 bf16 row scales.  kW4 results are scaled by kW4Unit before they are
+// act: [rows, K] activation bytes (rows = numel / act_div, kW4 in w4 order,
+// kBf16 / kW8A16 bf16), act_bytes its size (< 2^31); act_s: kFp8 [rows, K/128]
+// group scales, kW4 [rows, K/128] offset corrections, otherwise unused.  ws:
+// kFp8 / kW8A16 f32 block scales; kW4 bf16 row scales.  kW4 results are scaled by kW4Unit before they are
 // stored.
 //
 // Start-up order: the expert id is the only load the weight stream depends
@@ -164,8 +187,13 @@ constexpr bool gemv_stream1() { return MAXB == 1 && (KIND != kW4 || VS); }
 // w4 order with its block corrections, the token's row scale also written to
 // xs_out by the workgroup of the token's first route slot) instead of a
 // separate quantiser launch.
-constexpr int kGemvGrouped = 0, kGemvDirect = 1, kGemvCombine = 2, kGemvDirectQ = 3;
+// kGemvDense (a plain GEMV, one expert): every row of act is a route of
+// expert 0 in route-blocks of 16 consecutive rows; no alignment, no ids.
+constexpr int kGemvGrouped = 0, kGemvDirect = 1, kGemvCombine = 2, kGemvDirectQ = 3, kGemvDense = 4;
 constexpr int kMaxCombineSlots = 16;
+// kW8A16 holds twice the activation registers: its combine workgroups take
+// at most 8 slots, so that 256 VGPRs stay available.
+constexpr int combine_slots(int kind) { return kind == kW8A16 ? 8 : kMaxCombineSlots; }
 
 // Local expert of a route, -1 when it is dropped (negative id, not mapped,
 // or past the local experts) -- the rule of the alignment and of moe_sum.
@@ -177,7 +205,8 @@ __device__ __forceinline__ int route_expert(const int32_t* __restrict__ ids, int
 }
 
 template <int MAXB, int KIND, bool VS = false, int MODE = kGemvGrouped>
-__global__ __launch_bounds__((MODE == kGemvCombine ? kMaxCombineSlots : kMoeGemvWaves) * kWave, MAXB == 1 ? 3 : 2) void
+__global__ __launch_bounds__((MODE == kGemvCombine ? combine_slots(KIND) : kMoeGemvWaves) * kWave,
+                  MAXB == 1 && KIND != kW8A16 ? 3 : 2) void
 moe_gemv_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_div,
     int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
@@ -187,11 +216,15 @@ moe_gemv_kernel(
     const int32_t* __restrict__ ids, const int32_t* __restrict__ emap, int64_t emap_len, int E_,
     uint16_t* __restrict__ comb, const float* __restrict__ comb_w, float* __restrict__ xs_out) {
   using KB_ = KindBytes<KIND>;
+  using AF = typename KindOps<KIND>::AFrag;
+  constexpr bool kActS = KindOps<KIND>::kActScale, kBlkS = KindOps<KIND>::kBlockScale;
   constexpr int U = kGemvU;
   constexpr bool kStream1 = gemv_stream1<MAXB, KIND, VS>();
-  static_assert(MODE == kGemvGrouped || MAXB == 1, "direct route slots take one route per block");
+  static_assert(MODE == kGemvGrouped || MODE == kGemvDense || MAXB == 1,
+                "direct route slots take one route per block");
   constexpr bool kQx = MODE == kGemvDirectQ;
-  static_assert(!kQx || (KIND != kBf16 && VS && kStream1), "in-workgroup x quantiser: fp8 / w4, vector scales");
+  static_assert(!kQx || ((KIND == kFp8 || KIND == kW4) && VS && kStream1),
+                "in-workgroup x quantiser: fp8 / w4, vector scales");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const int li = lane % 16, lg = lane / 16;
   const int ntile = MODE == kGemvCombine ? static_cast<int>(blockIdx.x) : blockIdx.x * kMoeGemvWaves + wave;
@@ -209,6 +242,8 @@ moe_gemv_kernel(
     e = active[slot];
     const int na = num_active[0];
     if (slot >= na || e < 0) return;
+  } else if constexpr (MODE == kGemvDense) {
+    e = 0;
   } else if constexpr (MODE == kGemvDirect || MODE == kGemvDirectQ) {
     e = route_expert(ids, slot, emap, emap_len, E_);  // workgroup-uniform
     // kW4: the workgroup that writes the token's row scale runs the quantiser
@@ -255,21 +290,21 @@ moe_gemv_kernel(
   const int kb1 = min((split + 1) * groups / splits * kGemvU, KS);
   const int n = ntile * 16 + 4 * lg;
   const uint8_t* wrow = w + (static_cast<int64_t>(e) * N + ntile * 16 + li) * wrowb;
-  const float* wsr = nullptr;                        // kFp8: block scales of the 16 rows
+  const float* wsr = nullptr;                        // kFp8 / kW8A16: block scales of the 16 rows
   const uint16_t* wsw[4] = {nullptr, nullptr, nullptr, nullptr};  // kW4: scales of rows n..n+3
-  if constexpr (KIND == kFp8)
+  if constexpr (kBlkS)
     wsr = static_cast<const float*>(ws) + (static_cast<int64_t>(e) * NB + (ntile * 16) / 128) * KS;
   if constexpr (KIND == kW4) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       wsw[r] = static_cast<const uint16_t*>(ws) + (static_cast<int64_t>(e) * N + n + r) * KS;
   }
-  // kFp8 block scales of the wave's rows through a descriptor: uniform values
+  // Block scales of the wave's rows through a descriptor: uniform values
   // read by vector loads, which queue behind the weight loads instead of
   // making the weight stream wait for scalar loads.
-  const __amdgpu_buffer_rsrc_t wsrs = buffer_rsrc(wsr, KIND == kFp8 ? KS * 4 : 0);
+  const __amdgpu_buffer_rsrc_t wsrs = buffer_rsrc(wsr, kBlkS ? KS * 4 : 0);
   const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(act, act_bytes);
-  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(act_s, KIND != kBf16 ? act_bytes / 32 : 0);
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(act_s, kActS ? act_bytes / 32 : 0);
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
 
   // One K group of weights (U steps from kb, clamped to the split's range).
@@ -297,7 +332,7 @@ moe_gemv_kernel(
         wf[u] = weight_frag<KIND>(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
       if constexpr (!VS) sb[u] = 0.f;
       sw[u] = zero;
-      if constexpr (KIND == kFp8 && !VS)
+      if constexpr (kBlkS && !VS)
         sb[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsrs, k * 4, 0, 0));
       if constexpr (KIND == kW4 && !VS)
         sw[u] = v4f{bf16_to_f32(wsw[0][k]), bf16_to_f32(wsw[1][k]), bf16_to_f32(wsw[2][k]),
@@ -329,9 +364,9 @@ moe_gemv_kernel(
 #pragma unroll
     for (int b = 0; b < MAXB; ++b) {
       if (b < nb) {
-        v8i xf[U];
+        AF xf[U];
         float as[U];
-        if constexpr (VS) {  // scale byte offset = activation byte offset / 32
+        if constexpr (VS && kActS) {  // scale byte offset = activation byte offset / 32
           const uint32_t off = aoff[b] != kBufferOff ? aoff[b] / 32 + static_cast<uint32_t>(kb * 4) : kBufferOff;
           const v4f s4 = __builtin_bit_cast(
               v4f, __builtin_amdgcn_raw_buffer_load_b128(srs, static_cast<int>(off), 0, 0));
@@ -343,8 +378,8 @@ moe_gemv_kernel(
           const bool live = aoff[b] != kBufferOff && kb + u < kb1;
           const uint32_t off = live ? aoff[b] + static_cast<uint32_t>((kb + u) * KB_::kAct) : kBufferOff;
           xf[u] = buffer_frag<KIND>(ars, off, lg);
-          if constexpr (!VS) as[u] = 0.f;
-          if constexpr (KIND != kBf16 && !VS)  // scale byte offset = activation byte offset / 32
+          if constexpr (!VS || !kActS) as[u] = 0.f;
+          if constexpr (kActS && !VS)  // scale byte offset = activation byte offset / 32
             as[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                   srs, static_cast<int>(live ? off / 32 : kBufferOff), 0, 0));
         }
@@ -352,6 +387,8 @@ moe_gemv_kernel(
         for (int u = 0; u < U; ++u) {
           if constexpr (KIND == kFp8) {
             fma4(acc[b], mfma_fp8(wf[u], xf[u], zero), as[u] * sb[u]);
+          } else if constexpr (KIND == kW8A16) {
+            fma4(acc[b], mfma_w8a16(wf[u], xf[u], zero), sb[u]);
           } else if constexpr (KIND == kW4) {
             if constexpr (kRawW4)
               fma4v(acc[b], mfma_fp8(w4_frag(wraw[u]), xf[u], splat4(as[u])), w4_scales(u));
@@ -374,7 +411,7 @@ moe_gemv_kernel(
   // MFMA, so U steps stay in flight instead of draining at every group.
   // The weights of group kb0 were requested by the caller.
   auto stream1 = [&](int kbs) {
-    v8i xf[U];
+    AF xf[U];
     float as[U];
     auto load_act = [&](int kb, int u) {
       const bool live = aoff[0] != kBufferOff && kb + u < kb1;
@@ -391,7 +428,7 @@ moe_gemv_kernel(
       }
       const uint32_t off = live ? aoff[0] + static_cast<uint32_t>((kb + u) * KB_::kAct) : kBufferOff;
       xf[u] = buffer_frag<KIND>(ars, off, lg);
-      if constexpr (KIND != kBf16 && !VS)
+      if constexpr (kActS && !VS)
         as[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                               srs, static_cast<int>(live ? off / 32 : kBufferOff), 0, 0));
     };
@@ -406,17 +443,17 @@ moe_gemv_kernel(
         wraw[u] = ld16(wrow + static_cast<int64_t>(k) * KB_::kW + 16 * lg);
       else
         wf[u] = weight_frag<KIND>(wrow + static_cast<int64_t>(k) * KB_::kW, lg);
-      if constexpr (KIND == kFp8 && !VS)
+      if constexpr (kBlkS && !VS)
         sb[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsrs, k * 4, 0, 0));
       if constexpr (KIND == kW4 && !VS)
         sw[u] = v4f{bf16_to_f32(wsw[0][k]), bf16_to_f32(wsw[1][k]), bf16_to_f32(wsw[2][k]),
                     bf16_to_f32(wsw[3][k])};
     };
     v4f asn = zero;
-    if constexpr (VS && KIND != kBf16) asn = load_as_vs(kbs);
+    if constexpr (VS && kActS) asn = load_as_vs(kbs);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if constexpr (!VS) as[u] = 0.f;
+      if constexpr (!VS || !kActS) as[u] = 0.f;
       load_act(kbs, u);
     }
     for (int kb = kbs; kb < kb1; kb += U) {
@@ -429,11 +466,13 @@ moe_gemv_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) swc[r] = swr[r];
       if constexpr (VS) {
+        if constexpr (kActS) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) as[u] = asn[u];
+          for (int u = 0; u < U; ++u) as[u] = asn[u];
+        }
         if (more) {
-          if constexpr (KIND != kBf16) asn = load_as_vs(kb + U);
-          if constexpr (KIND == kFp8) {
+          if constexpr (kActS) asn = load_as_vs(kb + U);
+          if constexpr (kBlkS) {
             const v4f s4 = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(wsrs, (kb + U) * 4, 0, 0));
 #pragma unroll
             for (int u = 0; u < U; ++u) sb[u] = s4[u];
@@ -448,6 +487,8 @@ moe_gemv_kernel(
       for (int u = 0; u < U; ++u) {
         if constexpr (KIND == kFp8) {
           fma4(acc[0], mfma_fp8(wf[u], xf[u], zero), as[u] * (VS ? sbc[u] : sb[u]));
+        } else if constexpr (KIND == kW8A16) {
+          fma4(acc[0], mfma_w8a16(wf[u], xf[u], zero), VS ? sbc[u] : sb[u]);
         } else if constexpr (KIND == kW4) {
           v4f sc;
           if constexpr (VS) {
@@ -476,6 +517,8 @@ moe_gemv_kernel(
   if constexpr (MODE == kGemvGrouped) {
     seg0 = offsets[e];
     nblk = (offsets[e + 1] - seg0) / kGemvBlock;  // >= 1 for an active expert
+  } else if constexpr (MODE == kGemvDense) {
+    nblk = (numel + kGemvBlock - 1) / kGemvBlock;
   }
   int b0 = 0;
   if (!dead) do {
@@ -485,7 +528,9 @@ moe_gemv_kernel(
 #pragma unroll
     for (int b = 0; b < MAXB; ++b) {
       int r = numel;
-      if constexpr (MODE != kGemvGrouped) {
+      if constexpr (MODE == kGemvDense) {
+        r = b < nb ? (b0 + b) * kGemvBlock + li : numel;  // rows past numel are padding
+      } else if constexpr (MODE != kGemvGrouped) {
         r = li == 0 ? slot : numel;  // column 0 of the block holds the route
       } else if (b < nb) {
         const int32_t* bids = sorted + seg0 + (b0 + b) * kGemvBlock;
@@ -678,6 +723,68 @@ __global__ __launch_bounds__(256) void moe_act_bf16_kernel(const float* __restri
   *reinterpret_cast<uint4*>(a2 + static_cast<int64_t>(r) * I + c0) = o;
 }
 
+// A route's slot is live when its expert id is >= 0 and its local id
+// (through expert_map when given) lies in [0, E): the rule of the alignment,
+// which places no other route, so no other partial row is ever written.
+// Without ids (a plain GEMV) every route is live.
+__device__ __forceinline__ bool route_live(const int32_t* __restrict__ emap, int64_t emap_len, int E,
+                                           int e) {
+  if (e < 0) return false;
+  if (emap) {
+    if (e >= emap_len) return false;
+    e = emap[e];
+  }
+  return e >= 0 && e < E;
+}
+__device__ __forceinline__ bool route_live_at(const int32_t* __restrict__ ids, int64_t r,
+                                              const int32_t* __restrict__ emap, int64_t emap_len, int E) {
+  return ids == nullptr || route_live(emap, emap_len, E, ids[r]);
+}
+
+// The reference's GEMV-MoE activation (csrc/musa/gemv.mu:472-487): per
+// route r the gate/up sums of the W13 partials (split order), times
+// route_w[r] when given (before the activation), the gate clamped to <= L and
+// up to [-L, L] when L > 0, then g * sigmoid(g) * u in fp32 and one rounding
+// to bf16; nothing is rounded before.  Routes without a live expert write
+// zeros (gemv.mu:297-311).  8 columns per thread.
+template <int SPL>
+__global__ __launch_bounds__(256) void moe_act_native_kernel(const float* __restrict__ partial, int splits,
+                                                             int numel, int I, float limit,
+                                                             const float* __restrict__ route_w,
+                                                             const int32_t* __restrict__ ids,
+                                                             const int32_t* __restrict__ emap, int64_t emap_len,
+                                                             int E, uint16_t* __restrict__ a2) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int cpr = I / 8;
+  if (idx >= static_cast<int64_t>(numel) * cpr) return;
+  const int r = static_cast<int>(idx / cpr);
+  const int c0 = static_cast<int>(idx % cpr) * 8;
+  uint4 o = {0u, 0u, 0u, 0u};
+  if (route_live_at(ids, r, emap, emap_len, E)) {
+    float gv[8], uv[8], v[8];
+    if constexpr (SPL > 0)
+      gate_up8_fixed<SPL>(partial, numel, I, r, c0, gv, uv);
+    else
+      gate_up8(partial, splits, numel, I, r, c0, 1.0f, gv, uv);
+    const float rw = route_w ? route_w[r] : 1.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float g = route_w ? gv[j] * rw : gv[j];
+      float u = route_w ? uv[j] * rw : uv[j];
+      if (limit > 0.f) {
+        g = fminf(g, limit);
+        u = fminf(fmaxf(u, -limit), limit);
+      }
+      v[j] = g * (1.0f / (1.0f + expf(-g))) * u;
+    }
+    o.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+    o.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+    o.z = static_cast<uint32_t>(f32_to_bf16(v[4])) | (static_cast<uint32_t>(f32_to_bf16(v[5])) << 16);
+    o.w = static_cast<uint32_t>(f32_to_bf16(v[6])) | (static_cast<uint32_t>(f32_to_bf16(v[7])) << 16);
+  }
+  *reinterpret_cast<uint4*>(a2 + static_cast<int64_t>(r) * I + c0) = o;
+}
+
 // kW4 decode: moe_act_bf16_kernel<kW4> and the per-row a2 quantiser in one
 // pass, one kRowThreads block per route row: the bf16-rounded activations stay
 // in registers for the row maximum and the quantiser (the values the separate
@@ -764,21 +871,10 @@ static void launch_rowquant_w4(const uint16_t* a, int I, int64_t rows, const int
 #undef VMAMD_RQ
 }
 
-// A route's slot is live when its expert id is >= 0 and its local id
-// (through expert_map when given) lies in [0, E): the rule of the alignment,
-// which places no other route, so no other partial row is ever written.
-__device__ __forceinline__ bool route_live(const int32_t* __restrict__ emap, int64_t emap_len, int E,
-                                           int e) {
-  if (e < 0) return false;
-  if (emap) {
-    if (e >= emap_len) return false;
-    e = emap[e];
-  }
-  return e >= 0 && e < E;
-}
-
 // y[r, n] = bf16(sum_s partial[s, r, n] * w_r) for the W2 split path (kW4:
-// w_r is the a2 row scale).
+// w_r is the a2 row scale).  Rows of dead routes are left alone, or written
+// as zeros with ZERO_DEAD (the reference GEMV's rule, gemv.mu:297-311).
+template <bool ZERO_DEAD = false>
 __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(const float* __restrict__ partial,
                                                             int splits, int numel, int N,
                                                             const int32_t* __restrict__ ids,
@@ -790,7 +886,10 @@ __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(const float* __restr
   const int64_t mn = static_cast<int64_t>(numel) * N;
   if (i4 >= mn) return;
   const int r = static_cast<int>(i4 / N);
-  if (!route_live(emap, emap_len, E, ids[r])) return;
+  if (!route_live_at(ids, r, emap, emap_len, E)) {
+    if constexpr (ZERO_DEAD) *reinterpret_cast<uint2*>(y + i4) = uint2{0u, 0u};
+    return;
+  }
   float4 acc = *reinterpret_cast<const float4*>(partial + i4);
   for (int s = 1; s < splits; ++s) {
     const float4 v = *reinterpret_cast<const float4*>(partial + s * mn + i4);
@@ -1976,29 +2075,29 @@ static int gemv_act_bytes(int64_t rows, int64_t K) {
 // vs: the kFp8 scale layout allows one 16-byte load per group of scales.
 static bool gemv_one_block(int64_t numel, int E) { return numel <= 8 * static_cast<int64_t>(E); }
 
-template <int KIND, typename... Args>
+template <int KIND, int MODE = kGemvGrouped, typename... Args>
 static void launch_gemv(dim3 grid, hipStream_t st, bool one_block, bool vs, Args... args) {
   const int32_t* none = nullptr;
   if constexpr (KIND != kBf16) {
     if (vs) {
       if (one_block)
-        moe_gemv_kernel<1, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
+        moe_gemv_kernel<1, KIND, true, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
       else
-        moe_gemv_kernel<4, KIND, true><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
+        moe_gemv_kernel<4, KIND, true, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
       return;
     }
   }
   if (one_block)
-    moe_gemv_kernel<1, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
+    moe_gemv_kernel<1, KIND, false, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
   else
-    moe_gemv_kernel<4, KIND><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
+    moe_gemv_kernel<4, KIND, false, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
 }
 
 // The decode GEMV with direct route slots (kGemvDirect / kGemvCombine).
 template <int KIND, int MODE, typename... Args>
 static void launch_gemv_direct(dim3 grid, int threads, size_t lds, hipStream_t st, bool vs, Args... args) {
   if constexpr (MODE == kGemvDirectQ) {  // kFp8 / kW4 with vector scales only
-    if constexpr (KIND != kBf16) moe_gemv_kernel<1, KIND, true, MODE><<<grid, threads, lds, st>>>(args...);
+    if constexpr (KIND == kFp8 || KIND == kW4) moe_gemv_kernel<1, KIND, true, MODE><<<grid, threads, lds, st>>>(args...);
     return;
   }
   if constexpr (KIND != kBf16 && MODE != kGemvDirectQ) {
@@ -2019,24 +2118,46 @@ static bool gemv_vector_scales(int64_t K, const void* act_s, const void* w_s) {
   if constexpr (KIND == kFp8)
     return (K / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(act_s) % 16 == 0 &&
            reinterpret_cast<uintptr_t>(w_s) % 16 == 0;
+  if constexpr (KIND == kW8A16) return (K / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(w_s) % 16 == 0;
   if constexpr (KIND == kW4)
     return (K / 128) % kGemvU == 0 && reinterpret_cast<uintptr_t>(w_s) % 8 == 0 &&
            reinterpret_cast<uintptr_t>(act_s) % 16 == 0;
   return false;
 }
 
-// Launches of the two stages; arguments are validated by the callers.  kBf16:
-// xa is x itself, xs / w13_s / a2s unused.  kW4: xa in w4 order with the
-// block corrections xcorr, xs the token row scales; the decode path writes
-// a2 (w4 order) with a2s and a2corr, the prefill path the bf16 activation to
-// a2 (quantised per row by the caller).
+// The reference GEMV's activation (moe_act_native_kernel) over numel routes:
+// ids (with emap / E) name the dead routes, which get zero rows; null ids
+// make every route live.
+static int launch_act_native(const float* scratch, int splits, int numel, int I, float limit,
+                             const float* route_w, const int32_t* ids, const int32_t* emap,
+                             int64_t emap_len, int E, uint16_t* a2, hipStream_t st) {
+  const int64_t chunks = static_cast<int64_t>(numel) * (I / 8);
+  const int blocks = static_cast<int>((chunks + 255) / 256);
+#define VMAMD_ACTN(S)                                                                                 \
+  moe_act_native_kernel<S><<<blocks, 256, 0, st>>>(scratch, splits, numel, I, limit, route_w, ids, emap, \
+                                                   emap_len, E, a2)
+  switch (splits) {
+    case 1: VMAMD_ACTN(1); break;
+    case 2: VMAMD_ACTN(2); break;
+    case 3: VMAMD_ACTN(3); break;
+    case 4: VMAMD_ACTN(4); break;
+    default: VMAMD_ACTN(0); break;
+  }
+#undef VMAMD_ACTN
+  return check_launch("moe w13 (activation)");
+}
+
 // The decode path's activation: split-K sum of the W13 partials, SwiGLU and
 // a2 (kFp8: 1x128 quantiser; kW4: per-row quantiser in w4 order; kBf16: the
-// bf16 activation).
+// bf16 activation; kW8A16, and kBf16 with `native`: the reference GEMV's
+// activation, which keeps gate and up in fp32 through the SwiGLU).
 template <int KIND>
 static int launch_act_decode(const float* scratch, int s13, int numel, int I, float limit,
                              const float* route_w, const float* xs, int topk, uint8_t* a2,
-                             float* a2s, float* a2corr, hipStream_t st) {
+                             float* a2s, float* a2corr, hipStream_t st, bool native = false) {
+  if (KIND == kW8A16 || native)
+    return launch_act_native(scratch, s13, numel, I, limit, route_w, nullptr, nullptr, 0, 0,
+                             reinterpret_cast<uint16_t*>(a2), st);
   if constexpr (KIND == kFp8) {
     const int64_t groups = static_cast<int64_t>(numel) * (I / 128);
     const int blocks = static_cast<int>((groups + 15) / 16);
@@ -2061,16 +2182,23 @@ static int launch_act_decode(const float* scratch, int s13, int numel, int I, fl
   return check_launch("moe w13 (activation)");
 }
 
+// Launches of the two stages; arguments are validated by the callers.  kBf16:
+// xa is x itself, xs / w13_s / a2s unused; kW8A16 (decode path only): xa is
+// x itself, xs / a2s unused, a2 bf16.  kW4: xa in w4 order with the
+// block corrections xcorr, xs the token row scales; the decode path writes
+// a2 (w4 order) with a2s and a2corr, the prefill path the bf16 activation to
+// a2 (quantised per row by the caller).
 template <int KIND>
 static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, int T, int H, int topk,
                       const int32_t* sorted, int64_t cap, int block_m, const int32_t* offs,
                       const int32_t* ntpp, const int32_t* active, const int32_t* nact,
                       const uint8_t* w13, const void* w13_s, int E, int I, float limit,
                       const float* route_w, uint8_t* a2, float* a2s, float* a2corr, float* scratch,
-                      hipStream_t st, const int32_t* eids = nullptr) {
+                      hipStream_t st, const int32_t* eids = nullptr, bool native = false) {
   const int numel = T * topk;
   const float* act_s = KIND == kW4 ? xcorr : xs;  // per-step activation values the GEMV reads
-  if (block_m == kGemvBlock) {
+  VMAMD_REQUIRE(KIND != kW8A16 || block_m == kGemvBlock, "moe w13: bf16 x fp8 runs on the decode GEMV only");
+  if (KIND == kW8A16 || block_m == kGemvBlock) {
     const int s13 = w13_splits(numel, E, H, I, KIND);
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s13);
@@ -2080,9 +2208,10 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
                       static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr));
     int rc = check_launch("moe w13 (gemv)");
     if (rc) return rc;
-    return launch_act_decode<KIND>(scratch, s13, numel, I, limit, route_w, xs, topk, a2, a2s, a2corr, st);
+    return launch_act_decode<KIND>(scratch, s13, numel, I, limit, route_w, xs, topk, a2, a2s, a2corr, st,
+                                   native);
   }
-  if constexpr (KIND != kW4) {
+  if constexpr (KIND == kFp8 || KIND == kBf16) {
     if (block_m == kMoeBigBM) {
       constexpr int eb = KIND == kBf16 ? 2 : 1;  // bytes per element
       VMAMD_REQUIRE(big_fits(T, H * eb, 2ll * I, E), "moe w13: operands past 2 GiB for the 256-route GEMM");
@@ -2101,7 +2230,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
   if constexpr (KIND == kW4) {
     return launch_w4_gemm<true>(xa, T, xs, xcorr, topk, H, sorted, offs, ntpp, eids, E, numel, tiles, w13,
                                 w13_s, 2 * I, I, limit, reinterpret_cast<uint16_t*>(a2), st);
-  } else {
+  } else if constexpr (KIND == kFp8 || KIND == kBf16) {
     int rc = raise_dma_lds<KIND, true>();
     if (rc) return rc;
     const int64_t abytes = static_cast<int64_t>(T) * H * KindBytes<KIND>::kAct / KindBytes<KIND>::kElems;
@@ -2131,7 +2260,8 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
   const float* yscale = KIND == kW4 ? a2s : route_w;
   const float* act_s = KIND == kW4 ? a2corr : a2s;  // per-step activation values the GEMV reads
   if (combined) *combined = false;
-  if (block_m == kGemvBlock) {
+  VMAMD_REQUIRE(KIND != kW8A16 || block_m == kGemvBlock, "moe w2: bf16 x fp8 runs on the decode GEMV only");
+  if (KIND == kW8A16 || block_m == kGemvBlock) {
     const int s2 = w2_splits(numel, E, H, I, KIND);
     const int umax = static_cast<int>(moe_umax(numel, E));
     dim3 g2((H / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, umax, s2);
@@ -2161,11 +2291,11 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
     int rc = check_launch("moe w2 (gemv)");
     if (rc) return rc;
     const int64_t mn = static_cast<int64_t>(numel) * H;
-    moe_w2_reduce_kernel<<<static_cast<int>((mn / 4 + 255) / 256), 256, 0, st>>>(
+    moe_w2_reduce_kernel<false><<<static_cast<int>((mn / 4 + 255) / 256), 256, 0, st>>>(
         scratch, s2, numel, H, topk_ids, emap, emap_len, E, yscale, y);
     return check_launch("moe w2 (reduce)");
   }
-  if constexpr (KIND != kW4) {
+  if constexpr (KIND == kFp8 || KIND == kBf16) {
     if (block_m == kMoeBigBM) {
       constexpr int eb = KIND == kBf16 ? 2 : 1;  // bytes per element
       VMAMD_REQUIRE(big_fits(cap, I * eb, H, E), "moe w2: operands past 2 GiB for the 256-route GEMM");
@@ -2183,7 +2313,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
     const int tiles = max_blocks * ((H + W4Pipe::BN - 1) / W4Pipe::BN);
     return launch_w4_gemm<false>(a2, cap, a2s, a2corr, 1, I, sorted, offs, ntpp, eids, E, numel, tiles, w2,
                                  w2_s, H, I, 0.f, y, st);
-  } else {
+  } else if constexpr (KIND == kFp8 || KIND == kBf16) {
     const int tiles = max_blocks * ((H + 255) / 256);
     int rc = raise_dma_lds<KIND, false>();
     if (rc) return rc;
@@ -2210,7 +2340,7 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   const int64_t cap = numel + static_cast<int64_t>(E) * (bm - 1);
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o += al256(bytes); return at; };
-  if (kind != kBf16) {
+  if (kind == kFp8 || kind == kW4) {
     w.xq = take(T * H);
     w.xs = take(kind == kFp8 ? T * (H / 128) * 4 : T * 4);
   }
@@ -2223,7 +2353,7 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   w.nact = take(4);
   const int64_t arows = bm == kGemvBlock ? numel : cap;  // route order (decode) or padded order
   if (kind == kW4) w.abf = take(arows * I * 2);
-  w.a2 = take(arows * I * (kind == kBf16 ? 2 : 1));
+  w.a2 = take(arows * I * (kind == kBf16 || kind == kW8A16 ? 2 : 1));
   if (kind == kFp8) w.a2s = take(arows * (I / 128) * 4);
   if (kind == kW4) {
     w.a2s = take(arows * 4);
@@ -2248,7 +2378,7 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
 // layers), but the dispatch has no sight of the routing before the launch.
 // kW4: a2s are the a2 row scales (the W2 output scale) and the routed weights
 // enter the sum, as in the grouped form.
-static bool use_direct_slots(int64_t T, int topk) { return T == 1 && topk <= kMaxCombineSlots; }
+static bool use_direct_slots(int64_t T, int topk, int kind) { return T == 1 && topk <= combine_slots(kind); }
 // xa: x as the W13 GEMV reads it (kFp8 / kW4: quantised by the caller, with
 // xs the 1x128 scales / the row scales and xcorr the kW4 block corrections);
 // qx (kFp8 / kW4): xa is the bf16 x, quantised by each W13 workgroup in LDS
@@ -2259,7 +2389,7 @@ static int fused_direct(bool qx, const uint8_t* xa, const float* xs, const float
                         int E, int I, int topk, const float* topk_weights, const int32_t* topk_ids,
                         const int32_t* emap, int64_t emap_len, float limit, const float* w13_rw,
                         const float* w2_rw, float* scratch, uint8_t* a2, float* a2s, float* a2corr,
-                        uint16_t* out, hipStream_t st) {
+                        uint16_t* out, hipStream_t st, bool native = false) {
   const int numel = T * topk;
   const int32_t* none = nullptr;
   const float* act_s = KIND == kW4 ? xcorr : xs;
@@ -2281,7 +2411,7 @@ static int fused_direct(bool qx, const uint8_t* xa, const float* xs, const float
   }
   int rc = check_launch("moe w13 (gemv)");
   if (rc) return rc;
-  rc = launch_act_decode<KIND>(scratch, s13, numel, I, limit, w13_rw, xs, topk, a2, a2s, a2corr, st);
+  rc = launch_act_decode<KIND>(scratch, s13, numel, I, limit, w13_rw, xs, topk, a2, a2s, a2corr, st, native);
   if (rc) return rc;
   const float* a2_act_s = KIND == kW4 ? a2corr : a2s;
   const float* yscale = KIND == kW4 ? a2s : w2_rw;
@@ -2307,7 +2437,7 @@ static int fused_direct(bool qx, const uint8_t* xa, const float* xs, const float
 // H=2048, I=768, top-8) T=2048 -7 % / -10 %, T=4096 -12 % / 0, T=8192
 // -10 % / -17 %.
 static int moe_block_m(int64_t T, int topk, int E, int path, int kind) {
-  if (path == VMAMD_MOE_PATH_GEMV) return kGemvBlock;
+  if (path == VMAMD_MOE_PATH_GEMV || path == VMAMD_MOE_PATH_NATIVE_GEMV || kind == kW8A16) return kGemvBlock;
   const int64_t routes = T * topk;
   const int grouped = kind != kW4 && routes >= 128 * static_cast<int64_t>(E) ? kMoeBigBM : kMoeBM;
   if (path == VMAMD_MOE_PATH_GEMM) return grouped;
@@ -2339,9 +2469,15 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
                        const int32_t* expert_map, int64_t expert_map_len, float swiglu_limit,
                        bool weight_on_input, int path, void* out, void* workspace,
                        size_t workspace_bytes, vmamd_stream_t stream) {
-  VMAMD_REQUIRE(path >= VMAMD_MOE_PATH_AUTO && path <= VMAMD_MOE_PATH_GEMM, "%s: unknown path %d",
+  VMAMD_REQUIRE(path >= VMAMD_MOE_PATH_AUTO && path <= VMAMD_MOE_PATH_NATIVE_GEMV, "%s: unknown path %d",
                 who, path);
   VMAMD_REQUIRE(KIND != kW4 || !weight_on_input, "%s: apply_router_weight_on_input is not supported",
+                who);
+  // The reference GEMV's numerics: activations not quantised, gate / up kept
+  // in fp32 through the SwiGLU (kW8A16 for fp8 weights, kBf16 with the native
+  // activation for bf16 weights).
+  const bool native = KIND == kW8A16 || path == VMAMD_MOE_PATH_NATIVE_GEMV;
+  VMAMD_REQUIRE(!native || KIND == kW8A16 || KIND == kBf16, "%s: the native GEMV path takes fp8 or bf16 weights",
                 who);
   const int bm = moe_block_m(T, topk, E, path, KIND);
   const int64_t cap = T * topk + static_cast<int64_t>(E) * (bm - 1);
@@ -2370,7 +2506,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   int32_t* active = reinterpret_cast<int32_t*>(ws + L.active);
   int32_t* nact = reinterpret_cast<int32_t*>(ws + L.nact);
   uint8_t* a2 = ws + L.a2;
-  float* a2s = KIND == kBf16 ? nullptr : reinterpret_cast<float*>(ws + L.a2s);
+  float* a2s = KIND == kBf16 || KIND == kW8A16 ? nullptr : reinterpret_cast<float*>(ws + L.a2s);
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
   float* scratch = reinterpret_cast<float*>(ws + L.scratch);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -2381,14 +2517,14 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   // activation (apply_router_weight_on_input), otherwise in the W2 epilogue.
   const float* w13_rw = weight_on_input ? topk_weights : nullptr;
   const float* w2_rw = weight_on_input ? nullptr : topk_weights;
-  if (bm == kGemvBlock && use_direct_slots(T, topk)) {
+  if (bm == kGemvBlock && use_direct_slots(T, topk, KIND)) {
     const uint8_t* xd = static_cast<const uint8_t*>(x);
     float* xsd = nullptr;
     float* xcd = nullptr;
     // kFp8 / kW4: each W13 workgroup quantises its token's x row (vector-
     // loaded scales, whole workgroups of 16-row tiles); otherwise the
     // quantiser runs first.
-    const bool qx = KIND != kBf16 && (H / 128) % kGemvU == 0 &&
+    const bool qx = (KIND == kFp8 || KIND == kW4) && (H / 128) % kGemvU == 0 &&
                     reinterpret_cast<uintptr_t>(w13_s) % (KIND == kFp8 ? 16 : 8) == 0 &&
                     (2 * I) % (16 * kMoeGemvWaves) == 0 && H <= (KIND == kFp8 ? 32768 : 16384);
     if constexpr (KIND == kFp8) {
@@ -2412,7 +2548,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
                               static_cast<const uint8_t*>(w2), w2_s, E, i, topk, topk_weights, topk_ids,
                               expert_map, expert_map_len, swiglu_limit, w13_rw, w2_rw, scratch, a2, a2s,
                               KIND == kW4 ? reinterpret_cast<float*>(ws + L.a2corr) : nullptr,
-                              static_cast<uint16_t*>(out), st);
+                              static_cast<uint16_t*>(out), st, native);
   }
   const uint8_t* xa = static_cast<const uint8_t*>(x);
   const float* xs = nullptr;
@@ -2444,7 +2580,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   uint8_t* act_out = KIND == kW4 && bm != kGemvBlock ? ws + L.abf : a2;
   rc = launch_w13<KIND>(xa, xs, xcorr, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
                         static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, w13_rw, act_out,
-                        a2s, a2corr, scratch, st, eids);
+                        a2s, a2corr, scratch, st, eids, native);
   if (rc) return rc;
   if constexpr (KIND == kW4) {
     if (bm != kGemvBlock) {  // rows past the last block are skipped on the device
@@ -2524,6 +2660,169 @@ static int stage_w2(const char* who, const void* a2, const float* a2s, int64_t T
                          reinterpret_cast<hipStream_t>(stream));
 }
 
+// ------------------------------------------------ the reference GEMV ops --
+// musa_fused_gemv_moe / musa_fused_gemv (csrc/musa/gemv.mu:723-1170) on the
+// decode GEMV.  Route r = row * topk + k of A's rows uses expert topk_ids[r]
+// and writes row r of C; without ids (the dense op) every row is a route of
+// the one expert.  Up to kMaxCombineSlots routes each route is its own GEMV
+// slot (the reference's own grid: one slot per route); more are grouped per
+// expert by the alignment, so an expert's weights stream once per 16 routes.
+// The GEMV writes fp32 split-K partials and one epilogue launch finishes:
+// the reference activation (use_swiglu) or bf16(acc * w), dead routes zero.
+struct GemvOpWs {
+  size_t sorted, eids, ntpp, offs, active, nact, partial, total;
+};
+
+static bool gemv_op_direct(int64_t numel, bool dense) { return !dense && numel <= kMaxCombineSlots; }
+
+// GEMV slots along gridDim.y: 1 (dense), the routes (direct), or the experts
+// that can be active (grouped).
+static int64_t gemv_op_slots(int64_t numel, int E, bool dense) {
+  return dense ? 1 : gemv_op_direct(numel, dense) ? numel : moe_umax(numel, E);
+}
+
+static int gemv_op_kind(int a_dtype, int b_dtype) {
+  if (b_dtype == VMAMD_DTYPE_E4M3) {
+    if (a_dtype == kBF16) return kW8A16;
+    if (a_dtype == VMAMD_DTYPE_E4M3) return kFp8;
+  } else if (b_dtype == kBF16 && a_dtype == kBF16) {
+    return kBf16;
+  }
+  return -1;
+}
+
+static int gemv_op_splits(int64_t numel, int E, int64_t N, int64_t K, int kind, bool dense) {
+  return moe_splits(gemv_op_slots(numel, E, dense) * (N / 16), ksteps(K, kind));
+}
+
+static GemvOpWs gemv_op_layout(int64_t numel, int E, int64_t N, int64_t K, int kind, bool dense) {
+  GemvOpWs w{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) { const size_t at = o; o += al256(bytes); return at; };
+  if (!dense && !gemv_op_direct(numel, dense)) {
+    const int64_t cap = numel + static_cast<int64_t>(E) * (kGemvBlock - 1);
+    w.sorted = take(cap * 4);
+    w.eids = take(((cap + kGemvBlock - 1) / kGemvBlock) * 4);
+    w.ntpp = take(4);
+    w.offs = take((E + 1) * 4);
+    w.active = take(E * 4);
+    w.nact = take(4);
+  }
+  w.partial = take(static_cast<size_t>(gemv_op_splits(numel, E, N, K, kind, dense)) * numel * N * 4);
+  w.total = o;
+  return w;
+}
+
+// Host round to nearest even bf16 (the reference rounds swiglu_limit to the
+// activation dtype, gemv.mu:946-951).
+static float round_bf16_host(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return f;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  float r;
+  std::memcpy(&r, &u, 4);
+  return r;
+}
+
+template <int KIND>
+static int gemv_op_launch(const void* A, const float* A_scale, int64_t rows, int64_t K, const void* B,
+                          const float* B_scale, int E, int64_t N, const float* topk_weights,
+                          const int32_t* topk_ids, int topk, bool mul_rw, bool swiglu, float limit, void* C,
+                          uint8_t* ws, const GemvOpWs& L, hipStream_t st) {
+  const bool dense = topk_ids == nullptr;
+  const int numel = static_cast<int>(rows * topk);
+  const int n = static_cast<int>(N), k = static_cast<int>(K);
+  const int splits = gemv_op_splits(numel, E, N, K, KIND, dense);
+  const int act_bytes = gemv_act_bytes<KIND>(rows, K);
+  const bool vs = gemv_vector_scales<KIND>(K, A_scale, B_scale);
+  const uint8_t* act = static_cast<const uint8_t*>(A);
+  const uint8_t* w = static_cast<const uint8_t*>(B);
+  float* partial = reinterpret_cast<float*>(ws + L.partial);
+  const int32_t* none = nullptr;
+  const dim3 grid((n / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, static_cast<unsigned>(gemv_op_slots(numel, E, dense)),
+                  splits);
+  if (dense) {
+    launch_gemv<KIND, kGemvDense>(grid, st, numel <= 8, vs, act, act_bytes, A_scale, topk, k, none, none, none,
+                                  none, w, static_cast<const void*>(B_scale), n, numel, splits, partial,
+                                  static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr));
+  } else if (gemv_op_direct(numel, dense)) {
+    launch_gemv_direct<KIND, kGemvDirect>(
+        grid, kMoeGemvWaves * kWave, 0, st, vs, act, act_bytes, A_scale, topk, k, none, none, none, none, w,
+        static_cast<const void*>(B_scale), n, numel, splits, partial, static_cast<const float*>(nullptr),
+        static_cast<uint16_t*>(nullptr), topk_ids, none, int64_t{0}, E, static_cast<uint16_t*>(nullptr),
+        static_cast<const float*>(nullptr), static_cast<float*>(nullptr));
+  } else {
+    int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.sorted);
+    int32_t* offs = reinterpret_cast<int32_t*>(ws + L.offs);
+    int32_t* active = reinterpret_cast<int32_t*>(ws + L.active);
+    int32_t* nact = reinterpret_cast<int32_t*>(ws + L.nact);
+    const int64_t cap = numel + static_cast<int64_t>(E) * (kGemvBlock - 1);
+    int rc = vmamd_moe_align_block_size(topk_ids, numel, E, kGemvBlock, nullptr, 0, sorted, cap,
+                                        reinterpret_cast<int32_t*>(ws + L.eids),
+                                        reinterpret_cast<int32_t*>(ws + L.ntpp), offs, nullptr, active, nact,
+                                        reinterpret_cast<vmamd_stream_t>(st));
+    if (rc) return rc;
+    launch_gemv<KIND>(grid, st, gemv_one_block(numel, E), vs, act, act_bytes, A_scale, topk, k, sorted, offs,
+                      active, nact, w, static_cast<const void*>(B_scale), n, numel, splits, partial,
+                      static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr));
+  }
+  int rc = check_launch("fused_gemv (gemv)");
+  if (rc) return rc;
+  const float* rw = mul_rw ? topk_weights : nullptr;
+  if (swiglu)
+    return launch_act_native(partial, splits, numel, n / 2, limit, rw, topk_ids, nullptr, 0, E,
+                             static_cast<uint16_t*>(C), st);
+  const int64_t mn = static_cast<int64_t>(numel) * n;
+  moe_w2_reduce_kernel<true><<<static_cast<int>((mn / 4 + 255) / 256), 256, 0, st>>>(
+      partial, splits, numel, n, topk_ids, nullptr, 0, E, rw, static_cast<uint16_t*>(C));
+  return check_launch("fused_gemv (epilogue)");
+}
+
+static int gemv_op(const char* who, const void* A, int a_dtype, const float* A_scale, int64_t rows, int64_t K,
+                   const void* B, int b_dtype, const float* B_scale, int E, int64_t N, const float* topk_weights,
+                   const int32_t* topk_ids, int topk, bool mul_rw, bool swiglu, float limit, void* C,
+                   void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
+  const int kind = gemv_op_kind(a_dtype, b_dtype);
+  VMAMD_REQUIRE(kind >= 0, "%s: takes bf16 x e4m3 (W8A16), e4m3 x e4m3 (with A_scale) or bf16 x bf16 "
+                "(A dtype %d, B dtype %d)", who, a_dtype, b_dtype);
+  VMAMD_REQUIRE(rows >= 0 && topk > 0 && E > 0 && E <= 1024 && rows * topk < (1ll << 30),
+                "%s: bad sizes (rows=%lld topk=%d experts=%d)", who, (long long)rows, topk, E);
+  VMAMD_REQUIRE(N > 0 && N % (swiglu ? 32 : 16) == 0 && N < (1ll << 24),
+                "%s: output size %lld must be a positive multiple of %d", who, (long long)N, swiglu ? 32 : 16);
+  VMAMD_REQUIRE(K > 0 && K % (kind == kBf16 ? 64 : 128) == 0 && K < (1ll << 24),
+                "%s: reduction size %lld must be a positive multiple of %d", who, (long long)K,
+                kind == kBf16 ? 64 : 128);
+  VMAMD_REQUIRE(rows * K * (a_dtype == kBF16 ? 2 : 1) < (1ll << 31) && N * K < (1ll << 31),
+                "%s: operands past 2 GiB", who);
+  VMAMD_REQUIRE(kind == kBf16 || B_scale, "%s: fp8 weights need their 128x128 block scales", who);
+  VMAMD_REQUIRE(kind != kFp8 || A_scale, "%s: fp8 activations need their 1x128 group scales", who);
+  VMAMD_REQUIRE(!mul_rw || topk_weights, "%s: mul_routed_weight needs topk_weights", who);
+  if (rows == 0) return VMAMD_OK;
+  VMAMD_REQUIRE(A && B && C, "%s: null pointer", who);
+  VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(C) % 16 == 0 && reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
+                "%s: A, B and C must be 16-byte and the workspace 256-byte aligned", who);
+  const GemvOpWs L = gemv_op_layout(rows * topk, E, N, K, kind, topk_ids == nullptr);
+  VMAMD_REQUIRE(workspace && workspace_bytes >= L.total, "%s: workspace of %zu bytes required (got %zu)", who,
+                L.total, workspace_bytes);
+  if (a_dtype == kBF16 && limit > 0.f) limit = round_bf16_host(limit);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (kind) {
+    case kW8A16:
+      return gemv_op_launch<kW8A16>(A, A_scale, rows, K, B, B_scale, E, N, topk_weights, topk_ids, topk, mul_rw,
+                                    swiglu, limit, C, ws, L, st);
+    case kFp8:
+      return gemv_op_launch<kFp8>(A, A_scale, rows, K, B, B_scale, E, N, topk_weights, topk_ids, topk, mul_rw,
+                                  swiglu, limit, C, ws, L, st);
+    default:
+      return gemv_op_launch<kBf16>(A, nullptr, rows, K, B, nullptr, E, N, topk_weights, topk_ids, topk, mul_rw,
+                                   swiglu, limit, C, ws, L, st);
+  }
+}
+
 }  // namespace vmamd
 
 using namespace vmamd;
@@ -2562,7 +2861,8 @@ extern "C" int vmamd_moe_fp8_w2(const void* a2q, const float* a2s, int64_t T, in
 
 extern "C" size_t vmamd_fused_moe_fp8_workspace_size(int64_t T, int topk, int num_experts,
                                                      int64_t H, int64_t I, int path) {
-  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path, kFp8), kFp8).total;
+  const int kind = path == VMAMD_MOE_PATH_NATIVE_GEMV ? kW8A16 : kFp8;
+  return moe_layout(T, topk, num_experts, H, I, moe_block_m(T, topk, num_experts, path, kind), kind).total;
 }
 
 extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H,
@@ -2574,6 +2874,11 @@ extern "C" int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_
                                    void* out, void* workspace, size_t workspace_bytes,
                                    vmamd_stream_t stream) {
   VMAMD_REQUIRE(x_dtype == kBF16, "fused_moe_fp8: hidden states must be bf16");
+  if (path == VMAMD_MOE_PATH_NATIVE_GEMV)
+    return fused_layer<kW8A16>("fused_moe_fp8 (native gemv)", x, T, H, w13, w13_s, w2, w2_s, num_experts, I,
+                               topk_weights, topk_ids, topk, expert_map, expert_map_len, swiglu_limit,
+                               apply_router_weight_on_input != 0, path, out, workspace, workspace_bytes,
+                               stream);
   return fused_layer<kFp8>("fused_moe_fp8", x, T, H, w13, w13_s, w2, w2_s, num_experts, I,
                            topk_weights, topk_ids, topk, expert_map, expert_map_len, swiglu_limit,
                            apply_router_weight_on_input != 0, path, out, workspace,
@@ -2646,4 +2951,36 @@ extern "C" int vmamd_w4afp8_moe(const void* x, int64_t T, int64_t H, const void*
   return fused_layer<kW4>("w4afp8_moe", x, T, H, w13, w13_s, w2, w2_s, num_experts, I, topk_weights,
                           topk_ids, topk, expert_map, expert_map_len, swiglu_limit, false, path,
                           out, workspace, workspace_bytes, stream);
+}
+
+// ------------------------------------------------- reference GEMV ops ---
+extern "C" size_t vmamd_fused_gemv_moe_workspace_size(int64_t rows, int topk, int num_experts, int64_t N,
+                                                      int64_t K, int a_dtype, int b_dtype) {
+  const int kind = gemv_op_kind(a_dtype, b_dtype);
+  if (kind < 0 || rows <= 0 || topk <= 0 || num_experts <= 0) return 0;
+  return gemv_op_layout(rows * topk, num_experts, N, K, kind, false).total;
+}
+
+extern "C" int vmamd_fused_gemv_moe(const void* A, int a_dtype, const float* A_scale, int64_t rows, int64_t K,
+                                    const void* B, int b_dtype, const float* B_scale, int num_experts,
+                                    int64_t N, const float* topk_weights, const int32_t* topk_ids, int topk,
+                                    int mul_routed_weight, int use_swiglu, float swiglu_limit, void* C,
+                                    void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
+  VMAMD_REQUIRE(rows == 0 || topk_ids, "fused_gemv_moe: null topk_ids");
+  return gemv_op("fused_gemv_moe", A, a_dtype, A_scale, rows, K, B, b_dtype, B_scale, num_experts, N,
+                 topk_weights, topk_ids, topk, mul_routed_weight != 0, use_swiglu != 0, swiglu_limit, C,
+                 workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t vmamd_fused_gemv_workspace_size(int64_t M, int64_t N, int64_t K, int a_dtype, int b_dtype) {
+  const int kind = gemv_op_kind(a_dtype, b_dtype);
+  if (kind < 0 || M <= 0) return 0;
+  return gemv_op_layout(M, 1, N, K, kind, true).total;
+}
+
+extern "C" int vmamd_fused_gemv(const void* A, int a_dtype, const float* A_scale, int64_t M, int64_t K,
+                                const void* B, int b_dtype, const float* B_scale, int64_t N, int use_swiglu,
+                                void* C, void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
+  return gemv_op("fused_gemv", A, a_dtype, A_scale, M, K, B, b_dtype, B_scale, 1, N, nullptr, nullptr, 1,
+                 false, use_swiglu != 0, 0.f, C, workspace, workspace_bytes, stream);
 }

@@ -389,3 +389,226 @@ def router_gate_fp32(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor) -
         raise ValueError("router_gate_fp32: x must be float32 or bfloat16")
     call("vmamd_router_gate_fp32", ptr(x), dtype_code(x.dtype), m, k, ptr(weight), e, ptr(out),
          stream_of(x))
+
+
+# ------------------------------------------------------ reference GEMV ops --
+# musa_fused_gemv_moe / musa_fused_gemv with the reference's argument order
+# and numerics (csrc/musa/gemv.mu:249-514, 723-1170; Python wrappers
+# vllm_musa/_custom_ops.py:28-158): the activations are read as they are --
+# bf16 against the fp8 weights dequantised per 128x128 block, no activation
+# quantisation -- the sums are fp32 and the output is rounded once to bf16.
+# Checks the reference's native op makes with TORCH_CHECK raise RuntimeError,
+# as there; the asserts of its Python wrapper stay asserts.  The GEMV's own
+# tile request (block_n, block_k) is checked by the reference's rules
+# (gemv.mu:1037-1066) and then left to this library, which sizes its
+# launches itself: it is a performance hint there and changes no value.
+def _gemv_operand_dtype(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if t.dtype == FP8_DTYPE:
+        return _lib.DTYPE_E4M3
+    raise NotImplementedError(f"GEMV operands of dtype {t.dtype} are not on this path "
+                              "(bf16 activations, fp8 or bf16 weights)")
+
+
+def _check_requested_block(block_n: int, block_k: int, nr_n: int, hidden: int, vlen: int) -> None:
+    if (block_n == 0) != (block_k == 0):
+        raise RuntimeError("requested GEMV block must provide both block_n and block_k, got "
+                           f"{block_n}x{block_k}")
+    if block_n == 0:
+        return
+    if not (block_n > 0 and block_k > 0 and block_n * block_k <= 512):
+        raise RuntimeError("requested GEMV block must use positive sizes with block_n * "
+                           f"block_k <= 512, got {block_n}x{block_k}")
+    if nr_n % block_n or hidden % (block_k * vlen):
+        raise RuntimeError(f"requested GEMV block={block_n}x{block_k} is invalid for "
+                           f"nr_n={nr_n}, hidden_size={hidden}, vlen={vlen}")
+
+
+def _gemv_common(A, B, C, A_scale, B_scale, rows, K, N, use_swigelu):
+    """Shared argument checks; returns (a_dtype, b_dtype, A_scale, B_scale)
+    as the C ABI takes them."""
+    check_cuda(A, B, C, A_scale, B_scale)
+    for t, n in ((A, "A"), (B, "B"), (C, "C")):
+        _contig(t, n)
+    a_dt, b_dt = _gemv_operand_dtype(A), _gemv_operand_dtype(B)
+    if C.dtype != torch.bfloat16:
+        raise RuntimeError("the GEMV output C must be bfloat16")
+    if b_dt == _lib.DTYPE_E4M3:
+        if B_scale is None or B_scale.dtype != torch.float32:
+            raise RuntimeError("fp8 weights need float32 block scales")
+        B_scale = B_scale.contiguous()
+    else:
+        B_scale = None  # bf16 weights take no scales (gemv.mu:430-434)
+    if a_dt == _lib.DTYPE_E4M3:
+        if b_dt != _lib.DTYPE_E4M3:
+            raise RuntimeError("fp8 activations take fp8 weights")
+        if A_scale is None or A_scale.dtype != torch.float32 or \
+                A_scale.numel() != rows * (K // 128):
+            raise RuntimeError("fp8 activations need float32 1x128 group scales [rows, K/128]")
+        A_scale = A_scale.contiguous()
+    else:
+        A_scale = None  # bf16 activations are read as they are (gemv.mu:405-419)
+    n_out = N // 2 if use_swigelu else N
+    return a_dt, b_dt, A_scale, B_scale, n_out
+
+
+def musa_fused_gemv_moe(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
+                        A_scale: torch.Tensor | None, B_scale: torch.Tensor | None,
+                        topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                        mul_routed_weight: bool, topk: int, use_int4_w4a16: bool,
+                        use_swigelu: bool, block_n: int = 0, block_k: int = 0,
+                        swiglu_limit: float = 0.0) -> None:
+    """Reference: musa_fused_gemv_moe (vllm_musa/_custom_ops.py:28-59; op
+    csrc/musa/gemv.mu:927-1170).  A [rows, K]; B [E, N, K]; route
+    r = row * topk + k uses expert topk_ids.flat[r] and writes row r of C
+    ([rows * topk, N], or [rows * topk, N/2] with use_swigelu: gate rows
+    [0, N/2), up rows [N/2, N), silu(g) * u in fp32 with the clamp
+    swiglu_limit rounded to A's dtype).  mul_routed_weight multiplies the fp32
+    sums by topk_weights.flat[r] first.  An id outside [0, E) gives a zero
+    row.  The fused-MoE driver calls it twice per layer: W13 over the tokens
+    (topk = K, SwiGLU) and W2 over cache2's rows (topk = 1)."""
+    if use_int4_w4a16:
+        raise NotImplementedError("the int4 W4A16 GEMV-MoE is not on this path")
+    if A.dim() != 2:
+        raise RuntimeError("A must be dim 2.")
+    if B.dim() != 3:
+        raise RuntimeError("B must be dim 3.")
+    rows, K = A.shape
+    E, N, Kb = B.shape
+    if Kb != K:
+        raise RuntimeError(f"A has K={K}, B has K={Kb}")
+    vlen = 16 if B.dtype == FP8_DTYPE else 8
+    _check_requested_block(int(block_n), int(block_k), N // 2 if use_swigelu else N, K, vlen)
+    a_dt, b_dt, A_scale, B_scale, n_out = _gemv_common(A, B, C, A_scale, B_scale, rows, K, N,
+                                                       use_swigelu)
+    check_cuda(A, topk_weights, topk_ids)
+    if topk_ids.dtype != torch.int32 or topk_ids.numel() != rows * topk:
+        raise RuntimeError(f"topk_ids must be int32 with rows * topk = {rows * topk} entries")
+    if topk_weights.dtype != torch.float32 or topk_weights.numel() != rows * topk:
+        raise RuntimeError("topk_weights must be float32 with rows * topk entries")
+    if C.numel() != rows * topk * n_out:
+        raise RuntimeError(f"C must hold rows * topk x {n_out} elements")
+    if B_scale is not None and tuple(B_scale.shape) != (E, -(-N // 128), K // 128):
+        raise RuntimeError(f"B_scale must be [E, ceil(N/128), K/128] = {(E, -(-N // 128), K // 128)}")
+    ids = topk_ids.contiguous()
+    wts = topk_weights.contiguous()
+    lib = _lib.load()
+    nbytes = lib.vmamd_fused_gemv_moe_workspace_size(rows, topk, E, N, K, a_dt, b_dt)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=A.device)
+    call("vmamd_fused_gemv_moe", ptr(A), a_dt, ptr(A_scale), rows, K, ptr(B), b_dt, ptr(B_scale), E,
+         N, ptr(wts), ptr(ids), int(topk), int(bool(mul_routed_weight)), int(bool(use_swigelu)),
+         float(swiglu_limit), ptr(C), ptr(ws), nbytes, stream_of(A))
+
+
+def musa_fused_gemv_op(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
+                       A_scale: torch.Tensor | None, B_scale: torch.Tensor | None,
+                       use_int4_w4a16: bool, use_swigelu: bool, use_rms_norm: bool,
+                       gamma: torch.Tensor | None, eps: float) -> None:
+    """The raw op musa_fused_gemv in its schema's argument order
+    (csrc/musa/torch_bindings.cpp:17-21; gemv.mu:723-925): C [M, N or N/2] =
+    A [M, K] against one weight matrix B [N, K] (B_scale [ceil(N/128),
+    K/128] for fp8), as _musa_fp8_small_m_gemv_op calls it
+    (scaled_mm/deep_gemm.py:512-536)."""
+    if use_int4_w4a16:
+        raise NotImplementedError("the int4 W4A16 GEMV is not on this path")
+    if use_rms_norm:
+        raise NotImplementedError("the GEMV's fused RMS norm is not on this path")
+    if A.dim() != 2:
+        raise RuntimeError("A must be dim 2.")
+    if B.dim() != 2:
+        raise RuntimeError("B must be dim 2.")
+    M, K = A.shape
+    N, Kb = B.shape
+    if Kb != K:
+        raise RuntimeError(f"A has K={K}, B has K={Kb}")
+    a_dt, b_dt, A_scale, B_scale, n_out = _gemv_common(A, B, C, A_scale, B_scale, M, K, N,
+                                                       use_swigelu)
+    if tuple(C.shape) != (M, n_out):
+        raise RuntimeError(f"C must be [M, {n_out}]")
+    if B_scale is not None and tuple(B_scale.shape) != (-(-N // 128), K // 128):
+        raise RuntimeError("B_scale must be [ceil(N/128), K/128]")
+    lib = _lib.load()
+    nbytes = lib.vmamd_fused_gemv_workspace_size(M, N, K, a_dt, b_dt)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=A.device)
+    call("vmamd_fused_gemv", ptr(A), a_dt, ptr(A_scale), M, K, ptr(B), b_dt, ptr(B_scale), N,
+         int(bool(use_swigelu)), ptr(C), ptr(ws), nbytes, stream_of(A))
+
+
+def musa_fused_gemv(x: torch.Tensor, qweight: torch.Tensor, x_scales: torch.Tensor | None = None,
+                    qweight_scales: torch.Tensor | None = None, use_swigelu: bool = False,
+                    use_rms_norm: bool = False, gamma: torch.Tensor | None = None,
+                    eps: float = 1e-6, output: torch.Tensor | None = None) -> torch.Tensor:
+    """Reference: the Python wrapper musa_fused_gemv (vllm_musa/_custom_ops.py:62-158):
+    fp8 weights with block scales write into ``output`` (allocated when None,
+    else checked), bf16 weights into a new tensor of x's dtype."""
+    out_shape = x.shape[:-1] + (qweight.shape[0] if not use_swigelu else qweight.shape[0] // 2,)
+    assert not (use_swigelu and use_rms_norm), "gemv only fused one activation (swigelu or rms_norm)!"
+    if use_rms_norm and gamma is None:
+        raise AssertionError("rms_norm gamm is None!")
+    if qweight.dtype == FP8_DTYPE:
+        assert qweight_scales is not None, "FP8 grouped matmul weight scales is None!"
+        if output is None:
+            output = torch.empty(out_shape, device=x.device, dtype=torch.bfloat16)
+        else:
+            assert output.shape == out_shape
+            assert output.device == x.device
+            assert output.dtype == torch.bfloat16
+            assert output.is_contiguous()
+        musa_fused_gemv_op(x, qweight, output, x_scales, qweight_scales, False, use_swigelu,
+                           use_rms_norm, gamma, eps)
+        return output
+    if qweight_scales is not None:
+        raise NotImplementedError("the int4 W4A16 GEMV is not on this path")
+    assert output is None, "caller-owned output is only supported for FP8 GEMV"
+    output = torch.empty(out_shape, device=x.device, dtype=x.dtype)
+    musa_fused_gemv_op(x, qweight, output, None, None, False, use_swigelu, use_rms_norm, gamma, eps)
+    return output
+
+
+# The same two ops as torch.ops._C_musa_ops.musa_fused_gemv_moe / musa_fused_gemv
+# (schemas csrc/musa/torch_bindings.cpp:11-21), so call sites written against
+# the reference's extension -- its fused-MoE driver and its dense small-M
+# GEMV -- run unchanged; fake implementations let them be traced.
+_OPS_NS = "_C_musa_ops"
+
+
+def _register_reference_ops() -> None:
+    ns = getattr(torch.ops, _OPS_NS)
+    if not hasattr(ns, "musa_fused_gemv_moe"):
+        moe = torch.library.custom_op(f"{_OPS_NS}::musa_fused_gemv_moe", mutates_args=("C",))(
+            _gemv_moe_op_impl)
+        moe.register_fake(_gemv_moe_op_fake)
+    if not hasattr(ns, "musa_fused_gemv"):
+        dense = torch.library.custom_op(f"{_OPS_NS}::musa_fused_gemv", mutates_args=("C",))(
+            _gemv_op_impl)
+        dense.register_fake(_gemv_op_fake)
+
+
+def _gemv_moe_op_impl(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
+                      A_scale: torch.Tensor | None, B_scale: torch.Tensor | None,
+                      topk_weights: torch.Tensor, topk_ids: torch.Tensor, mul_routed_weight: bool,
+                      topk: int, use_int4_w4a16: bool, use_swigelu: bool, block_n: int = 0,
+                      block_k: int = 0, swiglu_limit: float = 0.0) -> None:
+    musa_fused_gemv_moe(A, B, C, A_scale, B_scale, topk_weights, topk_ids, mul_routed_weight,
+                        topk, use_int4_w4a16, use_swigelu, block_n, block_k, swiglu_limit)
+
+
+def _gemv_moe_op_fake(A, B, C, A_scale, B_scale, topk_weights, topk_ids, mul_routed_weight, topk,
+                      use_int4_w4a16, use_swigelu, block_n=0, block_k=0, swiglu_limit=0.0) -> None:
+    return None
+
+
+def _gemv_op_impl(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, A_scale: torch.Tensor | None,
+                  B_scale: torch.Tensor | None, use_int4_w4a16: bool, use_swigelu: bool,
+                  use_rms_norm: bool, gamma: torch.Tensor | None, eps: float) -> None:
+    musa_fused_gemv_op(A, B, C, A_scale, B_scale, use_int4_w4a16, use_swigelu, use_rms_norm, gamma,
+                       eps)
+
+
+def _gemv_op_fake(A, B, C, A_scale, B_scale, use_int4_w4a16, use_swigelu, use_rms_norm, gamma,
+                  eps) -> None:
+    return None
+
+
+_register_reference_ops()

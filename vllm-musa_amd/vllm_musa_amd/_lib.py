@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(_HERE, "libvllm_musa_amd.so")
 DTYPE_F32 = 0
 DTYPE_F16 = 1
 DTYPE_BF16 = 2
+DTYPE_E4M3 = 4  # fp8 operands of the GEMV ops
 
 _TORCH_DTYPE = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 
@@ -75,6 +76,11 @@ SIGNATURES: dict[str, list] = {
     "vmamd_w4afp8_moe_workspace_size": [_i64, _i32, _i32, _i64, _i64, _i32],
     "vmamd_w4afp8_moe": [_p, _i64, _i64, _p, _p, _p, _p, _i32, _i64, _p, _p, _i32, _p, _i64, _f32,
                          _i32, _p, _p, _sz, _p],
+    "vmamd_fused_gemv_moe_workspace_size": [_i64, _i32, _i32, _i64, _i64, _i32, _i32],
+    "vmamd_fused_gemv_moe": [_p, _i32, _p, _i64, _i64, _p, _i32, _p, _i32, _i64, _p, _p, _i32, _i32,
+                             _i32, _f32, _p, _p, _sz, _p],
+    "vmamd_fused_gemv_workspace_size": [_i64, _i64, _i64, _i32, _i32],
+    "vmamd_fused_gemv": [_p, _i32, _p, _i64, _i64, _p, _i32, _p, _i64, _i32, _p, _p, _sz, _p],
 }
 _RESTYPES = {"vmamd_last_error": ctypes.c_char_p,
              "vmamd_w4afp8_moe_workspace_size": ctypes.c_size_t,
@@ -82,7 +88,9 @@ _RESTYPES = {"vmamd_last_error": ctypes.c_char_p,
              "vmamd_moe_bf16_stage_workspace_size": ctypes.c_size_t,
              "vmamd_w8a8_block_fp8_matmul_workspace_size": ctypes.c_size_t,
              "vmamd_fused_moe_fp8_workspace_size": ctypes.c_size_t,
-             "vmamd_moe_fp8_stage_workspace_size": ctypes.c_size_t}
+             "vmamd_moe_fp8_stage_workspace_size": ctypes.c_size_t,
+             "vmamd_fused_gemv_moe_workspace_size": ctypes.c_size_t,
+             "vmamd_fused_gemv_workspace_size": ctypes.c_size_t}
 
 _lib = None
 _lock = threading.Lock()

@@ -46,7 +46,14 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: i
 
 
 # ---------------------------------------------------------------- experts --
-PATHS = {"auto": 0, "gemv": 1, "gemm": 2}
+# Kernel paths of the fused layer (VMAMD_MOE_PATH_*): "gemv" / "gemm" force
+# the W8A8 decode kernels / grouped GEMMs, "auto" lets the library pick by
+# routes per expert, "native_gemv" computes the reference's native GEMV-MoE
+# numerics (bf16 activations, gate and up in fp32 through the SwiGLU).
+PATHS = {"auto": 0, "gemv": 1, "gemm": 2, "native_gemv": 3}
+# Tokens per launch sequence: longer batches run in chunks of this many
+# tokens with one chunk's workspace (fused_moe.py:2126-2128).
+CHUNK_SIZE = 16384
 
 
 def _per_expert_scale(scale: torch.Tensor, e: int) -> torch.Tensor | None:
@@ -112,7 +119,7 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
                        block_shape: list[int] | None = None, w1_bias: torch.Tensor | None = None,
                        w2_bias: torch.Tensor | None = None,
                        gemm1_clamp_limit: float | None = None, *, inplace: bool = False,
-                       path: str = "auto") -> torch.Tensor:
+                       path: str = "auto", chunk_size: int = CHUNK_SIZE) -> torch.Tensor:
     """Drop-in for the reference's fused_experts_impl
     (vllm_musa/model_executor/layers/fused_moe/fused_moe.py:1935-1965, 2214-2240):
     out[t] = sum_k w[t,k] * W2[e] . act(W13[e] . x[t]) with the reference's
@@ -123,10 +130,16 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
     1x128 activation quantisation.  apply_router_weight_on_input multiplies
     the W13 output by the routed weight before the activation and leaves the
     W2 output unweighted (the reference's mul_routed_weight on its first GEMV,
-    fused_moe.py:2148-2177).  ``path`` forces the decode ("gemv") or prefill
-    ("gemm") kernels; "auto" asks the dispatch policy (the calibrated per-shape
-    table, the VLLM_MUSA_FUSED_MOE_DISPATCH override) and otherwise picks by
-    routes per expert."""
+    fused_moe.py:2148-2177).  ``path`` forces the W8A8 decode ("gemv") or
+    prefill ("gemm") kernels, or the reference's native GEMV-MoE numerics
+    ("native_gemv": x not quantised, gate and up in fp32 through the SwiGLU,
+    one rounding; gemv.mu:249-514); "auto" computes what the reference computes
+    for this call -- its native GEMV where its dispatcher would run it (its
+    calibrated shapes, the VLLM_MUSA_FUSED_MOE_DISPATCH=gemv override),
+    W8A8 elsewhere -- on the kernels MI355X's dispatch table picks.  Batches
+    longer than ``chunk_size`` tokens run in chunks of that many tokens with
+    one chunk's workspace, as the reference's driver loop does
+    (fused_moe.py:2126-2128)."""
     if activation != "silu":
         raise NotImplementedError(f"activation {activation!r}: only silu (SwiGLU) is on this path")
     if use_int8_w8a8 or use_int8_w8a16 or use_int4_w4a16 or ocp_mx_scheme or per_channel_quant:
@@ -167,44 +180,57 @@ def fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.
         w2_scale = _expand_fp8_scale(w2_scale, w2)
         block_shape = [128, 128]
     if path == "auto":
-        path = dispatch_policy.resolve_path(hidden_states, w1, w2,
-                                            w1_scale if use_fp8_w8a8 else None,
-                                            w2_scale if use_fp8_w8a8 else None, topk,
-                                            block_shape, expert_map)
+        path = dispatch_policy.resolve_path(
+            hidden_states, w1, w2, w1_scale if use_fp8_w8a8 else None,
+            w2_scale if use_fp8_w8a8 else None, topk, block_shape, expert_map,
+            topk_weights=topk_weights, topk_ids=topk_ids, use_fp8_w8a8=use_fp8_w8a8,
+            apply_router_weight_on_input=apply_router_weight_on_input,
+            global_num_experts=global_num_experts)
     code = PATHS[path]
+    if chunk_size <= 0:
+        raise ValueError("chunk_size must be positive")
     if use_fp8_w8a8:
         if w1.dtype != torch.float8_e4m3fn or w2.dtype != torch.float8_e4m3fn:
             raise ValueError("fp8 MoE weights must be float8_e4m3fn")
         s1, s2 = w1_scale, w2_scale
         w1c, w2c = w1.contiguous(), w2.contiguous()
         _lib.check_cuda(hidden_states, w1c, w2c, s1, s2, wts, ids, emap)
-        lib = _lib.load()
-        nbytes = lib.vmamd_fused_moe_fp8_workspace_size(t, topk, e, h, i, code)
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=hidden_states.device)
-        call("vmamd_fused_moe_fp8", ptr(hidden_states), _lib.DTYPE_BF16, t, h, ptr(w1c), ptr(s1),
-             ptr(w2c), ptr(s2), e, i, ptr(wts), ptr(ids), topk, ptr(emap),
-             0 if emap is None else emap.numel(), limit, on_input, code, ptr(out), ptr(ws), nbytes,
-             stream_of(hidden_states))
-        return out
-    if w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16:
+        size = _lib.load().vmamd_fused_moe_fp8_workspace_size
+
+        def launch(x, ci, cw, o, ws, nbytes):
+            call("vmamd_fused_moe_fp8", ptr(x), _lib.DTYPE_BF16, x.shape[0], h, ptr(w1c), ptr(s1),
+                 ptr(w2c), ptr(s2), e, i, ptr(cw), ptr(ci), topk, ptr(emap),
+                 0 if emap is None else emap.numel(), limit, on_input, code, ptr(o), ptr(ws),
+                 nbytes, stream_of(x))
+    elif w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16:
         if w1_scale is not None or w2_scale is not None:
             raise ValueError("bf16 MoE weights take no scales")
-        return _fused_experts_bf16(hidden_states, w1, w2, wts, ids, emap, limit, on_input, code, out)
-    raise NotImplementedError(f"MoE weights of dtype {w1.dtype} are not on this path")
+        w1c, w2c = w1.contiguous(), w2.contiguous()
+        _lib.check_cuda(hidden_states, w1c, w2c, wts, ids, emap)
+        size = _lib.load().vmamd_fused_moe_bf16_workspace_size
 
-
-def _fused_experts_bf16(x, w1, w2, wts, ids, emap, limit, on_input, code, out):
-    e, n2, h = w1.shape
-    i = n2 // 2
-    t, topk = ids.shape
-    w1c, w2c = w1.contiguous(), w2.contiguous()
-    _lib.check_cuda(x, w1c, w2c, wts, ids, emap)
-    nbytes = _lib.load().vmamd_fused_moe_bf16_workspace_size(t, topk, e, h, i, code)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
-    call("vmamd_fused_moe_bf16", ptr(x), t, h, ptr(w1c), ptr(w2c), e, i, ptr(wts), ptr(ids), topk,
-         ptr(emap), 0 if emap is None else emap.numel(), limit, on_input, code, ptr(out), ptr(ws),
-         nbytes, stream_of(x))
+        def launch(x, ci, cw, o, ws, nbytes):
+            call("vmamd_fused_moe_bf16", ptr(x), x.shape[0], h, ptr(w1c), ptr(w2c), e, i, ptr(cw),
+                 ptr(ci), topk, ptr(emap), 0 if emap is None else emap.numel(), limit, on_input,
+                 code, ptr(o), ptr(ws), nbytes, stream_of(x))
+    else:
+        raise NotImplementedError(f"MoE weights of dtype {w1.dtype} are not on this path")
+    _run_chunked(hidden_states, ids, wts, out, chunk_size,
+                 lambda tc: size(tc, topk, e, h, i, code), launch)
     return out
+
+
+def _run_chunked(x, ids, wts, out, chunk, size, launch):
+    """The layer over token chunks of at most ``chunk`` rows, in order, with
+    one workspace sized for the largest chunk (the full-size ones and the
+    remainder may take different kernels, so both are sized)."""
+    t = x.shape[0]
+    first = min(t, chunk)
+    nbytes = max(size(first), size(t % chunk) if t > chunk and t % chunk else 0)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    for c0 in range(0, t, chunk):
+        c1 = min(t, c0 + chunk)
+        launch(x[c0:c1], ids[c0:c1], wts[c0:c1], out[c0:c1], ws, nbytes)
 
 
 class MoeStages:
