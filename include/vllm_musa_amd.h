@@ -188,6 +188,27 @@ int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int num_e
                                int32_t* scatter_idx, int32_t* active_experts,
                                int32_t* num_active, vmamd_stream_t stream);
 
+/* moe_align_block_size (the outputs above, without scatter_idx) and the 1x128
+ * fp8 quantiser of the layer's bf16 activations x [rows, cols] into xq
+ * [rows, cols] e4m3 and row-major xs [rows, cols/128] f32 (eps 1e-10, fp8
+ * range +-448; the bytes vmamd_per_token_group_quant_fp8 writes), as one
+ * launch: the first two steps of the fp8 layer (vmamd_fused_moe_fp8 runs
+ * them so), for callers that drive the stage entry points.  cols % 128 == 0,
+ * xq 8-byte aligned.  Replaces the fused routing + 1x128 quantisation that
+ * opens the reference's DeepGEMM prefill, deep_gemm_contig_preprocess_fp8_tilelang
+ * (vllm_musa/jit_kernel/tilelang/deep_gemm_contig_preprocess.py:1105-1130,
+ * called at model_executor/layers/fused_moe/fused_moe.py:898-910), which
+ * also permutes x into route order; the grouped GEMMs here gather x rows by
+ * route instead. */
+int vmamd_moe_align_block_size_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_experts,
+                                         int block_size, const int32_t* expert_map,
+                                         int64_t expert_map_len, int32_t* sorted_token_ids,
+                                         int64_t capacity, int32_t* expert_ids,
+                                         int32_t* num_tokens_post_pad, int32_t* expert_offsets,
+                                         int32_t* active_experts, int32_t* num_active, const void* x,
+                                         int64_t rows, int64_t cols, void* xq, float* xs,
+                                         vmamd_stream_t stream);
+
 /* ---------------------------------------------------------------- combine --
  * out[t, h] = round(sum_{k<topk} x[t, k, h]) with an fp32 accumulator in slot
  * order.  x: [tokens, topk, hidden], out: [tokens, hidden], same dtype.

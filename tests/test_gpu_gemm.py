@@ -273,6 +273,39 @@ def test_block_fp8_splitk_gemm(M, N, K):
     _check(out.float().cpu().numpy()[np.ix_(rows, cols)], ref)
 
 
+def test_block_fp8_big_split_plan_on_128_row_tiles():
+    """512 x 7168 x 16384 plans the 256 x 256 kernel split over K.  With the
+    activation scales passed at a negative row stride (last row first),
+    which only the 128 x 256 kernel takes, the call runs that kernel with the
+    split its own model prices, within the workspace sized for the plan:
+    sampled outputs against the oracle, and the usual call's values to the
+    fp32 summation order."""
+    from vllm_musa_amd import _lib, synthetic
+    from vllm_musa_amd._lib import call, ptr, stream_of
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    M, N, K = 512, 7168, 16384
+    KB = K // 128
+    nbytes = _lib.load().vmamd_w8a8_block_fp8_matmul_workspace_size(M, N, K)
+    assert nbytes > 0
+    w, ws = synthetic.dense_fp8_weight(N, K, 81)
+    xq, xs = per_token_group_quant_fp8(synthetic.activations(M, K, 82), 128)
+    usual = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    rev = xs.flip(0).contiguous()  # rev[j] = xs[M - 1 - j]
+    work = torch.empty(nbytes, dtype=torch.uint8, device=xq.device)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=xq.device)
+    call("vmamd_w8a8_block_fp8_matmul", ptr(xq), rev.data_ptr() + (M - 1) * KB * 4, -KB, 1, ptr(w),
+         ptr(ws), ptr(out), M, N, K, 128, 128, ptr(work), nbytes, stream_of(xq))
+    g = np.random.Generator(np.random.PCG64(83))
+    rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 32)]))
+    cols = np.unique(np.concatenate([[0, N - 1], g.integers(0, N, 512)]))
+    ref = block_fp8_matmul_sampled(xq.view(torch.uint8).cpu().numpy(), xs.cpu().numpy(),
+                                   w.view(torch.uint8).cpu().numpy(), ws.cpu().numpy(), rows, cols)
+    _check(out.float().cpu().numpy()[np.ix_(rows, cols)], ref)
+    d = (out.float() - usual.float()).abs().max().item()
+    assert d <= 2 ** -7 * usual.float().abs().max().item()
+
+
 @pytest.mark.parametrize("M,N,K", [(40, 2112, 7168), (200, 2112, 7168)])
 def test_block_fp8_gemm_without_workspace(M, N, K):
     """Through the C ABI with a NULL workspace where the plan wants one: the

@@ -43,8 +43,11 @@ def _no_alloc(xq, xs, w, ws, out):
 
 # (first call, second smaller call): split-K plans share the scratch; the
 # last pair runs the GEMV / unsplit plans (no scratch) after a split plan.
+# 512 x 7168 x 16384 is a 256 x 256 split plan (4 splits of 32 K steps,
+# 58.7 MB of partials through the fixed scratch).
 PAIRS = [((512, 2112, 7168), (200, 2112, 7168)),
          ((130, 7168, 2048), (65, 576, 7168)),
+         ((512, 7168, 16384), (200, 2112, 7168)),
          ((200, 2112, 7168), (1, 2112, 7168))]
 
 

@@ -364,3 +364,19 @@ extern "C" int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel
       num_active);
   return check_launch("moe_align_block_size");
 }
+
+extern "C" int vmamd_moe_align_block_size_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_experts,
+                                                    int block_size, const int32_t* expert_map,
+                                                    int64_t expert_map_len, int32_t* sorted_token_ids,
+                                                    int64_t capacity, int32_t* expert_ids,
+                                                    int32_t* num_tokens_post_pad, int32_t* expert_offsets,
+                                                    int32_t* active_experts, int32_t* num_active,
+                                                    const void* x, int64_t rows, int64_t cols, void* xq,
+                                                    float* xs, vmamd_stream_t stream) {
+  VMAMD_REQUIRE(!active_experts == !num_active,
+                "moe_align_block_size_quant_fp8: active_experts and num_active go together");
+  return align_and_group_quant_fp8(topk_ids, numel, num_experts, block_size, expert_map, expert_map_len,
+                                   sorted_token_ids, capacity, expert_ids, num_tokens_post_pad, expert_offsets,
+                                   active_experts, num_active, x, rows, cols, static_cast<uint8_t*>(xq), xs,
+                                   reinterpret_cast<hipStream_t>(stream));
+}

@@ -198,9 +198,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemv_rsrc(const void* base, in
 // at M = 4096 instead of 1.75 -- measured 3 % slower there.)
 using BigPipe = BigTile;
 static_assert(BigTile::BM * 512 <= BigTile::kLds, "the bf16 output tile is staged in the stages' LDS");
-#ifndef VMAMD_BIG_ROW_STORE
-#define VMAMD_BIG_ROW_STORE 1
-#endif
 
 // as_bytes: the extent of As in bytes (< 2 GiB); the host keeps (M + 256) K
 // and (N + 256) K below 2^31.
@@ -396,7 +393,7 @@ static int launch_big(const uint8_t* a, const float* As, int64_t as_sm, int64_t 
   }
   const int TM = (m + P::BM - 1) / P::BM, TN = (n + P::BN - 1) / P::BN;
   if (splits <= 1) kper = k / 128;
-  const int row_store = VMAMD_BIG_ROW_STORE && splits <= 1 && n % 8 == 0 &&
+  const int row_store = splits <= 1 && n % 8 == 0 &&
                         reinterpret_cast<uintptr_t>(c) % 16 == 0;
   gemm_fp8_big_kernel<<<dim3(xcd_grid(TM * TN), splits), P::kThreads, P::kLds, st>>>(
       a, As, as_sm, as_sk, as_bytes, b, Bs, c, m, n, k, TM, TN, kper, splits > 1 ? partial : nullptr,
@@ -716,9 +713,6 @@ static int gemm_kper(int M, int N, int K, int bm = 128, double step = 1.0, doubl
   return best;
 }
 
-#ifndef VMAMD_BIG_SPLIT
-#define VMAMD_BIG_SPLIT 1
-#endif
 // K step of the 256 x 256 tile against the 128 x 256 tile's: the bytes it
 // moves per step, (256 + 256) / (128 + 256).  Its splits keep at least
 // kBigMinSteps K steps: with fewer, each workgroup's fixed costs (first load,
@@ -751,7 +745,7 @@ static DensePlan dense_plan(int M, int N, int K) {
   d.big = false;
   double cost = 0.0;
   d.kper = d.gemv ? KS : gemm_kper(M, N, K, 128, 1.0, &cost);
-  if (VMAMD_BIG_SPLIT && !d.gemv && d.kper < KS && M >= 512) {
+  if (!d.gemv && d.kper < KS && M >= 512) {
     double cost_big = 0.0;
     const int kper_big = gemm_kper(M, N, K, 256, kBigStep, &cost_big, kBigMinSteps);
     if (kper_big < KS && cost_big < cost) {
@@ -910,6 +904,18 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
       return launch_big(a, As, as_stride_m, as_stride_k, static_cast<int>(as_extent), b, Bs, c, m, n, k, st,
                         plan.splits, plan.kper, static_cast<float*>(workspace));
   }
+  // A split planned for the 256 x 256 kernel that it cannot take (an operand
+  // past its 2 GiB descriptors, or negative scale strides) runs on the
+  // 128 x 256 kernel with the split its own model prices for 128-row tiles,
+  // capped so that the partials fit the workspace sized for the plan.
+  if (plan.big && plan.splits > 1) {
+    const int KS = k / 128;
+    const int64_t max_splits = static_cast<int64_t>(workspace_bytes / (static_cast<size_t>(m) * n * 4));
+    int64_t kper = gemm_kper(m, n, k);
+    kper = max_splits < 2 ? KS : std::max<int64_t>(kper, (KS + max_splits - 1) / max_splits);
+    plan.kper = static_cast<int>(kper);
+    plan.splits = static_cast<int>((KS + kper - 1) / kper);
+  }
   static bool lds_raised = false;
   if (!lds_raised) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_fp8_dma_kernel),
@@ -935,25 +941,33 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
 // the array's name denotes a host-side stand-in, not device memory, so it is
 // never handed to a kernel: its device address comes from
 // hipGetSymbolAddress, taken once per device with that device current, and
-// only that address is used.  Every split writes its whole partial slab
-// before the reduce reads it, so nothing needs clearing between calls.
+// only that address is used.  The device is the one the call's stream
+// belongs to (the kernels run there), which need not be the current one.
+// Every split writes its whole partial slab before the reduce reads it, so
+// nothing needs clearing between calls.
 namespace vmamd {
 
 constexpr size_t kNoAllocScratchBytes = VMAMD_W8A8_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
-static int noalloc_scratch(void** out) {
+static int noalloc_scratch(hipStream_t stream, void** out) {
   static std::mutex mu;
   static void* per_device[64] = {};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    set_error("w8a8_block_fp8_matmul_noalloc: no current device below 64");
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("w8a8_block_fp8_matmul_noalloc: the stream's device is unknown or not below 64");
     return VMAMD_ERR_HIP;
   }
   std::lock_guard<std::mutex> lock(mu);
   if (per_device[dev] == nullptr) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess || (cur != dev && hipSetDevice(dev) != hipSuccess)) {
+      set_error("w8a8_block_fp8_matmul_noalloc: cannot make device %d current", dev);
+      return VMAMD_ERR_HIP;
+    }
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
     if (e != hipSuccess || p == nullptr) {
       set_error("w8a8_block_fp8_matmul_noalloc: hipGetSymbolAddress of the scratch array failed: %s",
                 hipGetErrorString(e));
@@ -980,7 +994,7 @@ extern "C" int vmamd_w8a8_block_fp8_matmul_noalloc(const void* A, const float* A
                 (long long)M, (long long)N, (long long)K, need, kNoAllocScratchBytes);
   void* ws = nullptr;
   if (need > 0) {
-    const int rc = noalloc_scratch(&ws);
+    const int rc = noalloc_scratch(reinterpret_cast<hipStream_t>(stream), &ws);
     if (rc) return rc;
   }
   return vmamd_w8a8_block_fp8_matmul(A, As, as_stride_m, as_stride_k, B, Bs, C, M, N, K, block_n,

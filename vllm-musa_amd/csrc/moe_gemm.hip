@@ -1055,9 +1055,6 @@ __device__ __forceinline__ void moe_tile_decode(int L, const int32_t* __restrict
   mb_out = b0 + local % nb;
 }
 
-#ifndef VMAMD_TILE_EIDS
-#define VMAMD_TILE_EIDS 1
-#endif
 template <int BM = kMoeBM>
 __device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* __restrict__ offsets,
                                          const int32_t* __restrict__ ntpp, const int32_t* __restrict__ eids,
@@ -1068,7 +1065,7 @@ __device__ __forceinline__ bool moe_tile(int wg, int max_tiles, const int32_t* _
   if (q >= per) return false;
   const int L = (wg % kXcds) * per + q;
   if (L >= used) return false;
-  if (VMAMD_TILE_EIDS && eids) {
+  if (eids) {
     // Tile L lies in block L / TN, whose expert the alignment recorded (its
     // block size is BM): one load, then the expert's two offsets together,
     // instead of a dependent binary search over the offsets.
@@ -1389,9 +1386,6 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
 // SiLU-and-mul and the 1x128 a2 quantiser; W2: 256 hidden rows, epilogue the
 // routed weight.
 constexpr int kMoeBigBM = 256;
-#ifndef VMAMD_W2_LDS_STORE
-#define VMAMD_W2_LDS_STORE 1
-#endif
 static_assert(kMoeBigBM * 512 <= BigTile::kLds, "the W2 output tile is staged in the stages' LDS");
 
 template <int KIND, bool W13>
@@ -1600,7 +1594,6 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
       }
     }
   } else {
-#if VMAMD_W2_LDS_STORE
     // y = bf16(acc * w) staged through LDS so that each store writes 16 bytes
     // per lane and whole 512-byte tile rows (the 8-byte fragment stores
     // scatter 32-byte pieces over 16 rows per instruction).  Row r of the
@@ -1630,22 +1623,6 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
       const uint4 v = *reinterpret_cast<const uint4*>(yt + row * 512 + ((c ^ (row & 31)) << 4));
       *reinterpret_cast<uint4*>(y + static_cast<int64_t>(r) * N + n) = v;
     }
-#else
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int r = sorted[base + wm * 64 + mt * 16 + li];
-      if (r >= numel) continue;
-      const float rw = route_w ? route_w[r] : 1.0f;
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int n = n0 + nw + nt * 16 + 4 * lg;
-        if (n >= N) continue;
-        const v4f a = acc[mt][nt];
-        *reinterpret_cast<uint2*>(y + static_cast<int64_t>(r) * N + n) =
-            pack_bf16x4(a[0] * rw, a[1] * rw, a[2] * rw, a[3] * rw);
-      }
-    }
-#endif
   }
 }
 

@@ -283,6 +283,42 @@ def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int, block_size: i
          ptr(active_experts), ptr(num_active), stream_of(topk_ids))
 
 
+def moe_align_block_size_quant_fp8(topk_ids: torch.Tensor, num_experts: int, block_size: int,
+                                   sorted_token_ids: torch.Tensor, experts_ids: torch.Tensor,
+                                   num_tokens_post_pad: torch.Tensor, x: torch.Tensor,
+                                   output_q: torch.Tensor, output_s: torch.Tensor,
+                                   maybe_expert_map: torch.Tensor | None = None,
+                                   expert_offsets: torch.Tensor | None = None,
+                                   active_experts: torch.Tensor | None = None,
+                                   num_active: torch.Tensor | None = None) -> None:
+    """moe_align_block_size and the 1x128 fp8 quantiser of bf16 x [rows, cols]
+    (eps 1e-10, row-major scales) in one launch, with the outputs of the two
+    separate ops: the opening of the fp8 layer, as the fused call runs it."""
+    check_cuda(topk_ids, sorted_token_ids, experts_ids, num_tokens_post_pad, x, output_q, output_s,
+               maybe_expert_map, expert_offsets, active_experts, num_active)
+    if topk_ids.dtype != torch.int32:
+        raise ValueError("topk_ids must be int32")
+    for t, n in ((topk_ids, "topk_ids"), (sorted_token_ids, "sorted_token_ids"),
+                 (experts_ids, "experts_ids"), (x, "x"), (output_q, "output_q"),
+                 (output_s, "output_s")):
+        _contig(t, n)
+    if x.dim() != 2 or x.dtype != torch.bfloat16:
+        raise ValueError("x must be a bf16 [rows, cols] tensor")
+    rows, cols = x.shape
+    if output_q.dtype != FP8_DTYPE or tuple(output_q.shape) != (rows, cols) or \
+            output_s.dtype != torch.float32 or tuple(output_s.shape) != (rows, cols // 128):
+        raise ValueError("output_q must be float8_e4m3fn [rows, cols] and output_s float32 "
+                         "[rows, cols/128]")
+    cap = sorted_token_ids.numel()
+    if experts_ids.numel() < -(-cap // block_size):
+        raise ValueError("experts_ids is shorter than ceil(len(sorted_token_ids) / block_size)")
+    emap = None if maybe_expert_map is None else maybe_expert_map.to(torch.int32).contiguous()
+    call("vmamd_moe_align_block_size_quant_fp8", ptr(topk_ids), topk_ids.numel(), num_experts,
+         block_size, ptr(emap), 0 if emap is None else emap.numel(), ptr(sorted_token_ids), cap,
+         ptr(experts_ids), ptr(num_tokens_post_pad), ptr(expert_offsets), ptr(active_experts),
+         ptr(num_active), ptr(x), rows, cols, ptr(output_q), ptr(output_s), stream_of(x))
+
+
 def moe_sum(input: torch.Tensor, output: torch.Tensor, topk_ids: torch.Tensor | None = None,
             expert_map: torch.Tensor | None = None) -> None:
     """Reference: _moe_C.moe_sum (schema 0041-…torch_bindings.cpp.patch:44-50) and

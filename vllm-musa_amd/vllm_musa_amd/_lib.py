@@ -49,6 +49,8 @@ SIGNATURES: dict[str, list] = {
                            _p],
     "vmamd_moe_align_block_size": [_p, _i64, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _p, _p, _p,
                                    _p, _p],
+    "vmamd_moe_align_block_size_quant_fp8": [_p, _i64, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _p,
+                                             _p, _p, _p, _i64, _i64, _p, _p, _p],
     "vmamd_moe_sum": [_p, _i32, _i64, _i32, _i64, _p, _p, _i64, _p, _p],
     "vmamd_w8a8_block_fp8_matmul_workspace_size": [_i64, _i64, _i64],
     "vmamd_w8a8_block_fp8_matmul": [_p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32,
