@@ -26,6 +26,11 @@ us / TFLOP/s / GB/s and the fraction of min(peak compute, AI x 8 TB/s):
   bf16_moe   bf16 layer E=128, top-8 softmax renorm, H=2048, I=768 at
              T = 1, 16, 128, 1024, 8192, uniform and skewed (+2.0 on 8 experts)
   w4afp8_moe w4afp8 layer E=128, top-8, H=4096, I=1536 at T = 1, 32, 512, 4096
+  native_gemv the reference's native GEMV-MoE numerics (bf16 activations
+             against the fp8 weights) where its dispatcher runs them: fp8
+             E=256, top-8, H=2048, I=128 at T = 1, 8, 13 (path auto), and the
+             DeepSeek-V3 layer at T = 1 (path native_gemv); each beside the
+             W8A8 decode kernels on the same call
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-sweep] [--no-cpu]
   python bench.py --traffic-probe   # the launches profiled for FETCH_SIZE / WRITE_SIZE
@@ -33,6 +38,7 @@ us / TFLOP/s / GB/s and the fraction of min(peak compute, AI x 8 TB/s):
   python bench.py --w4              # w4afp8 MoE layer, T = 1, 32, 512, 4096 (JSON lines)
   python bench.py --swiglu          # clamped SwiGLU + block-fp8 down projection (JSON lines)
   python bench.py --fold            # shared expert folded into the MoE vs run as dense GEMMs
+  python bench.py --native          # the native-GEMV numerics at their decode shapes (JSON lines)
 """
 from __future__ import annotations
 
@@ -428,9 +434,73 @@ def bf16_configs(torch, iters: int, flush, log) -> list:
             row = {"T": t, "skewed": skewed, "experts_touched": u,
                    **point(median_us(torch, step, iters, flush), fl, by, PEAK_BF16_TFLOPS)}
             row["graph_us"] = round(graph_median(torch, step, iters, flush) * 1e3, 1)
+            if t == C2_T[-1] and not skewed:
+                row["kernels"] = bf16_kernels(torch, x, w13, w2, logits, iters, flush)
             out.append(row)
         log(f"bench: bf16 layer ({'skewed' if skewed else 'uniform'}) done")
     del w13, w2
+    return out
+
+
+def bf16_layer(torch, t: int, skewed: bool = False, weights=None):
+    """The bf16 benchmark layer at T: (step, ids, weights); step = routing +
+    fused_experts_impl."""
+    from vllm_musa_amd import fused_topk, synthetic
+    from vllm_musa_amd.fused_moe import fused_experts_impl
+    w13, w2 = weights if weights is not None else synthetic.moe_bf16_weights(C2_E, C2_H, C2_I, 4000)
+    x = synthetic.activations(t, C2_H, 4001 + t)
+    logits = synthetic.router_logits(t, C2_E, 4002 + t, hot=8 if skewed else 0)
+
+    def step():
+        w, ids, _ = fused_topk(x, logits, TOPK, True)
+        return fused_experts_impl(x, w13, w2, w, ids)
+    return step, x, logits, (w13, w2)
+
+
+def profile_bf16(torch, t: int, warmup: int, steps: int, log) -> int:
+    step, _, _, _ = bf16_layer(torch, t)
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    for _ in range(warmup):
+        step()
+    for _ in range(steps):
+        flush_buf.max()
+        torch.cuda.synchronize()
+        step()
+    torch.cuda.synchronize()
+    a = torch.randn(4096, 4096, device="cuda").to(torch.bfloat16)
+    b = torch.randn(4096, 4096, device="cuda").to(torch.bfloat16)
+    for _ in range(3):
+        a @ b
+    torch.cuda.synchronize()
+    log(f"bench: bf16 profile run done ({steps} steps at T={t}, 3 calibration matmuls)")
+    return 0
+
+
+# rocprofv3 counter summary of the bf16 grouped GEMMs at T=8192
+# ("mfma_util_bf16_w13:" / "mfma_util_bf16_w2:" lines: MFMA busy fractions).
+BF16_MFMA_SUMMARY = os.path.join("profiles", "moe_bf16_c2_mfma_and_trace.md")
+
+
+def bf16_kernels(torch, x, w13, w2, logits, iters: int, flush) -> dict:
+    """The bf16 layer's two grouped GEMMs at this T, each timed alone with HIP
+    events on its launch stream (MoeStages), with their bf16-MFMA rooflines:
+    useful flops / time against the 2.5 PF dense bf16 peak, and the MFMA busy
+    fraction from the committed counter summary."""
+    from vllm_musa_amd import fused_topk
+    from vllm_musa_amd.fused_moe import MoeStages
+    t = x.shape[0]
+    w, ids, _ = fused_topk(x, logits, TOPK, True)
+    st = MoeStages(x, w13, None, w2, None, w, ids, path="auto")
+    st.align()
+    out = {"block_m": st.block_m}
+    for name, fn, fl in (("w13", st.w13_stage, 2.0 * t * TOPK * 2 * C2_I * C2_H),
+                         ("w2", st.w2_stage, 2.0 * t * TOPK * C2_H * C2_I)):
+        us = median_us(torch, fn, iters, flush)
+        out[name] = {"us": round(us, 1), "tflops": round(fl / (us * 1e-6) / 1e12, 1),
+                     "frac_bf16_peak": round(fl / (us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                     "mfma_util": read_summary_value(BF16_MFMA_SUMMARY, f"mfma_util_bf16_{name}", float)}
+    out["mfma_source"] = BF16_MFMA_SUMMARY
+    del st
     return out
 
 
@@ -464,6 +534,55 @@ def w4_configs(torch, iters: int, flush, log) -> list:
     log("bench: w4afp8 layer done")
     del w13, w2, s13, s2
     return out
+
+
+NATIVE_SHAPES = ((256, 2048, 128, 8, (1, 8, 13)), (256, 7168, 2048, 8, (1,)))
+
+
+def native_configs(torch, iters: int, flush, log) -> list:
+    """The layer with the reference's native GEMV-MoE numerics (bf16 x against
+    the fp8 weights, gate and up in fp32 through the SwiGLU): routing (top-k
+    softmax renorm on ~N(0,1) logits) + fused_experts_impl.  On its calibrated
+    decode shape (E=256, H=2048, I=128, top-8) path auto takes these numerics
+    up to T=13, as the reference's S5000 table does; the DeepSeek-V3 layer is
+    forced (path native_gemv, which the reference's VLLM_MUSA_FUSED_MOE_DISPATCH
+    =gemv selects).  `w8a8_us`: the same call on the W8A8 decode kernels.
+    Bytes = touched experts' fp8 weights and block scales + x in + out +
+    logits + routing."""
+    from vllm_musa_amd import fused_topk, synthetic
+    from vllm_musa_amd.fused_moe import fused_experts_impl
+    out = []
+    for e, h, i, k, ts in NATIVE_SHAPES:
+        w13, s13, w2, s2 = synthetic.moe_fp8_weights(e, h, i, 6000 + h)
+        per_expert = 3 * i * h + 4 * ((2 * i + 127) // 128 * (h // 128) + (h + 127) // 128 * (i // 128))
+        for t in ts:
+            x = synthetic.activations(t, h, 6001 + t)
+            logits = synthetic.router_logits(t, e, 6002 + t)
+            path = "auto" if h == 2048 else "native_gemv"
+
+            def step(p=path):
+                w, ids, _ = fused_topk(x, logits, k, True)
+                return fused_experts_impl(x, w13, w2, w, ids, use_fp8_w8a8=True, w1_scale=s13,
+                                          w2_scale=s2, block_shape=[128, 128], path=p)
+            _, ids, _ = fused_topk(x, logits, k, True)
+            u = int(torch.unique(ids).numel())
+            fl = 2.0 * t * k * 3 * h * i
+            by = u * per_expert + 4.0 * t * h + 4.0 * t * e + 8.0 * t * k
+            row = {"E": e, "H": h, "I": i, "topk": k, "T": t, "path": path, "experts_touched": u,
+                   **point(median_us(torch, step, iters, flush), fl, by, PEAK_FP8_TFLOPS)}
+            row["graph_us"] = round(graph_median(torch, step, iters, flush) * 1e3, 1)
+            row["w8a8_us"] = round(median_us(torch, lambda: step("gemv"), iters, flush), 1)
+            out.append(row)
+        log(f"bench: native-GEMV layer E={e} H={h} done")
+        del w13, s13, w2, s2
+    return out
+
+
+def native_sweep(torch, iters: int, log) -> int:
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    for row in native_configs(torch, iters, lambda: flush_buf.max(), log):
+        print(json.dumps(row), flush=True)
+    return 0
 
 
 def scales_sweep(torch, iters: int, log) -> int:
@@ -554,6 +673,10 @@ def main() -> int:
     ap.add_argument("--profile-t", type=int, default=0,
                     help="only run --steps layer steps at this T (caches flushed by a 1 GiB "
                          "read before each), for rocprofv3 --kernel-trace; prints no JSON")
+    ap.add_argument("--profile-bf16", type=int, default=0,
+                    help="only run --steps bf16-layer steps (E=128, top-8, H=2048, I=768) at this "
+                         "T (caches flushed by a 1 GiB read before each), then three 4096^3 bf16 "
+                         "matmuls (the MFMA counter calibration), for rocprofv3; prints no JSON")
     ap.add_argument("--dense", action="store_true",
                     help="only time the dense w8a8 block-fp8 GEMM / GEMV at the DeepSeek-V3 "
                          "linear shapes (one JSON line per shape)")
@@ -571,6 +694,9 @@ def main() -> int:
                     help="only time the checkpoint scale conversions (e8m0 -> f32 of the "
                          "DeepSeek-V3 MoE block scales, f32 -> bf16 + check of a w4afp8 layer's "
                          "group scales), one JSON line per workload")
+    ap.add_argument("--native", action="store_true",
+                    help="only time the layer with the reference's native GEMV numerics at its "
+                         "decode shapes (one JSON line per point)")
     ap.add_argument("--router", action="store_true",
                     help="only time the fp32 router gate (Nemotron-H, [M, 2688] x [128, 2688]^T) "
                          "against the platform fp32 GEMM at M = 1, 7, 115, 512")
@@ -599,6 +725,10 @@ def main() -> int:
         return scales_sweep(torch, args.sweep_iters, log)
     if args.router:
         return router_sweep(torch, args.sweep_iters, log)
+    if args.native:
+        return native_sweep(torch, args.sweep_iters, log)
+    if args.profile_bf16 > 0:
+        return profile_bf16(torch, args.profile_bf16, args.warmup, args.steps, log)
 
     log(f"bench: building E={E} H={H} I={I} fp8 expert stack")
     weights = synthetic.moe_fp8_weights(E, H, I, WEIGHT_SEED)
@@ -742,6 +872,7 @@ def main() -> int:
         extra["dense"] = dense_configs(torch, args.sweep_iters, flush, log)
         extra["bf16_moe"] = bf16_configs(torch, args.sweep_iters, flush, log)
         extra["w4afp8_moe"] = w4_configs(torch, args.sweep_iters, flush, log)
+        extra["native_gemv"] = native_configs(torch, args.sweep_iters, flush, log)
         del flush_buf
 
     cpu = None
