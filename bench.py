@@ -620,6 +620,56 @@ def scales_sweep(torch, iters: int, log) -> int:
     return 0
 
 
+def ceiling_sweep(torch, iters: int, log) -> int:
+    """The platform's own GEMMs at the dense benchmark shapes, beside this
+    package's block-fp8 GEMM: torch._scaled_mm in fp8 (e4m3fn operands, bf16
+    out) with one scale per tensor and, where the installed hipBLASLt takes
+    them, one scale per row of A and per column of B; and torch.matmul in
+    bf16.  Neither platform GEMM applies 128 x 128 block scales, so they bound
+    from above what an fp8 GEMM of this shape reaches on this GPU.  HIP-event
+    medians, caches flushed by a 1 GiB read before each call."""
+    from vllm_musa_amd import per_token_group_quant_fp8, synthetic
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    flush = lambda: flush_buf.max()
+    fp8 = torch.float8_e4m3fn
+    for n, k in C1_SHAPES:
+        w, ws = synthetic.dense_fp8_weight(n, k, 7)
+        for m in (512, 4096):
+            x = synthetic.activations(m, k, 8)
+            q, s = per_token_group_quant_fp8(x, 128)
+            fl = 2.0 * m * n * k
+            row = {"N": n, "K": k, "M": m}
+
+            def rec(name, fn):
+                try:
+                    us = median_us(torch, fn, iters, flush)
+                except RuntimeError as exc:  # a scaling mode this hipBLASLt does not take
+                    row[name] = {"error": str(exc).splitlines()[0][:120]}
+                    return
+                row[name] = {"us": round(us, 1),
+                             "frac_fp8_peak": round(fl / (us * 1e-6) / (PEAK_FP8_TFLOPS * 1e12), 3)}
+
+            rec("block_fp8_gemm", lambda: w8a8_block_fp8_matmul(q, w, s, ws, [128, 128]))
+            one = torch.ones((), dtype=torch.float32, device="cuda")
+            rec("scaled_mm_tensorwise", lambda: torch._scaled_mm(q, w.t(), one, one, out_dtype=torch.bfloat16))
+            sa = torch.rand(m, 1, dtype=torch.float32, device="cuda") + 0.5
+            sb = torch.rand(1, n, dtype=torch.float32, device="cuda") + 0.5
+            rec("scaled_mm_rowwise", lambda: torch._scaled_mm(q, w.t(), sa, sb, out_dtype=torch.bfloat16))
+            xb = x.to(torch.bfloat16)
+            wb = w.to(torch.bfloat16)
+            rec("bf16_matmul", lambda: torch.nn.functional.linear(xb, wb))
+            if "us" in row["bf16_matmul"]:
+                row["bf16_matmul"]["frac_bf16_peak"] = round(
+                    fl / (row["bf16_matmul"]["us"] * 1e-6) / (PEAK_BF16_TFLOPS * 1e12), 3)
+            print(json.dumps(row), flush=True)
+            del q, s, x, xb, wb
+        del w, ws
+        torch.cuda.empty_cache()
+    log("bench: platform GEMM ceiling done")
+    return 0
+
+
 def router_sweep(torch, iters: int, log) -> int:
     """The fp32 router gate of Nemotron-H (x [M, 2688] bf16 . W [128, 2688]^T fp32)
     at M = 1, 7, 115, 512: vmamd_router_gate_fp32 against the platform's fp32
@@ -697,6 +747,9 @@ def main() -> int:
     ap.add_argument("--native", action="store_true",
                     help="only time the layer with the reference's native GEMV numerics at its "
                          "decode shapes (one JSON line per point)")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="only time the platform's fp8 (torch._scaled_mm) and bf16 GEMMs beside "
+                         "the block-fp8 GEMM at the dense benchmark shapes, M = 512 and 4096")
     ap.add_argument("--router", action="store_true",
                     help="only time the fp32 router gate (Nemotron-H, [M, 2688] x [128, 2688]^T) "
                          "against the platform fp32 GEMM at M = 1, 7, 115, 512")
@@ -725,6 +778,8 @@ def main() -> int:
         return scales_sweep(torch, args.sweep_iters, log)
     if args.router:
         return router_sweep(torch, args.sweep_iters, log)
+    if args.ceiling:
+        return ceiling_sweep(torch, args.sweep_iters, log)
     if args.native:
         return native_sweep(torch, args.sweep_iters, log)
     if args.profile_bf16 > 0:
