@@ -66,6 +66,59 @@ def test_group_quant_nan_and_saturation():
     assert torch.all(qb[1, 128:] == 0xFE)
 
 
+def _e4m3_rounding_targets() -> np.ndarray:
+    """Quotients where e4m3 rounding is decided: every midpoint between two
+    e4m3 values from the subnormal range up to 432 (ties, which round to
+    even), the e4m3 values themselves, and each of them moved by 1-3 fp32
+    ulps either way; plus +-0 and values just below 2^-10."""
+    mids = [(2 * i + 1) * 2.0 ** -10 for i in range(8)]                    # subnormal range
+    vals = [i * 2.0 ** -9 for i in range(1, 8)]
+    for e in range(-6, 9):
+        for k in range(8):
+            vals.append((1 + k / 8) * 2.0 ** e)
+            mids.append((1 + (2 * k + 1) / 16) * 2.0 ** e)
+    base = np.array([m for m in mids + vals if m <= 448.0], np.float32)
+    out = [base]
+    up, down = base.copy(), base.copy()
+    for _ in range(3):
+        up = np.nextafter(up, np.float32(np.inf))
+        down = np.nextafter(down, np.float32(0))
+        out += [up.copy(), down.copy()]
+    tiny = np.nextafter(np.float32(2.0 ** -10), np.float32(0)) * np.ones(4, np.float32)
+    t = np.concatenate(out + [tiny, np.float32([0.0])])
+    t = t[t <= 448.0]
+    return np.concatenate([t, -t, np.float32([-0.0])])
+
+
+@pytest.mark.parametrize("scale", ["pow2_low", "pow2_one", "pow2_high", "random"])
+def test_group_quant_at_e4m3_rounding_boundaries(scale):
+    """Quotients x / s on and within 3 ulps of every e4m3 rounding boundary,
+    fp32 inputs: the bytes equal the oracle's (IEEE division, then
+    round-to-nearest-even), including the ties, the e4m3 subnormal range and
+    signed zeros.  A power-of-two scale (group max 448 * 2^k) makes x / s the
+    target exactly; a random scale puts it within an ulp or so of it."""
+    from vllm_musa_amd import per_token_group_quant_fp8
+    t = _e4m3_rounding_targets()
+    g = np.random.Generator(np.random.PCG64(17))
+    ngroups = -(-t.size // 127)
+    pad = np.zeros(ngroups * 127 - t.size, np.float32)
+    body = np.concatenate([t, pad])
+    g.shuffle(body)
+    if scale == "random":
+        s = g.uniform(0.01, 20.0, ngroups).astype(np.float32) / np.float32(448.0)
+    else:
+        k = {"pow2_low": -20, "pow2_one": 0, "pow2_high": 7}[scale]
+        s = np.full(ngroups, 2.0 ** k, np.float32)
+    x = np.empty((ngroups, 128), np.float32)
+    x[:, 0] = (np.float32(448.0) * s).astype(np.float32)          # the group's absolute maximum
+    x[:, 1:] = (body.reshape(ngroups, 127).astype(np.float64) * s[:, None]).astype(np.float32)
+    xt = torch.from_numpy(x.reshape(1, -1)).to(DEV)
+    q, sc = per_token_group_quant_fp8(xt, 128)
+    q_ref, s_ref = oquant.group_quant_fp8(x.reshape(1, -1))
+    np.testing.assert_array_equal(sc.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+
+
 def test_silu_and_mul_close():
     from vllm_musa_amd import _custom_ops as ops
     g = np.random.Generator(np.random.PCG64(11))

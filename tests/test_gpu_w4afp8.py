@@ -176,6 +176,35 @@ def test_per_token_quant_bit_exact(rows, cols):
     np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
 
 
+def test_per_token_quant_at_e4m3_rounding_boundaries():
+    """bf16 rows whose quotients x / s are exactly e4m3 midpoints (ties) or
+    e4m3 values (a power-of-two scale: the row maximum is 448 * 2^k), both
+    signs, zeros, and bf16 neighbours of each: bytes equal the oracle's."""
+    from vllm_musa_amd._custom_ops import per_token_quant_fp8
+    from oracle.numerics import bf16_round
+    mids = [(2 * i + 1) * 2.0 ** -10 for i in range(8)]
+    vals = [i * 2.0 ** -9 for i in range(8)]
+    for e in range(-6, 9):
+        for k in range(8):
+            vals.append((1 + k / 8) * 2.0 ** e)
+            mids.append((1 + (2 * k + 1) / 16) * 2.0 ** e)
+    t = np.array([m for m in mids + vals if m <= 448.0], np.float32)
+    t = np.concatenate([t, bf16_round(t * np.float32(1 + 2 ** -8)), bf16_round(t * np.float32(1 - 2 ** -8))])
+    t = np.concatenate([t[t <= 448.0], -t[t <= 448.0], np.float32([-0.0])])
+    rows = []
+    for k in (-12, 0, 3):
+        r = np.zeros(1536, np.float32)
+        r[0] = 448.0 * 2.0 ** k
+        r[1:1 + t.size] = t * np.float32(2.0 ** k)
+        rows.append(r)
+    x = np.stack(rows)
+    assert np.array_equal(bf16_round(x), x)
+    q, s = per_token_quant_fp8(torch.from_numpy(x).to(torch.bfloat16).to(DEV))
+    q_ref, s_ref = ow4.dynamic_fp8_rows(x)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+
+
 def test_weighted_sum_bit_exact():
     from vllm_musa_amd._custom_ops import moe_weighted_sum
     g = np.random.Generator(np.random.PCG64(9))
