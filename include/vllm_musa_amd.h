@@ -334,14 +334,15 @@ int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H, const 
  * block_size: 16 = decode (expert-major GEMV, each weight row streamed once
  * per call), 128 = prefill (grouped MFMA GEMM over 128-route blocks), 256 =
  * long prefill (256-route blocks; same results as 128).  The fused call
- * takes 256 from 128 routes per expert (fp8 and bf16).
+ * takes 256 from 128 routes per expert (fp8 and bf16; bf16 also 320, see
+ * below).
  *
  * W13:  a = bf16(silu(h_gate) * h_up), h = bf16(W13[e] . q(x[t])), then a is
  *       quantised per 1x128 group into a2q (fp8) / a2s (f32, [rows, I/128]).
  *       Rows of a2q/a2s are routes (r = t*topk + k, [T*topk, I]) for
  *       block_m 16, positions of sorted_token_ids ([capacity, I]) for 128 / 256.
  * W2:   y[r] = bf16(W2[e] . dequant(a2q[row(r)]) * topk_weights[r]),
- *       y [T*topk, H] bf16 (8-byte aligned; 16-byte for block_m 256); rows of
+ *       y [T*topk, H] bf16 (8-byte aligned; 16-byte for block_m 256 and 320); rows of
  *       dropped routes are left unwritten.
  * Scratch: vmamd_moe_fp8_stage_workspace_size() bytes, 16-byte aligned
  * (enough for either stage).
@@ -377,7 +378,12 @@ int vmamd_moe_fp8_w2(const void* a2q, const float* a2s, int64_t T, int topk,
  *   out[t] = bf16( sum_k bf16( W2[e] . a * w[t,k] ) ),
  *   a = bf16(silu(h_g) * h_u),  h = bf16(W13[e] . x[t])   (fp32 accumulation)
  * x [T, H] bf16; w13 [E, 2I, H] bf16; w2 [E, H, I] bf16; a2 bf16 rows as for
- * fp8 ([T*topk, I] for block_m 16, [capacity, I] for 128).  Routing,
+ * fp8 ([T*topk, I] for block_m 16, [capacity, I] for the grouped GEMMs).
+ * block_m: 16, 128, 256, or 320 (bf16 only: 320-route blocks on the same
+ * 256-row tiles, which the fused call takes from 128 routes per expert
+ * where the expected largest expert, mean + 3 sqrt(mean) routes, needs
+ * fewer 320-route blocks than 256-route ones, each counted 1.25x; same
+ * results).  Routing,
  * expert_map, swiglu_limit, path and workspace rules as for fp8;
  * NATIVE_GEMV keeps gate and up in fp32 through the SwiGLU, as the
  * reference's native bf16 GEMV-MoE does (csrc/musa/gemv.mu:430-434, 477-487):

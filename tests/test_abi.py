@@ -49,6 +49,27 @@ def test_argument_errors_are_reported_without_a_gpu():
                   None, None, None, None, None)
     msg = _lib.load().vmamd_last_error().decode()
     assert "capacity" in msg
+    # 320-route blocks are a bf16 tile: the fp8 stages refuse them
+    with pytest.raises(ValueError, match="bf16 weights only"):
+        _lib.call("vmamd_moe_fp8_w13", None, None, 1024, 512, 2, None, 1 << 20, 320, None, None, None,
+                  None, None, None, 8, 256, 0.0, None, None, None, 0, None)
+
+
+def test_bf16_large_block_rule():
+    """The bf16 grouped GEMMs take 320-route blocks where the expected largest
+    expert (mean + 3 sqrt(mean) routes) needs fewer of them than of 256-route
+    blocks, each counted 1.25x: mean 256 -> one 320 block instead of two;
+    mean 512 -> two instead of three; mean 1024 -> 256 (four 320 blocks
+    cost as much as five); mean 128, 175 and 384 -> 256 (as many blocks
+    either way)."""
+    from vllm_musa_amd.fused_moe import _bf16_big_block
+    assert _bf16_big_block(2048 * 8, 128) == 256       # mean 128
+    assert _bf16_big_block(4096 * 8, 128) == 320       # mean 256
+    assert _bf16_big_block(8192 * 8, 128) == 320       # mean 512
+    assert _bf16_big_block(16384 * 8, 128) == 256      # mean 1024: 5 vs 4 * 1.25
+    assert _bf16_big_block(6144 * 8, 128) == 256       # mean 384: 2 vs 2
+    assert _bf16_big_block(700 * 2, 8) == 256          # mean 175
+    assert _bf16_big_block(1024 * 2, 8) == 320
 
 
 def test_dense_workspace_query():

@@ -135,6 +135,61 @@ def test_bf16_moe_256_route_blocks_match_128(variant):
     assert torch.equal(_run(x, w13, w2, w, ids, "gemm", emap=emap, limit=limit), a)
 
 
+def test_bf16_moe_320_route_blocks_vs_oracle():
+    """320-route blocks (bf16 only): 2048 routes on 8 experts (mean 256, so
+    the fused call takes them); H = 640 leaves the last 256-row W2 tile half
+    outside the output, I = 384 gives three 128-column W13 tiles."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.fused_moe import MoeStages
+    w13, w2 = _weights(8, 640, 384, 54)
+    x = synthetic.activations(1024, 640, 55)
+    w, ids = _routing(1024, 8, 2, 56)
+    assert MoeStages(x, w13, None, w2, None, w, ids, path="gemm").block_m == 320
+    _check(_run(x, w13, w2, w, ids, "gemm"), _oracle(x, w13, w2, w, ids))
+
+
+@pytest.mark.parametrize("variant", ["plain", "hot", "expert_map", "limit"])
+def test_bf16_moe_320_route_blocks_match_256_and_128(variant):
+    """320-, 256- and 128-route blocks give the same bits.  A hot expert
+    (half the routes: its blocks run full, the last one partly padding), an
+    expert map with dropped routes, and the clamped SwiGLU."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.fused_moe import MoeStages
+    T, E = 1024, 8
+    w13, w2 = _weights(E, 512, 256, 65)
+    x = synthetic.activations(T, 512, 66)
+    w, ids = _routing(T, E, 2, 67)
+    emap, limit = None, None
+    if variant == "hot":
+        ids[: T // 2, 0] = 3
+        ids[: T // 2, 1] = torch.where(ids[: T // 2, 1] == 3, 5, ids[: T // 2, 1])
+    if variant == "expert_map":
+        g = torch.Generator().manual_seed(68)
+        ids = torch.stack([torch.randperm(12, generator=g)[:2] for _ in range(T)]).to(torch.int32).to(DEV)
+        emap = torch.full((12,), -1, dtype=torch.int32)
+        emap[4:] = torch.arange(8, dtype=torch.int32)
+        emap = emap.to(DEV)
+    if variant == "limit":
+        limit = 7.0
+    kw = dict(path="gemm", expert_map=emap, swiglu_limit=limit)
+    outs = {}
+    for bm in (320, 256, 128):
+        st = MoeStages(x, w13, None, w2, None, w, ids, block_m=bm, **kw)
+        outs[bm] = st.run().clone()
+    assert torch.equal(outs[320], outs[256]) and torch.equal(outs[320], outs[128])
+    assert torch.equal(_run(x, w13, w2, w, ids, "gemm", emap=emap, limit=limit), outs[320])
+
+
+def test_fp8_stages_refuse_320_route_blocks():
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.fused_moe import Fp8MoeStages
+    w13, s13, w2, s2 = synthetic.moe_fp8_weights(8, 256, 128, 57)
+    x = synthetic.activations(16, 256, 58)
+    w, ids = _routing(16, 8, 2, 59)
+    with pytest.raises(ValueError, match="block_m 320"):
+        Fp8MoeStages(x, w13, s13, w2, s2, w, ids, path="gemm", block_m=320)
+
+
 def test_bf16_moe_paths_agree_and_deterministic():
     from vllm_musa_amd import synthetic
     w13, w2 = _weights(32, 2048, 768, 21)

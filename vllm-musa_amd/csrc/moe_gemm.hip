@@ -39,6 +39,7 @@
 // per tile (interleaved by 16 so each lane holds matching gate/up values) and
 // fuses SiLU-and-mul (and the kFp8 1x128 a2 quantiser) into its epilogue.
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <type_traits>
 
@@ -1385,17 +1386,34 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
 // 128 up rows interleaved by 16 (n tile 2q gate, 2q + 1 up); epilogue
 // SiLU-and-mul and the 1x128 a2 quantiser; W2: 256 hidden rows, epilogue the
 // routed weight.
-constexpr int kMoeBigBM = 256;
-static_assert(kMoeBigBM * 512 <= BigTile::kLds, "the W2 output tile is staged in the stages' LDS");
+//
+// bf16 also runs the tile with 320 routes (MTV = 5: 80 routes per m-wave),
+// for the route counts that would leave a 256-route block nearly empty:
+// around 256 or 512 routes per expert an expert's last 256-route block
+// holds a few dozen routes yet streams the expert's whole weight tile.  fp8
+// keeps 256 routes (the promotion's registers leave no room for a fifth
+// m-tile: 256 VGPRs, and W13 at T=4096 measured 12 % slower).
+template <int MTV>
+struct MoeBigTile {
+  static constexpr int BM = 64 * MTV, BN = 256, WN = 2, MT = MTV, NT = 8, WTM = 16 * MTV, kThreads = 512;
+  static constexpr int kOffB = BM * 128;
+  static constexpr int kOffSA = (BM + BN) * 128;
+  static constexpr int kOffSB = kOffSA + BM * 4;
+  static constexpr int kStage = kOffSB + 256;  // the B-scale DMA writes 64 lanes x 4 bytes
+  // Two stages, or the W2 output tile staged for its stores if that is larger.
+  static constexpr int kLds = 2 * kStage > BM * 512 ? 2 * kStage : BM * 512;
+  static_assert(kLds <= 160 * 1024, "LDS stages exceed the CU's LDS");
+};
+constexpr int kMoeBigBM = 256, kMoeBig320 = 320;
 
-template <int KIND, bool W13>
+template <int KIND, bool W13, int MTV = 4>
 __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_s_bytes,
     int topk, int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ ntpp, const int32_t* __restrict__ eids, int E, int numel, int max_tiles, const uint8_t* __restrict__ w,
     const float* __restrict__ ws, int N, int I, float limit, const float* __restrict__ route_w,
     uint8_t* __restrict__ a2, float* __restrict__ a2s, uint16_t* __restrict__ y) {
-  using P = BigTile;
+  using P = MoeBigTile<MTV>;
   constexpr int BM = P::BM, NT = P::NT, MT = P::MT;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
   const int TN = W13 ? I / 128 : (N + P::BN - 1) / P::BN;
@@ -1431,15 +1449,16 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(act, act_bytes);
   const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(w + static_cast<int64_t>(e) * N * rowb, N * rowb);
   const uint32_t chunk = static_cast<uint32_t>(((lane % 8) ^ (lane / 8)) * 16);
-  uint32_t offA[4], offB[4];
-  uint64_t liveA[4];  // activation row groups holding a route (padding groups load nothing)
+  uint32_t offA[MT], offB[4];
+  uint64_t liveA[MT];  // activation row groups holding a route (padding groups load nothing)
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < MT; ++j) {
     const int r = (wave + 8 * j) * 8 + lane / 8;
     offA[j] = static_cast<uint32_t>(arow(r)) * rowb + chunk;
-    offB[j] = static_cast<uint32_t>(wrow(r)) * rowb + chunk;
     liveA[j] = __builtin_amdgcn_ballot_w64(sorted[base + r] < numel);
   }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) offB[j] = static_cast<uint32_t>(wrow((wave + 8 * j) * 8 + lane / 8)) * rowb + chunk;
   uint32_t offS = 0, stepS = 4;
   int ldsS = 0;
   __amdgpu_buffer_rsrc_t rs = buffer_rsrc(act_s, 0);
@@ -1458,7 +1477,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   auto issue = [&](uint8_t* stage, int step) {
     const uint32_t ks = static_cast<uint32_t>(step) * 128;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < MT; ++j)
       if (liveA[j]) buffer_dma16(ra, offA[j] + ks, stage + (wave + 8 * j) * 8 * 128);
 #pragma unroll
     for (int j = 0; j < 4; ++j) buffer_dma16(rb, offB[j] + ks, stage + P::kOffB + (wave + 8 * j) * 8 * 128);
@@ -1466,7 +1485,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   };
   // Padding routes close a block, so a wave whose first route is padding
   // holds none.
-  const bool wave_live = sorted[base + wm * 64] < numel;
+  const bool wave_live = sorted[base + wm * P::WTM] < numel;
 
   v4f acc[MT][NT];
 #pragma unroll
@@ -1485,12 +1504,12 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
       sb0 = lds_load<float>(st, P::kOffSB + (W13 ? 0 : 4 * wn));
       sb1 = W13 ? lds_load<float>(st, P::kOffSB + 4) : sb0;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) sa[mt] = lds_load<float>(st, P::kOffSA + (wm * 64 + mt * 16 + li) * 4);
+      for (int mt = 0; mt < MT; ++mt) sa[mt] = lds_load<float>(st, P::kOffSA + (wm * P::WTM + mt * 16 + li) * 4);
     }
     v8i wf[2], x[MT];
     wf[0] = lds_frag(st + P::kOffB, nw + li, lg);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) x[mt] = lds_frag(st, wm * 64 + mt * 16 + li, lg);
+    for (int mt = 0; mt < MT; ++mt) x[mt] = lds_frag(st, wm * P::WTM + mt * 16 + li, lg);
     __builtin_amdgcn_sched_barrier(0);
     v4f t[2];
     constexpr int NI = MT * NT;
@@ -1533,7 +1552,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     for (int mt = 0; mt < MT; ++mt) {
       rw[mt] = 1.0f;
       if (route_w) {
-        const int r = sorted[base + wm * 64 + mt * 16 + li];
+        const int r = sorted[base + wm * P::WTM + mt * 16 + li];
         rw[mt] = r < numel ? route_w[r] : 0.0f;
       }
     }
@@ -1541,7 +1560,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
       uint16_t* a2b = reinterpret_cast<uint16_t*>(a2);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int64_t row = base + wm * 64 + mt * 16 + li;
+        const int64_t row = base + wm * P::WTM + mt * 16 + li;
 #pragma unroll
         for (int q = 0; q < NT / 2; ++q) {
           float o[4];
@@ -1570,13 +1589,13 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
         }
       amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
       amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
-      if (lg == 0) red[wn * BM + wm * 64 + mt * 16 + li] = amax;
+      if (lg == 0) red[wn * BM + wm * P::WTM + mt * 16 + li] = amax;
     }
     __syncthreads();
     const int gpr = I / 128;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int ml = wm * 64 + mt * 16 + li;
+      const int ml = wm * P::WTM + mt * 16 + li;
       const float amax = fmaxf(1e-10f, fmaxf(red[ml], red[BM + ml]));
       const float scale = amax / 448.0f;
       const int64_t row = base + ml;
@@ -1601,7 +1620,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     uint8_t* yt = smem_dyn;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int row = wm * 64 + mt * 16 + li;
+      const int row = wm * P::WTM + mt * 16 + li;
       const int r = sorted[base + row];
       const float rw = r < numel && route_w ? route_w[r] : 1.0f;
 #pragma unroll
@@ -2016,17 +2035,26 @@ static int raise_dma_lds() {
   return VMAMD_OK;
 }
 
-template <int KIND, bool W13>
+template <int KIND, bool W13, int MTV>
 static int raise_big_lds() {
   static bool done = false;
   if (done) return VMAMD_OK;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_big_kernel<KIND, W13>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, BigTile::kLds) != hipSuccess) {
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_big_kernel<KIND, W13, MTV>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, MoeBigTile<MTV>::kLds) != hipSuccess) {
     set_error("moe gemm: cannot raise the LDS limit of the grouped GEMM kernel");
     return VMAMD_ERR_HIP;
   }
   done = true;
   return VMAMD_OK;
+}
+
+// moe_big_kernel with m-tiles of 16 * MTV routes per wave (block size 64 * MTV).
+template <int KIND, bool W13, int MTV, typename... Args>
+static int launch_big(int tiles, hipStream_t st, Args... args) {
+  int rc = raise_big_lds<KIND, W13, MTV>();
+  if (rc) return rc;
+  moe_big_kernel<KIND, W13, MTV><<<xcd_grid(tiles), MoeBigTile<MTV>::kThreads, MoeBigTile<MTV>::kLds, st>>>(args...);
+  return check_launch(W13 ? "moe w13 (gemm)" : "moe w2 (gemm)");
 }
 
 // The 256-route kernels read activations, scales and each expert's weights
@@ -2189,17 +2217,22 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
                                    native);
   }
   if constexpr (KIND == kFp8 || KIND == kBf16) {
-    if (block_m == kMoeBigBM) {
+    if (block_m == kMoeBigBM || block_m == kMoeBig320) {
       constexpr int eb = KIND == kBf16 ? 2 : 1;  // bytes per element
       VMAMD_REQUIRE(big_fits(T, H * eb, 2ll * I, E), "moe w13: operands past 2 GiB for the 256-route GEMM");
-      const int tiles = static_cast<int>((cap + kMoeBigBM - 1) / kMoeBigBM) * (I / 128);
-      int rc = raise_big_lds<KIND, true>();
-      if (rc) return rc;
-      moe_big_kernel<KIND, true><<<xcd_grid(tiles), BigTile::kThreads, BigTile::kLds, st>>>(
-          xa, static_cast<int>(static_cast<int64_t>(T) * H * eb), xs, static_cast<int>(static_cast<int64_t>(T) * (H / 128) * 4),
-          topk, H, sorted, offs, ntpp, eids, E, numel, tiles, w13, static_cast<const float*>(w13_s), 2 * I, I, limit,
-          route_w, a2, a2s, nullptr);
-      return check_launch("moe w13 (gemm)");
+      const int tiles = static_cast<int>((cap + block_m - 1) / block_m) * (I / 128);
+      const int abytes = static_cast<int>(static_cast<int64_t>(T) * H * eb);
+      const int sbytes = static_cast<int>(static_cast<int64_t>(T) * (H / 128) * 4);
+      const float* ws13 = static_cast<const float*>(w13_s);
+      if (block_m == kMoeBig320) {
+        if constexpr (KIND == kBf16)
+          return launch_big<KIND, true, 5>(tiles, st, xa, abytes, xs, sbytes, topk, static_cast<int>(H), sorted, offs,
+                                           ntpp, eids, E, numel, tiles, w13, ws13, 2 * I, I, limit, route_w, a2, a2s,
+                                           static_cast<uint16_t*>(nullptr));
+      }
+      return launch_big<KIND, true, 4>(tiles, st, xa, abytes, xs, sbytes, topk, static_cast<int>(H), sorted, offs, ntpp,
+                                       eids, E, numel, tiles, w13, ws13, 2 * I, I, limit, route_w, a2, a2s,
+                                       static_cast<uint16_t*>(nullptr));
     }
   }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
@@ -2273,16 +2306,21 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
     return check_launch("moe w2 (reduce)");
   }
   if constexpr (KIND == kFp8 || KIND == kBf16) {
-    if (block_m == kMoeBigBM) {
+    if (block_m == kMoeBigBM || block_m == kMoeBig320) {
       constexpr int eb = KIND == kBf16 ? 2 : 1;  // bytes per element
       VMAMD_REQUIRE(big_fits(cap, I * eb, H, E), "moe w2: operands past 2 GiB for the 256-route GEMM");
-      const int tiles = static_cast<int>((cap + kMoeBigBM - 1) / kMoeBigBM) * ((H + 255) / 256);
-      int rc = raise_big_lds<KIND, false>();
-      if (rc) return rc;
-      moe_big_kernel<KIND, false><<<xcd_grid(tiles), BigTile::kThreads, BigTile::kLds, st>>>(
-          a2, static_cast<int>(cap * I * eb), a2s, static_cast<int>(cap * (I / 128) * 4), 1, I, sorted, offs, ntpp, eids, E,
-          numel, tiles, w2, static_cast<const float*>(w2_s), H, I, 0.f, route_w, nullptr, nullptr, y);
-      return check_launch("moe w2 (gemm)");
+      const int tiles = static_cast<int>((cap + block_m - 1) / block_m) * ((H + 255) / 256);
+      const int abytes = static_cast<int>(cap * I * eb), sbytes = static_cast<int>(cap * (I / 128) * 4);
+      const float* ws2 = static_cast<const float*>(w2_s);
+      uint8_t* const none8 = nullptr;
+      float* const nonef = nullptr;
+      if (block_m == kMoeBig320) {
+        if constexpr (KIND == kBf16)
+          return launch_big<KIND, false, 5>(tiles, st, a2, abytes, a2s, sbytes, 1, I, sorted, offs, ntpp, eids, E,
+                                            numel, tiles, w2, ws2, H, I, 0.f, route_w, none8, nonef, y);
+      }
+      return launch_big<KIND, false, 4>(tiles, st, a2, abytes, a2s, sbytes, 1, I, sorted, offs, ntpp, eids, E, numel,
+                                        tiles, w2, ws2, H, I, 0.f, route_w, none8, nonef, y);
     }
   }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
@@ -2413,24 +2451,45 @@ static int fused_direct(bool qx, const uint8_t* xa, const float* xs, const float
 // -1 % / -6 %, T=6144 -8 % / -10 %, T=8192 -2 % / -10 %; bf16 (E=128,
 // H=2048, I=768, top-8) T=2048 -7 % / -10 %, T=4096 -12 % / 0, T=8192
 // -10 % / -17 %.
+// bf16 takes 320-route blocks where the expected largest expert, mean +
+// 3 sqrt(mean) routes, needs fewer of them than of 256-route blocks, each
+// 320-route block counted 1.25x (its share of the work when blocks are
+// full).  bf16 (E=128, H=2048, I=768, top-8), W13 + W2 stages, 256 vs 320
+// routes per block: T=1024 325 / 354 µs, T=2048 345 / 370, T=3072 364 / 396,
+// T=4096 (mean 256) 512 / 423, T=6144 621 / 719, T=8192 (mean 512) 797 /
+// 727, T=16384 1367 / 1418: the rule takes 320 at T=4096 and 8192 only.
+// Results are bitwise equal either way.
+static int bf16_big_block(int64_t routes, int E) {
+  const double mean = static_cast<double>(routes) / E;
+  const double top = mean + 3.0 * std::sqrt(mean);
+  const double b256 = std::ceil(top / kMoeBigBM), b320 = std::ceil(top / kMoeBig320);
+  return 1.25 * b320 < b256 ? kMoeBig320 : kMoeBigBM;
+}
+
 static int moe_block_m(int64_t T, int topk, int E, int path, int kind) {
   if (path == VMAMD_MOE_PATH_GEMV || path == VMAMD_MOE_PATH_NATIVE_GEMV || kind == kW8A16) return kGemvBlock;
   const int64_t routes = T * topk;
-  const int grouped = kind != kW4 && routes >= 128 * static_cast<int64_t>(E) ? kMoeBigBM : kMoeBM;
+  const int big = kind == kBf16 ? bf16_big_block(routes, E) : kMoeBigBM;
+  const int grouped = kind != kW4 && routes >= 128 * static_cast<int64_t>(E) ? big : kMoeBM;
   if (path == VMAMD_MOE_PATH_GEMM) return grouped;
   const int64_t limit = kind == kFp8 ? (5 * static_cast<int64_t>(E)) / 2 : 12 * static_cast<int64_t>(E);
   return routes <= limit ? kGemvBlock : grouped;
 }
 
-static int check_stage_common(const char* who, int64_t T, int topk, int E, int64_t H, int64_t I,
-                              int block_m, int64_t cap) {
+static int check_stage_common(const char* who, int kind, int64_t T, int topk, int E, int64_t H,
+                              int64_t I, int block_m, int64_t cap) {
   VMAMD_REQUIRE(T >= 0 && topk > 0 && E > 0 && E <= 1024, "%s: bad sizes (T=%lld topk=%d E=%d)",
                 who, (long long)T, topk, E);
   VMAMD_REQUIRE(H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0,
                 "%s: hidden (%lld) and intermediate (%lld) sizes must be multiples of 128", who,
                 (long long)H, (long long)I);
-  VMAMD_REQUIRE(block_m == kGemvBlock || block_m == kMoeBM || block_m == kMoeBigBM,
-                "%s: block_m must be %d, %d or %d (got %d)", who, kGemvBlock, kMoeBM, kMoeBigBM, block_m);
+  VMAMD_REQUIRE(block_m == kGemvBlock || block_m == kMoeBM || block_m == kMoeBigBM || block_m == kMoeBig320,
+                "%s: block_m must be %d, %d, %d or %d (got %d)", who, kGemvBlock, kMoeBM, kMoeBigBM, kMoeBig320,
+                block_m);
+  VMAMD_REQUIRE(block_m != kMoeBig320 || kind == kBf16, "%s: block_m %d is for bf16 weights only", who,
+                kMoeBig320);
+  VMAMD_REQUIRE(block_m != kMoeBigBM || kind == kFp8 || kind == kBf16, "%s: block_m %d needs fp8 or bf16 weights",
+                who, kMoeBigBM);
   VMAMD_REQUIRE(T * topk < (1ll << 30) && T * H < (1ll << 40), "%s: problem too large", who);
   VMAMD_REQUIRE(block_m != kGemvBlock || (T * H * 2 < (1ll << 31) && T * topk * I * 2 < (1ll << 31)),
                 "%s: the decode path (block_m 16) takes activations below 2 GiB", who);
@@ -2458,7 +2517,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
                 who);
   const int bm = moe_block_m(T, topk, E, path, KIND);
   const int64_t cap = T * topk + static_cast<int64_t>(E) * (bm - 1);
-  int rc = check_stage_common(who, T, topk, E, H, I, bm, cap);
+  int rc = check_stage_common(who, KIND, T, topk, E, H, I, bm, cap);
   if (rc) return rc;
   VMAMD_REQUIRE(KIND != kW4 || (H <= 16384 && I <= 16384),
                 "%s: per-row quantisation supports rows of up to 16384", who);
@@ -2585,7 +2644,7 @@ static int stage_w13(const char* who, const void* xa, const float* xs, int64_t T
                      const int32_t* ntpp, const int32_t* active, const int32_t* nact,
                      const void* w13, const void* w13_s, int E, int64_t I, float limit, void* a2,
                      float* a2s, void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
-  int rc = check_stage_common(who, T, topk, E, H, I, block_m, capacity);
+  int rc = check_stage_common(who, KIND, T, topk, E, H, I, block_m, capacity);
   if (rc) return rc;
   if (T == 0) return VMAMD_OK;
   VMAMD_REQUIRE(xa && sorted && offs && ntpp && w13 && a2 &&
@@ -2613,7 +2672,7 @@ static int stage_w2(const char* who, const void* a2, const float* a2s, int64_t T
                     const void* w2_s, int E, int64_t H, int64_t I, const float* topk_weights,
                     const int32_t* topk_ids, const int32_t* emap, int64_t emap_len, void* y,
                     void* workspace, size_t workspace_bytes, vmamd_stream_t stream) {
-  int rc = check_stage_common(who, T, topk, E, H, I, block_m, capacity);
+  int rc = check_stage_common(who, KIND, T, topk, E, H, I, block_m, capacity);
   if (rc) return rc;
   if (T == 0) return VMAMD_OK;
   VMAMD_REQUIRE(a2 && sorted && offs && ntpp && w2 && topk_ids && y &&
@@ -2626,7 +2685,7 @@ static int stage_w2(const char* who, const void* a2, const float* a2s, int64_t T
                 "%s: workspace of %zu bytes required (got %zu)", who, need, workspace_bytes);
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(a2) % 16 == 0 &&
-                    reinterpret_cast<uintptr_t>(y) % (block_m == kMoeBigBM ? 16 : 8) == 0,
+                    reinterpret_cast<uintptr_t>(y) % (block_m >= kMoeBigBM ? 16 : 8) == 0,
                 "%s: a2 and workspace must be 16-byte aligned, y 8-byte (16-byte for block_m %d)", who,
                 kMoeBigBM);
   return launch_w2<KIND>(static_cast<const uint8_t*>(a2), a2s, nullptr, static_cast<int>(T), topk, sorted,

@@ -10,6 +10,8 @@ kernels on the current stream; Python only validates and allocates.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _custom_ops as ops
@@ -233,6 +235,16 @@ def _run_chunked(x, ids, wts, out, chunk, size, launch):
         launch(x[c0:c1], ids[c0:c1], wts[c0:c1], out[c0:c1], ws, nbytes)
 
 
+def _bf16_big_block(routes: int, experts: int) -> int:
+    """The large route block of the bf16 grouped GEMMs: 320 where it needs
+    fewer blocks for the expected largest expert (mean + 3 sqrt(mean)
+    routes) than 256, each 320-route block counted 1.25x, else 256 -- the
+    rule of bf16_big_block (csrc/moe_gemm.hip)."""
+    mean = routes / experts
+    top = mean + 3.0 * math.sqrt(mean)
+    return 320 if 1.25 * math.ceil(top / 320) < math.ceil(top / 256) else 256
+
+
 class MoeStages:
     """One MoE layer as its separate launches, in the order the fused call
     enqueues them: ``quant`` (1x128 of x; fp8 only), ``align``
@@ -263,11 +275,15 @@ class MoeStages:
         # 2.5 routes per expert for fp8, 12 for bf16 (measured crossovers).
         limit = (5 * self.e) // 2 if self.fp8 else 12 * self.e
         gemv = path == "gemv" or (path == "auto" and numel <= limit)
-        # grouped GEMMs: 256-route blocks from 128 routes per expert
-        self.block_m = 16 if gemv else 256 if numel >= 128 * self.e else 128
-        if block_m is not None:  # the grouped GEMMs' route tile: 128 or 256
-            if gemv or block_m not in (128, 256):
-                raise ValueError(f"block_m {block_m} needs the grouped GEMMs (128 or 256)")
+        # grouped GEMMs: large route blocks from 128 routes per expert (256, or
+        # 320 for bf16 where that needs fewer blocks: bf16_big_block in
+        # csrc/moe_gemm.hip)
+        big = 256 if self.fp8 else _bf16_big_block(numel, self.e)
+        self.block_m = 16 if gemv else big if numel >= 128 * self.e else 128
+        if block_m is not None:  # the grouped GEMMs' route tile
+            allowed = (128, 256) if self.fp8 else (128, 256, 320)
+            if gemv or block_m not in allowed:
+                raise ValueError(f"block_m {block_m} needs the grouped GEMMs {allowed}")
             self.block_m = block_m
         self.w13, self.w2 = w13.contiguous(), w2.contiguous()
         if self.fp8:
