@@ -306,6 +306,39 @@ def test_block_fp8_big_split_plan_on_128_row_tiles():
     assert d <= 2 ** -7 * usual.float().abs().max().item()
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 7168, 2048), (512, 7168, 2048), (128, 2112, 7168),
+                                   (200, 2112, 7168), (128, 24576, 1536)])
+def test_block_fp8_gemm_128_column_tiles(M, N, K):
+    """Mid-size M on small N, where the time model takes 128 x 128 tiles
+    (unsplit at 512 x 7168 x 2048 and 128 x 24576 x 1536, whose workspace
+    query is 0; split over K elsewhere), including a last column tile half
+    outside N = 2112 and a ragged M = 200: every output against the oracle,
+    a repeat call bitwise equal, and the call without a workspace (unsplit)
+    equal to the fp32 summation order."""
+    from vllm_musa_amd import _lib, synthetic
+    from vllm_musa_amd._lib import call, ptr, stream_of
+    from vllm_musa_amd.block_fp8 import w8a8_block_fp8_matmul
+    from vllm_musa_amd.fp8_utils import per_token_group_quant_fp8
+    nbytes = _lib.load().vmamd_w8a8_block_fp8_matmul_workspace_size(M, N, K)
+    if (M, N, K) in ((512, 7168, 2048), (128, 24576, 1536)):
+        assert nbytes == 0
+    w, ws = synthetic.dense_fp8_weight(N, K, 91)
+    xq, xs = per_token_group_quant_fp8(synthetic.activations(M, K, 92 + M), 128)
+    out = w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128])
+    assert torch.equal(out, w8a8_block_fp8_matmul(xq, w, xs, ws, [128, 128]))
+    ref = block_fp8_matmul_sampled(xq.view(torch.uint8).cpu().numpy(), xs.cpu().numpy(),
+                                   w.view(torch.uint8).cpu().numpy(), ws.cpu().numpy(),
+                                   np.arange(M), np.arange(N))
+    _check(out.float().cpu().numpy(), ref)
+    unsplit = torch.empty(M, N, dtype=torch.bfloat16, device=xq.device)
+    call("vmamd_w8a8_block_fp8_matmul", ptr(xq), ptr(xs), xs.stride(0), xs.stride(1), ptr(w), ptr(ws),
+         ptr(unsplit), M, N, K, 128, 128, None, 0, stream_of(xq))
+    if nbytes == 0:
+        assert torch.equal(unsplit, out)
+    d = (unsplit.float() - out.float()).abs().max().item()
+    assert d <= 2 ** -7 * out.float().abs().max().item()
+
+
 @pytest.mark.parametrize("M,N,K", [(40, 2112, 7168), (200, 2112, 7168)])
 def test_block_fp8_gemm_without_workspace(M, N, K):
     """Through the C ABI with a NULL workspace where the plan wants one: the

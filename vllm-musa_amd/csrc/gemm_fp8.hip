@@ -31,14 +31,17 @@ namespace vmamd {
 // blockIdx.y takes K steps [blockIdx.y * kper, +kper) and, with `partial`
 // set, stores its fp32 tile at partial[blockIdx.y][M][N] for
 // splitk_reduce_kernel; without it, the bf16 tile at C.
+// DensePipeN: the same kernel on 128 x 128 tiles (8 waves of 64 x 32), for
+// mid-size M on small N, where 128 x 256 tiles are too few for the CUs.
 using DensePipe = TilePipe<true, 128, 256, 2, 4, 3>;
+using DensePipeN = TilePipe<true, 128, 128, 2, 4, 3>;
 
-__global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
+template <typename P>
+__global__ __launch_bounds__(P::kThreads, 1) void gemm_fp8_dma_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t as_sm, int64_t as_sk,
     const uint8_t* __restrict__ B, const float* __restrict__ Bs, uint16_t* __restrict__ C, int M,
     int N, int K, int TM, int TN, int kper, float* __restrict__ partial) {
-  using P = DensePipe;
-  constexpr int NS = 3, BM = 128, BN = 256, WN = 4;
+  constexpr int NS = 3, BM = P::kBM, BN = P::kBN, WN = P::kWN;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
   int tm, tn;
   if (!xcd_tile(blockIdx.x, TM, TN, tm, tn)) return;
@@ -95,7 +98,7 @@ __global__ __launch_bounds__(DensePipe::kThreads, 1) void gemm_fp8_dma_kernel(
     float sa[P::MT], sb;
   };
   auto read = [&](const uint8_t* st, Frags& f) {
-    f.sb = lds_load<float>(st, P::kOffSB + (wn / 2) * 4);
+    f.sb = lds_load<float>(st, P::kOffSB + (wn * P::WTN / 128) * 4);  // the wave's 128-row scale block
 #pragma unroll
     for (int mt = 0; mt < P::MT; ++mt) {
       f.sa[mt] = lds_load<float>(st, P::kOffSA + (wm * P::WTM + mt * 16 + li) * 4);
@@ -682,11 +685,12 @@ static int device_cus() {
 // 8091 us.  Returns the K steps per split.
 constexpr int64_t kSplitKMaxBytes = 256ll << 20;
 // step: the modelled time of one K step of the tile relative to the 128 x 256
-// tile's (the 256 x 256 tile: kBigStep); min_per: K steps a split keeps at
-// least.  *cost_out: the model's time (us).
+// tile's (the 256 x 256 tile: kBigStep, the 128 x 128 tile: kNarrowStep);
+// min_per: K steps a split keeps at least; bn: the tile's columns.
+// *cost_out: the model's time (us).
 static int gemm_kper(int M, int N, int K, int bm = 128, double step = 1.0, double* cost_out = nullptr,
-                     int min_per = 4) {
-  const int64_t T = static_cast<int64_t>((M + bm - 1) / bm) * ((N + 255) / 256), KS = K / 128;
+                     int min_per = 4, int bn = 256) {
+  const int64_t T = static_cast<int64_t>((M + bm - 1) / bm) * ((N + bn - 1) / bn), KS = K / 128;
   const int64_t cus = device_cus(), xcd_cus = max(1, static_cast<int>(cus / kXcds));
   const int64_t per_xcd = (T + kXcds - 1) / kXcds;
   auto gemm_us = [&](int64_t se, int64_t per) {
@@ -722,6 +726,16 @@ static int gemm_kper(int M, int N, int K, int bm = 128, double step = 1.0, doubl
 // 37.1 -> 44.0 us with splits of 4-8 steps).
 constexpr double kBigStep = 512.0 / 384.0;
 constexpr int kBigMinSteps = 32;
+// K step of the 128 x 128 tile (DensePipeN) against the 128 x 256 tile's:
+// (128 + 128) / (128 + 256).  With it the model takes the narrow tiles
+// where they measured faster on MI355X (7 shapes x M = 64..2048, none
+// slower: 7168 x 2048 at M = 128 / 256 / 512 21.5 / 24.2 / 28.4 -> 17.4 /
+// 18.9 / 19.7 µs, 24576 x 1536 at M = 128 25.0 -> 18.5, 2112 x 7168 at
+// M = 128 / 256 23.6 / 26.5 -> 19.2 / 22.3, 4096 x 7168 at M = 128
+// 26.0 -> 21.4), and leaves long K (7168 x 16384 / 18432) and large M on
+// 128 x 256 tiles, where those measured faster; a smaller factor (0.6)
+// also takes 24576 x 1536 at M = 512, measured 30 % slower there.
+constexpr double kNarrowStep = 256.0 / 384.0;
 
 // The dense path for an M x N x K product: the GEMV up to M = 16, and up to
 // M = 32 / 64 unless the split GEMM is faster there -- weights of 96 MiB and
@@ -736,6 +750,7 @@ constexpr int kBigMinSteps = 32;
 struct DensePlan {
   bool gemv, big;
   int kper, splits;
+  int bn;  // column width of the 128-row tiles: 256, or 128 (DensePipeN)
 };
 static DensePlan dense_plan(int M, int N, int K) {
   DensePlan d;
@@ -743,6 +758,7 @@ static DensePlan dense_plan(int M, int N, int K) {
   const bool heavy = static_cast<int64_t>(N) * K >= (96ll << 20);
   d.gemv = M <= 16 || (M <= 32 && !heavy) || (M <= kGemvMaxM && K < 4096 && !heavy);
   d.big = false;
+  d.bn = 256;
   double cost = 0.0;
   d.kper = d.gemv ? KS : gemm_kper(M, N, K, 128, 1.0, &cost);
   if (!d.gemv && d.kper < KS && M >= 512) {
@@ -751,6 +767,16 @@ static DensePlan dense_plan(int M, int N, int K) {
     if (kper_big < KS && cost_big < cost) {
       d.big = true;
       d.kper = kper_big;
+      cost = cost_big;
+    }
+  }
+  if (!d.gemv) {
+    double cost_n = 0.0;
+    const int kper_n = gemm_kper(M, N, K, 128, kNarrowStep, &cost_n, 4, 128);
+    if (cost_n < cost) {
+      d.big = false;
+      d.bn = 128;
+      d.kper = kper_n;
     }
   }
   d.splits = (KS + d.kper - 1) / d.kper;
@@ -833,6 +859,28 @@ extern "C" size_t vmamd_w8a8_block_fp8_matmul_workspace_size(int64_t M, int64_t 
   return w8a8_workspace_bytes(M, N, K);
 }
 
+namespace vmamd {
+// gemm_fp8_dma_kernel on pipe P: TM x TN tiles, `splits` K ranges of kper steps.
+template <typename P>
+static int launch_tile(const uint8_t* a, const float* As, int64_t as_sm, int64_t as_sk, const uint8_t* b,
+                       const float* Bs, uint16_t* c, int m, int n, int k, int kper, int splits, float* partial,
+                       hipStream_t st) {
+  static bool lds_raised = false;
+  if (!lds_raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_fp8_dma_kernel<P>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, P::kLds) != hipSuccess) {
+      set_error("w8a8_block_fp8_matmul: cannot raise the LDS limit of the GEMM kernel");
+      return VMAMD_ERR_HIP;
+    }
+    lds_raised = true;
+  }
+  const int TM = (m + P::kBM - 1) / P::kBM, TN = (n + P::kBN - 1) / P::kBN;
+  gemm_fp8_dma_kernel<P><<<dim3(xcd_grid(TM * TN), splits), P::kThreads, P::kLds, st>>>(
+      a, As, as_sm, as_sk, b, Bs, c, m, n, k, TM, TN, kper, partial);
+  return VMAMD_OK;
+}
+}  // namespace vmamd
+
 extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64_t as_stride_m,
                                            int64_t as_stride_k, const void* B, const float* Bs,
                                            void* C, int64_t M, int64_t N, int64_t K, int block_n,
@@ -898,7 +946,7 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
     const int64_t as_extent = ((m - 1) * as_stride_m + (k / 128 - 1) * as_stride_k + 1) * 4;
     const bool big_ok = static_cast<int64_t>(m + 256) * k < (1ll << 31) &&
                         static_cast<int64_t>(n + 256) * k < (1ll << 31) && as_extent < (1ll << 31);
-    if (plan.splits == 1 && use_big_gemm(m, n, k, as_extent))
+    if (plan.splits == 1 && plan.bn == 256 && use_big_gemm(m, n, k, as_extent))
       return launch_big(a, As, as_stride_m, as_stride_k, static_cast<int>(as_extent), b, Bs, c, m, n, k, st);
     if (plan.splits > 1 && plan.big && big_ok)
       return launch_big(a, As, as_stride_m, as_stride_k, static_cast<int>(as_extent), b, Bs, c, m, n, k, st,
@@ -916,21 +964,14 @@ extern "C" int vmamd_w8a8_block_fp8_matmul(const void* A, const float* As, int64
     plan.kper = static_cast<int>(kper);
     plan.splits = static_cast<int>((KS + kper - 1) / kper);
   }
-  static bool lds_raised = false;
-  if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_fp8_dma_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, DensePipe::kLds) != hipSuccess) {
-      set_error("w8a8_block_fp8_matmul: cannot raise the LDS limit of the GEMM kernel");
-      return VMAMD_ERR_HIP;
-    }
-    lds_raised = true;
-  }
-  const int TM = (m + 127) / 128, TN = (n + 255) / 256;
   const int kper = plan.kper, splits = plan.splits;
   VMAMD_REQUIRE(splits >= 1 && splits <= 16, "w8a8_block_fp8_matmul: %d K splits planned", splits);
   float* partial = splits > 1 ? static_cast<float*>(workspace) : nullptr;
-  gemm_fp8_dma_kernel<<<dim3(xcd_grid(TM * TN), splits), DensePipe::kThreads, DensePipe::kLds, st>>>(
-      a, As, as_stride_m, as_stride_k, b, Bs, c, m, n, k, TM, TN, kper, partial);
+  const int rc = plan.bn == 128 ? launch_tile<DensePipeN>(a, As, as_stride_m, as_stride_k, b, Bs, c, m, n, k, kper,
+                                                          splits, partial, st)
+                                : launch_tile<DensePipe>(a, As, as_stride_m, as_stride_k, b, Bs, c, m, n, k, kper,
+                                                         splits, partial, st);
+  if (rc) return rc;
   if (splits > 1) splitk_reduce(partial, splits, static_cast<int64_t>(m) * n, c, st);
   return check_launch("w8a8_block_fp8_matmul(gemm)");
 }

@@ -83,6 +83,7 @@ struct BigTile {
 
 template <bool SCALED, int BM, int BN, int WM, int WN, int NS>
 struct TilePipe {
+  static constexpr int kBM = BM, kBN = BN, kWN = WN;  // the tile and the waves across N
   static constexpr int kWaves = WM * WN, kThreads = kWaves * kWave;
   static constexpr int WTM = BM / WM, WTN = BN / WN, MT = WTM / 16, NT = WTN / 16;
   static constexpr int kOffB = BM * 128;
