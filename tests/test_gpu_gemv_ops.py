@@ -314,9 +314,12 @@ def test_native_gemv_layer_matches_oracle(e, i, h, k, t):
     _check(out, _layer_oracle(x, w13, s13, w2, s2, w, ids))
 
 
-def test_native_gemv_layer_input_weight_and_limit():
+@pytest.mark.parametrize("t", [6, 1])
+def test_native_gemv_layer_input_weight_and_limit(t):
+    """T=1 runs the direct route slots, whose W13 launch writes the
+    activation itself."""
     from vllm_musa_amd.fused_moe import fused_experts_impl
-    x, w13, s13, w2, s2, w, ids = _layer_case(64, 256, 1024, 4, 6, 90)
+    x, w13, s13, w2, s2, w, ids = _layer_case(64, 256, 1024, 4, t, 90)
     x = x * 30
     out = fused_experts_impl(x, w13, w2, w, ids, use_fp8_w8a8=True, w1_scale=s13, w2_scale=s2,
                              block_shape=[128, 128], apply_router_weight_on_input=True,

@@ -190,11 +190,27 @@ constexpr bool gemv_stream1() { return MAXB == 1 && (KIND != kW4 || VS); }
 // separate quantiser launch.
 // kGemvDense (a plain GEMV, one expert): every row of act is a route of
 // expert 0 in route-blocks of 16 consecutive rows; no alignment, no ids.
-constexpr int kGemvGrouped = 0, kGemvDirect = 1, kGemvCombine = 2, kGemvDirectQ = 3, kGemvDense = 4;
+// kGemvDirectAct (kBf16 / kW8A16 W13, one token): the workgroup is one
+// 16-column tile j of the activation for one route slot; wave w computes
+// split w % splits of the gate rows (w < splits) or the up rows, the
+// partials meet in LDS and are summed in split order -- the order of the
+// activation kernels -- so the bf16 activation row is written by the W13
+// launch itself, no partials and no activation launch.
+constexpr int kGemvGrouped = 0, kGemvDirect = 1, kGemvCombine = 2, kGemvDirectQ = 3, kGemvDense = 4,
+              kGemvDirectAct = 5;
 constexpr int kMaxCombineSlots = 16;
 // kW8A16 holds twice the activation registers: its combine workgroups take
 // at most 8 slots, so that 256 VGPRs stay available.
 constexpr int combine_slots(int kind) { return kind == kW8A16 ? 8 : kMaxCombineSlots; }
+// Workgroup size bound of a mode: the combine one wave per slot, the fused
+// activation two per split (kBf16 up to 8 splits; kW8A16, with twice the
+// activation registers, up to 4).
+constexpr int gemv_waves(int mode, int kind) {
+  return mode == kGemvCombine ? combine_slots(kind) : mode == kGemvDirectAct ? (kind == kW8A16 ? 8 : 16) : kMoeGemvWaves;
+}
+constexpr int gemv_min_blocks(int mode, int maxb, int kind) {
+  return mode == kGemvDirectAct ? 1 : (maxb == 1 && kind != kW8A16 ? 3 : 2);
+}
 
 // Local expert of a route, -1 when it is dropped (negative id, not mapped,
 // or past the local experts) -- the rule of the alignment and of moe_sum.
@@ -206,8 +222,7 @@ __device__ __forceinline__ int route_expert(const int32_t* __restrict__ ids, int
 }
 
 template <int MAXB, int KIND, bool VS = false, int MODE = kGemvGrouped>
-__global__ __launch_bounds__((MODE == kGemvCombine ? combine_slots(KIND) : kMoeGemvWaves) * kWave,
-                  MAXB == 1 && KIND != kW8A16 ? 3 : 2) void
+__global__ __launch_bounds__(gemv_waves(MODE, KIND) * kWave, gemv_min_blocks(MODE, MAXB, KIND)) void
 moe_gemv_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int act_div,
     int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
@@ -215,7 +230,8 @@ moe_gemv_kernel(
     const uint8_t* __restrict__ w, const void* __restrict__ ws, int N, int numel, int splits,
     float* __restrict__ partial, const float* __restrict__ route_w, uint16_t* __restrict__ y,
     const int32_t* __restrict__ ids, const int32_t* __restrict__ emap, int64_t emap_len, int E_,
-    uint16_t* __restrict__ comb, const float* __restrict__ comb_w, float* __restrict__ xs_out) {
+    uint16_t* __restrict__ comb, const float* __restrict__ comb_w, float* __restrict__ xs_out,
+    float act_limit, int act_native) {
   using KB_ = KindBytes<KIND>;
   using AF = typename KindOps<KIND>::AFrag;
   constexpr bool kActS = KindOps<KIND>::kActScale, kBlkS = KindOps<KIND>::kBlockScale;
@@ -226,14 +242,20 @@ moe_gemv_kernel(
   constexpr bool kQx = MODE == kGemvDirectQ;
   static_assert(!kQx || ((KIND == kFp8 || KIND == kW4) && VS && kStream1),
                 "in-workgroup x quantiser: fp8 / w4, vector scales");
+  constexpr bool kComb = MODE == kGemvCombine, kAct = MODE == kGemvDirectAct;
+  static_assert(!kAct || KIND == kBf16 || KIND == kW8A16, "fused decode activation: bf16 activations");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
   const int li = lane % 16, lg = lane / 16;
-  const int ntile = MODE == kGemvCombine ? static_cast<int>(blockIdx.x) : blockIdx.x * kMoeGemvWaves + wave;
-  // Wave-uniform (workgroup-uniform for kGemvCombine, whose only barrier
-  // comes after it); kGemvDirectQ leaves after its barrier.
+  // kGemvDirectAct: wave -> (gate / up half, split); N / 32 = I / 16 tiles per half.
+  const int act_splits = kAct ? splits : 1;
+  const int ntile = kComb ? static_cast<int>(blockIdx.x)
+                    : kAct ? (wave / act_splits) * (N / 32) + static_cast<int>(blockIdx.x)
+                           : blockIdx.x * kMoeGemvWaves + wave;
+  // Wave-uniform (workgroup-uniform for the combine and kGemvDirectAct,
+  // whose only barrier comes after it); kGemvDirectQ leaves after its barrier.
   if (!kQx && ntile * 16 >= N) return;
-  const int slot = MODE == kGemvCombine ? static_cast<int>(blockIdx.y * (blockDim.x / kWave)) + wave
-                                        : static_cast<int>(blockIdx.y);
+  const int slot = kComb ? static_cast<int>(blockIdx.y * (blockDim.x / kWave)) + wave
+                         : static_cast<int>(blockIdx.y);
   int e;
   bool dead = false;  // kGemvCombine: a dropped route still takes part in the sum's barrier
   if constexpr (MODE == kGemvGrouped) {
@@ -245,12 +267,17 @@ moe_gemv_kernel(
     if (slot >= na || e < 0) return;
   } else if constexpr (MODE == kGemvDense) {
     e = 0;
-  } else if constexpr (MODE == kGemvDirect || MODE == kGemvDirectQ) {
+  } else if constexpr (MODE == kGemvDirect || MODE == kGemvDirectQ || kAct) {
     e = route_expert(ids, slot, emap, emap_len, E_);  // workgroup-uniform
     // kW4: the workgroup that writes the token's row scale runs the quantiser
     // even when its route is dropped.
     const bool writes_xs = KIND == kW4 && kQx && blockIdx.x == 0 && blockIdx.z == 0 && slot % act_div == 0;
-    if (e < 0 && !writes_xs) return;
+    if (e < 0 && !writes_xs) {
+      if constexpr (kAct) {  // a dropped route's activation columns are zeros
+        if (wave == 0 && lane < 16) y[static_cast<int64_t>(slot) * (N / 2) + static_cast<int>(blockIdx.x) * 16 + lane] = 0;
+      }
+      return;
+    }
   } else {
     e = route_expert(ids, slot, emap, emap_len, E_);
     dead = e < 0;
@@ -281,7 +308,7 @@ moe_gemv_kernel(
     }
     if (ntile * 16 >= N) return;
   }
-  const int split = blockIdx.z;
+  const int split = kAct ? wave % act_splits : static_cast<int>(blockIdx.z);
   const int KS = K / KB_::kElems;                    // K steps
   const int arowb = KS * KB_::kAct;
   const int64_t wrowb = static_cast<int64_t>(KS) * KB_::kW;
@@ -561,8 +588,8 @@ moe_gemv_kernel(
       if (b >= nb || rr[b] < 0) continue;
       const int r = rr[b];
       const v4f a = KIND == kW4 ? acc[b] * kW4Unit : acc[b];
-      if constexpr (MODE == kGemvCombine) {
-        break;  // the sum below
+      if constexpr (kComb || kAct) {
+        break;  // the sum / the activation below
       } else if (y) {
         const float rw = route_w ? route_w[r] : 1.0f;
         *reinterpret_cast<uint2*>(y + static_cast<int64_t>(r) * N + n) =
@@ -574,7 +601,43 @@ moe_gemv_kernel(
     }
     b0 += MAXB;
   } while (b0 < nblk);
-  if constexpr (MODE == kGemvCombine) {
+  if constexpr (kAct) {
+    // Gate / up sums over the splits in split order, times route_w (null:
+    // times 1, exact), then the activation of the decode activation kernels:
+    // act_native the reference GEMV's (fp32 through the SwiGLU, one rounding),
+    // otherwise swiglu_bf16 on the bf16-rounded gate and up.
+    __shared__ float apart[gemv_waves(kGemvDirectAct, KIND) * 16];
+    if (li == 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) apart[wave * 16 + 4 * lg + q] = acc[0][q];
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+      float g = apart[lane], u = apart[act_splits * 16 + lane];
+      for (int s = 1; s < act_splits; ++s) {
+        g += apart[s * 16 + lane];
+        u += apart[(act_splits + s) * 16 + lane];
+      }
+      const int I = N / 2;
+      float v;
+      if (act_native) {
+        if (route_w) {
+          g *= route_w[slot];
+          u *= route_w[slot];
+        }
+        if (act_limit > 0.f) {
+          g = fminf(g, act_limit);
+          u = fminf(fmaxf(u, -act_limit), act_limit);
+        }
+        v = g * (1.0f / (1.0f + expf(-g))) * u;
+      } else {
+        const float sc = route_w ? route_w[slot] : 1.0f;
+        v = swiglu_bf16(bf16r(g * sc), bf16r(u * sc), act_limit);
+      }
+      y[static_cast<int64_t>(slot) * I + static_cast<int>(blockIdx.x) * 16 + lane] = f32_to_bf16(v);
+    }
+  }
+  if constexpr (kComb) {
     // y_k = bf16(acc * route_w[k]) for the 16 rows (lanes of column 0), as
     // the per-route epilogue above; then the layer output = bf16 of the fp32
     // sum over the live slots in slot order, y_k times comb_w[k] by one fma
@@ -2086,19 +2149,19 @@ static void launch_gemv(dim3 grid, hipStream_t st, bool one_block, bool vs, Args
   if constexpr (KIND != kBf16) {
     if (vs) {
       if (one_block)
-        moe_gemv_kernel<1, KIND, true, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
+        moe_gemv_kernel<1, KIND, true, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr, 0.f, 0);
       else
-        moe_gemv_kernel<4, KIND, true, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
+        moe_gemv_kernel<4, KIND, true, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr, 0.f, 0);
       return;
     }
   }
   if (one_block)
-    moe_gemv_kernel<1, KIND, false, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
+    moe_gemv_kernel<1, KIND, false, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr, 0.f, 0);
   else
-    moe_gemv_kernel<4, KIND, false, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr);
+    moe_gemv_kernel<4, KIND, false, MODE><<<grid, kMoeGemvWaves * kWave, 0, st>>>(args..., none, none, 0, 0, nullptr, nullptr, nullptr, 0.f, 0);
 }
 
-// The decode GEMV with direct route slots (kGemvDirect / kGemvCombine).
+// The decode GEMV with direct route slots (kGemvDirect, kGemvDirectAct, the combines).
 template <int KIND, int MODE, typename... Args>
 static void launch_gemv_direct(dim3 grid, int threads, size_t lds, hipStream_t st, bool vs, Args... args) {
   if constexpr (MODE == kGemvDirectQ) {  // kFp8 / kW4 with vector scales only
@@ -2394,6 +2457,29 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
 // kW4: a2s are the a2 row scales (the W2 output scale) and the routed weights
 // enter the sum, as in the grouped form.
 static bool use_direct_slots(int64_t T, int topk, int kind) { return T == 1 && topk <= combine_slots(kind); }
+// The W13 launch writes the activation itself (kGemvDirectAct) when its
+// split count fits one workgroup.
+static bool direct_act(int kind, int s13) {
+  return (kind == kBf16 || kind == kW8A16) && s13 <= gemv_waves(kGemvDirectAct, kind) / 2;
+}
+
+// The W2 GEMV of one token with the top-k sum (kGemvCombine).
+template <int KIND>
+static int launch_combine(const uint8_t* a2, const float* a2s, const float* a2corr, int T, int H, int I, int numel,
+                          int topk, const uint8_t* w2, const void* w2_s, const float* topk_weights,
+                          const int32_t* topk_ids, const int32_t* emap, int64_t emap_len, int E,
+                          const float* w2_rw, uint16_t* out, hipStream_t st) {
+  const int32_t* none = nullptr;
+  const float* a2_act_s = KIND == kW4 ? a2corr : a2s;
+  const float* yscale = KIND == kW4 ? a2s : w2_rw;
+  launch_gemv_direct<KIND, kGemvCombine>(
+      dim3(H / 16, T, 1), topk * kWave, 0, st, gemv_vector_scales<KIND>(I, a2_act_s, w2_s), a2,
+      gemv_act_bytes<KIND>(numel, I), a2_act_s, 1, I, none, none, none, none, w2, w2_s, H, numel, 1,
+      static_cast<float*>(nullptr), yscale, static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E, out,
+      KIND == kW4 ? topk_weights : static_cast<const float*>(nullptr), static_cast<float*>(nullptr), 0.f, 0);
+  return check_launch("moe w2 (gemv + top-k sum)");
+}
+
 // xa: x as the W13 GEMV reads it (kFp8 / kW4: quantised by the caller, with
 // xs the 1x128 scales / the row scales and xcorr the kW4 block corrections);
 // qx (kFp8 / kW4): xa is the bf16 x, quantised by each W13 workgroup in LDS
@@ -2410,33 +2496,42 @@ static int fused_direct(bool qx, const uint8_t* xa, const float* xs, const float
   const float* act_s = KIND == kW4 ? xcorr : xs;
   const int s13 = w13_splits(numel, E, H, I, KIND);
   const dim3 g13((2 * I / 16 + kMoeGemvWaves - 1) / kMoeGemvWaves, numel, s13);
+  int rc = VMAMD_OK;
+  if constexpr (KIND == kBf16 || KIND == kW8A16) {
+    if (direct_act(KIND, s13)) {
+      launch_gemv_direct<KIND, kGemvDirectAct>(
+          dim3(I / 16, numel, 1), 2 * s13 * kWave, 0, st, gemv_vector_scales<KIND>(H, act_s, w13_s), xa,
+          gemv_act_bytes<KIND>(T, H), act_s, topk, H, none, none, none, none, w13, w13_s, 2 * I, numel, s13,
+          static_cast<float*>(nullptr), w13_rw, reinterpret_cast<uint16_t*>(a2), topk_ids, emap, emap_len, E,
+          static_cast<uint16_t*>(nullptr), static_cast<const float*>(nullptr), static_cast<float*>(nullptr), limit,
+          KIND == kW8A16 || native ? 1 : 0);
+      rc = check_launch("moe w13 (gemv + activation)");
+      if (rc) return rc;
+      return launch_combine<KIND>(a2, a2s, a2corr, T, H, I, numel, topk, w2, w2_s, topk_weights, topk_ids, emap,
+                                  emap_len, E, w2_rw, out, st);
+    }
+  }
   if (qx) {
     launch_gemv_direct<KIND, kGemvDirectQ>(
         g13, kMoeGemvWaves * kWave, static_cast<size_t>(H) + (H / 128) * 4 + (KIND == kW4 ? 32 : 0), st, true,
         xa, static_cast<int>(static_cast<int64_t>(T) * H * 2), static_cast<const float*>(nullptr), topk, H, none,
         none, none, none, w13, w13_s, 2 * I, numel, s13, scratch, static_cast<const float*>(nullptr),
         static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E, static_cast<uint16_t*>(nullptr),
-        static_cast<const float*>(nullptr), KIND == kW4 ? const_cast<float*>(xs) : static_cast<float*>(nullptr));
+        static_cast<const float*>(nullptr), KIND == kW4 ? const_cast<float*>(xs) : static_cast<float*>(nullptr),
+        0.f, 0);
   } else {
     launch_gemv_direct<KIND, kGemvDirect>(
         g13, kMoeGemvWaves * kWave, 0, st, gemv_vector_scales<KIND>(H, act_s, w13_s), xa,
         gemv_act_bytes<KIND>(T, H), act_s, topk, H, none, none, none, none, w13, w13_s, 2 * I, numel, s13,
         scratch, static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len,
-        E, static_cast<uint16_t*>(nullptr), static_cast<const float*>(nullptr), static_cast<float*>(nullptr));
+        E, static_cast<uint16_t*>(nullptr), static_cast<const float*>(nullptr), static_cast<float*>(nullptr), 0.f, 0);
   }
-  int rc = check_launch("moe w13 (gemv)");
+  rc = check_launch("moe w13 (gemv)");
   if (rc) return rc;
   rc = launch_act_decode<KIND>(scratch, s13, numel, I, limit, w13_rw, xs, topk, a2, a2s, a2corr, st, native);
   if (rc) return rc;
-  const float* a2_act_s = KIND == kW4 ? a2corr : a2s;
-  const float* yscale = KIND == kW4 ? a2s : w2_rw;
-  const dim3 g2(H / 16, T, 1);
-  launch_gemv_direct<KIND, kGemvCombine>(
-      g2, topk * kWave, 0, st, gemv_vector_scales<KIND>(I, a2_act_s, w2_s), static_cast<const uint8_t*>(a2),
-      gemv_act_bytes<KIND>(numel, I), a2_act_s, 1, I, none, none, none, none, w2, w2_s, H, numel, 1,
-      static_cast<float*>(nullptr), yscale, static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E,
-      out, KIND == kW4 ? topk_weights : static_cast<const float*>(nullptr), static_cast<float*>(nullptr));
-  return check_launch("moe w2 (gemv + top-k sum)");
+  return launch_combine<KIND>(a2, a2s, a2corr, T, H, I, numel, topk, w2, w2_s, topk_weights, topk_ids, emap,
+                              emap_len, E, w2_rw, out, st);
 }
 
 // Path choice of `auto`: the decode kernels (GEMV over 16-route blocks) up to
@@ -2783,12 +2878,22 @@ static int gemv_op_launch(const void* A, const float* A_scale, int64_t rows, int
     launch_gemv<KIND, kGemvDense>(grid, st, numel <= 8, vs, act, act_bytes, A_scale, topk, k, none, none, none,
                                   none, w, static_cast<const void*>(B_scale), n, numel, splits, partial,
                                   static_cast<const float*>(nullptr), static_cast<uint16_t*>(nullptr));
+  } else if (gemv_op_direct(numel, dense) && swiglu && direct_act(KIND, splits)) {
+    if constexpr (KIND == kBf16 || KIND == kW8A16) {  // the W13 GEMV writes the activation (zeros if dropped)
+      launch_gemv_direct<KIND, kGemvDirectAct>(
+          dim3(n / 32, numel, 1), 2 * splits * kWave, 0, st, vs, act, act_bytes, A_scale, topk, k, none, none, none,
+          none, w, static_cast<const void*>(B_scale), n, numel, splits, static_cast<float*>(nullptr),
+          mul_rw ? topk_weights : static_cast<const float*>(nullptr), static_cast<uint16_t*>(C), topk_ids, none,
+          int64_t{0}, E, static_cast<uint16_t*>(nullptr), static_cast<const float*>(nullptr),
+          static_cast<float*>(nullptr), limit, 1);
+    }
+    return check_launch("fused_gemv (gemv + activation)");
   } else if (gemv_op_direct(numel, dense)) {
     launch_gemv_direct<KIND, kGemvDirect>(
         grid, kMoeGemvWaves * kWave, 0, st, vs, act, act_bytes, A_scale, topk, k, none, none, none, none, w,
         static_cast<const void*>(B_scale), n, numel, splits, partial, static_cast<const float*>(nullptr),
         static_cast<uint16_t*>(nullptr), topk_ids, none, int64_t{0}, E, static_cast<uint16_t*>(nullptr),
-        static_cast<const float*>(nullptr), static_cast<float*>(nullptr));
+        static_cast<const float*>(nullptr), static_cast<float*>(nullptr), 0.f, 0);
   } else {
     int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.sorted);
     int32_t* offs = reinterpret_cast<int32_t*>(ws + L.offs);
