@@ -707,6 +707,30 @@ def router_sweep(torch, iters: int, log) -> int:
     return 0
 
 
+def launch_floor(torch, iters: int, log) -> int:
+    """The timing floor of this file's method: n = 1, 2, 4, 8 back-to-back
+    launches of a trivial kernel (an in-place add on 1024 floats), timed as
+    the decode and dense points are -- HIP events around the call after an
+    untimed 1 GiB read, eager and as a HIP-graph replay.  One JSON line per
+    n; what a decode layer or a small GEMM adds above these is its own time."""
+    flush_buf = torch.ones(1 << 28, dtype=torch.int32, device="cuda")
+    flush = lambda: flush_buf.max()
+    x = torch.zeros(1024, device="cuda")
+    for n in (1, 2, 4, 8):
+        def step(n=n):
+            for _ in range(n):
+                x.add_(1.0)
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        eager = statistics.median(time_events(torch, step, iters, flush)) * 1e3
+        graph = graph_median(torch, step, iters, flush) * 1e3
+        print(json.dumps({"kernels": n, "eager_us": round(eager, 1), "graph_us": round(graph, 1),
+                          "graph_minus_eager_us": round(graph - eager, 1)}), flush=True)
+    log("bench: launch floor done")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -750,6 +774,9 @@ def main() -> int:
     ap.add_argument("--ceiling", action="store_true",
                     help="only time the platform's fp8 (torch._scaled_mm) and bf16 GEMMs beside "
                          "the block-fp8 GEMM at the dense benchmark shapes, M = 512 and 4096")
+    ap.add_argument("--launch-floor", action="store_true",
+                    help="only time 1, 2, 4 and 8 trivial kernel launches eager and as a graph "
+                         "replay, by the method of the decode and dense points (one JSON line each)")
     ap.add_argument("--router", action="store_true",
                     help="only time the fp32 router gate (Nemotron-H, [M, 2688] x [128, 2688]^T) "
                          "against the platform fp32 GEMM at M = 1, 7, 115, 512")
@@ -780,6 +807,8 @@ def main() -> int:
         return router_sweep(torch, args.sweep_iters, log)
     if args.ceiling:
         return ceiling_sweep(torch, args.sweep_iters, log)
+    if args.launch_floor:
+        return launch_floor(torch, args.sweep_iters, log)
     if args.native:
         return native_sweep(torch, args.sweep_iters, log)
     if args.profile_bf16 > 0:
