@@ -1546,9 +1546,15 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     for (int j = 0; j < 4; ++j) buffer_dma16(rb, offB[j] + ks, stage + P::kOffB + (wave + 8 * j) * 8 * 128);
     if (kScaled && wave <= BM / 64) buffer_dma4(rs, offS + step * stepS, stage + ldsS);
   };
-  // Padding routes close a block, so a wave whose first route is padding
-  // holds none.
-  const bool wave_live = sorted[base + wm * P::WTM] < numel;
+  // Padding routes close a block, so the wave's 16-route m-tiles that hold a
+  // route are a prefix: mlive of them (0: the wave holds none and skips its
+  // MFMAs).  The MFMAs of the m-tiles past it are skipped too (their
+  // accumulators stay zero; they hold only padding routes, whose outputs
+  // nothing reads).
+  int mlive = 0;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) mlive += sorted[base + wm * P::WTM + mt * 16] < numel ? 1 : 0;
+  mlive = __builtin_amdgcn_readfirstlane(mlive);
 
   v4f acc[MT][NT];
 #pragma unroll
@@ -1558,27 +1564,29 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
   const int nw = wn * 16 * NT;  // the wave's first local weight row
 
-  // One K step from LDS stage `st` (see gemm_fp8_big_kernel).  W13: n tile
-  // nt takes the gate (even) or up (odd) block scale.  bf16: two chained
-  // MFMAs per fragment pair into the accumulators, no scales.
-  auto mma = [&](const uint8_t* st) {
+  // One K step from LDS stage `st` (see gemm_fp8_big_kernel) over the first
+  // ML m-tiles.  W13: n tile nt takes the gate (even) or up (odd) block
+  // scale.  bf16: two chained MFMAs per fragment pair into the accumulators,
+  // no scales.
+  auto mma = [&](const uint8_t* st, auto ml_tag) {
+    constexpr int ML = decltype(ml_tag)::value;
     float sb0 = 0.f, sb1 = 0.f, sa[MT], sc[MT][2];
     if constexpr (kScaled) {
       sb0 = lds_load<float>(st, P::kOffSB + (W13 ? 0 : 4 * wn));
       sb1 = W13 ? lds_load<float>(st, P::kOffSB + 4) : sb0;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) sa[mt] = lds_load<float>(st, P::kOffSA + (wm * P::WTM + mt * 16 + li) * 4);
+      for (int mt = 0; mt < ML; ++mt) sa[mt] = lds_load<float>(st, P::kOffSA + (wm * P::WTM + mt * 16 + li) * 4);
     }
     v8i wf[2], x[MT];
     wf[0] = lds_frag(st + P::kOffB, nw + li, lg);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) x[mt] = lds_frag(st, wm * P::WTM + mt * 16 + li, lg);
+    for (int mt = 0; mt < ML; ++mt) x[mt] = lds_frag(st, wm * P::WTM + mt * 16 + li, lg);
     __builtin_amdgcn_sched_barrier(0);
     v4f t[2];
-    constexpr int NI = MT * NT;
+    constexpr int NI = ML * NT;
 #pragma unroll
     for (int i = 0; i <= NI; ++i) {
-      const int nt = i / MT, mt = i % MT;
+      const int nt = i / ML, mt = i % ML;
       if (i < NI) {
         if constexpr (kScaled)
           t[i & 1] = mfma_fp8(wf[nt & 1], x[mt], zero);
@@ -1589,7 +1597,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
       if (kScaled && i > 0) {
-        const int j = i - 1, jm = j % MT, jn = j / MT;
+        const int j = i - 1, jm = j % ML, jn = j / ML;
         if (jn < 2) sc[jm][jn] = sa[jm] * (jn ? sb1 : sb0);  // at first use
         fma4(acc[jm][jn], t[j & 1], sc[jm][W13 ? (jn & 1) : 0]);
       }
@@ -1597,13 +1605,37 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     }
   };
 
-  issue(smem_dyn, 0);
-  wait_lgkmcnt0();
-  for (int kb = 0; kb < KS; ++kb) {
-    wait_vmcnt<0>();  // this wave's DMAs of step kb have landed
-    barrier_lds();    // ... every wave's, and step kb - 1's buffer is no longer read
-    if (kb + 1 < KS) issue(smem_dyn + ((kb + 1) & 1) * P::kStage, kb + 1);
-    if (wave_live) mma(smem_dyn + (kb & 1) * P::kStage);
+  // The K loop, one copy per live m-tile count (ML = 0: DMAs and barriers only).
+  auto kloop = [&](auto ml_tag) {
+    constexpr int ML = decltype(ml_tag)::value;
+    issue(smem_dyn, 0);
+    wait_lgkmcnt0();
+    for (int kb = 0; kb < KS; ++kb) {
+      wait_vmcnt<0>();  // this wave's DMAs of step kb have landed
+      barrier_lds();    // ... every wave's, and step kb - 1's buffer is no longer read
+      if (kb + 1 < KS) issue(smem_dyn + ((kb + 1) & 1) * P::kStage, kb + 1);
+      if constexpr (ML > 0) mma(smem_dyn + (kb & 1) * P::kStage, ml_tag);
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  using I4 = std::integral_constant<int, 4>;
+  using I5 = std::integral_constant<int, 5>;
+  static_assert(MT == 4 || MT == 5, "m-tiles per wave");
+  if (MT == 5 && mlive >= 5) {
+    if constexpr (MT == 5) kloop(I5{});
+  } else if (mlive >= 4) {
+    kloop(I4{});
+  } else if (mlive == 3) {
+    kloop(I3{});
+  } else if (mlive == 2) {
+    kloop(I2{});
+  } else if (mlive == 1) {
+    kloop(I1{});
+  } else {
+    kloop(I0{});
   }
   barrier_lds();  // every wave is done with the stages before LDS is reused
 
