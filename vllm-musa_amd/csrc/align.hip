@@ -15,9 +15,11 @@
 //      in LDS, and the rank across steps and earlier chunks from a running
 //      per-expert counter that starts at the count before the chunk.
 // Workgroup 0 also writes the per-call outputs (num_tokens_post_pad, offsets,
-// active experts, expert_ids) and the sentinel `numel` at every position of
-// sorted_token_ids that no route takes, exactly once, so no ordering between
-// writers is needed.
+// active experts, expert_ids).  The sentinel `numel` goes to every position
+// of sorted_token_ids that no route takes, exactly once, so no ordering
+// between writers is needed: expert e's padding by one wave of workgroup
+// e % nblk (64 consecutive positions per store), the unused tail by all
+// workgroups in turn.
 #include "quant_dev.h"
 
 namespace vmamd {
@@ -41,7 +43,7 @@ __device__ __forceinline__ int mapped_expert(const int32_t* __restrict__ ids, in
 constexpr int64_t kAlignChunk = kAlignThreads;
 
 __device__ __forceinline__ void align_body(
-    int blk, const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int E, int bs,
+    int blk, int nblk, const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int E, int bs,
     const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ scatter_idx, int32_t* __restrict__ active_out,
@@ -62,16 +64,25 @@ __device__ __forceinline__ void align_body(
   }
   __syncthreads();
 
-  // 1. histograms: all routes (cnt) and the routes before this chunk (run)
+  // 1. histograms of the routes before this chunk (run) and of the others
+  // (cnt, then cnt += run: all routes), one LDS add per route; each thread
+  // has 8 ids in flight (one per strided slot) before its adds.
   const int64_t c_begin = static_cast<int64_t>(blk) * chunk;
   const int64_t c_end = min(numel, c_begin + chunk);
-  for (int64_t r = tid; r < numel; r += kAlignThreads) {
-    const int e = mapped_expert(ids, r, E, map, map_len);
-    if (e >= 0) {
-      atomicAdd(&cnt[e], 1);
-      if (r < c_begin) atomicAdd(&run[e], 1);
+  constexpr int kHistU = 8;
+  for (int64_t r0 = tid; r0 < numel; r0 += kHistU * kAlignThreads) {
+    int ev[kHistU];
+#pragma unroll
+    for (int u = 0; u < kHistU; ++u) {
+      const int64_t r = r0 + u * kAlignThreads;
+      ev[u] = r < numel ? mapped_expert(ids, r, E, map, map_len) : -1;
     }
+#pragma unroll
+    for (int u = 0; u < kHistU; ++u)
+      if (ev[u] >= 0) atomicAdd(r0 + u * kAlignThreads < c_begin ? &run[ev[u]] : &cnt[ev[u]], 1);
   }
+  __syncthreads();
+  for (int e = tid; e < E; e += kAlignThreads) cnt[e] += run[e];
   __syncthreads();
   const bool lead = blk == 0;  // writes the per-call outputs
 
@@ -128,11 +139,11 @@ __device__ __forceinline__ void align_body(
   }
   // sentinel for the padding of each segment and the unused tail
   const int32_t sentinel = static_cast<int32_t>(numel);
-  if (lead) {
-    for (int e = tid; e < E; e += kAlignThreads)
-      for (int p = base[e] + cnt[e]; p < base[e + 1]; ++p) sorted[p] = sentinel;
-    for (int64_t p = total + tid; p < capacity; p += kAlignThreads) sorted[p] = sentinel;
-  }
+  for (int e = blk + nblk * wave; e < E; e += nblk * kAlignWaves)
+    for (int p = base[e] + cnt[e] + lane; p < base[e + 1]; p += kWave) sorted[p] = sentinel;
+  for (int64_t p = total + static_cast<int64_t>(blk) * kAlignThreads + tid; p < capacity;
+       p += static_cast<int64_t>(nblk) * kAlignThreads)
+    sorted[p] = sentinel;
 
   // 3. stable placement
   int nbits = 1;
@@ -181,7 +192,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ scatter_idx, int32_t* __restrict__ active_out,
     int32_t* __restrict__ num_active_out) {
-  align_body(blockIdx.x, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids, ntpp,
+  align_body(blockIdx.x, gridDim.x, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids, ntpp,
              offsets_out, scatter_idx, active_out, num_active_out);
 }
 
@@ -196,7 +207,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_quant_kernel(
     const uint16_t* __restrict__ x, int64_t groups_per_row, int64_t num_groups, bool vec,
     uint8_t* __restrict__ xq, float* __restrict__ xs) {
   if (static_cast<int>(blockIdx.x) < align_groups) {
-    align_body(blockIdx.x, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids,
+    align_body(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids,
                ntpp, offsets_out, nullptr, active_out, num_active_out);
     return;
   }
@@ -222,7 +233,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_rowquant_kernel(
     const uint16_t* __restrict__ x, int64_t rows, int cols, uint8_t* __restrict__ xq,
     float* __restrict__ xs, float* __restrict__ xcorr) {
   if (static_cast<int>(blockIdx.x) < align_groups) {
-    align_body(blockIdx.x, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids,
+    align_body(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids,
                ntpp, offsets_out, nullptr, active_out, num_active_out);
     return;
   }
