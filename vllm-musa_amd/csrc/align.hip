@@ -14,6 +14,12 @@
 //      rank across the 16 waves of the step from a [wave][expert] count table
 //      in LDS, and the rank across steps and earlier chunks from a running
 //      per-expert counter that starts at the count before the chunk.
+// With a counts buffer (the fused layers' workspace) step 1 runs as its own
+// launch instead: each workgroup histograms only its chunk into
+// counts[blk][E] (PHASE 1), and the placement launch (PHASE 2) sums the
+// chunk histograms, all of them and those before its chunk.  Adds to LDS
+// run at about one route per clock per CU, so histogramming all routes in
+// every workgroup (PHASE 0) costs numel clocks: 29 us at 65536 routes.
 // Workgroup 0 also writes the per-call outputs (num_tokens_post_pad, offsets,
 // active experts, expert_ids).  The sentinel `numel` goes to every position
 // of sorted_token_ids that no route takes, exactly once, so no ordering
@@ -42,12 +48,13 @@ __device__ __forceinline__ int mapped_expert(const int32_t* __restrict__ ids, in
 // workgroup only beyond 256 workgroups).
 constexpr int64_t kAlignChunk = kAlignThreads;
 
+template <int PHASE>
 __device__ __forceinline__ void align_body(
     int blk, int nblk, const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int E, int bs,
     const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ scatter_idx, int32_t* __restrict__ active_out,
-    int32_t* __restrict__ num_active_out) {
+    int32_t* __restrict__ num_active_out, int32_t* __restrict__ counts) {
   __shared__ int cnt[kMaxAlignExperts];
   __shared__ int base[kMaxAlignExperts + 1];
   __shared__ int run[kMaxAlignExperts];
@@ -69,8 +76,34 @@ __device__ __forceinline__ void align_body(
   // has 8 ids in flight (one per strided slot) before its adds.
   const int64_t c_begin = static_cast<int64_t>(blk) * chunk;
   const int64_t c_end = min(numel, c_begin + chunk);
+  if constexpr (PHASE == 1) {  // this chunk's histogram only
+    for (int64_t r = c_begin + tid; r < c_end; r += kAlignThreads) {
+      const int e = mapped_expert(ids, r, E, map, map_len);
+      if (e >= 0) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += kAlignThreads) counts[static_cast<int64_t>(blk) * E + e] = cnt[e];
+    return;
+  }
   constexpr int kHistU = 8;
-  for (int64_t r0 = tid; r0 < numel; r0 += kHistU * kAlignThreads) {
+  if constexpr (PHASE == 2) {  // the chunk histograms: all (cnt) and before this chunk (run)
+    for (int e = tid; e < E; e += kAlignThreads) {
+      int all = 0, before = 0;
+      for (int b0 = 0; b0 < nblk; b0 += kHistU) {
+        int v[kHistU];
+#pragma unroll
+        for (int u = 0; u < kHistU; ++u) v[u] = b0 + u < nblk ? counts[static_cast<int64_t>(b0 + u) * E + e] : 0;
+#pragma unroll
+        for (int u = 0; u < kHistU; ++u) {
+          all += v[u];
+          before += b0 + u < blk ? v[u] : 0;
+        }
+      }
+      cnt[e] = all;
+      run[e] = before;
+    }
+  }
+  for (int64_t r0 = tid; PHASE == 0 && r0 < numel; r0 += kHistU * kAlignThreads) {
     int ev[kHistU];
 #pragma unroll
     for (int u = 0; u < kHistU; ++u) {
@@ -82,7 +115,8 @@ __device__ __forceinline__ void align_body(
       if (ev[u] >= 0) atomicAdd(r0 + u * kAlignThreads < c_begin ? &run[ev[u]] : &cnt[ev[u]], 1);
   }
   __syncthreads();
-  for (int e = tid; e < E; e += kAlignThreads) cnt[e] += run[e];
+  if constexpr (PHASE == 0)
+    for (int e = tid; e < E; e += kAlignThreads) cnt[e] += run[e];
   __syncthreads();
   const bool lead = blk == 0;  // writes the per-call outputs
 
@@ -186,29 +220,33 @@ __device__ __forceinline__ void align_body(
 }
 
 
+template <int PHASE>
 __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int E, int bs,
     const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ scatter_idx, int32_t* __restrict__ active_out,
-    int32_t* __restrict__ num_active_out) {
-  align_body(blockIdx.x, gridDim.x, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids, ntpp,
-             offsets_out, scatter_idx, active_out, num_active_out);
+    int32_t* __restrict__ num_active_out, int32_t* __restrict__ counts) {
+  align_body<PHASE>(blockIdx.x, gridDim.x, ids, numel, chunk, E, bs, map, map_len, sorted, capacity,
+                    expert_ids, ntpp, offsets_out, scatter_idx, active_out, num_active_out, counts);
 }
 
 // The MoE layer's two independent first steps in one launch: workgroups
-// [0, align_groups) run moe_align_block_size, the others the 1x128 fp8
-// quantiser of the bf16 activations (kAlignThreads / 16 groups each).
+// [0, align_groups) run moe_align_block_size (PHASE 1: only the chunk
+// histograms, the placement following as moe_align_kernel<2>), the others
+// the 1x128 fp8 quantiser of the bf16 activations (kAlignThreads / 16
+// groups each).
+template <int PHASE>
 __global__ __launch_bounds__(kAlignThreads) void moe_align_quant_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int align_groups, int E, int bs,
     const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ active_out, int32_t* __restrict__ num_active_out,
     const uint16_t* __restrict__ x, int64_t groups_per_row, int64_t num_groups, bool vec,
-    uint8_t* __restrict__ xq, float* __restrict__ xs) {
+    uint8_t* __restrict__ xq, float* __restrict__ xs, int32_t* __restrict__ counts) {
   if (static_cast<int>(blockIdx.x) < align_groups) {
-    align_body(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids,
-               ntpp, offsets_out, nullptr, active_out, num_active_out);
+    align_body<PHASE>(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity,
+                      expert_ids, ntpp, offsets_out, nullptr, active_out, num_active_out, counts);
     return;
   }
   constexpr int kGroupsPerAlignBlock = kAlignThreads / kLanesPerGroup;
@@ -224,17 +262,17 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_quant_kernel(
 // block corrections).  CPL > 0: a quant workgroup quantises one row per wave
 // (cols <= 512 * CPL); CPL = 0: kAlignThreads / kRowThreads rows, one per
 // 256-thread part.
-template <int CPL>
+template <int CPL, int PHASE>
 __global__ __launch_bounds__(kAlignThreads) void moe_align_rowquant_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int align_groups, int E, int bs,
     const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ active_out, int32_t* __restrict__ num_active_out,
     const uint16_t* __restrict__ x, int64_t rows, int cols, uint8_t* __restrict__ xq,
-    float* __restrict__ xs, float* __restrict__ xcorr) {
+    float* __restrict__ xs, float* __restrict__ xcorr, int32_t* __restrict__ counts) {
   if (static_cast<int>(blockIdx.x) < align_groups) {
-    align_body(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity, expert_ids,
-               ntpp, offsets_out, nullptr, active_out, num_active_out);
+    align_body<PHASE>(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity,
+                      expert_ids, ntpp, offsets_out, nullptr, active_out, num_active_out, counts);
     return;
   }
   if constexpr (CPL > 0) {
@@ -263,12 +301,50 @@ static void align_grid(int64_t numel, int64_t& chunk, int& groups) {
   groups = static_cast<int>((numel + chunk - 1) / chunk);
 }
 
+size_t align_counts_bytes(int64_t numel, int E) {
+  int64_t chunk;
+  int groups;
+  align_grid(numel, chunk, groups);
+  return static_cast<size_t>(std::max(groups, 1)) * E * 4;
+}
+
+// The placement launch after a PHASE 1 histogram launch.
+static void align_place(const int32_t* ids, int64_t numel, int64_t chunk, int groups, int E, int bs,
+                        const int32_t* map, int64_t map_len, int32_t* sorted, int64_t capacity, int32_t* expert_ids,
+                        int32_t* ntpp, int32_t* offsets, int32_t* active, int32_t* num_active, int32_t* counts,
+                        hipStream_t st) {
+  moe_align_kernel<2><<<groups, kAlignThreads, 0, st>>>(ids, numel, chunk, E, bs, map, map_len, sorted, capacity,
+                                                        expert_ids, ntpp, offsets, nullptr, active, num_active,
+                                                        counts);
+}
+
+int align_routes(const int32_t* topk_ids, int64_t numel, int num_experts, int block_size,
+                 const int32_t* expert_map, int64_t expert_map_len, int32_t* sorted, int64_t capacity,
+                 int32_t* expert_ids, int32_t* ntpp, int32_t* offsets, int32_t* active, int32_t* num_active,
+                 int32_t* counts, hipStream_t st) {
+  int64_t chunk;
+  int groups;
+  align_grid(numel, chunk, groups);
+  if (counts == nullptr || groups <= 1)
+    return vmamd_moe_align_block_size(topk_ids, numel, num_experts, block_size, expert_map, expert_map_len, sorted,
+                                      capacity, expert_ids, ntpp, offsets, nullptr, active, num_active,
+                                      reinterpret_cast<vmamd_stream_t>(st));
+  moe_align_kernel<1><<<groups, kAlignThreads, 0, st>>>(topk_ids, numel, chunk, num_experts, block_size, expert_map,
+                                                        expert_map_len, sorted, capacity, expert_ids, ntpp, offsets,
+                                                        nullptr, active, num_active, counts);
+  int rc = check_launch("moe align (histograms)");
+  if (rc) return rc;
+  align_place(topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted, capacity,
+              expert_ids, ntpp, offsets, active, num_active, counts, st);
+  return check_launch("moe align (placement)");
+}
+
 int align_and_group_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_experts,
                               int block_size, const int32_t* expert_map, int64_t expert_map_len,
                               int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
                               int32_t* offsets, int32_t* active, int32_t* num_active,
                               const void* x, int64_t rows, int64_t cols, uint8_t* xq, float* xs,
-                              hipStream_t st) {
+                              hipStream_t st, int32_t* counts) {
   const char* who = "moe align + quant";
   VMAMD_REQUIRE(num_experts > 0 && num_experts <= kMaxAlignExperts && block_size > 0, "%s: bad sizes",
                 who);
@@ -288,10 +364,21 @@ int align_and_group_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_ex
   const int64_t num_groups = rows * groups_per_row;
   const int64_t qblocks = (num_groups + kAlignThreads / kLanesPerGroup - 1) / (kAlignThreads / kLanesPerGroup);
   const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;  // rows of cols % 128 == 0 bf16 stay aligned
-  moe_align_quant_kernel<<<static_cast<int>(groups + qblocks), kAlignThreads, 0, st>>>(
-      topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted,
-      capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),
-      groups_per_row, num_groups, vec, xq, xs);
+  const bool two = counts != nullptr && groups > 1;
+  if (two)
+    moe_align_quant_kernel<1><<<static_cast<int>(groups + qblocks), kAlignThreads, 0, st>>>(
+        topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted,
+        capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),
+        groups_per_row, num_groups, vec, xq, xs, counts);
+  else
+    moe_align_quant_kernel<0><<<static_cast<int>(groups + qblocks), kAlignThreads, 0, st>>>(
+        topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted,
+        capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),
+        groups_per_row, num_groups, vec, xq, xs, nullptr);
+  int rc = check_launch(who);
+  if (rc || !two) return rc;
+  align_place(topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted, capacity,
+              expert_ids, ntpp, offsets, active, num_active, counts, st);
   return check_launch(who);
 }
 int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_experts,
@@ -299,7 +386,7 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
                             int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
                             int32_t* offsets, int32_t* active, int32_t* num_active, const void* x,
                             int64_t rows, int64_t cols, uint8_t* xq, float* xs, float* xcorr,
-                            hipStream_t st) {
+                            hipStream_t st, int32_t* counts) {
   const char* who = "moe align + row quant";
   VMAMD_REQUIRE(num_experts > 0 && num_experts <= kMaxAlignExperts && block_size > 0, "%s: bad sizes",
                 who);
@@ -326,19 +413,27 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
   const int rows_per_block = cpl > 0 ? kAlignThreads / kWave : kAlignThreads / kRowThreads;
   const int64_t qblocks = (rows + rows_per_block - 1) / rows_per_block;
   const dim3 grid(static_cast<unsigned>(groups + qblocks));
-#define VMAMD_ARQ(C)                                                                              \
-  moe_align_rowquant_kernel<C><<<grid, kAlignThreads, 0, st>>>(                                   \
+  const bool two = counts != nullptr && groups > 1 && numel > 0;
+#define VMAMD_ARQ(C, PH)                                                                          \
+  moe_align_rowquant_kernel<C, PH><<<grid, kAlignThreads, 0, st>>>(                               \
       topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted, \
       capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),     \
-      rows, static_cast<int>(cols), xq, xs, xcorr)
+      rows, static_cast<int>(cols), xq, xs, xcorr, counts)
+#define VMAMD_ARQ2(C) \
+  if (two) VMAMD_ARQ(C, 1); else VMAMD_ARQ(C, 0);
   switch (cpl) {
-    case 1: VMAMD_ARQ(1); break;
-    case 2: VMAMD_ARQ(2); break;
-    case 3: VMAMD_ARQ(3); break;
-    case 4: VMAMD_ARQ(4); break;
-    default: VMAMD_ARQ(0); break;
+    case 1: VMAMD_ARQ2(1); break;
+    case 2: VMAMD_ARQ2(2); break;
+    case 3: VMAMD_ARQ2(3); break;
+    case 4: VMAMD_ARQ2(4); break;
+    default: VMAMD_ARQ2(0); break;
   }
+#undef VMAMD_ARQ2
 #undef VMAMD_ARQ
+  int rc = check_launch(who);
+  if (rc || !two) return rc;
+  align_place(topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted, capacity,
+              expert_ids, ntpp, offsets, active, num_active, counts, st);
   return check_launch(who);
 }
 }  // namespace vmamd
@@ -369,10 +464,10 @@ extern "C" int vmamd_moe_align_block_size(const int32_t* topk_ids, int64_t numel
   int64_t chunk;
   int groups;
   align_grid(numel, chunk, groups);
-  moe_align_kernel<<<groups > 0 ? groups : 1, kAlignThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+  moe_align_kernel<0><<<groups > 0 ? groups : 1, kAlignThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
       topk_ids, numel, chunk, num_experts, block_size, expert_map, expert_map_len, sorted_token_ids,
       capacity, expert_ids, num_tokens_post_pad, expert_offsets, scatter_idx, active_experts,
-      num_active);
+      num_active, nullptr);
   return check_launch("moe_align_block_size");
 }
 
@@ -389,5 +484,5 @@ extern "C" int vmamd_moe_align_block_size_quant_fp8(const int32_t* topk_ids, int
   return align_and_group_quant_fp8(topk_ids, numel, num_experts, block_size, expert_map, expert_map_len,
                                    sorted_token_ids, capacity, expert_ids, num_tokens_post_pad, expert_offsets,
                                    active_experts, num_active, x, rows, cols, static_cast<uint8_t*>(xq), xs,
-                                   reinterpret_cast<hipStream_t>(stream));
+                                   reinterpret_cast<hipStream_t>(stream), nullptr);
 }

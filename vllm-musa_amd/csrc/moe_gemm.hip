@@ -2441,7 +2441,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
 // scratch shares one region.  kFp8 / kW4 add the quantised x and scales; kW4
 // also keeps the bf16 activation before its row quantiser.
 struct MoeWs {
-  size_t xq, xs, xcorr, sorted, eids, ntpp, offs, active, nact, abf, a2, a2s, a2corr, y, scratch, total;
+  size_t xq, xs, xcorr, sorted, eids, ntpp, offs, active, nact, acnt, abf, a2, a2s, a2corr, y, scratch, total;
 };
 
 static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm, int kind) {
@@ -2461,6 +2461,7 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   w.offs = take((E + 1) * 4);
   w.active = take(E * 4);
   w.nact = take(4);
+  w.acnt = take(align_counts_bytes(numel, E));
   const int64_t arows = bm == kGemvBlock ? numel : cap;  // route order (decode) or padded order
   if (kind == kW4) w.abf = take(arows * I * 2);
   w.a2 = take(arows * I * (kind == kBf16 || kind == kW8A16 ? 2 : 1));
@@ -2721,7 +2722,8 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     uint8_t* xq = ws + L.xq;
     float* xsw = reinterpret_cast<float*>(ws + L.xs);
     rc = align_and_group_quant_fp8(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
-                                   eids, ntpp, offs, active, nact, x, T, H, xq, xsw, st);
+                                   eids, ntpp, offs, active, nact, x, T, H, xq, xsw, st,
+                                   reinterpret_cast<int32_t*>(ws + L.acnt));
     if (rc) return rc;
     xa = xq;
     xs = xsw;
@@ -2729,13 +2731,14 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     uint8_t* xq = ws + L.xq;
     float* xsw = reinterpret_cast<float*>(ws + L.xs);
     rc = align_and_row_quant_fp8(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
-                                 eids, ntpp, offs, active, nact, x, T, H, xq, xsw, xcorr, st);
+                                 eids, ntpp, offs, active, nact, x, T, H, xq, xsw, xcorr, st,
+                                 reinterpret_cast<int32_t*>(ws + L.acnt));
     if (rc) return rc;
     xa = xq;
     xs = xsw;
   } else {
-    rc = vmamd_moe_align_block_size(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
-                                    eids, ntpp, offs, nullptr, active, nact, stream);
+    rc = align_routes(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap, eids, ntpp, offs, active,
+                      nact, reinterpret_cast<int32_t*>(ws + L.acnt), st);
     if (rc) return rc;
   }
   // kW4 prefill: bf16 activation, quantised per row below (the decode path
