@@ -283,31 +283,7 @@ moe_gemv_kernel(
     dead = e < 0;
     e = dead ? 0 : e;
   }
-  // kQx LDS: [K] fp8 (kW4: w4 order), [K/128] f32 (kFp8: group scales,
-  // kW4: block corrections), kW4 then the row scale and 4 wave maxima.
   extern __shared__ __attribute__((aligned(16))) uint8_t qx_lds[];
-  if constexpr (kQx) {
-    const int gpr = K / 128;
-    const uint16_t* xrow = reinterpret_cast<const uint16_t*>(act) + static_cast<int64_t>(slot / act_div) * K;
-    float* qs = reinterpret_cast<float*>(qx_lds + K);
-    if constexpr (KIND == kFp8) {
-      for (int g0 = 0; g0 < gpr; g0 += static_cast<int>(blockDim.x) / kLanesPerGroup) {
-        const int g = g0 + static_cast<int>(threadIdx.x) / kLanesPerGroup;  // uniform over a group's lanes
-        if (g < gpr)
-          group_quant_group<kBF16>(xrow, K, gpr, g, threadIdx.x % kLanesPerGroup, true, 1e-10f, -448.f, 448.f,
-                                   qx_lds, K, qs, 0, 1);
-      }
-      __syncthreads();
-    } else {  // one kRowThreads part: the whole workgroup (it synchronises the block)
-      float* rs = qs + gpr;
-      row_quant_part<true>(xrow, K, K, 1e-4f, -448.f, 448.f, qx_lds, rs, 0, true, threadIdx.x, rs + 1, qs);
-      __syncthreads();
-      if (blockIdx.x == 0 && blockIdx.z == 0 && slot % act_div == 0 && threadIdx.x == 0)
-        xs_out[slot / act_div] = rs[0];
-      if (e < 0) return;  // the row scale's writer of a dropped route
-    }
-    if (ntile * 16 >= N) return;
-  }
   const int split = kAct ? wave % act_splits : static_cast<int>(blockIdx.z);
   const int KS = K / KB_::kElems;                    // K steps
   const int arowb = KS * KB_::kAct;
@@ -541,6 +517,40 @@ moe_gemv_kernel(
     }
   };
 
+  // kQx with kFp8: the first K group of weights is requested before the
+  // workgroup quantises its token's row (the weights do not depend on it), so
+  // the weight stream starts with the x loads instead of after the quantiser
+  // (DeepSeek-V3 W13 at one token 47.8 -> 45.6 us).  kW4's row quantiser,
+  // whose row maximum waits behind those loads, measured 15.0 -> 15.7 us and
+  // keeps the order.
+  constexpr bool kEarlyW = kQx && KIND == kFp8;
+  if constexpr (kEarlyW) {
+    if (e >= 0 && ntile * 16 < N) load_w(kb0);
+  }
+  // kQx LDS: [K] fp8 (kW4: w4 order), [K/128] f32 (kFp8: group scales,
+  // kW4: block corrections), kW4 then the row scale and 4 wave maxima.
+  if constexpr (kQx) {
+    const int gpr = K / 128;
+    const uint16_t* xrow = reinterpret_cast<const uint16_t*>(act) + static_cast<int64_t>(slot / act_div) * K;
+    float* qs = reinterpret_cast<float*>(qx_lds + K);
+    if constexpr (KIND == kFp8) {
+      for (int g0 = 0; g0 < gpr; g0 += static_cast<int>(blockDim.x) / kLanesPerGroup) {
+        const int g = g0 + static_cast<int>(threadIdx.x) / kLanesPerGroup;  // uniform over a group's lanes
+        if (g < gpr)
+          group_quant_group<kBF16>(xrow, K, gpr, g, threadIdx.x % kLanesPerGroup, true, 1e-10f, -448.f, 448.f,
+                                   qx_lds, K, qs, 0, 1);
+      }
+      __syncthreads();
+    } else {  // one kRowThreads part: the whole workgroup (it synchronises the block)
+      float* rs = qs + gpr;
+      row_quant_part<true>(xrow, K, K, 1e-4f, -448.f, 448.f, qx_lds, rs, 0, true, threadIdx.x, rs + 1, qs);
+      __syncthreads();
+      if (blockIdx.x == 0 && blockIdx.z == 0 && slot % act_div == 0 && threadIdx.x == 0)
+        xs_out[slot / act_div] = rs[0];
+      if (e < 0) return;  // the row scale's writer of a dropped route
+    }
+    if (ntile * 16 >= N) return;
+  }
   int seg0 = 0, nblk = 1;
   if constexpr (MODE == kGemvGrouped) {
     seg0 = offsets[e];
@@ -550,7 +560,7 @@ moe_gemv_kernel(
   }
   int b0 = 0;
   if (!dead) do {
-    load_w(kb0);  // first group: in flight while the routes are resolved
+    if (!kEarlyW) load_w(kb0);  // first group: in flight while the routes are resolved
     const int nb = min(MAXB, nblk - b0);
     int rr[MAXB];
 #pragma unroll
