@@ -14,8 +14,8 @@
 //      rank across the 16 waves of the step from a [wave][expert] count table
 //      in LDS, and the rank across steps and earlier chunks from a running
 //      per-expert counter that starts at the count before the chunk.
-// With a counts buffer (the fused layers' workspace) step 1 runs as its own
-// launch instead: each workgroup histograms only its chunk into
+// With a counts buffer (the bf16 layers' workspace, align_routes) step 1
+// runs as its own launch instead: each workgroup histograms only its chunk into
 // counts[blk][E] (PHASE 1), and the placement launch (PHASE 2) sums the
 // chunk histograms, all of them and those before its chunk.  Adds to LDS
 // run at about one route per clock per CU, so histogramming all routes in
@@ -232,21 +232,21 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
 }
 
 // The MoE layer's two independent first steps in one launch: workgroups
-// [0, align_groups) run moe_align_block_size (PHASE 1: only the chunk
-// histograms, the placement following as moe_align_kernel<2>), the others
-// the 1x128 fp8 quantiser of the bf16 activations (kAlignThreads / 16
-// groups each).
-template <int PHASE>
+// [0, align_groups) run moe_align_block_size, the others the 1x128 fp8
+// quantiser of the bf16 activations (kAlignThreads / 16 groups each).  The
+// alignment keeps its one-launch form here: its all-route histogram runs
+// beside the quantiser's workgroups (measured at T=4096: one launch 34.0 us,
+// histograms + quantiser then placement 27.3 + 9.8 us).
 __global__ __launch_bounds__(kAlignThreads) void moe_align_quant_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int align_groups, int E, int bs,
     const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ active_out, int32_t* __restrict__ num_active_out,
     const uint16_t* __restrict__ x, int64_t groups_per_row, int64_t num_groups, bool vec,
-    uint8_t* __restrict__ xq, float* __restrict__ xs, int32_t* __restrict__ counts) {
+    uint8_t* __restrict__ xq, float* __restrict__ xs) {
   if (static_cast<int>(blockIdx.x) < align_groups) {
-    align_body<PHASE>(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity,
-                      expert_ids, ntpp, offsets_out, nullptr, active_out, num_active_out, counts);
+    align_body<0>(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity,
+                  expert_ids, ntpp, offsets_out, nullptr, active_out, num_active_out, nullptr);
     return;
   }
   constexpr int kGroupsPerAlignBlock = kAlignThreads / kLanesPerGroup;
@@ -259,20 +259,21 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_quant_kernel(
 }
 
 // As moe_align_quant_kernel, with the w4afp8 per-row quantiser (w4 order and
-// block corrections).  CPL > 0: a quant workgroup quantises one row per wave
+// block corrections; one launch measured 26.2 us at T=4096 against 22.1 + 8.6
+// for histograms + quantiser then placement).  CPL > 0: a quant workgroup quantises one row per wave
 // (cols <= 512 * CPL); CPL = 0: kAlignThreads / kRowThreads rows, one per
 // 256-thread part.
-template <int CPL, int PHASE>
+template <int CPL>
 __global__ __launch_bounds__(kAlignThreads) void moe_align_rowquant_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int align_groups, int E, int bs,
     const int32_t* __restrict__ map, int64_t map_len, int32_t* __restrict__ sorted, int64_t capacity,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ active_out, int32_t* __restrict__ num_active_out,
     const uint16_t* __restrict__ x, int64_t rows, int cols, uint8_t* __restrict__ xq,
-    float* __restrict__ xs, float* __restrict__ xcorr, int32_t* __restrict__ counts) {
+    float* __restrict__ xs, float* __restrict__ xcorr) {
   if (static_cast<int>(blockIdx.x) < align_groups) {
-    align_body<PHASE>(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity,
-                      expert_ids, ntpp, offsets_out, nullptr, active_out, num_active_out, counts);
+    align_body<0>(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity,
+                  expert_ids, ntpp, offsets_out, nullptr, active_out, num_active_out, nullptr);
     return;
   }
   if constexpr (CPL > 0) {
@@ -344,7 +345,7 @@ int align_and_group_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_ex
                               int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
                               int32_t* offsets, int32_t* active, int32_t* num_active,
                               const void* x, int64_t rows, int64_t cols, uint8_t* xq, float* xs,
-                              hipStream_t st, int32_t* counts) {
+                              hipStream_t st) {
   const char* who = "moe align + quant";
   VMAMD_REQUIRE(num_experts > 0 && num_experts <= kMaxAlignExperts && block_size > 0, "%s: bad sizes",
                 who);
@@ -364,21 +365,10 @@ int align_and_group_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_ex
   const int64_t num_groups = rows * groups_per_row;
   const int64_t qblocks = (num_groups + kAlignThreads / kLanesPerGroup - 1) / (kAlignThreads / kLanesPerGroup);
   const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0;  // rows of cols % 128 == 0 bf16 stay aligned
-  const bool two = counts != nullptr && groups > 1;
-  if (two)
-    moe_align_quant_kernel<1><<<static_cast<int>(groups + qblocks), kAlignThreads, 0, st>>>(
-        topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted,
-        capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),
-        groups_per_row, num_groups, vec, xq, xs, counts);
-  else
-    moe_align_quant_kernel<0><<<static_cast<int>(groups + qblocks), kAlignThreads, 0, st>>>(
-        topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted,
-        capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),
-        groups_per_row, num_groups, vec, xq, xs, nullptr);
-  int rc = check_launch(who);
-  if (rc || !two) return rc;
-  align_place(topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted, capacity,
-              expert_ids, ntpp, offsets, active, num_active, counts, st);
+  moe_align_quant_kernel<<<static_cast<int>(groups + qblocks), kAlignThreads, 0, st>>>(
+      topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted,
+      capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),
+      groups_per_row, num_groups, vec, xq, xs);
   return check_launch(who);
 }
 int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_experts,
@@ -386,7 +376,7 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
                             int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
                             int32_t* offsets, int32_t* active, int32_t* num_active, const void* x,
                             int64_t rows, int64_t cols, uint8_t* xq, float* xs, float* xcorr,
-                            hipStream_t st, int32_t* counts) {
+                            hipStream_t st) {
   const char* who = "moe align + row quant";
   VMAMD_REQUIRE(num_experts > 0 && num_experts <= kMaxAlignExperts && block_size > 0, "%s: bad sizes",
                 who);
@@ -413,27 +403,19 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
   const int rows_per_block = cpl > 0 ? kAlignThreads / kWave : kAlignThreads / kRowThreads;
   const int64_t qblocks = (rows + rows_per_block - 1) / rows_per_block;
   const dim3 grid(static_cast<unsigned>(groups + qblocks));
-  const bool two = counts != nullptr && groups > 1 && numel > 0;
-#define VMAMD_ARQ(C, PH)                                                                          \
-  moe_align_rowquant_kernel<C, PH><<<grid, kAlignThreads, 0, st>>>(                               \
+#define VMAMD_ARQ(C)                                                                              \
+  moe_align_rowquant_kernel<C><<<grid, kAlignThreads, 0, st>>>(                                   \
       topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted, \
       capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),     \
-      rows, static_cast<int>(cols), xq, xs, xcorr, counts)
-#define VMAMD_ARQ2(C) \
-  if (two) VMAMD_ARQ(C, 1); else VMAMD_ARQ(C, 0);
+      rows, static_cast<int>(cols), xq, xs, xcorr)
   switch (cpl) {
-    case 1: VMAMD_ARQ2(1); break;
-    case 2: VMAMD_ARQ2(2); break;
-    case 3: VMAMD_ARQ2(3); break;
-    case 4: VMAMD_ARQ2(4); break;
-    default: VMAMD_ARQ2(0); break;
+    case 1: VMAMD_ARQ(1); break;
+    case 2: VMAMD_ARQ(2); break;
+    case 3: VMAMD_ARQ(3); break;
+    case 4: VMAMD_ARQ(4); break;
+    default: VMAMD_ARQ(0); break;
   }
-#undef VMAMD_ARQ2
 #undef VMAMD_ARQ
-  int rc = check_launch(who);
-  if (rc || !two) return rc;
-  align_place(topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted, capacity,
-              expert_ids, ntpp, offsets, active, num_active, counts, st);
   return check_launch(who);
 }
 }  // namespace vmamd
@@ -484,5 +466,5 @@ extern "C" int vmamd_moe_align_block_size_quant_fp8(const int32_t* topk_ids, int
   return align_and_group_quant_fp8(topk_ids, numel, num_experts, block_size, expert_map, expert_map_len,
                                    sorted_token_ids, capacity, expert_ids, num_tokens_post_pad, expert_offsets,
                                    active_experts, num_active, x, rows, cols, static_cast<uint8_t*>(xq), xs,
-                                   reinterpret_cast<hipStream_t>(stream), nullptr);
+                                   reinterpret_cast<hipStream_t>(stream));
 }

@@ -28,15 +28,13 @@ int check_launch(const char* what);
 
 // moe_align_block_size and the 1x128 fp8 quantiser of bf16 activations
 // x [rows, cols] (into xq [rows, cols], xs [rows, cols / 128]) as one launch
-// (align.hip).  counts (align_counts_bytes, or null): scratch for the chunk
-// histograms, with which the alignment takes a second, placement launch
-// instead of every workgroup histogramming all routes.
+// (align.hip).
 int align_and_group_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_experts,
                               int block_size, const int32_t* expert_map, int64_t expert_map_len,
                               int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
                               int32_t* offsets, int32_t* active, int32_t* num_active,
                               const void* x, int64_t rows, int64_t cols, uint8_t* xq, float* xs,
-                              hipStream_t st, int32_t* counts = nullptr);
+                              hipStream_t st);
 // The same with the w4afp8 per-row quantiser (eps 1e-4): xs [rows]; xq in
 // w4 order with the block corrections xcorr [rows, cols / 128] (cols a
 // multiple of 128).
@@ -45,8 +43,10 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
                             int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
                             int32_t* offsets, int32_t* active, int32_t* num_active, const void* x,
                             int64_t rows, int64_t cols, uint8_t* xq, float* xs, float* xcorr,
-                            hipStream_t st, int32_t* counts = nullptr);
-// moe_align_block_size alone, with the chunk-histogram scratch as above.
+                            hipStream_t st);
+// moe_align_block_size alone; with counts (align_counts_bytes of scratch)
+// in two launches, the chunk histograms then the placement, instead of every
+// workgroup histogramming all routes.
 int align_routes(const int32_t* topk_ids, int64_t numel, int num_experts, int block_size,
                  const int32_t* expert_map, int64_t expert_map_len, int32_t* sorted, int64_t capacity,
                  int32_t* expert_ids, int32_t* ntpp, int32_t* offsets, int32_t* active, int32_t* num_active,

@@ -2471,7 +2471,7 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   w.offs = take((E + 1) * 4);
   w.active = take(E * 4);
   w.nact = take(4);
-  w.acnt = take(align_counts_bytes(numel, E));
+  if (kind == kBf16 || kind == kW8A16) w.acnt = take(align_counts_bytes(numel, E));  // align_routes
   const int64_t arows = bm == kGemvBlock ? numel : cap;  // route order (decode) or padded order
   if (kind == kW4) w.abf = take(arows * I * 2);
   w.a2 = take(arows * I * (kind == kBf16 || kind == kW8A16 ? 2 : 1));
@@ -2732,8 +2732,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     uint8_t* xq = ws + L.xq;
     float* xsw = reinterpret_cast<float*>(ws + L.xs);
     rc = align_and_group_quant_fp8(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
-                                   eids, ntpp, offs, active, nact, x, T, H, xq, xsw, st,
-                                   reinterpret_cast<int32_t*>(ws + L.acnt));
+                                   eids, ntpp, offs, active, nact, x, T, H, xq, xsw, st);
     if (rc) return rc;
     xa = xq;
     xs = xsw;
@@ -2741,8 +2740,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     uint8_t* xq = ws + L.xq;
     float* xsw = reinterpret_cast<float*>(ws + L.xs);
     rc = align_and_row_quant_fp8(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
-                                 eids, ntpp, offs, active, nact, x, T, H, xq, xsw, xcorr, st,
-                                 reinterpret_cast<int32_t*>(ws + L.acnt));
+                                 eids, ntpp, offs, active, nact, x, T, H, xq, xsw, xcorr, st);
     if (rc) return rc;
     xa = xq;
     xs = xsw;
