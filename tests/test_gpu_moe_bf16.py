@@ -251,3 +251,52 @@ def test_bf16_moe_rejects_scales():
     w, ids = _routing(2, 4, 2, 43)
     with pytest.raises(ValueError):
         fused_experts_impl(x, w13, w2, w, ids, w1_scale=torch.ones(1, device=DEV))
+
+
+@pytest.mark.parametrize("H,I,K", [(2048, 256, 8), (1024, 512, 4)])
+def test_bf16_direct_decode_fused_activation_split_counts(H, I, K):
+    """One token: the W13 launch writes the bf16 activation itself, one
+    workgroup per (route, 16 columns) holding 2 x splits waves (H=2048,
+    I=256: 8 splits, 16 waves; H=1024, I=512: 4 splits), summed in split
+    order in LDS.  H=1024, I=512, top-4 also splits the grouped W2 GEMV's K
+    in two, which the one-token W2 + top-k sum follows at the split
+    boundary.  Bit for bit the grouped decode stages, and the oracle."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.fused_moe import MoeStages
+    E = 16
+    w13, w2 = _weights(E, H, I, 91 + H)
+    x = synthetic.activations(1, H, 92)
+    w, ids = _routing(1, E, K, 93)
+    st = MoeStages(x, w13, None, w2, None, w, ids, path="gemv")
+    grouped = st.run().clone()
+    direct = _run(x, w13, w2, w, ids, "gemv")
+    assert torch.equal(direct, grouped)
+    _check(direct, _oracle(x, w13, w2, w, ids))
+
+
+@pytest.mark.parametrize("variant", ["plain", "expert_map"])
+def test_bf16_layer_two_launch_alignment_long_batch(variant):
+    """The bf16 layer aligns its routes in two launches (chunk histograms in
+    the workspace, then the placement); at 320,000 routes each workgroup
+    places 2048 of them.  Bit for bit the stage-by-stage call, whose
+    alignment is the one-launch standalone kernel; rows of the oracle."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.fused_moe import MoeStages
+    E, H, I, K, T = 16, 256, 128, 8, 40000
+    w13, w2 = _weights(E, H, I, 94)
+    x = synthetic.activations(T, H, 95)
+    w, ids = _routing(T, E, K, 96)
+    emap = None
+    if variant == "expert_map":  # global ids 0..23, local experts = global 8..23; ids 0..7 dropped
+        g = torch.Generator().manual_seed(97)
+        ids = torch.stack([torch.randperm(24, generator=g)[:K] for _ in range(T)]).to(torch.int32).to(DEV)
+        emap = torch.full((24,), -1, dtype=torch.int32)
+        emap[8:] = torch.arange(16, dtype=torch.int32)
+        emap = emap.to(DEV)
+    from vllm_musa_amd.fused_moe import fused_experts_impl
+    out = fused_experts_impl(x, w13, w2, w, ids, expert_map=emap, path="gemm", chunk_size=T)
+    st = MoeStages(x, w13, None, w2, None, w, ids, path="gemm", expert_map=emap)
+    assert torch.equal(out, st.run())
+    rows = np.array([0, 1, 19999, 20000, T - 1])
+    ref = _oracle(x[rows], w13, w2, w[rows], ids[rows], emap=emap)
+    _check(out[rows], ref)

@@ -290,8 +290,10 @@ moe_gemv_kernel(
   const int64_t wrowb = static_cast<int64_t>(KS) * KB_::kW;
   const int NB = (N + 127) / 128;
   const int groups = (KS + kGemvU - 1) / kGemvU;  // splits start on group boundaries
-  const int kb0 = split * groups / splits * kGemvU;
-  const int kb1 = min((split + 1) * groups / splits * kGemvU, KS);
+  // The combine runs all of K in one chain (splits: the grouped W2 path's
+  // count, at most groups, so no split is empty).
+  const int kb0 = kComb ? 0 : split * groups / splits * kGemvU;
+  const int kb1 = kComb ? KS : min((split + 1) * groups / splits * kGemvU, KS);
   const int n = ntile * 16 + 4 * lg;
   const uint8_t* wrow = w + (static_cast<int64_t>(e) * N + ntile * 16 + li) * wrowb;
   const float* wsr = nullptr;                        // kFp8 / kW8A16: block scales of the 16 rows
@@ -361,6 +363,23 @@ moe_gemv_kernel(
   };
   uint32_t aoff[MAXB];  // byte offset of each block's activation row (kBufferOff: padding)
   v4f acc[MAXB];
+  // kGemvCombine: at each split boundary of the grouped W2 GEMV the split's
+  // accumulator (times kW4Unit for kW4, as its partials) joins the sum of the
+  // finished splits, added in split order as moe_w2_reduce_kernel adds them,
+  // and the next split starts from zero.  Boundaries fall on group starts.
+  v4f tot = zero;
+  int cut = kComb && splits > 1 ? groups / splits * kGemvU : KS, cuts = 1;
+  auto fold = [&](int kb) {
+    if constexpr (kComb) {
+      if (kb == cut) {  // uniform
+        const v4f a = KIND == kW4 ? acc[0] * kW4Unit : acc[0];
+        tot = cuts == 1 ? a : tot + a;
+        acc[0] = zero;
+        ++cuts;
+        cut = cuts < splits ? cuts * groups / splits * kGemvU : KS;
+      }
+    }
+  };
   // Activation loads and MFMAs of the group at kb with the weights in wf.
   // Steps past the split's end take masked (zero) activations, so the group
   // has no branches: their products are exactly zero.
@@ -462,6 +481,7 @@ moe_gemv_kernel(
     }
     for (int kb = kbs; kb < kb1; kb += U) {
       const bool more = kb + U < kb1;  // uniform
+      fold(kb);
       // This group's vector-loaded scales, then the next group's requests.
       float sbc[U];
       uint2 swc[4];
@@ -590,6 +610,7 @@ moe_gemv_kernel(
       group(kb0, nb);
       for (int kb = kb0 + U; kb < kb1; kb += U) {
         load_w(kb);
+        fold(kb);
         group(kb, nb);
       }
     }
@@ -611,6 +632,10 @@ moe_gemv_kernel(
     }
     b0 += MAXB;
   } while (b0 < nblk);
+  if constexpr (kComb) {  // the last split
+    const v4f a = KIND == kW4 ? acc[0] * kW4Unit : acc[0];
+    tot = cuts == 1 ? a : tot + a;
+  }
   if constexpr (kAct) {
     // Gate / up sums over the splits in split order, times route_w (null:
     // times 1, exact), then the activation of the decode activation kernels:
@@ -655,10 +680,9 @@ moe_gemv_kernel(
     __shared__ float part[kMaxCombineSlots * 16];
     __shared__ int live[kMaxCombineSlots];
     if (li == 0 && !dead) {
-      const v4f a = KIND == kW4 ? acc[0] * kW4Unit : acc[0];
       const float rw = route_w ? route_w[slot] : 1.0f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) part[wave * 16 + 4 * lg + q] = bf16r(a[q] * rw);
+      for (int q = 0; q < 4; ++q) part[wave * 16 + 4 * lg + q] = bf16r(tot[q] * rw);
     }
     if (lane == 0) live[wave] = dead ? 0 : 1;
     __syncthreads();
@@ -2506,7 +2530,9 @@ static bool direct_act(int kind, int s13) {
   return (kind == kBf16 || kind == kW8A16) && s13 <= gemv_waves(kGemvDirectAct, kind) / 2;
 }
 
-// The W2 GEMV of one token with the top-k sum (kGemvCombine).
+// The W2 GEMV of one token with the top-k sum (kGemvCombine), over the K
+// splits the grouped W2 GEMV takes for the same routes, so that the sums are
+// its bits.
 template <int KIND>
 static int launch_combine(const uint8_t* a2, const float* a2s, const float* a2corr, int T, int H, int I, int numel,
                           int topk, const uint8_t* w2, const void* w2_s, const float* topk_weights,
@@ -2517,8 +2543,9 @@ static int launch_combine(const uint8_t* a2, const float* a2s, const float* a2co
   const float* yscale = KIND == kW4 ? a2s : w2_rw;
   launch_gemv_direct<KIND, kGemvCombine>(
       dim3(H / 16, T, 1), topk * kWave, 0, st, gemv_vector_scales<KIND>(I, a2_act_s, w2_s), a2,
-      gemv_act_bytes<KIND>(numel, I), a2_act_s, 1, I, none, none, none, none, w2, w2_s, H, numel, 1,
-      static_cast<float*>(nullptr), yscale, static_cast<uint16_t*>(nullptr), topk_ids, emap, emap_len, E, out,
+      gemv_act_bytes<KIND>(numel, I), a2_act_s, 1, I, none, none, none, none, w2, w2_s, H, numel,
+      w2_splits(numel, E, H, I, KIND), static_cast<float*>(nullptr), yscale, static_cast<uint16_t*>(nullptr),
+      topk_ids, emap, emap_len, E, out,
       KIND == kW4 ? topk_weights : static_cast<const float*>(nullptr), static_cast<float*>(nullptr), 0.f, 0);
   return check_launch("moe w2 (gemv + top-k sum)");
 }
