@@ -1490,15 +1490,31 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
 // holds a few dozen routes yet streams the expert's whole weight tile.  fp8
 // keeps 256 routes (the promotion's registers leave no room for a fifth
 // m-tile: 256 VGPRs, and W13 at T=4096 measured 12 % slower).
+//
+// A block whose live routes fit in kRows3 = 160 rows (an expert's only
+// block at up to 160 routes, or its last one) runs a three-stage ring
+// instead (fp8): its activation slot holds 160 rows, so three stages fit in
+// the LDS and two K steps are in flight while one is computed.  Such a tile
+// is bound by the latency of its weight stream, not by its few MFMAs.
+template <int MTV, int NS>
+struct MoeBigRing {
+  static constexpr int kNS = NS;
+  static constexpr int kRowsA = NS == 2 ? 64 * MTV : 160;  // activation slot rows
+  static constexpr int kOffB = kRowsA * 128;
+  static constexpr int kOffSA = kOffB + 256 * 128;
+  static constexpr int kOffSB = kOffSA + 64 * MTV * 4;  // waves 0 .. BM/64 - 1 write 64 A scales each
+  static constexpr int kStage = kOffSB + 256;           // the B-scale DMA writes 64 lanes x 4 bytes
+};
 template <int MTV>
 struct MoeBigTile {
   static constexpr int BM = 64 * MTV, BN = 256, WN = 2, MT = MTV, NT = 8, WTM = 16 * MTV, kThreads = 512;
-  static constexpr int kOffB = BM * 128;
-  static constexpr int kOffSA = (BM + BN) * 128;
-  static constexpr int kOffSB = kOffSA + BM * 4;
-  static constexpr int kStage = kOffSB + 256;  // the B-scale DMA writes 64 lanes x 4 bytes
-  // Two stages, or the W2 output tile staged for its stores if that is larger.
-  static constexpr int kLds = 2 * kStage > BM * 512 ? 2 * kStage : BM * 512;
+  using R2 = MoeBigRing<MTV, 2>;
+  using R3 = MoeBigRing<MTV, 3>;
+  static constexpr bool kRing3 = MTV == 4;  // (fp8 only, chosen in the kernel)
+  static constexpr int kRows3 = R3::kRowsA;
+  // The ring's stages, or the W2 output tile staged for its stores if that is larger.
+  static constexpr int kRingLds = kRing3 && 3 * R3::kStage > 2 * R2::kStage ? 3 * R3::kStage : 2 * R2::kStage;
+  static constexpr int kLds = kRingLds > BM * 512 ? kRingLds : BM * 512;
   static_assert(kLds <= 160 * 1024, "LDS stages exceed the CU's LDS");
 };
 constexpr int kMoeBigBM = 256, kMoeBig320 = 320;
@@ -1557,29 +1573,36 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
 #pragma unroll
   for (int j = 0; j < 4; ++j) offB[j] = static_cast<uint32_t>(wrow((wave + 8 * j) * 8 + lane / 8)) * rowb + chunk;
   uint32_t offS = 0, stepS = 4;
-  int ldsS = 0;
+  const bool sa_wave = wave < BM / 64;
   __amdgpu_buffer_rsrc_t rs = buffer_rsrc(act_s, 0);
   if (!kScaled) {
-  } else if (wave < BM / 64) {  // activation scales of tile rows 64 * wave + lane
+  } else if (sa_wave) {  // activation scales of tile rows 64 * wave + lane
     rs = buffer_rsrc(act_s, act_s_bytes);
     offS = static_cast<uint32_t>(arow(64 * wave + lane)) * KS * 4;
-    ldsS = P::kOffSA + 64 * wave * 4;
   } else {  // weight-block scales: W13 gate / up block, W2 the tile's two 128-row blocks
     const int slot = min(lane, 1);
     const int brow = W13 ? (slot ? (I + n0) / 128 : n0 / 128) : min(n0 / 128 + slot, NB - 1);
     rs = buffer_rsrc(ws, E * NB * KS * 4);
     offS = static_cast<uint32_t>((e * NB + brow) * KS) * 4;
-    ldsS = P::kOffSB;
   }
-  auto issue = [&](uint8_t* stage, int step) {
+  // One stage of the ring R (the activation row groups that hold a route,
+  // the weight rows, the scales).
+  auto issue = [&](uint8_t* stage, int step, auto ring) {
+    using R = decltype(ring);
     const uint32_t ks = static_cast<uint32_t>(step) * 128;
 #pragma unroll
     for (int j = 0; j < MT; ++j)
       if (liveA[j]) buffer_dma16(ra, offA[j] + ks, stage + (wave + 8 * j) * 8 * 128);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) buffer_dma16(rb, offB[j] + ks, stage + P::kOffB + (wave + 8 * j) * 8 * 128);
-    if (kScaled && wave <= BM / 64) buffer_dma4(rs, offS + step * stepS, stage + ldsS);
+    for (int j = 0; j < 4; ++j) buffer_dma16(rb, offB[j] + ks, stage + R::kOffB + (wave + 8 * j) * 8 * 128);
+    if (kScaled && wave <= BM / 64)
+      buffer_dma4(rs, offS + step * stepS, stage + (sa_wave ? R::kOffSA + 64 * wave * 4 : R::kOffSB));
   };
+  // This wave's loads per stage, for the three-stage ring's vmcnt.
+  int dmas = 4 + (kScaled && wave <= BM / 64 ? 1 : 0);
+#pragma unroll
+  for (int j = 0; j < MT; ++j) dmas += liveA[j] ? 1 : 0;
+  dmas = __builtin_amdgcn_readfirstlane(dmas);
   // Padding routes close a block, so the wave's 16-route m-tiles that hold a
   // route are a prefix: mlive of them (0: the wave holds none and skips its
   // MFMAs).  The MFMAs of the m-tiles past it are skipped too (their
@@ -1602,17 +1625,18 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   // ML m-tiles.  W13: n tile nt takes the gate (even) or up (odd) block
   // scale.  bf16: two chained MFMAs per fragment pair into the accumulators,
   // no scales.
-  auto mma = [&](const uint8_t* st, auto ml_tag) {
+  auto mma = [&](const uint8_t* st, auto ml_tag, auto ring) {
     constexpr int ML = decltype(ml_tag)::value;
+    using R = decltype(ring);
     float sb0 = 0.f, sb1 = 0.f, sa[MT], sc[MT][2];
     if constexpr (kScaled) {
-      sb0 = lds_load<float>(st, P::kOffSB + (W13 ? 0 : 4 * wn));
-      sb1 = W13 ? lds_load<float>(st, P::kOffSB + 4) : sb0;
+      sb0 = lds_load<float>(st, R::kOffSB + (W13 ? 0 : 4 * wn));
+      sb1 = W13 ? lds_load<float>(st, R::kOffSB + 4) : sb0;
 #pragma unroll
-      for (int mt = 0; mt < ML; ++mt) sa[mt] = lds_load<float>(st, P::kOffSA + (wm * P::WTM + mt * 16 + li) * 4);
+      for (int mt = 0; mt < ML; ++mt) sa[mt] = lds_load<float>(st, R::kOffSA + (wm * P::WTM + mt * 16 + li) * 4);
     }
     v8i wf[2], x[MT];
-    wf[0] = lds_frag(st + P::kOffB, nw + li, lg);
+    wf[0] = lds_frag(st + R::kOffB, nw + li, lg);
 #pragma unroll
     for (int mt = 0; mt < ML; ++mt) x[mt] = lds_frag(st, wm * P::WTM + mt * 16 + li, lg);
     __builtin_amdgcn_sched_barrier(0);
@@ -1627,7 +1651,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
         else
           acc[mt][nt] = mfma_bf16x2(wf[nt & 1], x[mt], acc[mt][nt]);
         __builtin_amdgcn_sched_barrier(0);
-        if (mt == 0 && nt + 1 < NT) wf[(nt + 1) & 1] = lds_frag(st + P::kOffB, nw + (nt + 1) * 16 + li, lg);
+        if (mt == 0 && nt + 1 < NT) wf[(nt + 1) & 1] = lds_frag(st + R::kOffB, nw + (nt + 1) * 16 + li, lg);
       }
       __builtin_amdgcn_sched_barrier(0);
       if (kScaled && i > 0) {
@@ -1639,16 +1663,42 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     }
   };
 
-  // The K loop, one copy per live m-tile count (ML = 0: DMAs and barriers only).
-  auto kloop = [&](auto ml_tag) {
+  // The K loop, one copy per live m-tile count (ML = 0: DMAs and barriers
+  // only) and ring.  Two stages: one K step in flight while the other is
+  // computed.  Three: two in flight; before step kb a wave waits until only
+  // its loads of step kb + 1 are outstanding (dmas per stage; past the last
+  // issued stage, none).
+  auto kloop = [&](auto ml_tag, auto ring) {
     constexpr int ML = decltype(ml_tag)::value;
-    issue(smem_dyn, 0);
+    using R = decltype(ring);
+    constexpr int NS = R::kNS;
+    issue(smem_dyn, 0, ring);
+    if constexpr (NS == 3) {
+      if (KS > 1) issue(smem_dyn + R::kStage, 1, ring);
+    }
     wait_lgkmcnt0();
+    int cur = 0;  // stage of step kb
     for (int kb = 0; kb < KS; ++kb) {
-      wait_vmcnt<0>();  // this wave's DMAs of step kb have landed
-      barrier_lds();    // ... every wave's, and step kb - 1's buffer is no longer read
-      if (kb + 1 < KS) issue(smem_dyn + ((kb + 1) & 1) * P::kStage, kb + 1);
-      if constexpr (ML > 0) mma(smem_dyn + (kb & 1) * P::kStage, ml_tag);
+      if constexpr (NS == 2) {
+        wait_vmcnt<0>();  // this wave's DMAs of step kb have landed
+      } else if (kb + 1 < KS) {
+        switch (dmas) {  // wave-uniform
+          case 4: wait_vmcnt<4>(); break;
+          case 5: wait_vmcnt<5>(); break;
+          case 6: wait_vmcnt<6>(); break;
+          case 7: wait_vmcnt<7>(); break;
+          case 8: wait_vmcnt<8>(); break;
+          case 9: wait_vmcnt<9>(); break;
+          default: wait_vmcnt<0>(); break;
+        }
+      } else {
+        wait_vmcnt<0>();
+      }
+      barrier_lds();  // ... every wave's, and step kb - 1's buffer is no longer read
+      const int nxt = cur + NS - 1 >= NS ? cur - 1 : cur + NS - 1;  // stage of step kb + NS - 1
+      if (kb + NS - 1 < KS) issue(smem_dyn + nxt * R::kStage, kb + NS - 1, ring);
+      if constexpr (ML > 0) mma(smem_dyn + cur * R::kStage, ml_tag, ring);
+      cur = cur + 1 == NS ? 0 : cur + 1;
     }
   };
   using I0 = std::integral_constant<int, 0>;
@@ -1658,18 +1708,29 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   using I4 = std::integral_constant<int, 4>;
   using I5 = std::integral_constant<int, 5>;
   static_assert(MT == 4 || MT == 5, "m-tiles per wave");
-  if (MT == 5 && mlive >= 5) {
-    if constexpr (MT == 5) kloop(I5{});
-  } else if (mlive >= 4) {
-    kloop(I4{});
-  } else if (mlive == 3) {
-    kloop(I3{});
-  } else if (mlive == 2) {
-    kloop(I2{});
-  } else if (mlive == 1) {
-    kloop(I1{});
+  auto run = [&](auto ring) {
+    if (MT == 5 && mlive >= 5) {
+      if constexpr (MT == 5) kloop(I5{}, ring);
+    } else if (mlive >= 4) {
+      kloop(I4{}, ring);
+    } else if (mlive == 3) {
+      kloop(I3{}, ring);
+    } else if (mlive == 2) {
+      kloop(I2{}, ring);
+    } else if (mlive == 1) {
+      kloop(I1{}, ring);
+    } else {
+      kloop(I0{}, ring);
+    }
+  };
+  // Padding closes the block, so its live routes fit the three-stage ring's
+  // activation slot when row kRows3 is padding (workgroup-uniform).
+  bool ring3 = false;
+  if constexpr (kScaled && P::kRing3) ring3 = __builtin_amdgcn_readfirstlane(sorted[base + P::kRows3] >= numel ? 1 : 0) != 0;
+  if (ring3) {
+    if constexpr (kScaled && P::kRing3) run(typename P::R3{});
   } else {
-    kloop(I0{});
+    run(typename P::R2{});
   }
   barrier_lds();  // every wave is done with the stages before LDS is reused
 
