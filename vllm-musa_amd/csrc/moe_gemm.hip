@@ -781,12 +781,11 @@ __global__ __launch_bounds__(256) void moe_act_quant_kernel(const float* __restr
   amax = group_max<16>(amax);
   const float scale = amax / 448.0f;
   if (sub == 0) a2s[static_cast<int64_t>(r) * gpr + c0 / 128] = scale;
-  float q[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) q[j] = v[j] != v[j] ? -448.0f : fminf(fmaxf(v[j] / scale, -448.0f), 448.0f);
+  const float rs = 1.0f / scale;
+  const float lo[4] = {v[0], v[1], v[2], v[3]}, hi[4] = {v[4], v[5], v[6], v[7]};
   uint2 out;
-  out.x = f32x4_to_fp8x4(q[0], q[1], q[2], q[3]);
-  out.y = f32x4_to_fp8x4(q[4], q[5], q[6], q[7]);
+  out.x = quant4_e4m3(lo, scale, rs);
+  out.y = quant4_e4m3(hi, scale, rs);
   *reinterpret_cast<uint2*>(a2q + static_cast<int64_t>(r) * I + c0) = out;
 }
 
@@ -1418,19 +1417,13 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
         float amax = 1e-10f;
 #pragma unroll
         for (int w4 = 0; w4 < WN; ++w4) amax = fmaxf(amax, red[w4 * BM + ml]);
-        const float scale = amax / 448.0f;
+        const float scale = amax / 448.0f, rs = 1.0f / scale;
         const int64_t row = static_cast<int64_t>(mb) * BM + ml;
         if (wn == 0 && lg == 0) a2s[row * gpr + tn] = scale;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-          float o[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float x = v[mt][q][r];
-            o[r] = x != x ? -448.0f : fminf(fmaxf(x / scale, -448.0f), 448.0f);
-          }
           const int col = n0 + (wn * 2 + q) * 16 + 4 * lg;
-          *reinterpret_cast<uint32_t*>(a2 + row * I + col) = f32x4_to_fp8x4(o[0], o[1], o[2], o[3]);
+          *reinterpret_cast<uint32_t*>(a2 + row * I + col) = quant4_e4m3(v[mt][q], scale, rs);
         }
       }
     } else {
@@ -1787,19 +1780,13 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     for (int mt = 0; mt < MT; ++mt) {
       const int ml = wm * P::WTM + mt * 16 + li;
       const float amax = fmaxf(1e-10f, fmaxf(red[ml], red[BM + ml]));
-      const float scale = amax / 448.0f;
+      const float scale = amax / 448.0f, rs = 1.0f / scale;
       const int64_t row = base + ml;
       if (wn == 0 && lg == 0) a2s[row * gpr + tn] = scale;
 #pragma unroll
       for (int q = 0; q < NT / 2; ++q) {
-        float o[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float xv = v[mt][q][r];
-          o[r] = xv != xv ? -448.0f : fminf(fmaxf(xv / scale, -448.0f), 448.0f);
-        }
         const int col = n0 + (4 * wn + q) * 16 + 4 * lg;
-        *reinterpret_cast<uint32_t*>(a2 + row * I + col) = f32x4_to_fp8x4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint32_t*>(a2 + row * I + col) = quant4_e4m3(v[mt][q], scale, rs);
       }
     }
   } else {

@@ -40,8 +40,14 @@ __device__ __forceinline__ void load8(const typename Elem<DT>::T* p, bool vec, f
 
 __device__ __forceinline__ uint2 quant8(const float (&v)[8], float s, float qmin, float qmax) {
   float q[8];
+  if (s < __builtin_inff()) {  // one division for the eight quotients (div_rn)
+    const float r = 1.0f / s;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = fminf(fmaxf(v[i] / s, qmin), qmax);
+    for (int i = 0; i < 8; ++i) q[i] = fminf(fmaxf(div_rn(v[i], s, r), qmin), qmax);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = fminf(fmaxf(v[i] / s, qmin), qmax);
+  }
   uint2 out;
   out.x = f32x4_to_fp8x4(q[0], q[1], q[2], q[3]);
   out.y = f32x4_to_fp8x4(q[4], q[5], q[6], q[7]);
