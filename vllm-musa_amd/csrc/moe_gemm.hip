@@ -68,7 +68,13 @@ template <int KIND> struct KindOps {
 };
 
 // --------------------------------------------------------------- helpers --
-__device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+// x rounded to bf16 (nearest even) and back: v_cvt_pk_bf16_f32, the rounding
+// of f32_to_bf16 for every number in one instruction (a NaN stays a NaN,
+// with the hardware's payload; outputs go through f32_to_bf16).
+__device__ __forceinline__ float bf16r(float x) {
+  const __bf16 h = static_cast<__bf16>(x);
+  return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h)) << 16);
+}
 
 // SiLU-and-mul on bf16-materialised gate/up; limit > 0 applies the clamped
 // variant (gate <= L, up in [-L, L], sigmoid / silu / product each rounded to
