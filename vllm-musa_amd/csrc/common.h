@@ -75,12 +75,21 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
 }
 
 // Round-to-nearest-even float -> bf16 bits; NaN maps to the canonical quiet
-// NaN 0x7fc0 (the same rule torch uses on the CPU).
+// NaN 0x7fc0 (the same rule torch uses on the CPU).  v_cvt_pk_bf16_f32 after
+// replacing a NaN by 0x7fc00000: equal to the integer form (add 0x7fff plus
+// the lowest kept bit, keep the top half; NaN -> 0x7fc0) on all 2^32 inputs,
+// checked exhaustively on an MI355X.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const float g = f != f ? __uint_as_float(0x7fc00000u) : f;
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(g));
+}
+// Two at once (a in the low half): one conversion instruction for both.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const float qn = __uint_as_float(0x7fc00000u);
+  const f32x2_t v = {a != a ? qn : a, b != b ? qn : b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {

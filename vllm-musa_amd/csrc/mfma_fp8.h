@@ -160,8 +160,8 @@ __device__ __forceinline__ void fma4v(v4f& acc, const v4f& p, const v4f& s) {
 
 __device__ __forceinline__ uint2 pack_bf16x4(float a, float b, float c, float d) {
   uint2 r;
-  r.x = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
-  r.y = static_cast<uint32_t>(f32_to_bf16(c)) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16);
+  r.x = f32x2_to_bf16x2(a, b);
+  r.y = f32x2_to_bf16x2(c, d);
   return r;
 }
 
