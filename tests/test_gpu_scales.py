@@ -72,6 +72,27 @@ def test_convert_scales_bit_exact(src, dst, n, offset):
         assert float(dbuf[0]) == 7.0  # nothing written before the destination
 
 
+def test_convert_f32_to_bf16_every_rounding_class():
+    """f32 -> bf16 on every upper half (sign, exponent, 7 kept mantissa bits)
+    with the lower halves that decide the rounding: exact, just below, at
+    and just above the tie, the largest, and random ones -- NaN payloads,
+    infinities, subnormals and carries into the exponent included (the
+    kernels' conversion instruction against the integer rounding rule)."""
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    rng = np.random.default_rng(5)
+    lows = [0x0000, 0x7FFF, 0x8000, 0x8001, 0xFFFF, 0x0001]
+    bits = np.concatenate([hi | np.uint32(lo) for lo in lows] +
+                          [hi | rng.integers(0, 1 << 16, hi.size, dtype=np.uint32)])
+    a = bits.view(np.float32)
+    want, want_bad = osc.convert_scales(a, "f32", "bf16")
+    d = torch.empty(a.size, dtype=torch.bfloat16, device=DEV)
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    from vllm_musa_amd import _custom_ops as ops
+    ops.convert_scales(torch.from_numpy(a).to(DEV), d, bad)
+    assert np.array_equal(_bits(d), want)
+    assert int(bad.item()) == want_bad
+
+
 def test_convert_scales_aliasing_and_empty():
     from vllm_musa_amd import _custom_ops as ops
     x = torch.rand(1000, device=DEV) + 0.5
