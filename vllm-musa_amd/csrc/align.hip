@@ -263,6 +263,29 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_quant_kernel(
 // for histograms + quantiser then placement).  CPL > 0: a quant workgroup quantises one row per wave
 // (cols <= 512 * CPL); CPL = 0: kAlignThreads / kRowThreads rows, one per
 // 256-thread part.
+// One thread per row of a W4ScalesT matrix (row n of expert e: kp words in,
+// word p to out[e][p][n]): the row read 8 bytes at a time, each word
+// written where the threads of neighbouring rows write its neighbours.
+__device__ __forceinline__ void w4_scales_t_rows(const W4ScalesT& t, int64_t g) {
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int64_t nrow = static_cast<int64_t>(t.E) * t.n[m];
+    if (t.in[m] && g < nrow) {
+      const int kp = t.kp[m], n = t.n[m];
+      const int64_t e = g / n, r = g - e * n;
+      const uint2* src = reinterpret_cast<const uint2*>(t.in[m] + g * kp);
+      uint32_t* dst = t.out[m] + e * kp * n + r;
+      for (int p = 0; p < kp; p += 2) {
+        const uint2 v = src[p / 2];
+        dst[static_cast<int64_t>(p) * n] = v.x;
+        dst[static_cast<int64_t>(p + 1) * n] = v.y;
+      }
+      return;
+    }
+    if (t.in[m]) g -= nrow;
+  }
+}
+
 template <int CPL>
 __global__ __launch_bounds__(kAlignThreads) void moe_align_rowquant_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int64_t chunk, int align_groups, int E, int bs,
@@ -270,10 +293,15 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_rowquant_kernel(
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int32_t* __restrict__ offsets_out,
     int32_t* __restrict__ active_out, int32_t* __restrict__ num_active_out,
     const uint16_t* __restrict__ x, int64_t rows, int cols, uint8_t* __restrict__ xq,
-    float* __restrict__ xs, float* __restrict__ xcorr) {
+    float* __restrict__ xs, float* __restrict__ xcorr, int quant_groups, W4ScalesT sct) {
   if (static_cast<int>(blockIdx.x) < align_groups) {
     align_body<0>(blockIdx.x, align_groups, ids, numel, chunk, E, bs, map, map_len, sorted, capacity,
                   expert_ids, ntpp, offsets_out, nullptr, active_out, num_active_out, nullptr);
+    return;
+  }
+  if (static_cast<int>(blockIdx.x) >= align_groups + quant_groups) {  // the scale transpositions
+    w4_scales_t_rows(sct, static_cast<int64_t>(blockIdx.x - align_groups - quant_groups) * kAlignThreads +
+                              threadIdx.x);
     return;
   }
   if constexpr (CPL > 0) {
@@ -376,7 +404,7 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
                             int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
                             int32_t* offsets, int32_t* active, int32_t* num_active, const void* x,
                             int64_t rows, int64_t cols, uint8_t* xq, float* xs, float* xcorr,
-                            hipStream_t st) {
+                            hipStream_t st, const W4ScalesT* sct) {
   const char* who = "moe align + row quant";
   VMAMD_REQUIRE(num_experts > 0 && num_experts <= kMaxAlignExperts && block_size > 0, "%s: bad sizes",
                 who);
@@ -402,12 +430,24 @@ int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_expe
   const int cpl = cpl0 <= 4 ? cpl0 : 0;
   const int rows_per_block = cpl > 0 ? kAlignThreads / kWave : kAlignThreads / kRowThreads;
   const int64_t qblocks = (rows + rows_per_block - 1) / rows_per_block;
-  const dim3 grid(static_cast<unsigned>(groups + qblocks));
+  W4ScalesT t{};
+  int64_t trows = 0;
+  if (sct) {
+    t = *sct;
+    for (int m = 0; m < 2; ++m) {
+      VMAMD_REQUIRE(!t.in[m] || (t.out[m] && t.kp[m] > 0 && t.kp[m] % 2 == 0 &&
+                                 reinterpret_cast<uintptr_t>(t.in[m]) % 8 == 0),
+                    "%s: weight scales must be 8-byte aligned with an even count of word pairs per row", who);
+      if (t.in[m]) trows += static_cast<int64_t>(t.E) * t.n[m];
+    }
+  }
+  const int64_t tblocks = (trows + kAlignThreads - 1) / kAlignThreads;
+  const dim3 grid(static_cast<unsigned>(groups + qblocks + tblocks));
 #define VMAMD_ARQ(C)                                                                              \
   moe_align_rowquant_kernel<C><<<grid, kAlignThreads, 0, st>>>(                                   \
       topk_ids, numel, chunk, groups, num_experts, block_size, expert_map, expert_map_len, sorted, \
       capacity, expert_ids, ntpp, offsets, active, num_active, static_cast<const uint16_t*>(x),     \
-      rows, static_cast<int>(cols), xq, xs, xcorr)
+      rows, static_cast<int>(cols), xq, xs, xcorr, static_cast<int>(qblocks), t)
   switch (cpl) {
     case 1: VMAMD_ARQ(1); break;
     case 2: VMAMD_ARQ(2); break;

@@ -35,15 +35,25 @@ int align_and_group_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_ex
                               int32_t* offsets, int32_t* active, int32_t* num_active,
                               const void* x, int64_t rows, int64_t cols, uint8_t* xq, float* xs,
                               hipStream_t st);
+// Transposed copies of the w4afp8 weight scales for the grouped GEMMs:
+// in[m] = bf16 [E, n[m], 2 kp[m]] read as 32-bit words [E, n[m], kp[m]]
+// (kp[m] even), out[m] = [E, kp[m], n[m]] (m = 0: W13, 1: W2; null in[m]:
+// none).
+struct W4ScalesT {
+  const uint32_t* in[2];
+  uint32_t* out[2];
+  int n[2], kp[2];
+  int E;
+};
 // The same with the w4afp8 per-row quantiser (eps 1e-4): xs [rows]; xq in
 // w4 order with the block corrections xcorr [rows, cols / 128] (cols a
-// multiple of 128).
+// multiple of 128); sct: also the scale transpositions (null: none).
 int align_and_row_quant_fp8(const int32_t* topk_ids, int64_t numel, int num_experts,
                             int block_size, const int32_t* expert_map, int64_t expert_map_len,
                             int32_t* sorted, int64_t capacity, int32_t* expert_ids, int32_t* ntpp,
                             int32_t* offsets, int32_t* active, int32_t* num_active, const void* x,
                             int64_t rows, int64_t cols, uint8_t* xq, float* xs, float* xcorr,
-                            hipStream_t st);
+                            hipStream_t st, const W4ScalesT* sct = nullptr);
 // moe_align_block_size alone; with counts (align_counts_bytes of scratch)
 // in two launches, the chunk histograms then the placement, instead of every
 // workgroup histogramming all routes.

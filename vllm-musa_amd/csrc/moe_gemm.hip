@@ -1838,8 +1838,9 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
 //    an MFMA accumulator input as read]
 //   [weight-scale words 256 x 4 B: the aligned 4 bytes holding row r's bf16
 //    scale of the step, next to that of the step before or after it]
-//   [256 x 4 B that waves 4-7 fill with a copy of the scale words, so every
-//    wave issues the same number of loads per stage (the waits count per wave)]
+//   [256 x 4 B that waves 4-7 fill with one shared word (with transposed
+//    scales: a copy of the scale words), so every wave issues the same number
+//    of loads per stage (the waits count per wave); nothing reads it]
 // The weights cross LDS packed; each wave expands its fragments after the LDS
 // read (w4_frag), with the offset correction as the MFMA accumulator input
 // and the bf16 weight scale applied per step (acc += p * s, 4 FMAs per MFMA).
@@ -1878,9 +1879,13 @@ __device__ __forceinline__ int w4_lds_off(int r, int c) { return r * 64 + ((c ^ 
 // act: W13 the quantised x [T, K] (rows = tokens), W2 a2 [rows, K] in padded
 // route order, act_bytes its size (< 2^31); act_scale: W13 the token row
 // scales, W2 the a2 row scales; act_corr: [rows, K/128] offset corrections;
-// ws: bf16 [E, N, K/128].
+// ws: bf16 [E, N, K/128]; SCT (K / 128 even): the same scales as 32-bit
+// words of two K steps, transposed to [E, K/256, N] (W4ScalesT, in the
+// alignment's launch), so that one stage's 256 rows read consecutive words
+// instead of one 128-byte line per row (at K = 4096 the rows lie 64 bytes
+// apart).
 // out: W13 bf16 activation [padded rows, I]; W2 y [numel, N].
-template <bool W13, bool EVEN>
+template <bool W13, bool EVEN, bool SCT = false>
 __global__ __launch_bounds__(512, 1) void moe_w4_gemm_kernel(
     const uint8_t* __restrict__ act, const float* __restrict__ act_scale,
     const float* __restrict__ act_corr, int act_bytes, int topk, int K,
@@ -1939,8 +1944,11 @@ __global__ __launch_bounds__(512, 1) void moe_w4_gemm_kernel(
   const int64_t rc = arow(wave * 16 + lane / 4);
   const uint32_t offC = rc >= 0 ? static_cast<uint32_t>(rc * KS * 4) : kBufferOff;
   const int ldsC = P::kOffC + wave * 256;
+  static_assert(!SCT || EVEN, "transposed scale words pair two K steps");
   const int64_t rowKS = (static_cast<int64_t>(e) * N + wrow((wave % 4) * 64 + lane)) * KS;
   const uint8_t* wsb = reinterpret_cast<const uint8_t*>(ws);
+  // SCT: word (K step pair 0) of the lane's row; pair p is p * N words on.
+  const uint8_t* wst = wsb + (static_cast<int64_t>(e) * (KS / 2) * N + wrow((wave % 4) * 64 + lane)) * 4;
   const int ldsS = (wave < 4 ? P::kOffS : P::kOffD) + (wave % 4) * 256;
   auto issue = [&](uint8_t* st, int step) {
 #pragma unroll
@@ -1948,7 +1956,11 @@ __global__ __launch_bounds__(512, 1) void moe_w4_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < 2; ++j) dma16(srcB[j] + static_cast<int64_t>(step) * 64, st + ldsB[j]);
     buffer_dma4(crs, offC + static_cast<uint32_t>(step) * 4, st + ldsC);
-    dma4(wsb + ((rowKS + step) & ~static_cast<int64_t>(1)) * 2, st + ldsS);
+    if constexpr (SCT)
+      dma4(wst + static_cast<int64_t>(step / 2) * N * 4, st + ldsS);
+    else  // waves 4-7 keep the load count only: one shared word (a copy of the 256
+          // scattered words cost 5 % at T=512)
+      dma4(wave < 4 ? wsb + ((rowKS + step) & ~static_cast<int64_t>(1)) * 2 : wsb, st + ldsS);
   };
   // Padding routes close a block, so a wave whose first route is padding
   // holds none.
@@ -2162,11 +2174,11 @@ static size_t stage_scratch(int64_t numel, int E, int64_t H, int64_t I, int bloc
                   w2_scratch(numel, E, H, I, block_m, kind));
 }
 
-template <bool W13, bool EVEN>
+template <bool W13, bool EVEN, bool SCT = false>
 static int raise_w4_lds() {
   static bool done = false;
   if (done) return VMAMD_OK;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_w4_gemm_kernel<W13, EVEN>),
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_w4_gemm_kernel<W13, EVEN, SCT>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, W4Pipe::kLds) != hipSuccess) {
     set_error("w4afp8 moe: cannot raise the LDS limit of the grouped GEMM kernel");
     return VMAMD_ERR_HIP;
@@ -2175,21 +2187,32 @@ static int raise_w4_lds() {
   return VMAMD_OK;
 }
 
+// True when the w4afp8 GEMMs over K can read their scales transposed (SCT;
+// the transposition moves 8 bytes at a time: an even count of word pairs).
+static bool w4_sct(int64_t K) { return (K / 128) % 4 == 0; }
+
 // kW4 grouped GEMM launch (W13: N = 2I, out = bf16 activation; W2: N = H,
 // out = y).  The scale words are read 4 bytes at a time, so the scale array
-// must be 4-byte aligned.
+// must be 4-byte aligned; wst: the same scales transposed (W4ScalesT), or
+// null.
 template <bool W13>
 static int launch_w4_gemm(const uint8_t* act, int64_t act_rows, const float* act_scale,
                           const float* act_corr, int topk, int K, const int32_t* sorted,
                           const int32_t* offs, const int32_t* ntpp, const int32_t* eids, int E, int numel,
                           int tiles, const uint8_t* w, const void* ws, int N, int I, float limit, uint16_t* out,
-                          hipStream_t st) {
+                          hipStream_t st, const uint32_t* wst = nullptr) {
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(ws) % 4 == 0,
                 "w4afp8 moe: weight scales must be 4-byte aligned for the grouped GEMMs");
   VMAMD_REQUIRE(act_rows * K < (1ll << 31), "w4afp8 moe: the grouped GEMMs take activations below 2 GiB");
   const int act_bytes = static_cast<int>(act_rows * K);
   const uint16_t* wsh = static_cast<const uint16_t*>(ws);
-  if ((K / 128) % 2 == 0) {
+  if (wst && w4_sct(K)) {
+    int rc = raise_w4_lds<W13, true, true>();
+    if (rc) return rc;
+    moe_w4_gemm_kernel<W13, true, true><<<xcd_grid(tiles), 512, W4Pipe::kLds, st>>>(
+        act, act_scale, act_corr, act_bytes, topk, K, sorted, offs, ntpp, eids, E, numel, tiles, w,
+        reinterpret_cast<const uint16_t*>(wst), N, I, limit, out);
+  } else if ((K / 128) % 2 == 0) {
     int rc = raise_w4_lds<W13, true>();
     if (rc) return rc;
     moe_w4_gemm_kernel<W13, true><<<xcd_grid(tiles), 512, W4Pipe::kLds, st>>>(
@@ -2382,7 +2405,8 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
                       const int32_t* ntpp, const int32_t* active, const int32_t* nact,
                       const uint8_t* w13, const void* w13_s, int E, int I, float limit,
                       const float* route_w, uint8_t* a2, float* a2s, float* a2corr, float* scratch,
-                      hipStream_t st, const int32_t* eids = nullptr, bool native = false) {
+                      hipStream_t st, const int32_t* eids = nullptr, bool native = false,
+                      const uint32_t* w4st = nullptr) {
   const int numel = T * topk;
   const float* act_s = KIND == kW4 ? xcorr : xs;  // per-step activation values the GEMV reads
   VMAMD_REQUIRE(KIND != kW8A16 || block_m == kGemvBlock, "moe w13: bf16 x fp8 runs on the decode GEMV only");
@@ -2422,7 +2446,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
   const int tiles = max_blocks * (I / 128);
   if constexpr (KIND == kW4) {
     return launch_w4_gemm<true>(xa, T, xs, xcorr, topk, H, sorted, offs, ntpp, eids, E, numel, tiles, w13,
-                                w13_s, 2 * I, I, limit, reinterpret_cast<uint16_t*>(a2), st);
+                                w13_s, 2 * I, I, limit, reinterpret_cast<uint16_t*>(a2), st, w4st);
   } else if constexpr (KIND == kFp8 || KIND == kBf16) {
     int rc = raise_dma_lds<KIND, true>();
     if (rc) return rc;
@@ -2448,7 +2472,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
                      int E, int H, int I, const float* topk_weights, const float* route_w,
                      const int32_t* topk_ids, const int32_t* emap, int64_t emap_len, uint16_t* y,
                      float* scratch, hipStream_t st, uint16_t* combined_out = nullptr,
-                     bool* combined = nullptr, const int32_t* eids = nullptr) {
+                     bool* combined = nullptr, const int32_t* eids = nullptr, const uint32_t* w4st = nullptr) {
   const int numel = T * topk;
   const float* yscale = KIND == kW4 ? a2s : route_w;
   const float* act_s = KIND == kW4 ? a2corr : a2s;  // per-step activation values the GEMV reads
@@ -2510,7 +2534,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
   if constexpr (KIND == kW4) {
     const int tiles = max_blocks * ((H + W4Pipe::BN - 1) / W4Pipe::BN);
     return launch_w4_gemm<false>(a2, cap, a2s, a2corr, 1, I, sorted, offs, ntpp, eids, E, numel, tiles, w2,
-                                 w2_s, H, I, 0.f, y, st);
+                                 w2_s, H, I, 0.f, y, st, w4st);
   } else if constexpr (KIND == kFp8 || KIND == kBf16) {
     const int tiles = max_blocks * ((H + 255) / 256);
     int rc = raise_dma_lds<KIND, false>();
@@ -2529,7 +2553,9 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
 // scratch shares one region.  kFp8 / kW4 add the quantised x and scales; kW4
 // also keeps the bf16 activation before its row quantiser.
 struct MoeWs {
-  size_t xq, xs, xcorr, sorted, eids, ntpp, offs, active, nact, acnt, abf, a2, a2s, a2corr, y, scratch, total;
+  size_t xq, xs, xcorr, sorted, eids, ntpp, offs, active, nact, acnt, abf, a2, a2s, a2corr, y, scratch, wst13,
+      wst2, total;
+  bool sct13, sct2;  // kW4 grouped GEMMs: the transposed weight scales (W4ScalesT) at wst13 / wst2
 };
 
 static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm, int kind) {
@@ -2560,6 +2586,10 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   }
   w.y = take(numel * H * 2);
   w.scratch = take(stage_scratch(numel, E, H, I, bm, kind));
+  w.sct13 = kind == kW4 && bm != kGemvBlock && w4_sct(H);
+  w.sct2 = kind == kW4 && bm != kGemvBlock && w4_sct(I);
+  if (w.sct13) w.wst13 = take(static_cast<size_t>(E) * 2 * I * (H / 128) * 2);
+  if (w.sct2) w.wst2 = take(static_cast<size_t>(E) * H * (I / 128) * 2);
   w.total = o;
   return w;
 }
@@ -2808,6 +2838,8 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   const uint8_t* xa = static_cast<const uint8_t*>(x);
   const float* xs = nullptr;
   float* xcorr = KIND == kW4 ? reinterpret_cast<float*>(ws + L.xcorr) : nullptr;
+  uint32_t* wst13 = nullptr;  // kW4 grouped GEMMs: the transposed weight scales
+  uint32_t* wst2 = nullptr;
   float* a2corr = KIND == kW4 ? reinterpret_cast<float*>(ws + L.a2corr) : nullptr;
   if constexpr (KIND == kFp8) {  // quantiser and alignment in one launch
     uint8_t* xq = ws + L.xq;
@@ -2817,11 +2849,28 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     if (rc) return rc;
     xa = xq;
     xs = xsw;
-  } else if constexpr (KIND == kW4) {  // per-row quantiser and alignment in one launch
+  } else if constexpr (KIND == kW4) {  // per-row quantiser and alignment in one launch, with the
+                                       // grouped GEMMs' transposed weight scales
     uint8_t* xq = ws + L.xq;
     float* xsw = reinterpret_cast<float*>(ws + L.xs);
+    W4ScalesT sct{};
+    sct.E = E;
+    if (L.sct13) {
+      wst13 = reinterpret_cast<uint32_t*>(ws + L.wst13);
+      sct.in[0] = static_cast<const uint32_t*>(w13_s);
+      sct.out[0] = wst13;
+      sct.n[0] = 2 * i;
+      sct.kp[0] = h / 256;
+    }
+    if (L.sct2) {
+      wst2 = reinterpret_cast<uint32_t*>(ws + L.wst2);
+      sct.in[1] = static_cast<const uint32_t*>(w2_s);
+      sct.out[1] = wst2;
+      sct.n[1] = h;
+      sct.kp[1] = i / 256;
+    }
     rc = align_and_row_quant_fp8(topk_ids, numel, E, bm, expert_map, expert_map_len, sorted, cap,
-                                 eids, ntpp, offs, active, nact, x, T, H, xq, xsw, xcorr, st);
+                                 eids, ntpp, offs, active, nact, x, T, H, xq, xsw, xcorr, st, &sct);
     if (rc) return rc;
     xa = xq;
     xs = xsw;
@@ -2835,7 +2884,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   uint8_t* act_out = KIND == kW4 && bm != kGemvBlock ? ws + L.abf : a2;
   rc = launch_w13<KIND>(xa, xs, xcorr, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
                         static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, w13_rw, act_out,
-                        a2s, a2corr, scratch, st, eids, native);
+                        a2s, a2corr, scratch, st, eids, native, wst13);
   if (rc) return rc;
   if constexpr (KIND == kW4) {
     if (bm != kGemvBlock) {  // rows past the last block are skipped on the device
@@ -2848,7 +2897,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   rc = launch_w2<KIND>(a2, a2s, a2corr, t, topk, sorted, cap, bm, offs, ntpp, active, nact,
                        static_cast<const uint8_t*>(w2), w2_s, E, h, i, topk_weights, w2_rw, topk_ids,
                        expert_map, expert_map_len, y, scratch, st, static_cast<uint16_t*>(out),
-                       &combined, eids);
+                       &combined, eids, wst2);
   if (rc || combined) return rc;
   // Slots of dropped routes (negative ids, or non-local experts) hold no
   // expert output and are skipped by the combine.
