@@ -1467,6 +1467,28 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
   }
 }
 
+// The fp8 layer's x scales in route order for the 256-route W13 GEMM: out
+// [(b * KS + k) * bm + j] = scale k of the token of route sorted[b * bm + j]
+// (padding rows: token 0), over the used blocks (ntpp).  The W13 tiles then
+// read one K step's scales of their 256 routes from 1 KiB in a row instead
+// of one gathered token row per lane (DeepSeek-V3 T=4096: 256 lines a step).
+__global__ __launch_bounds__(256) void route_scales_kernel(const float* __restrict__ xs,
+                                                           const int32_t* __restrict__ sorted,
+                                                           const int32_t* __restrict__ ntpp, int numel, int topk,
+                                                           int KS, int bm, float* __restrict__ out) {
+  const int64_t total = static_cast<int64_t>(ntpp[0]) * KS;
+  const int64_t per_block = static_cast<int64_t>(KS) * bm;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t b = i / per_block;
+    const int rem = static_cast<int>(i - b * per_block);
+    const int k = rem / bm, j = rem - k * bm;
+    const int sr = sorted[b * bm + j];
+    const int t = sr < numel ? sr / topk : 0;
+    out[i] = xs[static_cast<int64_t>(t) * KS + k];
+  }
+}
+
 // ------------------------------- fp8 prefill GEMMs on 256-route tiles ----
 // For long prefills (block size 256): a CU's loads stream at the rate its
 // vector cache keeps requests in flight, so the bytes a workgroup moves per
@@ -1524,7 +1546,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     int topk, int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ ntpp, const int32_t* __restrict__ eids, int E, int numel, int max_tiles, const uint8_t* __restrict__ w,
     const float* __restrict__ ws, int N, int I, float limit, const float* __restrict__ route_w,
-    uint8_t* __restrict__ a2, float* __restrict__ a2s, uint16_t* __restrict__ y) {
+    uint8_t* __restrict__ a2, float* __restrict__ a2s, uint16_t* __restrict__ y, int act_s_routes = 0) {
   using P = MoeBigTile<MTV>;
   constexpr int BM = P::BM, NT = P::NT, MT = P::MT;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
@@ -1577,7 +1599,12 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   if (!kScaled) {
   } else if (sa_wave) {  // activation scales of tile rows 64 * wave + lane
     rs = buffer_rsrc(act_s, act_s_bytes);
-    offS = static_cast<uint32_t>(arow(64 * wave + lane)) * KS * 4;
+    if (W13 && act_s_routes) {  // route order (route_scales_kernel): one step's scales of a block side by side
+      offS = static_cast<uint32_t>((static_cast<int64_t>(mb) * KS * BM + 64 * wave + lane) * 4);
+      stepS = BM * 4;
+    } else {
+      offS = static_cast<uint32_t>(arow(64 * wave + lane)) * KS * 4;
+    }
   } else {  // weight-block scales: W13 gate / up block, W2 the tile's two 128-row blocks
     const int slot = min(lane, 1);
     const int brow = W13 ? (slot ? (I + n0) / 128 : n0 / 128) : min(n0 / 128 + slot, NB - 1);
@@ -2406,7 +2433,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
                       const uint8_t* w13, const void* w13_s, int E, int I, float limit,
                       const float* route_w, uint8_t* a2, float* a2s, float* a2corr, float* scratch,
                       hipStream_t st, const int32_t* eids = nullptr, bool native = false,
-                      const uint32_t* w4st = nullptr) {
+                      const uint32_t* w4st = nullptr, const float* xs_routes = nullptr) {
   const int numel = T * topk;
   const float* act_s = KIND == kW4 ? xcorr : xs;  // per-step activation values the GEMV reads
   VMAMD_REQUIRE(KIND != kW8A16 || block_m == kGemvBlock, "moe w13: bf16 x fp8 runs on the decode GEMV only");
@@ -2437,6 +2464,11 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
                                            ntpp, eids, E, numel, tiles, w13, ws13, 2 * I, I, limit, route_w, a2, a2s,
                                            static_cast<uint16_t*>(nullptr));
       }
+      if (xs_routes)  // route-ordered scales (route_scales_kernel)
+        return launch_big<KIND, true, 4>(tiles, st, xa, abytes, xs_routes,
+                                         static_cast<int>(cap * (H / 128) * 4), topk, static_cast<int>(H), sorted, offs,
+                                         ntpp, eids, E, numel, tiles, w13, ws13, 2 * I, I, limit, route_w, a2, a2s,
+                                         static_cast<uint16_t*>(nullptr), 1);
       return launch_big<KIND, true, 4>(tiles, st, xa, abytes, xs, sbytes, topk, static_cast<int>(H), sorted, offs, ntpp,
                                        eids, E, numel, tiles, w13, ws13, 2 * I, I, limit, route_w, a2, a2s,
                                        static_cast<uint16_t*>(nullptr));
@@ -2554,7 +2586,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
 // also keeps the bf16 activation before its row quantiser.
 struct MoeWs {
   size_t xq, xs, xcorr, sorted, eids, ntpp, offs, active, nact, acnt, abf, a2, a2s, a2corr, y, scratch, wst13,
-      wst2, total;
+      wst2, xsr, total;
   bool sct13, sct2;  // kW4 grouped GEMMs: the transposed weight scales (W4ScalesT) at wst13 / wst2
 };
 
@@ -2590,6 +2622,7 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   w.sct2 = kind == kW4 && bm != kGemvBlock && w4_sct(I);
   if (w.sct13) w.wst13 = take(static_cast<size_t>(E) * 2 * I * (H / 128) * 2);
   if (w.sct2) w.wst2 = take(static_cast<size_t>(E) * H * (I / 128) * 2);
+  if (kind == kFp8 && bm == kMoeBigBM) w.xsr = take(cap * (H / 128) * 4);  // route_scales_kernel
   w.total = o;
   return w;
 }
@@ -2840,6 +2873,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   float* xcorr = KIND == kW4 ? reinterpret_cast<float*>(ws + L.xcorr) : nullptr;
   uint32_t* wst13 = nullptr;  // kW4 grouped GEMMs: the transposed weight scales
   uint32_t* wst2 = nullptr;
+  float* xsr = nullptr;  // kFp8 256-route W13: x scales in route order
   float* a2corr = KIND == kW4 ? reinterpret_cast<float*>(ws + L.a2corr) : nullptr;
   if constexpr (KIND == kFp8) {  // quantiser and alignment in one launch
     uint8_t* xq = ws + L.xq;
@@ -2849,6 +2883,12 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     if (rc) return rc;
     xa = xq;
     xs = xsw;
+    if (bm == kMoeBigBM && cap * (H / 128) * 4 < (1ll << 31)) {
+      xsr = reinterpret_cast<float*>(ws + L.xsr);
+      route_scales_kernel<<<1024, 256, 0, st>>>(xsw, sorted, ntpp, numel, topk, static_cast<int>(H / 128), bm, xsr);
+      rc = check_launch("fused_moe (x scales in route order)");
+      if (rc) return rc;
+    }
   } else if constexpr (KIND == kW4) {  // per-row quantiser and alignment in one launch, with the
                                        // grouped GEMMs' transposed weight scales
     uint8_t* xq = ws + L.xq;
@@ -2884,7 +2924,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   uint8_t* act_out = KIND == kW4 && bm != kGemvBlock ? ws + L.abf : a2;
   rc = launch_w13<KIND>(xa, xs, xcorr, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
                         static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, w13_rw, act_out,
-                        a2s, a2corr, scratch, st, eids, native, wst13);
+                        a2s, a2corr, scratch, st, eids, native, wst13, xsr);
   if (rc) return rc;
   if constexpr (KIND == kW4) {
     if (bm != kGemvBlock) {  // rows past the last block are skipped on the device
