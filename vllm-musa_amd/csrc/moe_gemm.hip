@@ -1472,20 +1472,27 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
 // (padding rows: token 0), over the used blocks (ntpp).  The W13 tiles then
 // read one K step's scales of their 256 routes from 1 KiB in a row instead
 // of one gathered token row per lane (DeepSeek-V3 T=4096: 256 lines a step).
+// One thread per route row: its token's KS scales in 16-byte loads (KS % 4
+// == 0, the host's condition), each K step's store coalesced across the
+// wave's consecutive rows.
 __global__ __launch_bounds__(256) void route_scales_kernel(const float* __restrict__ xs,
                                                            const int32_t* __restrict__ sorted,
                                                            const int32_t* __restrict__ ntpp, int numel, int topk,
                                                            int KS, int bm, float* __restrict__ out) {
-  const int64_t total = static_cast<int64_t>(ntpp[0]) * KS;
-  const int64_t per_block = static_cast<int64_t>(KS) * bm;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t b = i / per_block;
-    const int rem = static_cast<int>(i - b * per_block);
-    const int k = rem / bm, j = rem - k * bm;
-    const int sr = sorted[b * bm + j];
+  const int rows = ntpp[0];
+  for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+    const int b = r / bm, j = r - b * bm;
+    const int sr = sorted[r];
     const int t = sr < numel ? sr / topk : 0;
-    out[i] = xs[static_cast<int64_t>(t) * KS + k];
+    const float4* src = reinterpret_cast<const float4*>(xs + static_cast<int64_t>(t) * KS);
+    float* dst = out + static_cast<int64_t>(b) * KS * bm + j;
+    for (int k4 = 0; k4 < KS / 4; ++k4) {
+      const float4 v = src[k4];
+      dst[(4 * k4 + 0) * bm] = v.x;
+      dst[(4 * k4 + 1) * bm] = v.y;
+      dst[(4 * k4 + 2) * bm] = v.z;
+      dst[(4 * k4 + 3) * bm] = v.w;
+    }
   }
 }
 
@@ -2883,9 +2890,10 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     if (rc) return rc;
     xa = xq;
     xs = xsw;
-    if (bm == kMoeBigBM && cap * (H / 128) * 4 < (1ll << 31)) {
+    if (bm == kMoeBigBM && (H / 128) % 4 == 0 && cap * (H / 128) * 4 < (1ll << 31)) {
       xsr = reinterpret_cast<float*>(ws + L.xsr);
-      route_scales_kernel<<<1024, 256, 0, st>>>(xsw, sorted, ntpp, numel, topk, static_cast<int>(H / 128), bm, xsr);
+      route_scales_kernel<<<static_cast<int>((cap + 255) / 256), 256, 0, st>>>(xsw, sorted, ntpp, numel, topk,
+                                                                             static_cast<int>(H / 128), bm, xsr);
       rc = check_launch("fused_moe (x scales in route order)");
       if (rc) return rc;
     }
