@@ -2194,7 +2194,14 @@ static int w2_splits(int64_t numel, int E, int64_t H, int64_t I, int kind) {
 static size_t al256(size_t x) { return (x + 255) / 256 * 256; }
 
 // Stage scratch: fp32 split-K partials of the decode GEMVs (none for GEMMs).
+// Bytes of route_scales_kernel's copy for the fp8 256-route W13 (0 where it
+// is not used): cap rows of H / 128 scales.
+static size_t route_scales_bytes(int64_t cap, int64_t H, int block_m, int kind) {
+  const size_t b = static_cast<size_t>(cap) * (H / 128) * 4;
+  return kind == kFp8 && block_m == kMoeBigBM && (H / 128) % 4 == 0 && b < (1ull << 31) ? b : 0;
+}
 static size_t w13_scratch(int64_t numel, int E, int64_t H, int64_t I, int block_m, int kind) {
+  if (block_m == kMoeBigBM) return route_scales_bytes(numel + static_cast<int64_t>(E) * (block_m - 1), H, block_m, kind);
   if (block_m != kGemvBlock) return 0;
   return al256(static_cast<size_t>(w13_splits(numel, E, H, I, kind)) * numel * 2 * I * 4);
 }
@@ -2629,7 +2636,7 @@ static MoeWs moe_layout(int64_t T, int topk, int E, int64_t H, int64_t I, int bm
   w.sct2 = kind == kW4 && bm != kGemvBlock && w4_sct(I);
   if (w.sct13) w.wst13 = take(static_cast<size_t>(E) * 2 * I * (H / 128) * 2);
   if (w.sct2) w.wst2 = take(static_cast<size_t>(E) * H * (I / 128) * 2);
-  if (kind == kFp8 && bm == kMoeBigBM) w.xsr = take(cap * (H / 128) * 4);  // route_scales_kernel
+  w.xsr = take(route_scales_bytes(cap, H, bm, kind));  // route_scales_kernel
   w.total = o;
   return w;
 }
@@ -2890,7 +2897,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     if (rc) return rc;
     xa = xq;
     xs = xsw;
-    if (bm == kMoeBigBM && (H / 128) % 4 == 0 && cap * (H / 128) * 4 < (1ll << 31)) {
+    if (route_scales_bytes(cap, H, bm, KIND) > 0) {
       xsr = reinterpret_cast<float*>(ws + L.xsr);
       route_scales_kernel<<<static_cast<int>((cap + 255) / 256), 256, 0, st>>>(xsw, sorted, ntpp, numel, topk,
                                                                              static_cast<int>(H / 128), bm, xsr);
@@ -2974,11 +2981,22 @@ static int stage_w13(const char* who, const void* xa, const float* xs, int64_t T
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(xa) % 16 == 0 && reinterpret_cast<uintptr_t>(a2) % 16 == 0,
                 "%s: activations, a2 and workspace must be 16-byte aligned", who);
+  // The fp8 256-route W13 reads its x scales in route order when the
+  // workspace holds the copy for this capacity (route_scales_kernel).
+  float* xsr = nullptr;
+  const size_t rsb = route_scales_bytes(capacity, H, block_m, KIND);
+  if (rsb > 0 && workspace_bytes >= rsb) {
+    xsr = static_cast<float*>(workspace);
+    route_scales_kernel<<<static_cast<int>((capacity + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+        xs, sorted, ntpp, static_cast<int>(T * topk), topk, static_cast<int>(H / 128), block_m, xsr);
+    rc = check_launch("moe_fp8_w13 (x scales in route order)");
+    if (rc) return rc;
+  }
   return launch_w13<KIND>(static_cast<const uint8_t*>(xa), xs, nullptr, static_cast<int>(T), static_cast<int>(H),
                           topk, sorted, capacity, block_m, offs, ntpp, active, nact,
                           static_cast<const uint8_t*>(w13), w13_s, E, static_cast<int>(I), limit,
                           nullptr, static_cast<uint8_t*>(a2), a2s, nullptr, static_cast<float*>(workspace),
-                          reinterpret_cast<hipStream_t>(stream));
+                          reinterpret_cast<hipStream_t>(stream), nullptr, false, nullptr, xsr);
 }
 
 template <int KIND>
