@@ -1467,6 +1467,12 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
   }
 }
 
+// moe_big_kernel's scale_order bits.  kActScalesInRoutes: the A operand's
+// 1x128 scales are laid out [block, K step, BM routes] (W13: route_scales_kernel's
+// copy of the x scales; W2: the a2 scales as a W13 launch with kA2ScalesInRoutes
+// wrote them), so a K step's BM scales are one contiguous load.
+constexpr int kActScalesInRoutes = 1, kA2ScalesInRoutes = 2;
+
 // The fp8 layer's x scales in route order for the 256-route W13 GEMM: out
 // [(b * KS + k) * bm + j] = scale k of the token of route sorted[b * bm + j]
 // (padding rows: token 0), over the used blocks (ntpp).  The W13 tiles then
@@ -1553,7 +1559,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
     int topk, int K, const int32_t* __restrict__ sorted, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ ntpp, const int32_t* __restrict__ eids, int E, int numel, int max_tiles, const uint8_t* __restrict__ w,
     const float* __restrict__ ws, int N, int I, float limit, const float* __restrict__ route_w,
-    uint8_t* __restrict__ a2, float* __restrict__ a2s, uint16_t* __restrict__ y, int act_s_routes = 0) {
+    uint8_t* __restrict__ a2, float* __restrict__ a2s, uint16_t* __restrict__ y, int scale_order = 0) {
   using P = MoeBigTile<MTV>;
   constexpr int BM = P::BM, NT = P::NT, MT = P::MT;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_dyn[];
@@ -1606,7 +1612,7 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
   if (!kScaled) {
   } else if (sa_wave) {  // activation scales of tile rows 64 * wave + lane
     rs = buffer_rsrc(act_s, act_s_bytes);
-    if (W13 && act_s_routes) {  // route order (route_scales_kernel): one step's scales of a block side by side
+    if (scale_order & kActScalesInRoutes) {  // [block, K step, BM routes]: one step's scales side by side
       offS = static_cast<uint32_t>((static_cast<int64_t>(mb) * KS * BM + 64 * wave + lane) * 4);
       stepS = BM * 4;
     } else {
@@ -1822,7 +1828,12 @@ __global__ __launch_bounds__(512, 1) void moe_big_kernel(
       const float amax = fmaxf(1e-10f, fmaxf(red[ml], red[BM + ml]));
       const float scale = amax / 448.0f, rs = 1.0f / scale;
       const int64_t row = base + ml;
-      if (wn == 0 && lg == 0) a2s[row * gpr + tn] = scale;
+      if (wn == 0 && lg == 0) {
+        if (scale_order & kA2ScalesInRoutes)  // [block, I / 128, BM routes], as the W2 tiles read them
+          a2s[(static_cast<int64_t>(mb) * gpr + tn) * BM + ml] = scale;
+        else
+          a2s[row * gpr + tn] = scale;
+      }
 #pragma unroll
       for (int q = 0; q < NT / 2; ++q) {
         const int col = n0 + (4 * wn + q) * 16 + 4 * lg;
@@ -2447,7 +2458,7 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
                       const uint8_t* w13, const void* w13_s, int E, int I, float limit,
                       const float* route_w, uint8_t* a2, float* a2s, float* a2corr, float* scratch,
                       hipStream_t st, const int32_t* eids = nullptr, bool native = false,
-                      const uint32_t* w4st = nullptr, const float* xs_routes = nullptr) {
+                      const uint32_t* w4st = nullptr, const float* xs_routes = nullptr, bool a2s_routes = false) {
   const int numel = T * topk;
   const float* act_s = KIND == kW4 ? xcorr : xs;  // per-step activation values the GEMV reads
   VMAMD_REQUIRE(KIND != kW8A16 || block_m == kGemvBlock, "moe w13: bf16 x fp8 runs on the decode GEMV only");
@@ -2478,14 +2489,13 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
                                            ntpp, eids, E, numel, tiles, w13, ws13, 2 * I, I, limit, route_w, a2, a2s,
                                            static_cast<uint16_t*>(nullptr));
       }
-      if (xs_routes)  // route-ordered scales (route_scales_kernel)
-        return launch_big<KIND, true, 4>(tiles, st, xa, abytes, xs_routes,
-                                         static_cast<int>(cap * (H / 128) * 4), topk, static_cast<int>(H), sorted, offs,
-                                         ntpp, eids, E, numel, tiles, w13, ws13, 2 * I, I, limit, route_w, a2, a2s,
-                                         static_cast<uint16_t*>(nullptr), 1);
-      return launch_big<KIND, true, 4>(tiles, st, xa, abytes, xs, sbytes, topk, static_cast<int>(H), sorted, offs, ntpp,
-                                       eids, E, numel, tiles, w13, ws13, 2 * I, I, limit, route_w, a2, a2s,
-                                       static_cast<uint16_t*>(nullptr));
+      // xs_routes: route_scales_kernel's copy of the x scales; a2s_routes:
+      // a2s written in route order for a W2 launch with a2s_routes.
+      const int order = (xs_routes ? kActScalesInRoutes : 0) | (a2s_routes ? kA2ScalesInRoutes : 0);
+      return launch_big<KIND, true, 4>(tiles, st, xa, abytes, xs_routes ? xs_routes : xs,
+                                       xs_routes ? static_cast<int>(cap * (H / 128) * 4) : sbytes, topk,
+                                       static_cast<int>(H), sorted, offs, ntpp, eids, E, numel, tiles, w13, ws13,
+                                       2 * I, I, limit, route_w, a2, a2s, static_cast<uint16_t*>(nullptr), order);
     }
   }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
@@ -2518,7 +2528,8 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
                      int E, int H, int I, const float* topk_weights, const float* route_w,
                      const int32_t* topk_ids, const int32_t* emap, int64_t emap_len, uint16_t* y,
                      float* scratch, hipStream_t st, uint16_t* combined_out = nullptr,
-                     bool* combined = nullptr, const int32_t* eids = nullptr, const uint32_t* w4st = nullptr) {
+                     bool* combined = nullptr, const int32_t* eids = nullptr, const uint32_t* w4st = nullptr,
+                     bool a2s_routes = false) {
   const int numel = T * topk;
   const float* yscale = KIND == kW4 ? a2s : route_w;
   const float* act_s = KIND == kW4 ? a2corr : a2s;  // per-step activation values the GEMV reads
@@ -2573,7 +2584,8 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
                                             numel, tiles, w2, ws2, H, I, 0.f, route_w, none8, nonef, y);
       }
       return launch_big<KIND, false, 4>(tiles, st, a2, abytes, a2s, sbytes, 1, I, sorted, offs, ntpp, eids, E, numel,
-                                        tiles, w2, ws2, H, I, 0.f, route_w, none8, nonef, y);
+                                        tiles, w2, ws2, H, I, 0.f, route_w, none8, nonef, y,
+                                        a2s_routes ? kActScalesInRoutes : 0);
     }
   }
   const int max_blocks = static_cast<int>((cap + kMoeBM - 1) / kMoeBM);
@@ -2937,9 +2949,12 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   // kW4 prefill: bf16 activation, quantised per row below (the decode path
   // writes the quantised a2 directly).
   uint8_t* act_out = KIND == kW4 && bm != kGemvBlock ? ws + L.abf : a2;
+  // kFp8 on 256-route blocks: W13 writes the a2 scales in route order and W2
+  // reads them so (the a2 scales stay inside this call).
+  const bool a2s_routes = KIND == kFp8 && bm == kMoeBigBM;
   rc = launch_w13<KIND>(xa, xs, xcorr, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
                         static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, w13_rw, act_out,
-                        a2s, a2corr, scratch, st, eids, native, wst13, xsr);
+                        a2s, a2corr, scratch, st, eids, native, wst13, xsr, a2s_routes);
   if (rc) return rc;
   if constexpr (KIND == kW4) {
     if (bm != kGemvBlock) {  // rows past the last block are skipped on the device
@@ -2952,7 +2967,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   rc = launch_w2<KIND>(a2, a2s, a2corr, t, topk, sorted, cap, bm, offs, ntpp, active, nact,
                        static_cast<const uint8_t*>(w2), w2_s, E, h, i, topk_weights, w2_rw, topk_ids,
                        expert_map, expert_map_len, y, scratch, st, static_cast<uint16_t*>(out),
-                       &combined, eids, wst2);
+                       &combined, eids, wst2, a2s_routes);
   if (rc || combined) return rc;
   // Slots of dropped routes (negative ids, or non-local experts) hold no
   // expert output and are skipped by the combine.
