@@ -20,6 +20,9 @@ order), and on a sample of rows against the oracle:
       against the oracle, every output.
   apply_router_weight_on_input on the 256-route kernels (fp8 and bf16):
       against the oracle, and bitwise against the 128-route kernels.
+  the fp8 256-route stages (x scales copied in route order by the W13 stage)
+      bitwise against the fused call (x and a2 scales in route order), with
+      an expert map, and against the oracle.
 
 Tolerance (the path's bar for bf16/fp8 outputs): rel-L2 <= 1e-2 and
 max-abs <= 2e-2 * max|ref|."""
@@ -282,3 +285,31 @@ def test_long_batch_runs_in_chunks():
     assert torch.equal(small, torch.cat([fused_experts_impl(x[c:c + 5000], w13, w2, w[c:c + 5000],
                                                             ids[c:c + 5000], **kw)
                                          for c in range(0, T, 5000)]))
+
+
+def test_fp8_256_route_stages_equal_fused_with_expert_map():
+    """The 256-route fp8 kernels read their activation scales in route order:
+    the fused call copies the x scales (and has W13 write the a2 scales) so,
+    the W13 stage entry point copies the x scales into its workspace and W2
+    reads the a2 scales row by row.  Stages at block 256, the fused call and
+    the oracle agree, with an expert map that drops a third of the routes and
+    H / 128 = 12 scales per row."""
+    from vllm_musa_amd import synthetic
+    from vllm_musa_amd.fused_moe import MoeStages, fused_experts_impl
+    E, H, I, T, K = 12, 1536, 256, 800, 2  # 1600 routes >= 128 * E: 256-route blocks
+    w13, s13, w2, s2 = synthetic.moe_fp8_weights(E, H, I, 810)
+    x = synthetic.activations(T, H, 811)
+    g = torch.Generator().manual_seed(812)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(torch.int32).to(DEV)
+    w = (torch.rand(T, K, generator=g) * 0.9 + 0.1).to(DEV)
+    emap = torch.tensor([i if i % 3 else -1 for i in range(E)], dtype=torch.int32, device=DEV)
+    kw = dict(use_fp8_w8a8=True, block_shape=[128, 128], path="gemm", expert_map=emap)
+    out = fused_experts_impl(x, w13, w2, w, ids, w1_scale=s13, w2_scale=s2, **kw)
+    st = MoeStages(x, w13, s13, w2, s2, w, ids, path="gemm", expert_map=emap, block_m=256)
+    assert st.block_m == 256
+    assert torch.equal(out, st.run())
+    ref = omoe.fused_experts_fp8(x.float().cpu().numpy(), w13.view(torch.uint8).cpu().numpy(),
+                                 s13.cpu().numpy(), w2.view(torch.uint8).cpu().numpy(),
+                                 s2.cpu().numpy(), w.cpu().numpy(), ids.cpu().numpy(),
+                                 expert_map=emap.cpu().numpy())
+    _check_np(out, ref)
