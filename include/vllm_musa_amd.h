@@ -345,7 +345,9 @@ int vmamd_fused_moe_fp8(const void* x, int x_dtype, int64_t T, int64_t H, const 
  *       y [T*topk, H] bf16 (8-byte aligned; 16-byte for block_m 256 and 320); rows of
  *       dropped routes are left unwritten.
  * Scratch: vmamd_moe_fp8_stage_workspace_size() bytes, 16-byte aligned
- * (enough for either stage).
+ * (enough for either stage).  At block_m 256 (H / 128 a multiple of 4) it
+ * holds W13's copy of the x scales in route order, capacity x H/128 floats;
+ * given less, W13 reads the scales by token row instead (same result).
  * Replace the two invoke_fused_moe_kernel launches of the upstream
  * fused_experts_impl (block-scaled accumulate:
  * vllm_musa/patches/series/0081-MUSA-vllm.model_executor.layers.fused_moe.fused_moe.patch:64-108;
