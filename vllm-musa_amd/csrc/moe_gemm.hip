@@ -1200,6 +1200,13 @@ using MoePipeBf16 = TilePipe<false, 128, 256, 2, 4, 3>;
 template <int KIND>
 using MoePipe = typename std::conditional<KIND == kFp8, MoePipeFp8, MoePipeBf16>::type;
 
+// scale_order bits of the fp8 grouped GEMMs (moe_gemm_dma_kernel,
+// moe_big_kernel).  kActScalesInRoutes: the A operand's 1x128 scales are laid
+// out [block, K step, BM routes] (W13: route_scales_kernel's copy of the x
+// scales; W2: the a2 scales as a W13 launch with kA2ScalesInRoutes wrote
+// them), so a K step's BM scales are one contiguous load.
+constexpr int kActScalesInRoutes = 1, kA2ScalesInRoutes = 2;
+
 template <int KIND, bool W13>
 __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
     const uint8_t* __restrict__ act, int act_bytes, const float* __restrict__ act_s, int topk, int K,
@@ -1207,7 +1214,7 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
     const int32_t* __restrict__ ntpp, const int32_t* __restrict__ eids, int E, int numel, int max_tiles,
     const uint8_t* __restrict__ w, const float* __restrict__ ws, int N, int I, float limit,
     const float* __restrict__ route_w, uint8_t* __restrict__ a2, float* __restrict__ a2s,
-    uint16_t* __restrict__ y) {
+    uint16_t* __restrict__ y, int scale_order) {
   using P = MoePipe<KIND>;
   using KB_ = KindBytes<KIND>;
   constexpr int NS = 3, BM = 128, BN = 256, WN = 4, MT = P::MT, NT = P::NT;
@@ -1262,7 +1269,9 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
   }
   if constexpr (KIND == kFp8) {
     if (wave < BM / 64) {  // activation group scales of tile rows 64*wave + lane
-      p.srcS = reinterpret_cast<const uint8_t*>(act_s + max(arow(64 * wave + lane), int64_t{0}) * KS);
+      p.srcS = scale_order & kActScalesInRoutes
+                   ? reinterpret_cast<const uint8_t*>(act_s + static_cast<int64_t>(mb) * KS * BM + 64 * wave + lane)
+                   : reinterpret_cast<const uint8_t*>(act_s + max(arow(64 * wave + lane), int64_t{0}) * KS);
       p.ldsS = P::kOffSA + 64 * wave * 4;
     } else {  // weight-block scales: W13 gate / up block, W2 the tile's two 128-row blocks
       const int slot = min(lane, 1);
@@ -1270,7 +1279,7 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
       p.srcS = reinterpret_cast<const uint8_t*>(ws + (static_cast<int64_t>(e) * NB + brow) * KS);
       p.ldsS = P::kOffSB;
     }
-    p.stepS = 4;
+    p.stepS = wave < BM / 64 && (scale_order & kActScalesInRoutes) ? BM * 4 : 4;
   }
   // Padding routes close a block, so a wave whose first route is padding
   // holds none.
@@ -1425,7 +1434,12 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
         for (int w4 = 0; w4 < WN; ++w4) amax = fmaxf(amax, red[w4 * BM + ml]);
         const float scale = amax / 448.0f, rs = 1.0f / scale;
         const int64_t row = static_cast<int64_t>(mb) * BM + ml;
-        if (wn == 0 && lg == 0) a2s[row * gpr + tn] = scale;
+        if (wn == 0 && lg == 0) {
+          if (scale_order & kA2ScalesInRoutes)  // [block, I / 128, BM routes], as the W2 tiles read them
+            a2s[(static_cast<int64_t>(mb) * gpr + tn) * BM + ml] = scale;
+          else
+            a2s[row * gpr + tn] = scale;
+        }
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const int col = n0 + (wn * 2 + q) * 16 + 4 * lg;
@@ -1467,16 +1481,10 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_dma_kernel(
   }
 }
 
-// moe_big_kernel's scale_order bits.  kActScalesInRoutes: the A operand's
-// 1x128 scales are laid out [block, K step, BM routes] (W13: route_scales_kernel's
-// copy of the x scales; W2: the a2 scales as a W13 launch with kA2ScalesInRoutes
-// wrote them), so a K step's BM scales are one contiguous load.
-constexpr int kActScalesInRoutes = 1, kA2ScalesInRoutes = 2;
-
-// The fp8 layer's x scales in route order for the 256-route W13 GEMM: out
+// The fp8 layer's x scales in route order for the grouped W13 GEMMs: out
 // [(b * KS + k) * bm + j] = scale k of the token of route sorted[b * bm + j]
 // (padding rows: token 0), over the used blocks (ntpp).  The W13 tiles then
-// read one K step's scales of their 256 routes from 1 KiB in a row instead
+// read one K step's scales of their BM routes from BM * 4 bytes in a row instead
 // of one gathered token row per lane (DeepSeek-V3 T=4096: 256 lines a step).
 // One thread per route row: its token's KS scales in 16-byte loads (KS % 4
 // == 0, the host's condition), each K step's store coalesced across the
@@ -2205,14 +2213,14 @@ static int w2_splits(int64_t numel, int E, int64_t H, int64_t I, int kind) {
 static size_t al256(size_t x) { return (x + 255) / 256 * 256; }
 
 // Stage scratch: fp32 split-K partials of the decode GEMVs (none for GEMMs).
-// Bytes of route_scales_kernel's copy for the fp8 256-route W13 (0 where it
-// is not used): cap rows of H / 128 scales.
+// Bytes of route_scales_kernel's copy for the fp8 grouped W13 on 128- and
+// 256-route blocks (0 where it is not used): cap rows of H / 128 scales.
 static size_t route_scales_bytes(int64_t cap, int64_t H, int block_m, int kind) {
   const size_t b = static_cast<size_t>(cap) * (H / 128) * 4;
-  return kind == kFp8 && block_m == kMoeBigBM && (H / 128) % 4 == 0 && b < (1ull << 31) ? b : 0;
+  return kind == kFp8 && (block_m == kMoeBigBM || block_m == kMoeBM) && (H / 128) % 4 == 0 && b < (1ull << 31) ? b : 0;
 }
 static size_t w13_scratch(int64_t numel, int E, int64_t H, int64_t I, int block_m, int kind) {
-  if (block_m == kMoeBigBM) return route_scales_bytes(numel + static_cast<int64_t>(E) * (block_m - 1), H, block_m, kind);
+  if (block_m != kGemvBlock) return route_scales_bytes(numel + static_cast<int64_t>(E) * (block_m - 1), H, block_m, kind);
   if (block_m != kGemvBlock) return 0;
   return al256(static_cast<size_t>(w13_splits(numel, E, H, I, kind)) * numel * 2 * I * 4);
 }
@@ -2508,9 +2516,10 @@ static int launch_w13(const uint8_t* xa, const float* xs, const float* xcorr, in
     if (rc) return rc;
     const int64_t abytes = static_cast<int64_t>(T) * H * KindBytes<KIND>::kAct / KindBytes<KIND>::kElems;
     VMAMD_REQUIRE(abytes < (1ll << 31), "moe w13: activations past 2 GiB for the grouped GEMM");
+    const int order = (xs_routes ? kActScalesInRoutes : 0) | (a2s_routes ? kA2ScalesInRoutes : 0);
     moe_gemm_dma_kernel<KIND, true><<<xcd_grid(tiles), 512, MoePipe<KIND>::kLds, st>>>(
-        xa, static_cast<int>(abytes), xs, topk, H, sorted, offs, ntpp, eids, E, numel, tiles, w13,
-        static_cast<const float*>(w13_s), 2 * I, I, limit, route_w, a2, a2s, nullptr);
+        xa, static_cast<int>(abytes), xs_routes ? xs_routes : xs, topk, H, sorted, offs, ntpp, eids, E, numel,
+        tiles, w13, static_cast<const float*>(w13_s), 2 * I, I, limit, route_w, a2, a2s, nullptr, order);
   }
   return check_launch("moe w13 (gemm)");
 }
@@ -2601,7 +2610,7 @@ static int launch_w2(const uint8_t* a2, const float* a2s, const float* a2corr, i
     VMAMD_REQUIRE(abytes < (1ll << 31), "moe w2: activations past 2 GiB for the grouped GEMM");
     moe_gemm_dma_kernel<KIND, false><<<xcd_grid(tiles), 512, MoePipe<KIND>::kLds, st>>>(
         a2, static_cast<int>(abytes), a2s, 1, I, sorted, offs, ntpp, eids, E, numel, tiles, w2, static_cast<const float*>(w2_s), H,
-        I, 0.f, route_w, nullptr, nullptr, y);
+        I, 0.f, route_w, nullptr, nullptr, y, a2s_routes ? kActScalesInRoutes : 0);
   }
   return check_launch("moe w2 (gemm)");
 }
@@ -2899,7 +2908,7 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   float* xcorr = KIND == kW4 ? reinterpret_cast<float*>(ws + L.xcorr) : nullptr;
   uint32_t* wst13 = nullptr;  // kW4 grouped GEMMs: the transposed weight scales
   uint32_t* wst2 = nullptr;
-  float* xsr = nullptr;  // kFp8 256-route W13: x scales in route order
+  float* xsr = nullptr;  // kFp8 grouped W13: x scales in route order
   float* a2corr = KIND == kW4 ? reinterpret_cast<float*>(ws + L.a2corr) : nullptr;
   if constexpr (KIND == kFp8) {  // quantiser and alignment in one launch
     uint8_t* xq = ws + L.xq;
@@ -2949,9 +2958,9 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
   // kW4 prefill: bf16 activation, quantised per row below (the decode path
   // writes the quantised a2 directly).
   uint8_t* act_out = KIND == kW4 && bm != kGemvBlock ? ws + L.abf : a2;
-  // kFp8 on 256-route blocks: W13 writes the a2 scales in route order and W2
-  // reads them so (the a2 scales stay inside this call).
-  const bool a2s_routes = KIND == kFp8 && bm == kMoeBigBM;
+  // kFp8 grouped GEMMs: W13 writes the a2 scales in route order and W2 reads
+  // them so (the a2 scales stay inside this call).
+  const bool a2s_routes = KIND == kFp8 && (bm == kMoeBigBM || bm == kMoeBM);
   rc = launch_w13<KIND>(xa, xs, xcorr, t, h, topk, sorted, cap, bm, offs, ntpp, active, nact,
                         static_cast<const uint8_t*>(w13), w13_s, E, i, swiglu_limit, w13_rw, act_out,
                         a2s, a2corr, scratch, st, eids, native, wst13, xsr, a2s_routes);
@@ -2996,7 +3005,7 @@ static int stage_w13(const char* who, const void* xa, const float* xs, int64_t T
   VMAMD_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(xa) % 16 == 0 && reinterpret_cast<uintptr_t>(a2) % 16 == 0,
                 "%s: activations, a2 and workspace must be 16-byte aligned", who);
-  // The fp8 256-route W13 reads its x scales in route order when the
+  // The fp8 grouped W13 reads its x scales in route order when the
   // workspace holds the copy for this capacity (route_scales_kernel).
   float* xsr = nullptr;
   const size_t rsb = route_scales_bytes(capacity, H, block_m, KIND);
