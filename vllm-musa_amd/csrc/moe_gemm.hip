@@ -2918,7 +2918,9 @@ static int fused_layer(const char* who, const void* x, int64_t T, int64_t H, con
     if (rc) return rc;
     xa = xq;
     xs = xsw;
-    if (route_scales_bytes(cap, H, bm, KIND) > 0) {
+    // 128-route blocks: the copy from 32 routes per expert (fewer: the blocks
+    // are mostly padding and the launch costs what the loads save).
+    if (route_scales_bytes(cap, H, bm, KIND) > 0 && (bm != kMoeBM || numel >= 32ll * E)) {
       xsr = reinterpret_cast<float*>(ws + L.xsr);
       route_scales_kernel<<<static_cast<int>((cap + 255) / 256), 256, 0, st>>>(xsw, sorted, ntpp, numel, topk,
                                                                              static_cast<int>(H / 128), bm, xsr);
